@@ -1,0 +1,129 @@
+/* qpack_hip.h - C ABI of the MI355X (gfx950) Llama-family token loop.
+ *
+ * This is the drop-in boundary for qpack's GPU model (`LlamaCuda`, /root/reference/src/model_llama_cuda.cu:445-632),
+ * selected by QPACK_DEVICE in load_model (/root/reference/src/model_llama.cpp:221-235).  Each model entry point replaces
+ * one method of the C++ interface qp::Model (/root/reference/include/qpack/qpack.h:128-171); the reference-side adapter
+ * a maintainer adds (a qp::Model subclass forwarding to these functions) is shown in INTEGRATION.md.
+ *
+ * Conventions
+ *   - Every function returns int status: 0 = ok, -1 = error; qph_last_error() gives the calling thread's message.  The C++
+ *     adapter turns a non-zero status into std::runtime_error, the reference's error convention.
+ *   - Plain pointers and sizes only.  Host pointers unless a parameter says "device".
+ *   - A model is not re-entrant: one host thread per model at a time (the reference's contract; qpack-server serialises
+ *     through a mutex, /root/reference/tools/qpack-server.cpp:31).  Each model owns one HIP stream on the current device.
+ *   - Weights are copied into HBM by qph_create / qph_load; the caller's buffers (or the mmap) may be released afterwards.
+ */
+#ifndef QPACK_HIP_H
+#define QPACK_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct qph_model qph_model;
+
+/* tensor kinds (the QPACK2 kinds the Llama path reads, /root/reference/QPACK2.md table) */
+enum { QPH_F32 = 0, QPH_Q8 = 1, QPH_Q4 = 2 };
+
+/* Model config: the config.json keys read by the reference (/root/reference/src/model_llama.cpp:21-27). */
+typedef struct {
+  int hidden, layers, heads, kv_heads, head_dim, ffn, vocab;
+  int tied;       /* tie_embeddings: the output head is `embed` */
+  int qkv_bias;   /* bq / bk / bv present */
+  int max_pos;    /* max_position_embeddings */
+  float rms_eps;
+  double rope_theta;
+} qph_config;
+
+/* One tensor with the canonical name (/root/reference/python/qpack/convert_llama.py:5-11):
+ * q8: data int8 [rows, cols], scale f32 [rows];  q4: data u8 [rows, cols/2], scale fp16 [rows, cols/32];  f32: data only. */
+typedef struct {
+  const char *name;
+  int kind;
+  int64_t rows, cols;
+  const void *data;
+  const void *scale;
+} qph_tensor;
+
+const char *qph_last_error(void);
+/* number of visible HIP devices (0 on a machine without a GPU) */
+int qph_device_count(int *n);
+
+/* ---- construction (LlamaCuda::LlamaCuda, model_llama_cuda.cu:447-484; make_llama_cuda, qpack.h:175) */
+/* max_ctx <= 0 picks min(4096, max_pos) like the reference (model_llama.cpp:27). */
+int qph_create(const qph_config *cfg, const qph_tensor *tensors, int n_tensors, int max_ctx, qph_model **out);
+/* load_model(path, max_ctx) for arch "llama" (model_llama.cpp:221-235): mmap a QPACK1/QPACK2 file, read config.json and
+ * the manifest, upload to HBM */
+int qph_load(const char *path, int max_ctx, qph_model **out);
+void qph_destroy(qph_model *m);   /* ~LlamaCuda */
+
+/* ---- qp::Model queries (qpack.h:131-134, :164) */
+int qph_vocab(const qph_model *m);
+int qph_hidden(const qph_model *m);
+int qph_max_ctx(const qph_model *m);
+int qph_pos(const qph_model *m);
+int qph_config_of(const qph_model *m, qph_config *out);
+
+/* ---- token loop */
+/* Model::step (qpack.h:136): want 0 = state only, 1 = logits (vocab floats into out), 2 = final normed hidden state
+ * (hidden floats into out).  Errors: token out of range, context full (model_llama.cpp:169-170). */
+int qph_step(qph_model *m, int token, int want, float *out);
+/* Model::prefill (qpack.h:138): n prompt tokens, `want` applies to the last one */
+int qph_prefill(qph_model *m, const int *tokens, int n, int want, float *out);
+/* Model::greedy_run (qpack.h:143): out[i] = argmax after feeding token i; token i+1 = out[i].  Runs on the device with
+ * no host round trip per token; returns the number of tokens produced in *produced (fewer when the context fills). */
+int qph_greedy_run(qph_model *m, int token, int n, int *out, int *produced);
+/* Model::prefill_all (qpack.h:152): logits of every position, n x vocab floats */
+int qph_prefill_all(qph_model *m, const int *tokens, int n, float *logits);
+/* Model::reset (qpack.h:150) */
+int qph_reset(qph_model *m);
+/* Model::rewind (qpack.h:160): keep the first pos tokens (0 <= pos <= current); *ok = 0 when pos is out of range */
+int qph_rewind(qph_model *m, int pos, int *ok);
+/* Model::checkpoint / rollback (qpack.h:157-158, model_llama.cpp:47-48): the position alone */
+int qph_set_pos(qph_model *m, int pos);
+/* Model::snapshot / restore (qpack.h:162-163) in the reference layout (model_llama.cpp:55-63): int32 pos, then per layer
+ * the first pos rows of the fp16 K cache followed by the first pos rows of the fp16 V cache.  qph_snapshot_size gives the
+ * byte count for the current position. */
+int qph_snapshot_size(const qph_model *m, int64_t *bytes);
+int qph_snapshot(qph_model *m, uint8_t *buf, int64_t cap);
+int qph_restore(qph_model *m, const uint8_t *buf, int64_t n);
+
+/* ---- measurement (no reference counterpart: qpack-bench times with the host clock, tools/qpack-bench.cpp:40-47) */
+/* Runs n greedy decode steps from token/position as greedy_run does and reports the HIP-event time of the whole run
+ * on the model's stream (*ms). */
+int qph_time_greedy(qph_model *m, int token, int n, float *ms);
+/* Replays one decode-step kernel `iters` times on the model's stream and reports its mean HIP-event duration and its
+ * algorithmic HBM bytes per launch.  which: 0 = layer-0 fused gate/up matvec, 1 = layer-0 down matvec, 2 = layer-0 qkv
+ * matvec, 3 = layer-0 wo matvec, 4 = output head matvec, 5 = layer-0 attention at the current position. */
+int qph_time_kernel(qph_model *m, int which, int iters, float *ms, double *bytes);
+
+/* ---- parity hooks (no reference counterpart; the int32 contract of rows_q8 / rows_q4, kernels_x86.cpp:55-106) */
+/* Runs the product's matvec kernel on one matrix (host buffers in, host buffers out): activation quantisation of x,
+ * y[rows] = W x, and, when sums != NULL, the exact int32 accumulators: q8 one per (row, 128-column block)
+ * [rows, cols/128], q4 one per (row, 32-column group) [rows, cols/32].  xq / bs (optional) receive the int16 activations
+ * and the per-block scales the kernel used. */
+int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int cols, const float *x, float *y,
+                      int32_t *sums, int16_t *xq, float *bs);
+/* Runs the product's prefill matrix kernel: Y[B, rows] = X[B, cols] W^T with per-token activation quantisation. */
+int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y);
+
+/* ---- synthetic models (no reference counterpart: the reference's files come from convert_llama.py / qpack-quantize).
+ * Writes a seeded random-init Llama-family QPACK2 file; see qpack_amd/csrc/host/synth.cpp for the exact rules. */
+typedef struct {
+  int hidden, layers, heads, kv_heads, head_dim, ffn, vocab;
+  int tied, qkv_bias, max_pos;
+  int q4;        /* 0: every matrix q8; 1: layer matrices q4 (groups of 32), embed / head q8 */
+  int q4m_alt;   /* with q4: wv and the w_down of even layers stay q8 */
+  float rms_eps;
+  double rope_theta;
+  float std;     /* weight standard deviation (0.02) */
+  uint64_t seed;
+  char model_type[32];
+} qph_synth_spec;
+int qph_synth_write(const qph_synth_spec *spec, const char *path, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QPACK_HIP_H */

@@ -1,0 +1,12 @@
+"""qpack_amd: the MI355X (gfx950) Llama-family token loop of qpack behind a C ABI.
+
+  HipLlama.load(path)   - a QPACK1/QPACK2 file on the GPU (the qp::Model surface: step / prefill / greedy_run / ...)
+  write_synthetic(...)  - seeded random-init QPACK2 models of the BASELINE shapes
+  kernel_matvec(...)    - the product's matvec kernel on one matrix, with its exact int32 accumulators (parity hook)
+"""
+from ._lib import LIB_PATH, QPH_F32, QPH_Q4, QPH_Q8, QphError, device_count, lib
+from .model import HipLlama, kernel_matvec
+from .synth import CONFIGS, Shape, write_synthetic
+
+__all__ = ["HipLlama", "kernel_matvec", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
+           "QPH_F32", "QPH_Q8", "QPH_Q4"]

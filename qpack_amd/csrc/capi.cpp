@@ -1,0 +1,187 @@
+// extern "C" entry points of libqpack_hip.so (declared in include/qpack_hip.h).  Each one catches every C++ exception
+// and turns it into status -1 plus a thread-local message, so no exception crosses the C boundary.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/qpack_hip.h"
+#include "hip/launch.hpp"
+#include "hip/model.hpp"
+#include "host/container.hpp"
+#include "host/synth.hpp"
+
+struct qph_model {
+  std::unique_ptr<qph::HipLlama> m;
+};
+
+static thread_local std::string g_err;
+
+#define QPH_API_TRY(...)                  \
+  try {                                   \
+    __VA_ARGS__;                          \
+    return 0;                             \
+  } catch (std::exception & e) {          \
+    g_err = e.what();                     \
+    return -1;                            \
+  } catch (...) {                         \
+    g_err = "unknown C++ exception";      \
+    return -1;                            \
+  }
+
+static void need(const void *p, const char *what) {
+  if (!p) throw std::invalid_argument(std::string(what) + " is NULL");
+}
+static void hck(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string("hip: ") + hipGetErrorString(e) + " (" + what + ")");
+}
+
+extern "C" {
+
+const char *qph_last_error(void) { return g_err.c_str(); }
+
+int qph_device_count(int *n) {
+  QPH_API_TRY({
+    need(n, "n"); int c = 0;
+    if (hipGetDeviceCount(&c) != hipSuccess) c = 0;
+    *n = c;
+  });
+}
+
+int qph_create(const qph_config *cfg, const qph_tensor *tensors, int n_tensors, int max_ctx, qph_model **out) {
+  QPH_API_TRY({
+    need(cfg, "cfg"); need(tensors, "tensors"); need(out, "out");
+    *out = nullptr;
+    auto *h = new qph_model;
+    try { h->m.reset(new qph::HipLlama(*cfg, tensors, n_tensors, max_ctx)); } catch (...) { delete h; throw; }
+    *out = h;
+  });
+}
+
+int qph_load(const char *path, int max_ctx, qph_model **out) {
+  QPH_API_TRY({
+    need(path, "path"); need(out, "out");
+    *out = nullptr;
+    qph::Container c(path);
+    const qph::Json &j = c.config();
+    if (j["arch"].string() != "llama") throw std::runtime_error(std::string(path) + ": arch '" + j["arch"].string() + "' is not a Llama-family model");
+    qph_config cfg{};
+    cfg.hidden = (int)j["hidden_size"].integer(0); cfg.layers = (int)j["num_hidden_layers"].integer(0);
+    cfg.heads = (int)j["num_attention_heads"].integer(0); cfg.kv_heads = (int)j["num_key_value_heads"].integer(0);
+    cfg.head_dim = (int)j["head_dim"].integer(cfg.heads > 0 ? cfg.hidden / cfg.heads : 0);
+    cfg.ffn = (int)j["intermediate_size"].integer(0); cfg.vocab = (int)j["vocab_size"].integer(0);
+    cfg.rms_eps = (float)j["rms_norm_eps"].number(1e-6); cfg.rope_theta = j["rope_theta"].number(10000);
+    cfg.tied = j["tie_embeddings"].boolean(false) ? 1 : 0;
+    cfg.max_pos = (int)j["max_position_embeddings"].integer(1 << 20);
+    std::vector<qph_tensor> ts;
+    for (const qph::Json &e : c.manifest()["tensors"].arr) {
+      const qph::TensorView &t = c.at(e["name"].string());
+      if (t.kind == qph::Kind::F16) continue;   // 2-D f16 matrices are not on the HIP path; a required one is reported missing
+      qph_tensor q{}; q.name = t.name.c_str(); q.data = t.data; q.scale = t.scale;
+      if (t.shape.size() == 1) { q.rows = t.shape[0]; q.cols = 1; } else { q.rows = t.rows(); q.cols = t.cols(); }
+      q.kind = t.kind == qph::Kind::Q8 ? QPH_Q8 : t.kind == qph::Kind::Q4 ? QPH_Q4 : QPH_F32;
+      ts.push_back(q);
+    }
+    cfg.qkv_bias = c.get("layers.0.bq") ? 1 : 0;
+    auto *h = new qph_model;
+    try { h->m.reset(new qph::HipLlama(cfg, ts.data(), (int)ts.size(), max_ctx)); } catch (...) { delete h; throw; }
+    *out = h;
+  });
+}
+
+void qph_destroy(qph_model *m) { delete m; }
+
+int qph_vocab(const qph_model *m) { return m ? m->m->config().vocab : -1; }
+int qph_hidden(const qph_model *m) { return m ? m->m->config().hidden : -1; }
+int qph_max_ctx(const qph_model *m) { return m ? m->m->max_ctx() : -1; }
+int qph_pos(const qph_model *m) { return m ? m->m->pos() : -1; }
+int qph_config_of(const qph_model *m, qph_config *out) { QPH_API_TRY({ need(m, "model"); need(out, "out"); *out = m->m->config(); }); }
+
+int qph_step(qph_model *m, int token, int want, float *out) {
+  QPH_API_TRY({
+    need(m, "model");
+    if (want < 0 || want > 2) throw std::invalid_argument("want must be 0, 1 or 2");
+    if (want) need(out, "out");
+    m->m->step(token, want, out);
+  });
+}
+int qph_prefill(qph_model *m, const int *tokens, int n, int want, float *out) {
+  QPH_API_TRY({
+    need(m, "model"); need(tokens, "tokens");
+    if (want < 0 || want > 2) throw std::invalid_argument("want must be 0, 1 or 2");
+    if (want) need(out, "out");
+    m->m->prefill(tokens, n, want, out);
+  });
+}
+int qph_greedy_run(qph_model *m, int token, int n, int *out, int *produced) {
+  QPH_API_TRY({
+    need(m, "model"); need(out, "out");
+    const int r = m->m->greedy_run(token, n, out);
+    if (produced) *produced = r;
+  });
+}
+int qph_prefill_all(qph_model *m, const int *tokens, int n, float *logits) {
+  QPH_API_TRY({ need(m, "model"); need(tokens, "tokens"); need(logits, "logits"); m->m->prefill_all(tokens, n, logits); });
+}
+int qph_reset(qph_model *m) { QPH_API_TRY({ need(m, "model"); m->m->reset(); }); }
+int qph_rewind(qph_model *m, int pos, int *ok) {
+  QPH_API_TRY({ need(m, "model"); const bool r = m->m->rewind(pos); if (ok) *ok = r ? 1 : 0; });
+}
+int qph_set_pos(qph_model *m, int pos) { QPH_API_TRY({ need(m, "model"); m->m->set_pos(pos); }); }
+int qph_snapshot_size(const qph_model *m, int64_t *bytes) { QPH_API_TRY({ need(m, "model"); need(bytes, "bytes"); *bytes = m->m->snapshot_size(); }); }
+int qph_snapshot(qph_model *m, uint8_t *buf, int64_t cap) { QPH_API_TRY({ need(m, "model"); need(buf, "buf"); m->m->snapshot(buf, cap); }); }
+int qph_restore(qph_model *m, const uint8_t *buf, int64_t n) { QPH_API_TRY({ need(m, "model"); need(buf, "buf"); m->m->restore(buf, n); }); }
+
+int qph_time_greedy(qph_model *m, int token, int n, float *ms) {
+  QPH_API_TRY({ need(m, "model"); need(ms, "ms"); *ms = m->m->time_greedy(token, n); });
+}
+int qph_time_kernel(qph_model *m, int which, int iters, float *ms, double *bytes) {
+  QPH_API_TRY({ need(m, "model"); need(ms, "ms"); need(bytes, "bytes"); *ms = m->m->time_kernel(which, iters, bytes); });
+}
+
+int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int cols, const float *x, float *y,
+                      int32_t *sums, int16_t *xq, float *bs) {
+  QPH_API_TRY({
+    need(q, "q"); need(scale, "scale"); need(x, "x"); need(y, "y");
+    if (rows <= 0 || cols <= 0 || cols % 128) throw std::invalid_argument("matvec: rows > 0 and cols a positive multiple of 128 required");
+    if (kind != QPH_Q8 && kind != QPH_Q4) throw std::invalid_argument("matvec: kind must be QPH_Q8 or QPH_Q4");
+    const size_t qb = kind == QPH_Q8 ? (size_t)rows * cols : (size_t)rows * cols / 2;
+    const size_t sb = kind == QPH_Q8 ? 4ull * rows : 2ull * rows * (cols / 32);
+    const size_t nsum = kind == QPH_Q8 ? (size_t)rows * (cols / 128) : (size_t)rows * (cols / 32);
+    std::vector<void *> bufs;
+    auto alloc = [&](size_t n) { void *p = nullptr; hck(hipMalloc(&p, n), "hipMalloc"); bufs.push_back(p); return p; };
+    try {
+      void *dq = alloc(qb), *ds = alloc(sb); float *dx = (float *)alloc(4ull * cols), *dy = (float *)alloc(4ull * rows);
+      int32_t *dsum = sums ? (int32_t *)alloc(4 * nsum) : nullptr;
+      int16_t *dxq = xq ? (int16_t *)alloc(2ull * cols) : nullptr;
+      float *dbs = bs ? (float *)alloc(4ull * (cols / 128)) : nullptr;
+      hck(hipMemcpy(dq, q, qb, hipMemcpyHostToDevice), "upload q");
+      hck(hipMemcpy(ds, scale, sb, hipMemcpyHostToDevice), "upload scale");
+      hck(hipMemcpy(dx, x, 4ull * cols, hipMemcpyHostToDevice), "upload x");
+      qph::MvArgs a{}; a.m[0].q = dq; a.m[0].s = ds; a.m[0].rows = rows; a.m[0].cols = cols; a.m[0].kind = kind == QPH_Q8 ? qph::MK_Q8 : qph::MK_Q4;
+      a.nseg = 1; a.x = dx; a.out[0] = dy; a.dbg_sums = dsum; a.dbg_xq = dxq; a.dbg_bs = dbs;
+      qph::mv_plan(a, qph::EPI_STORE);
+      hck(qph::launch_matvec(qph::PRO_QUANT, qph::EPI_STORE, a, 1024, nullptr), "launch matvec");
+      hck(hipDeviceSynchronize(), "matvec");
+      hck(hipMemcpy(y, dy, 4ull * rows, hipMemcpyDeviceToHost), "download y");
+      if (sums) hck(hipMemcpy(sums, dsum, 4 * nsum, hipMemcpyDeviceToHost), "download sums");
+      if (xq) hck(hipMemcpy(xq, dxq, 2ull * cols, hipMemcpyDeviceToHost), "download xq");
+      if (bs) hck(hipMemcpy(bs, dbs, 4ull * (cols / 128), hipMemcpyDeviceToHost), "download bs");
+    } catch (...) { for (void *p : bufs) (void)hipFree(p); throw; }
+    for (void *p : bufs) (void)hipFree(p);
+  });
+}
+
+int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y) {
+  QPH_API_TRY({ (void)kind; (void)q; (void)scale; (void)rows; (void)cols; (void)X; (void)B; (void)Y;
+                throw std::runtime_error("qph_kernel_matmul: the batched prefill kernel is not built yet"); });
+}
+
+int qph_synth_write(const qph_synth_spec *spec, const char *path, int threads) {
+  QPH_API_TRY({ need(spec, "spec"); need(path, "path"); qph::synth_write(*spec, path, threads); });
+}
+
+}  // extern "C"

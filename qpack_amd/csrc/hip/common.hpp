@@ -1,0 +1,83 @@
+// Shared device-side definitions of the gfx950 token-loop kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qph {
+
+constexpr int kQB = 128;            // activation block (/root/reference/src/kernels_impl.h:13)
+constexpr float kActMax = 32767.f;  // x86 kActMax (/root/reference/src/kernels_impl.h:19)
+constexpr int kWave = 64;
+
+enum MatKind : int { MK_F32 = 0, MK_Q8 = 1, MK_Q4 = 2 };
+
+// a weight matrix resident in HBM, row-major as in the QPACK2 file
+struct DMat {
+  const void *q;       // q8: int8 [rows, cols]; q4: u8 [rows, cols / 2]; f32: float [rows, cols]
+  const void *s;       // q8: f32 [rows]; q4: fp16 [rows, cols / 32]
+  int rows, cols, kind;
+};
+
+// device-resident decode control block: the token to embed, its position, and the greedy output cursor
+struct Ctl {
+  int tok;
+  int pos;
+  int n_out;   // greedy tokens written so far in this run
+  int pad;
+};
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// exp256 of /root/reference/src/kernels_x86.cpp:406-417 for one lane: clamp to [-87, 88], k = rint(x log2 e),
+// two-constant reduction, degree-6 polynomial, scale by 2^k.  Written with explicit fmaf so it is bit-identical.
+__device__ __forceinline__ float exp_poly(float x) {
+  x = x > -87.f ? x : -87.f;
+  x = 88.f > x ? x : 88.f;
+  const float k = __builtin_rintf(x * 1.44269504088896341f);
+  const float r = __builtin_fmaf(-k, 0.693359375f, __builtin_fmaf(-k, -2.12194440e-4f, x));
+  float p = 1.9875691500e-4f;
+  p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+  p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+  p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+  p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+  p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+  p = __builtin_fmaf(p * r, r, r + 1.f);
+  const int e = ((int)k + 127) << 23;
+  return p * __builtin_bit_cast(float, e);
+}
+
+// DPP cross-lane moves (bound_ctrl, full row / bank masks)
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true)); }
+constexpr int kDppQuadXor1 = 0xb1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4e;       // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;    // row_half_mirror: lane i <-> 7 - i within 8 lanes
+
+// sum over aligned groups of 8 lanes, result in every lane of the group (exact for integers)
+__device__ __forceinline__ int sum8_i(int v) {
+  v += dpp_i<kDppQuadXor1>(v);
+  v += dpp_i<kDppQuadXor2>(v);
+  v += dpp_i<kDppHalfMirror>(v);
+  return v;
+}
+__device__ __forceinline__ float max8_f(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  return v;
+}
+
+// full-wave reductions (shuffles; not on the hot inner loops)
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+}  // namespace qph

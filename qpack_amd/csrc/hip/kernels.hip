@@ -1,0 +1,552 @@
+// gfx950 kernels of the qpack Llama decode step.
+//
+// Matvec (the HBM-bound hot path): y = W x with W int8 (q8, f32 row scale) or int4 (q4, fp16 scale per 32 columns) and
+// x quantised to int16 per 128-column block exactly as quant_rows does (/root/reference/src/kernels.cpp:17-31).
+//   - Each workgroup first builds the activation in LDS as two byte planes, h = q >> 8 (signed) and l = q & 255
+//     (unsigned), so one 4-byte weight word costs one v_dot4_i32_i8 (w . h) and one v_dot4_u32_u8 ((w ^ 0x80) . l):
+//     w . q = 256 (w . h) + (w + 128) . l - 128 sum(l)   (q8)     nib . q = 256 (nib . h) + nib . l   (q4, nib = q + 8)
+//     Every int32 accumulator is therefore exact and equal to the reference's _mm256_madd_epi16 sums.
+//   - Weights stream once, coalesced: lane i of a wave reads bytes [16 i, 16 i + 16) of each 1 KiB row chunk.
+//   - q8: the eight lanes of a 128-column block are summed with DPP; the block sums go to LDS and one lane per row
+//     replays rows_q8's float epilogue in block order (acc = fma(bs[b], (float)isum, acc); y = acc * scale, kernels_x86.cpp:
+//     57-69), so q8 rows are bit-identical to the reference given the same activation.
+//   - q4: one lane owns one 32-column group (16 bytes); per-group exact int32 sums, fma with f16(scale) * bs in the lane,
+//     then a fixed-order wave reduction (float order differs from rows_q4's 8-lane split: within the logit tolerance).
+// The prologue optionally fuses RMSNorm (PRO_NORM); epilogues fuse bias, residual add, SwiGLU and the argmax partials.
+#include <math.h>
+
+#include "launch.hpp"
+
+namespace qph {
+
+constexpr int kThreads = 256;
+
+// ------------------------------------------------------------------ LDS activation layout
+struct ActView {
+  int8_t *xh;    // [cols] high bytes (signed)
+  uint8_t *xl;   // [cols] low bytes (unsigned)
+  float *bs;     // [nb] block scales
+  int *lsum;     // [nb] sum of the low bytes per 128-column block
+  int *gsum;     // [cols / 32] sum of q per 32-column group
+  float *red;    // [16] reduction scratch
+  int *sums;     // [waves][slots][nbp] q8 block sums
+  int nbp;
+};
+
+__host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
+
+__device__ inline ActView act_view(char *smem, int cols) {
+  ActView v; const int nb = cols / kQB, G = cols / 32;
+  v.nbp = round_up(nb, 4);
+  v.xh = (int8_t *)smem;
+  v.xl = (uint8_t *)(smem + cols);
+  v.bs = (float *)(smem + 2 * cols);
+  v.lsum = (int *)(v.bs + v.nbp);
+  v.gsum = v.lsum + v.nbp;
+  v.red = (float *)(v.gsum + round_up(G, 4));
+  v.sums = (int *)(v.red + 16);
+  return v;
+}
+size_t mv_lds_bytes(int cols) {
+  const int nb = cols / kQB, G = cols / 32, nbp = round_up(nb, 4);
+  return (size_t)2 * cols + 4 * (size_t)nbp * 2 + 4 * (size_t)round_up(G, 4) + 16 * 4 + 4 * (size_t)kMvWaves * kMvSlots * nbp;
+}
+
+// 1 / sqrt(sum(x^2) / n + eps) over the workgroup: per-thread fma sums over a 256-stride, a butterfly per wave and the
+// four wave sums added in a fixed order.  (The reference sums sequentially, kernels.cpp:185; the order differs.)
+__device__ float block_rms_inv(const float *x, int n, float eps, float *red) {
+  float s = 0;
+  for (int i = threadIdx.x; i < n; i += kThreads) s = __builtin_fmaf(x[i], x[i], s);
+  s = wave_sum(s);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = s;
+  __syncthreads();
+  const float ss = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return 1.f / sqrtf(ss / (float)n + eps);
+}
+
+// builds the int16 activation of x (optionally RMSNorm(x) * w first) in LDS.  Eight lanes own a 128-column block,
+// 16 columns each.  Arithmetic of quant_rows: mx = max |v|, isx = mx > 0 ? 32767 / mx : 0, bs = mx / 32767,
+// q = rint(v * isx).
+template <int PRO>
+__device__ void build_act(const float *x, const float *w, float eps, int cols, const ActView &a) {
+  float inv = 1.f;
+  if (PRO == PRO_NORM) inv = block_rms_inv(x, cols, eps, a.red);
+  const int nb = cols / kQB, tid = threadIdx.x, sub = tid & 7;
+  for (int b0 = 0; b0 < nb; b0 += kThreads / 8) {
+    const int b = b0 + (tid >> 3);
+    if (b < nb) {
+      const int c0 = b * kQB + sub * 16;
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float4 t = *(const float4 *)(x + c0 + 4 * k);
+        v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+      }
+      if (PRO == PRO_NORM) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float4 t = *(const float4 *)(w + c0 + 4 * k);
+          v[4 * k] = v[4 * k] * inv * t.x; v[4 * k + 1] = v[4 * k + 1] * inv * t.y;
+          v[4 * k + 2] = v[4 * k + 2] * inv * t.z; v[4 * k + 3] = v[4 * k + 3] * inv * t.w;
+        }
+      }
+      float m = 0;
+#pragma unroll
+      for (int k = 0; k < 16; k++) m = fmaxf(m, fabsf(v[k]));
+      m = max8_f(m);
+      const float isx = m > 0 ? kActMax / m : 0.f;
+      if (sub == 0) a.bs[b] = m / kActMax;
+      uint32_t hw[4], lw[4]; int ls = 0, gs = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint32_t hh = 0, ll = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int q = (int)__builtin_rintf(v[4 * k + j] * isx);
+          hh |= (uint32_t)((q >> 8) & 0xff) << (8 * j);
+          ll |= (uint32_t)(q & 0xff) << (8 * j);
+          ls += q & 0xff; gs += q;
+        }
+        hw[k] = hh; lw[k] = ll;
+      }
+      *(uint4 *)(a.xh + c0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      *(uint4 *)(a.xl + c0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      ls = sum8_i(ls);
+      if (sub == 0) a.lsum[b] = ls;
+      gs += dpp_i<kDppQuadXor1>(gs);
+      if ((sub & 1) == 0) a.gsum[c0 / 32] = gs;
+    }
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------ dot products of row slots
+// one 16-byte weight load (global_load_dwordx4)
+__device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
+
+// q8: NS rows against the LDS activation; block sums (already corrected by -128 sum(l)) go to sums[s * nbp + b].
+template <int NS>
+__device__ __forceinline__ void dot_q8(const int8_t *const rowp[NS], int cols, const ActView &a, int lane, int *sums) {
+  constexpr int U = 4;
+  const int nch = (cols + 1023) >> 10;
+  for (int c0 = 0; c0 < nch; c0 += U) {
+    uint4 w[U][NS];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int col = (c0 + u) * 1024 + lane * 16;
+#pragma unroll
+      for (int s = 0; s < NS; s++)
+        w[u][s] = (c0 + u < nch && col < cols) ? ld16(rowp[s] + col) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int c = c0 + u;
+      if (c >= nch) break;
+      const int col = c * 1024 + lane * 16;
+      const bool act = col < cols;
+      const uint4 h = act ? *(const uint4 *)(a.xh + col) : make_uint4(0, 0, 0, 0);
+      const uint4 l = act ? *(const uint4 *)(a.xl + col) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int s = 0; s < NS; s++) {
+        const uint4 ww = w[u][s];
+        int A = __builtin_amdgcn_sdot4((int)ww.x, (int)h.x, 0, false);
+        A = __builtin_amdgcn_sdot4((int)ww.y, (int)h.y, A, false);
+        A = __builtin_amdgcn_sdot4((int)ww.z, (int)h.z, A, false);
+        A = __builtin_amdgcn_sdot4((int)ww.w, (int)h.w, A, false);
+        uint32_t B = __builtin_amdgcn_udot4(ww.x ^ 0x80808080u, l.x, 0u, false);
+        B = __builtin_amdgcn_udot4(ww.y ^ 0x80808080u, l.y, B, false);
+        B = __builtin_amdgcn_udot4(ww.z ^ 0x80808080u, l.z, B, false);
+        B = __builtin_amdgcn_udot4(ww.w ^ 0x80808080u, l.w, B, false);
+        const int p = sum8_i(A * 256 + (int)B);
+        if (act && (lane & 7) == 0) {
+          const int b = c * 8 + (lane >> 3);
+          sums[s * a.nbp + b] = p - 128 * a.lsum[b];
+        }
+      }
+    }
+  }
+}
+
+// q4: NS rows; returns each row's value (identical in every lane).  Optional exact group sums into dbg[s][g].
+template <int NS>
+__device__ __forceinline__ void dot_q4(const uint8_t *const rowq[NS], const uint16_t *const rows_s[NS], int cols, const ActView &a,
+                                       int lane, float out[NS], int32_t *const dbg[NS]) {
+  const int G = cols / 32, nch = (G + 63) >> 6;
+  float acc[NS];
+#pragma unroll
+  for (int s = 0; s < NS; s++) acc[s] = 0.f;
+  for (int c = 0; c < nch; c++) {
+    const int g = c * 64 + lane;
+    if (g < G) {
+      uint4 w[NS]; uint16_t sc[NS];
+#pragma unroll
+      for (int s = 0; s < NS; s++) { w[s] = ld16(rowq[s] + 16 * g); sc[s] = rows_s[s][g]; }
+      const uint4 h0 = *(const uint4 *)(a.xh + 32 * g), h1 = *(const uint4 *)(a.xh + 32 * g + 16);
+      const uint4 l0 = *(const uint4 *)(a.xl + 32 * g), l1 = *(const uint4 *)(a.xl + 32 * g + 16);
+      const int hx[8] = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+      const uint32_t lx[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+      const int corr = 8 * a.gsum[g];
+      const float bsg = a.bs[g >> 2];
+#pragma unroll
+      for (int s = 0; s < NS; s++) {
+        const uint32_t wd[4] = {w[s].x, w[s].y, w[s].z, w[s].w};
+        int A = 0; uint32_t B = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const uint32_t lo = wd[k] & 0x0f0f0f0fu, hi = (wd[k] >> 4) & 0x0f0f0f0fu;
+          A = __builtin_amdgcn_sdot4((int)lo, hx[k], A, false);
+          A = __builtin_amdgcn_sdot4((int)hi, hx[4 + k], A, false);
+          B = __builtin_amdgcn_udot4(lo, lx[k], B, false);
+          B = __builtin_amdgcn_udot4(hi, lx[4 + k], B, false);
+        }
+        const int isum = A * 256 + (int)B - corr;
+        if (dbg[s]) dbg[s][g] = isum;
+        acc[s] = __builtin_fmaf(half_bits_to_float(sc[s]) * bsg, (float)isum, acc[s]);
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NS; s++) out[s] = wave_sum(acc[s]);
+}
+
+__device__ __forceinline__ float lane_bcast(float v, int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane)); }
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+// ------------------------------------------------------------------ the matvec kernel
+template <int PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void k_matvec(MvArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  const int cols = a.m[0].cols;
+  const ActView av = act_view(smem, cols);
+  build_act<PRO>(a.x, a.norm_w, a.eps, cols, av);
+  if (blockIdx.x == 0 && (a.dbg_xq || a.dbg_bs)) {
+    for (int c = threadIdx.x; c < cols; c += kThreads)
+      if (a.dbg_xq) a.dbg_xq[c] = (int16_t)(((int)av.xh[c] << 8) | av.xl[c]);
+    for (int b = threadIdx.x; b < cols / kQB; b += kThreads)
+      if (a.dbg_bs) a.dbg_bs[b] = av.bs[b];
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nb = cols / kQB;
+  int *sums = av.sums + wave * kMvSlots * av.nbp;
+  const int total = a.seg_tile0[a.nseg];
+  float best_v = -INFINITY; int best_i = 0x7fffffff;
+  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+    int seg = 0;
+    while (seg + 1 < a.nseg && tile >= a.seg_tile0[seg + 1]) seg++;
+    const DMat *mats[kMvSlots]; int rows_[kMvSlots];
+    if (EPI == EPI_SWIGLU) {
+      const int r = (tile - a.seg_tile0[0]) * kMvWaves + wave;
+      mats[0] = &a.m[0]; mats[1] = &a.m[1]; rows_[0] = rows_[1] = r;
+    } else {
+      const int r0 = (tile - a.seg_tile0[seg]) * (kMvWaves * kMvSlots) + wave * kMvSlots;
+#pragma unroll
+      for (int s = 0; s < kMvSlots; s++) { mats[s] = &a.m[seg]; rows_[s] = r0 + s; }
+    }
+    int rc[kMvSlots];   // clamped rows: out-of-range slots compute row rows-1 and store nothing
+#pragma unroll
+    for (int s = 0; s < kMvSlots; s++) rc[s] = rows_[s] < mats[s]->rows ? rows_[s] : mats[s]->rows - 1;
+    float val[kMvSlots];
+    const int kind = mats[0]->kind;
+    if (kind == MK_Q8) {
+      const int8_t *rp[kMvSlots];
+#pragma unroll
+      for (int s = 0; s < kMvSlots; s++) rp[s] = (const int8_t *)mats[s]->q + (size_t)rc[s] * cols;
+      dot_q8<kMvSlots>(rp, cols, av, lane, sums);
+      __syncthreads();
+      float acc = 0.f;
+      if (lane < kMvSlots) {
+        const int *ss = sums + lane * av.nbp;
+        for (int b = 0; b < nb; b++) acc = __builtin_fmaf(av.bs[b], (float)ss[b], acc);
+        int rl = rc[0]; const float *scl = (const float *)mats[0]->s;
+#pragma unroll
+        for (int s = 1; s < kMvSlots; s++) if (lane == s) { rl = rc[s]; scl = (const float *)mats[s]->s; }
+        acc = acc * scl[rl];
+      }
+#pragma unroll
+      for (int s = 0; s < kMvSlots; s++) val[s] = lane_bcast(acc, s);
+      if (a.dbg_sums && seg == 0) {
+        for (int s = 0; s < kMvSlots; s++)
+          if (rows_[s] < mats[s]->rows)
+            for (int b = lane; b < nb; b += kWave) a.dbg_sums[(size_t)rows_[s] * nb + b] = sums[s * av.nbp + b];
+      }
+      __syncthreads();
+    } else {
+      const uint8_t *rq[kMvSlots]; const uint16_t *rs[kMvSlots]; int32_t *dbg[kMvSlots];
+      const int G = cols / 32;
+#pragma unroll
+      for (int s = 0; s < kMvSlots; s++) {
+        rq[s] = (const uint8_t *)mats[s]->q + (size_t)rc[s] * (cols / 2);
+        rs[s] = (const uint16_t *)mats[s]->s + (size_t)rc[s] * G;
+        dbg[s] = (a.dbg_sums && seg == 0 && rows_[s] < mats[s]->rows && EPI != EPI_SWIGLU) ? a.dbg_sums + (size_t)rows_[s] * G : nullptr;
+      }
+      dot_q4<kMvSlots>(rq, rs, cols, av, lane, val, dbg);
+    }
+    if (lane == 0) {
+      if (EPI == EPI_STORE) {
+#pragma unroll
+        for (int s = 0; s < kMvSlots; s++)
+          if (rows_[s] < mats[s]->rows) {
+            float y = val[s];
+            if (a.bias[seg]) y = y + a.bias[seg][rows_[s]];
+            a.out[seg][rows_[s]] = y;
+          }
+      } else if (EPI == EPI_RESID) {
+#pragma unroll
+        for (int s = 0; s < kMvSlots; s++)
+          if (rows_[s] < mats[s]->rows) a.out[0][rows_[s]] = a.out[0][rows_[s]] + val[s];
+      } else if (EPI == EPI_SWIGLU) {
+        if (rows_[0] < mats[0]->rows) {
+          const float g = val[0], u = val[1];
+          a.out[0][rows_[0]] = g / (1.f + exp_poly(0.f - g)) * u;   // silu_mul, kernels_x86.cpp:427-431
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < kMvSlots; s++)
+          if (rows_[s] < mats[s]->rows) {
+            a.out[0][rows_[s]] = val[s];
+            if (better(val[s], rows_[s], best_v, best_i)) { best_v = val[s]; best_i = rows_[s]; }
+          }
+      }
+    }
+  }
+  if (EPI == EPI_ARGMAX) {
+    __syncthreads();
+    float *rv = av.red; int *ri = (int *)(av.red + 8);
+    if (lane == 0) { rv[wave] = best_v; ri[wave] = best_i; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = rv[0]; int bi = ri[0];
+      for (int w = 1; w < kMvWaves; w++) if (better(rv[w], ri[w], bv, bi)) { bv = rv[w]; bi = ri[w]; }
+      a.amax[blockIdx.x] = make_float2(bv, __builtin_bit_cast(float, bi));
+    }
+  }
+}
+
+int mv_tile_rows(int epi) { return epi == EPI_SWIGLU ? kMvWaves : kMvWaves * kMvSlots; }
+void mv_plan(MvArgs &a, int epi) {
+  const int tr = mv_tile_rows(epi); int t = 0;
+  const int nseg = epi == EPI_SWIGLU ? 1 : a.nseg;
+  for (int s = 0; s < nseg; s++) { a.seg_tile0[s] = t; t += (a.m[s].rows + tr - 1) / tr; }
+  a.seg_tile0[nseg] = t;
+  if (epi == EPI_SWIGLU) a.nseg = 1;
+}
+
+template <int PRO, int EPI>
+static hipError_t launch_mv_t(const MvArgs &a, int grid_cap, hipStream_t st) {
+  const int tiles = a.seg_tile0[a.nseg];
+  const int grid = tiles < grid_cap ? tiles : grid_cap;
+  const size_t lds = mv_lds_bytes(a.m[0].cols);
+  hipLaunchKernelGGL((k_matvec<PRO, EPI>), dim3(grid), dim3(kThreads), lds, st, a);
+  return hipGetLastError();
+}
+hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st) {
+#define QPH_MV(P, E) if (pro == P && epi == E) return launch_mv_t<P, E>(a, grid_cap, st);
+  QPH_MV(PRO_QUANT, EPI_STORE) QPH_MV(PRO_QUANT, EPI_RESID) QPH_MV(PRO_NORM, EPI_STORE) QPH_MV(PRO_NORM, EPI_SWIGLU)
+  QPH_MV(PRO_NORM, EPI_ARGMAX) QPH_MV(PRO_QUANT, EPI_ARGMAX)
+#undef QPH_MV
+  return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------ embedding, norm
+__global__ __launch_bounds__(kThreads) void k_embed(DMat e, const Ctl *ctl, float *x) {
+  int tok = ctl->tok;
+  tok = tok < 0 ? 0 : (tok >= e.rows ? e.rows - 1 : tok);
+  const int n = e.cols;
+  if (e.kind == MK_Q8) {
+    const int8_t *q = (const int8_t *)e.q + (size_t)tok * n; const float s = ((const float *)e.s)[tok];
+    for (int i = threadIdx.x; i < n; i += kThreads) x[i] = (float)q[i] * s;
+  } else if (e.kind == MK_Q4) {
+    const uint8_t *q = (const uint8_t *)e.q + (size_t)tok * (n / 2); const uint16_t *s = (const uint16_t *)e.s + (size_t)tok * (n / 32);
+    for (int i = threadIdx.x; i < n / 2; i += kThreads) {
+      const int g = i / 16, j = i % 16; const float sc = half_bits_to_float(s[g]); const uint8_t b = q[i];
+      x[32 * g + j] = (float)((int)(b & 15) - 8) * sc; x[32 * g + j + 16] = (float)((int)(b >> 4) - 8) * sc;
+    }
+  } else {
+    const float *q = (const float *)e.q + (size_t)tok * n;
+    for (int i = threadIdx.x; i < n; i += kThreads) x[i] = q[i];
+  }
+}
+hipError_t launch_embed(const DMat &embed, const Ctl *ctl, float *x, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(kThreads), 0, st, embed, ctl, x);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(kThreads) void k_rmsnorm(const float *x, const float *w, int n, float eps, float *out) {
+  __shared__ float red[16];
+  const float inv = block_rms_inv(x, n, eps, red);
+  for (int i = threadIdx.x; i < n; i += kThreads) out[i] = x[i] * inv * w[i];
+}
+hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, float *out, hipStream_t st) {
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, st, x, w, n, eps, out);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ decode attention (split-K over the context)
+// grid (kv group g, chunk c of `chunk` positions).  The workgroup applies RoPE to its rep query heads (rotate-half with
+// the reference's contraction: a' = fma(a, cos, -(b sin)), b' = fma(b, cos, a sin), model_llama.cpp:176), and the
+// workgroup owning the current position writes the rotated k and v as fp16 into the cache.  Positions are staged in LDS
+// 64 at a time; online softmax per head; partials [m, l, o] per (head, chunk) are merged by k_attn_merge.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void k_attention(AttnArgs a) {
+  constexpr int TP = 64, KS = HD + 2, HALF = HD / 2, JMAX = 8;
+  constexpr int TPI = kThreads / HD;   // head groups of the output accumulation
+  constexpr int JPT = (JMAX + TPI - 1) / TPI;
+  __shared__ float qs[JMAX][HD];
+  __shared__ uint16_t ks[TP][KS];
+  __shared__ uint16_t vs[TP][HD];
+  __shared__ float ps[JMAX][TP];
+  __shared__ float m_run[JMAX], l_run[JMAX], corr[JMAX];
+  __shared__ uint16_t knew[HD], vnew[HD];
+  const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, c = blockIdx.y, rep = a.nh / a.nkv, kvd = a.nkv * HD;
+  const int t0 = c * a.chunk;
+  if (t0 >= T) return;
+  const int t1 = t0 + a.chunk < T ? t0 + a.chunk : T;
+  const float *cs = a.cos_t + (size_t)pos * HALF, *sn = a.sin_t + (size_t)pos * HALF;
+  for (int e = threadIdx.x; e < rep * HALF; e += kThreads) {
+    const int j = e / HALF, i = e % HALF; const float *qh = a.q + (size_t)(g * rep + j) * HD;
+    const float x0 = qh[i], x1 = qh[i + HALF];
+    qs[j][i] = __builtin_fmaf(x0, cs[i], -(x1 * sn[i]));
+    qs[j][i + HALF] = __builtin_fmaf(x1, cs[i], x0 * sn[i]);
+  }
+  const bool own = t0 <= pos && pos < t1;
+  if (own) {
+    for (int i = threadIdx.x; i < HALF; i += kThreads) {
+      const float *kh = a.k + (size_t)g * HD; const float x0 = kh[i], x1 = kh[i + HALF];
+      const uint16_t k0 = float_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
+      const uint16_t k1 = float_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
+      knew[i] = k0; knew[i + HALF] = k1;
+      a.kc[(size_t)pos * kvd + g * HD + i] = k0; a.kc[(size_t)pos * kvd + g * HD + i + HALF] = k1;
+    }
+    for (int i = threadIdx.x; i < HD; i += kThreads) {
+      const uint16_t v = float_to_half_bits(a.v[(size_t)g * HD + i]);
+      vnew[i] = v; a.vc[(size_t)pos * kvd + g * HD + i] = v;
+    }
+  }
+  if (threadIdx.x < JMAX) { m_run[threadIdx.x] = -INFINITY; l_run[threadIdx.x] = 0.f; }
+  const float scl = 1.f / sqrtf((float)HD);
+  float o[JPT];
+#pragma unroll
+  for (int jj = 0; jj < JPT; jj++) o[jj] = 0.f;
+  const int oi = threadIdx.x % HD, oj0 = threadIdx.x / HD;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  for (int ts = t0; ts < t1; ts += TP) {
+    const int n = t1 - ts < TP ? t1 - ts : TP;
+    // stage K (padded rows) and V
+    for (int e = threadIdx.x; e < n * (HD / 2); e += kThreads) {
+      const int t = e / (HD / 2), i2 = e % (HD / 2), tp = ts + t;
+      uint32_t kw, vw;
+      if (tp == pos) { kw = knew[2 * i2] | ((uint32_t)knew[2 * i2 + 1] << 16); vw = vnew[2 * i2] | ((uint32_t)vnew[2 * i2 + 1] << 16); }
+      else {
+        kw = *(const uint32_t *)(a.kc + (size_t)tp * kvd + g * HD + 2 * i2);
+        vw = *(const uint32_t *)(a.vc + (size_t)tp * kvd + g * HD + 2 * i2);
+      }
+      *(uint32_t *)&ks[t][2 * i2] = kw;
+      *(uint32_t *)&vs[t][2 * i2] = vw;
+    }
+    __syncthreads();
+    // scores: wave w takes heads w, w + 4; lane = position
+    for (int j = wave; j < rep; j += kMvWaves) {
+      float s = -INFINITY;
+      if (lane < n) {
+        float acc = 0.f;
+#pragma unroll 8
+        for (int i = 0; i < HD; i += 2) {
+          const uint32_t kw = *(const uint32_t *)&ks[lane][i];
+          acc = __builtin_fmaf(qs[j][i], half_bits_to_float((uint16_t)(kw & 0xffff)), acc);
+          acc = __builtin_fmaf(qs[j][i + 1], half_bits_to_float((uint16_t)(kw >> 16)), acc);
+        }
+        s = acc * scl;
+      }
+      const float mt = wave_max(s);
+      const float mo = m_run[j], mn = fmaxf(mo, mt);
+      const float p = lane < n ? expf(s - mn) : 0.f;
+      const float sum = wave_sum(p);
+      ps[j][lane] = p;
+      if (lane == 0) {
+        const float cf = expf(mo - mn);   // 0 on the first tile (mo = -inf)
+        corr[j] = cf; m_run[j] = mn; l_run[j] = l_run[j] * cf + sum;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < JPT; jj++) {
+      const int j = oj0 + jj * TPI;
+      if (j < rep) {
+        float acc = o[jj] * corr[j];
+        for (int t = 0; t < n; t++) acc = __builtin_fmaf(ps[j][t], half_bits_to_float(vs[t][oi]), acc);
+        o[jj] = acc;
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int jj = 0; jj < JPT; jj++) {
+    const int j = oj0 + jj * TPI;
+    if (j < rep) {
+      float *pp = a.part + ((size_t)(g * rep + j) * a.max_chunks + c) * (HD + 2);
+      if (oi == 0) { pp[0] = m_run[j]; pp[1] = l_run[j]; }
+      pp[2 + oi] = o[jj];
+    }
+  }
+}
+
+// merge of the chunk partials per head (the fixed-order merge of model_llama.cpp:160-165): M = max m_c,
+// L = sum l_c e^(m_c - M), out = (sum o_c e^(m_c - M)) * (1 / L)
+template <int HD>
+__global__ void k_attn_merge(AttnArgs a) {
+  const int h = blockIdx.x, i = threadIdx.x, T = a.ctl->pos + 1, nc = (T + a.chunk - 1) / a.chunk;
+  const float *ph = a.part + (size_t)h * a.max_chunks * (HD + 2);
+  float M = -INFINITY;
+  for (int c = 0; c < nc; c++) M = fmaxf(M, ph[(size_t)c * (HD + 2)]);
+  float L = 0.f, o = 0.f;
+  for (int c = 0; c < nc; c++) {
+    const float *pc = ph + (size_t)c * (HD + 2); const float f = expf(pc[0] - M);
+    L = __builtin_fmaf(pc[1], f, L); o = __builtin_fmaf(f, pc[2 + i], o);
+  }
+  a.att[(size_t)h * HD + i] = o * (1.f / L);
+}
+
+hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
+  if (a.nh / a.nkv > 8) return hipErrorInvalidValue;
+  const dim3 grid(a.nkv, a.max_chunks);
+  if (a.hd == 64) {
+    hipLaunchKernelGGL(k_attention<64>, grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(k_attn_merge<64>, dim3(a.nh), dim3(64), 0, st, a);
+  } else if (a.hd == 128) {
+    hipLaunchKernelGGL(k_attention<128>, grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.nh), dim3(128), 0, st, a);
+  } else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ greedy pick
+__global__ __launch_bounds__(kThreads) void k_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens) {
+  __shared__ float bv_s[kThreads]; __shared__ int bi_s[kThreads];
+  float bv = -INFINITY; int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const float v = amax[i].x; const int idx = __builtin_bit_cast(int, amax[i].y);
+    if (better(v, idx, bv, bi)) { bv = v; bi = idx; }
+  }
+  bv_s[threadIdx.x] = bv; bi_s[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s && better(bv_s[threadIdx.x + s], bi_s[threadIdx.x + s], bv_s[threadIdx.x], bi_s[threadIdx.x])) {
+      bv_s[threadIdx.x] = bv_s[threadIdx.x + s]; bi_s[threadIdx.x] = bi_s[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    int t = bi_s[0]; if (t == 0x7fffffff) t = 0;
+    out_tokens[ctl->n_out] = t;
+    ctl->tok = t; ctl->pos = ctl->pos + 1; ctl->n_out = ctl->n_out + 1;
+  }
+}
+hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st) {
+  hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(kThreads), 0, st, amax, n, ctl, out_tokens);
+  return hipGetLastError();
+}
+
+}  // namespace qph

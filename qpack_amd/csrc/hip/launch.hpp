@@ -1,0 +1,66 @@
+// Host-side launchers of the gfx950 token-loop kernels (implemented in kernels.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace qph {
+
+// how a matvec kernel builds its int16 activation vector in LDS
+enum Prologue : int {
+  PRO_QUANT = 0,   // quantise x as is (wo input, down input, test hook)
+  PRO_NORM = 1,    // RMSNorm(x) * w, then quantise (qkv, gate/up, output head)
+};
+// what a matvec kernel does with each finished row value y = W x
+enum Epilogue : int {
+  EPI_STORE = 0,    // out[seg][row] = y (+ bias[seg][row])          up to 3 segments (q / k / v)
+  EPI_RESID = 1,    // out[0][row] += y                             (wo, down: residual stream)
+  EPI_SWIGLU = 2,   // out[0][row] = silu(y_gate) * y_up            (segments 0 = gate, 1 = up, same rows)
+  EPI_ARGMAX = 3,   // out[0][row] = y and one (max, index) per workgroup into amax (output head)
+};
+
+struct MvArgs {
+  DMat m[3];
+  int nseg;
+  int seg_tile0[4];       // first tile of each segment (prefix sums), seg_tile0[nseg] = total tiles
+  const float *x;         // input vector [cols]
+  const float *norm_w;    // PRO_NORM weights [cols]
+  float eps;
+  float *out[3];
+  const float *bias[3];
+  float2 *amax;           // EPI_ARGMAX: one (value, index-as-float-bits) per workgroup
+  int32_t *dbg_sums;      // optional: exact int32 accumulators [rows, cols/128] (q8) or [rows, cols/32] (q4), segment 0
+  int16_t *dbg_xq;        // optional: the quantised activation (workgroup 0 writes it)
+  float *dbg_bs;          // optional: the activation block scales
+};
+
+// rows per workgroup tile for the matvec kernel (4 waves x 2 row slots; EPI_SWIGLU pairs gate/up rows: 4 rows)
+constexpr int kMvWaves = 4;
+constexpr int kMvSlots = 2;
+int mv_tile_rows(int epi);
+size_t mv_lds_bytes(int cols);
+// fills seg_tile0 from the segment row counts
+void mv_plan(MvArgs &a, int epi);
+hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st);
+
+// x[0..d) = row ctl->tok of the embedding (row_f32 semantics, /root/reference/src/kernels.cpp:146-162)
+hipError_t launch_embed(const DMat &embed, const Ctl *ctl, float *x, hipStream_t st);
+// out = RMSNorm(x) * w (single workgroup; identical arithmetic to the PRO_NORM prologue)
+hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, float *out, hipStream_t st);
+
+struct AttnArgs {
+  const float *q, *k, *v;      // this step's projections (bias added, RoPE not yet applied)
+  uint16_t *kc, *vc;           // this layer's fp16 caches [ctx][kvd]
+  const float *cos_t, *sin_t;  // RoPE tables [ctx][hd / 2]
+  const Ctl *ctl;
+  float *part;                 // [nh][max_chunks][hd + 2]: running max, sum, unnormalised output
+  float *att;                  // merged output [nh * hd]
+  int nh, nkv, hd, chunk, max_chunks;
+};
+hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+
+// greedy pick over the head's per-workgroup (max, index) pairs; advances ctl (tok = pick, pos += 1, n_out += 1) and
+// writes the pick to out_tokens[ctl->n_out]
+hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st);
+
+}  // namespace qph

@@ -1,0 +1,362 @@
+#include "model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+
+#include "launch.hpp"
+
+namespace qph {
+
+#define QPH_CK(x)                                                                                           \
+  do {                                                                                                      \
+    hipError_t e_ = (x);                                                                                    \
+    if (e_ != hipSuccess) throw std::runtime_error(std::string("hip: ") + hipGetErrorString(e_) + " at " + #x); \
+  } while (0)
+
+static constexpr unsigned kRing = 256;   // pinned control slots (one per host-driven step in flight)
+
+void *HipLlama::dalloc(size_t bytes) {
+  void *p = nullptr;
+  QPH_CK(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+  allocs_.push_back(p);
+  return p;
+}
+
+DMat HipLlama::upload(const qph_tensor &t) {
+  DMat m{}; m.rows = (int)t.rows; m.cols = (int)t.cols;
+  size_t qb = 0, sb = 0;
+  if (t.kind == QPH_Q8) { m.kind = MK_Q8; qb = (size_t)t.rows * t.cols; sb = 4ull * t.rows; }
+  else if (t.kind == QPH_Q4) {
+    if (t.cols % 32) throw std::runtime_error(std::string("hip: q4 tensor ") + t.name + " needs cols % 32 == 0");
+    m.kind = MK_Q4; qb = (size_t)t.rows * t.cols / 2; sb = 2ull * t.rows * (t.cols / 32);
+  } else throw std::runtime_error(std::string("hip: matrix ") + t.name + " must be q8 or q4");
+  if (!t.data || !t.scale) throw std::runtime_error(std::string("hip: tensor ") + t.name + " has no data");
+  void *q = dalloc(qb), *s = dalloc(sb);
+  QPH_CK(hipMemcpy(q, t.data, qb, hipMemcpyHostToDevice));
+  QPH_CK(hipMemcpy(s, t.scale, sb, hipMemcpyHostToDevice));
+  m.q = q; m.s = s;
+  return m;
+}
+
+const float *HipLlama::upload_f32(const qph_tensor &t, int64_t n) {
+  if (t.kind != QPH_F32) throw std::runtime_error(std::string("hip: tensor ") + t.name + " must be f32");
+  if (t.rows * std::max<int64_t>(t.cols, 1) != n) throw std::runtime_error(std::string("hip: tensor ") + t.name + " has the wrong size");
+  void *p = dalloc(4ull * n);
+  QPH_CK(hipMemcpy(p, t.data, 4ull * n, hipMemcpyHostToDevice));
+  return (const float *)p;
+}
+
+HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int max_ctx) : cfg_(cfg) {
+  const int d = cfg.hidden, nh = cfg.heads, nkv = cfg.kv_heads, hd = cfg.head_dim, ff = cfg.ffn, V = cfg.vocab;
+  if (d <= 0 || cfg.layers <= 0 || nh <= 0 || nkv <= 0 || ff <= 0 || V <= 0) throw std::runtime_error("hip: bad model config");
+  if (hd != 64 && hd != 128) throw std::runtime_error("hip: head_dim must be 64 or 128");
+  if (nh % nkv || nh / nkv > 8) throw std::runtime_error("hip: unsupported GQA ratio (heads / kv_heads must be an integer <= 8)");
+  qd_ = nh * hd; kvd_ = nkv * hd;
+  if (d % 128 || ff % 128 || qd_ % 128) throw std::runtime_error("hip: hidden, ffn and heads * head_dim must be multiples of 128");
+  const int limit = cfg.max_pos > 0 ? cfg.max_pos : (1 << 20);
+  ctx_ = max_ctx > 0 ? max_ctx : std::min(4096, limit);
+  std::map<std::string, const qph_tensor *> by;
+  for (int i = 0; i < n; i++) by[tensors[i].name] = &tensors[i];
+  auto need = [&](const std::string &nm) -> const qph_tensor & {
+    auto it = by.find(nm);
+    if (it == by.end()) throw std::runtime_error("hip: missing tensor " + nm);
+    return *it->second;
+  };
+  auto opt = [&](const std::string &nm) -> const qph_tensor * { auto it = by.find(nm); return it == by.end() ? nullptr : it->second; };
+  auto shape = [&](const DMat &m, int r, int c, const std::string &nm) {
+    if (m.rows != r || m.cols != c) throw std::runtime_error("hip: tensor " + nm + " has an unexpected shape");
+  };
+  int dev = 0;
+  QPH_CK(hipGetDevice(&dev));
+  QPH_CK(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
+  QPH_CK(hipStreamCreateWithFlags(&st_, hipStreamNonBlocking));
+  embed_ = upload(need("embed")); shape(embed_, V, d, "embed");
+  if (cfg.tied) head_ = embed_;
+  else { head_ = upload(need("lm_head")); shape(head_, V, d, "lm_head"); }
+  fnorm_ = upload_f32(need("final_norm"), d);
+  for (int l = 0; l < cfg.layers; l++) {
+    const std::string p = "layers." + std::to_string(l) + ".";
+    Layer ly;
+    ly.an = upload_f32(need(p + "attn_norm"), d); ly.fn = upload_f32(need(p + "ffn_norm"), d);
+    ly.wq = upload(need(p + "wq")); shape(ly.wq, qd_, d, p + "wq");
+    ly.wk = upload(need(p + "wk")); shape(ly.wk, kvd_, d, p + "wk");
+    ly.wv = upload(need(p + "wv")); shape(ly.wv, kvd_, d, p + "wv");
+    ly.wo = upload(need(p + "wo")); shape(ly.wo, d, qd_, p + "wo");
+    ly.wg = upload(need(p + "w_gate")); shape(ly.wg, ff, d, p + "w_gate");
+    ly.wu = upload(need(p + "w_up")); shape(ly.wu, ff, d, p + "w_up");
+    ly.wd = upload(need(p + "w_down")); shape(ly.wd, d, ff, p + "w_down");
+    if (ly.wg.kind != ly.wu.kind) throw std::runtime_error("hip: w_gate and w_up of layer " + std::to_string(l) + " must have the same kind");
+    const qph_tensor *bq = opt(p + "bq");
+    if (bq) { ly.bq = upload_f32(*bq, qd_); ly.bk = upload_f32(need(p + "bk"), kvd_); ly.bv = upload_f32(need(p + "bv"), kvd_); }
+    layers_.push_back(ly);
+  }
+  // attention split: enough (group, chunk) workgroups to cover the chip at full context
+  chunk_ = 64;
+  while ((int64_t)nkv * ((ctx_ + chunk_ - 1) / chunk_) > 4ll * cus_ && chunk_ < 1024) chunk_ *= 2;
+  max_chunks_ = (ctx_ + chunk_ - 1) / chunk_;
+  const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
+  kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
+  QPH_CK(hipMemset(kc_, 0, kvn * 2)); QPH_CK(hipMemset(vc_, 0, kvn * 2));
+  x_ = (float *)dalloc(4ull * d); xn_ = (float *)dalloc(4ull * d); q_ = (float *)dalloc(4ull * qd_);
+  k_ = (float *)dalloc(4ull * kvd_); v_ = (float *)dalloc(4ull * kvd_); att_ = (float *)dalloc(4ull * qd_);
+  h_ = (float *)dalloc(4ull * ff); logits_ = (float *)dalloc(4ull * V);
+  part_ = (float *)dalloc(4ull * nh * max_chunks_ * (hd + 2));
+  head_grid_ = std::min((V + mv_tile_rows(EPI_ARGMAX) - 1) / mv_tile_rows(EPI_ARGMAX), 4 * cus_);
+  amax_ = (float2 *)dalloc(sizeof(float2) * head_grid_);
+  ctl_ = (Ctl *)dalloc(sizeof(Ctl));
+  out_tok_ = (int *)dalloc(4ull * (ctx_ + 1));
+  // RoPE tables in the reference's precision: inv_i = 1 / theta^(2i/hd) and angle pos * inv_i in double, cos / sin
+  // rounded to float (model_llama.cpp:39, :173-175)
+  const int half = hd / 2;
+  std::vector<float> cs((size_t)ctx_ * half), sn((size_t)ctx_ * half);
+  for (int i = 0; i < half; i++) {
+    const double inv = 1.0 / std::pow(cfg.rope_theta, (2.0 * i) / hd);
+    for (int p = 0; p < ctx_; p++) { const double a = p * inv; cs[(size_t)p * half + i] = (float)std::cos(a); sn[(size_t)p * half + i] = (float)std::sin(a); }
+  }
+  cos_ = (float *)dalloc(cs.size() * 4); sin_ = (float *)dalloc(sn.size() * 4);
+  QPH_CK(hipMemcpy(cos_, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  QPH_CK(hipMemcpy(sin_, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  QPH_CK(hipHostMalloc((void **)&hctl_, kRing * sizeof(Ctl), hipHostMallocDefault));
+  QPH_CK(hipHostMalloc((void **)&hout_, 4ull * std::max(V, d), hipHostMallocDefault));
+  QPH_CK(hipHostMalloc((void **)&htok_, 4ull * (ctx_ + 1), hipHostMallocDefault));
+  memset(hctl_, 0, kRing * sizeof(Ctl));
+  QPH_CK(hipMemset(ctl_, 0, sizeof(Ctl)));
+  build_graphs();
+}
+
+HipLlama::~HipLlama() {
+  if (st_) (void)hipStreamSynchronize(st_);
+  for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_}) if (g) (void)hipGraphExecDestroy(g);
+  for (void *p : allocs_) (void)hipFree(p);
+  if (hctl_) (void)hipHostFree(hctl_);
+  if (hout_) (void)hipHostFree(hout_);
+  if (htok_) (void)hipHostFree(htok_);
+  if (st_) (void)hipStreamDestroy(st_);
+}
+
+void HipLlama::enqueue_layer(int l) {
+  const Layer &ly = layers_[l];
+  const int cap = 4 * cus_;
+  const float eps = cfg_.rms_eps;
+  {  // RMSNorm + q/k/v (+ bias)
+    MvArgs a{}; a.m[0] = ly.wq; a.m[1] = ly.wk; a.m[2] = ly.wv; a.nseg = 3; a.x = x_; a.norm_w = ly.an; a.eps = eps;
+    a.out[0] = q_; a.out[1] = k_; a.out[2] = v_; a.bias[0] = ly.bq; a.bias[1] = ly.bk; a.bias[2] = ly.bv;
+    mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_NORM, EPI_STORE, a, cap, st_));
+  }
+  {  // RoPE, fp16 KV append, split-K attention, merge
+    AttnArgs a{}; a.q = q_; a.k = k_; a.v = v_;
+    a.kc = kc_ + (size_t)l * ctx_ * kvd_; a.vc = vc_ + (size_t)l * ctx_ * kvd_;
+    a.cos_t = cos_; a.sin_t = sin_; a.ctl = ctl_; a.part = part_; a.att = att_;
+    a.nh = cfg_.heads; a.nkv = cfg_.kv_heads; a.hd = cfg_.head_dim; a.chunk = chunk_; a.max_chunks = max_chunks_;
+    QPH_CK(launch_attention(a, st_));
+  }
+  {  // wo + residual
+    MvArgs a{}; a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = x_;
+    mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_));
+  }
+  {  // RMSNorm + gate / up + SwiGLU
+    MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
+    mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM, EPI_SWIGLU, a, cap, st_));
+  }
+  {  // down + residual
+    MvArgs a{}; a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = x_;
+    mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_));
+  }
+}
+
+void HipLlama::enqueue_layers() {
+  QPH_CK(launch_embed(embed_, ctl_, x_, st_));
+  for (int l = 0; l < cfg_.layers; l++) enqueue_layer(l);
+}
+
+void HipLlama::enqueue_head() {
+  MvArgs a{}; a.m[0] = head_; a.nseg = 1; a.x = x_; a.norm_w = fnorm_; a.eps = cfg_.rms_eps; a.out[0] = logits_; a.amax = amax_;
+  mv_plan(a, EPI_ARGMAX);
+  QPH_CK(launch_matvec(PRO_NORM, EPI_ARGMAX, a, head_grid_, st_));
+}
+
+hipGraphExec_t HipLlama::capture(int parts) {
+  hipGraph_t g = nullptr; hipGraphExec_t ge = nullptr;
+  QPH_CK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
+  try {
+    enqueue_layers();
+    if (parts >= 1) enqueue_head();
+    if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
+  } catch (...) {
+    (void)hipStreamEndCapture(st_, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  QPH_CK(hipStreamEndCapture(st_, &g));
+  QPH_CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+  QPH_CK(hipGraphDestroy(g));
+  return ge;
+}
+
+void HipLlama::build_graphs() {
+  g_state_ = capture(0);
+  g_logits_ = capture(1);
+  g_greedy_ = capture(2);
+}
+
+void HipLlama::write_ctl(int tok, int pos) {
+  // ring of pinned slots: a slot is rewritten only after kRing / 2 later steps, and the host waits for the stream every
+  // kRing / 2 steps, so a copy still in flight never sees its source change (the reference's scheme,
+  // model_llama_cuda.cu:530-533)
+  Ctl &c = hctl_[slot_ % kRing];
+  c.tok = tok; c.pos = pos; c.n_out = 0; c.pad = 0;
+  QPH_CK(hipMemcpyAsync(ctl_, &c, sizeof(Ctl), hipMemcpyHostToDevice, st_));
+  slot_++;
+  if (slot_ % (kRing / 2) == 0) QPH_CK(hipStreamSynchronize(st_));
+}
+
+void HipLlama::step(int tok, int want, float *out) {
+  if (pos_ >= ctx_) throw std::runtime_error("context window full (" + std::to_string(ctx_) + " tokens)");
+  if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
+  write_ctl(tok, pos_);
+  if (want == 1) {
+    QPH_CK(hipGraphLaunch(g_logits_, st_));
+    QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
+  } else {
+    QPH_CK(hipGraphLaunch(g_state_, st_));
+    if (want == 2) {
+      QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
+      QPH_CK(hipMemcpyAsync(hout_, xn_, 4ull * cfg_.hidden, hipMemcpyDeviceToHost, st_));
+    }
+  }
+  pos_++;
+  if (want) {
+    QPH_CK(hipStreamSynchronize(st_));
+    if (out) memcpy(out, hout_, 4ull * (want == 1 ? cfg_.vocab : cfg_.hidden));
+  }
+}
+
+void HipLlama::prefill(const int *toks, int n, int want, float *out) {
+  if (n <= 0) return;
+  if (pos_ + n > ctx_) throw std::runtime_error("context window full (" + std::to_string(ctx_) + " tokens)");
+  for (int i = 0; i < n; i++) if (toks[i] < 0 || toks[i] >= cfg_.vocab) throw std::runtime_error("token id out of range");
+  for (int i = 0; i < n; i++) step(toks[i], i + 1 == n ? want : 0, i + 1 == n ? out : nullptr);
+  if (!want) QPH_CK(hipStreamSynchronize(st_));
+}
+
+int HipLlama::greedy_run(int tok, int n, int *out) {
+  n = std::min(n, ctx_ - pos_);
+  if (n <= 0) return 0;
+  if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
+  write_ctl(tok, pos_);
+  for (int i = 0; i < n; i++) QPH_CK(hipGraphLaunch(g_greedy_, st_));
+  QPH_CK(hipMemcpyAsync(htok_, out_tok_, 4ull * n, hipMemcpyDeviceToHost, st_));
+  QPH_CK(hipStreamSynchronize(st_));
+  memcpy(out, htok_, 4ull * n);
+  pos_ += n;
+  return n;
+}
+
+void HipLlama::prefill_all(const int *toks, int n, float *logits) {
+  if (pos_ + n > ctx_) throw std::runtime_error("context window full (" + std::to_string(ctx_) + " tokens)");
+  for (int i = 0; i < n; i++) step(toks[i], 1, logits + (size_t)i * cfg_.vocab);
+}
+
+void HipLlama::set_pos(int pos) {
+  if (pos < 0 || pos > ctx_) throw std::runtime_error("position out of range");
+  pos_ = pos;
+}
+
+void HipLlama::snapshot(uint8_t *buf, int64_t cap) {
+  if (cap < snapshot_size()) throw std::runtime_error("snapshot buffer too small");
+  QPH_CK(hipStreamSynchronize(st_));
+  memcpy(buf, &pos_, 4); uint8_t *p = buf + 4; const size_t nb = (size_t)pos_ * kvd_ * 2;
+  for (int l = 0; l < cfg_.layers; l++)
+    for (uint16_t *c : {kc_, vc_}) { QPH_CK(hipMemcpy(p, c + (size_t)l * ctx_ * kvd_, nb, hipMemcpyDeviceToHost)); p += nb; }
+}
+
+void HipLlama::restore(const uint8_t *buf, int64_t n) {
+  if (n < 4) throw std::runtime_error("snapshot too short");
+  int pos; memcpy(&pos, buf, 4);
+  if (pos < 0 || pos > ctx_) throw std::runtime_error("snapshot position out of range");
+  const size_t nb = (size_t)pos * kvd_ * 2;
+  if (n < (int64_t)(4 + 2 * nb * cfg_.layers)) throw std::runtime_error("snapshot too short");
+  QPH_CK(hipStreamSynchronize(st_));
+  const uint8_t *p = buf + 4;
+  for (int l = 0; l < cfg_.layers; l++)
+    for (uint16_t *c : {kc_, vc_}) { QPH_CK(hipMemcpy(c + (size_t)l * ctx_ * kvd_, p, nb, hipMemcpyHostToDevice)); p += nb; }
+  pos_ = pos;
+}
+
+float HipLlama::time_greedy(int tok, int n) {
+  n = std::min(n, ctx_ - pos_);
+  if (n <= 0) throw std::runtime_error("context window full");
+  hipEvent_t e0, e1;
+  QPH_CK(hipEventCreate(&e0)); QPH_CK(hipEventCreate(&e1));
+  write_ctl(tok, pos_);
+  QPH_CK(hipEventRecord(e0, st_));
+  for (int i = 0; i < n; i++) QPH_CK(hipGraphLaunch(g_greedy_, st_));
+  QPH_CK(hipEventRecord(e1, st_));
+  QPH_CK(hipEventSynchronize(e1));
+  float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
+  pos_ += n;
+  return ms;
+}
+
+static double mat_bytes(const DMat &m) {
+  return m.kind == MK_Q8 ? (double)m.rows * m.cols + 4.0 * m.rows : (double)m.rows * m.cols / 2 + 2.0 * m.rows * (m.cols / 32);
+}
+
+float HipLlama::time_kernel(int which, int iters, double *bytes) {
+  if (iters <= 0) iters = 1;
+  const Layer &ly = layers_[0];
+  const int cap = 4 * cus_, d = cfg_.hidden;
+  const float eps = cfg_.rms_eps;
+  write_ctl(0, std::min(pos_, ctx_ - 1));
+  auto launch = [&]() {
+    MvArgs a{};
+    switch (which) {
+      case 0:
+        a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
+        mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM, EPI_SWIGLU, a, cap, st_)); break;
+      case 1:
+        a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = xn_;
+        mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); break;
+      case 2:
+        a.m[0] = ly.wq; a.m[1] = ly.wk; a.m[2] = ly.wv; a.nseg = 3; a.x = x_; a.norm_w = ly.an; a.eps = eps;
+        a.out[0] = q_; a.out[1] = k_; a.out[2] = v_;
+        mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_NORM, EPI_STORE, a, cap, st_)); break;
+      case 3:
+        a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = xn_;
+        mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); break;
+      case 4: enqueue_head(); break;
+      case 5: {
+        AttnArgs t{}; t.q = q_; t.k = k_; t.v = v_; t.kc = kc_; t.vc = vc_; t.cos_t = cos_; t.sin_t = sin_; t.ctl = ctl_;
+        t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim; t.chunk = chunk_;
+        t.max_chunks = max_chunks_;
+        QPH_CK(launch_attention(t, st_)); break;
+      }
+      default: throw std::runtime_error("time_kernel: unknown kernel id");
+    }
+  };
+  switch (which) {
+    case 0: *bytes = mat_bytes(ly.wg) + mat_bytes(ly.wu) + 4.0 * d; break;
+    case 1: *bytes = mat_bytes(ly.wd); break;
+    case 2: *bytes = mat_bytes(ly.wq) + mat_bytes(ly.wk) + mat_bytes(ly.wv) + 4.0 * d; break;
+    case 3: *bytes = mat_bytes(ly.wo); break;
+    case 4: *bytes = mat_bytes(head_) + 4.0 * d + 4.0 * cfg_.vocab; break;
+    case 5: *bytes = 4.0 * (double)(pos_ + 1) * kvd_; break;
+    default: throw std::runtime_error("time_kernel: unknown kernel id");
+  }
+  launch();   // warm-up
+  hipEvent_t e0, e1;
+  QPH_CK(hipEventCreate(&e0)); QPH_CK(hipEventCreate(&e1));
+  QPH_CK(hipEventRecord(e0, st_));
+  for (int i = 0; i < iters; i++) launch();
+  QPH_CK(hipEventRecord(e1, st_));
+  QPH_CK(hipEventSynchronize(e1));
+  float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
+  return ms / iters;
+}
+
+}  // namespace qph

@@ -1,0 +1,79 @@
+// The HIP Llama model: the host side of the gfx950 token loop, shaped like qp::Model
+// (/root/reference/include/qpack/qpack.h:128-171) and the reference GPU model LlamaCuda
+// (/root/reference/src/model_llama_cuda.cu:445-632).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../../include/qpack_hip.h"
+#include "common.hpp"
+
+namespace qph {
+
+class HipLlama {
+ public:
+  HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int max_ctx);
+  ~HipLlama();
+  HipLlama(const HipLlama &) = delete;
+  HipLlama &operator=(const HipLlama &) = delete;
+
+  const qph_config &config() const { return cfg_; }
+  int max_ctx() const { return ctx_; }
+  int pos() const { return pos_; }
+
+  void step(int tok, int want, float *out);
+  void prefill(const int *toks, int n, int want, float *out);
+  int greedy_run(int tok, int n, int *out);
+  void prefill_all(const int *toks, int n, float *logits);
+  void reset() { pos_ = 0; }
+  bool rewind(int pos) { if (pos < 0 || pos > pos_) return false; pos_ = pos; return true; }
+  void set_pos(int pos);
+  int64_t snapshot_size() const { return 4 + 4ll * cfg_.layers * pos_ * kvd_; }
+  void snapshot(uint8_t *buf, int64_t cap);
+  void restore(const uint8_t *buf, int64_t n);
+
+  float time_greedy(int tok, int n);
+  float time_kernel(int which, int iters, double *bytes);
+
+ private:
+  struct Layer {
+    DMat wq, wk, wv, wo, wg, wu, wd;
+    const float *an = nullptr, *fn = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  };
+  qph_config cfg_;
+  int ctx_ = 0, kvd_ = 0, qd_ = 0, chunk_ = 64, max_chunks_ = 1, cus_ = 256, head_grid_ = 0;
+  int pos_ = 0;
+  unsigned slot_ = 0;
+  hipStream_t st_ = nullptr;
+  std::vector<void *> allocs_;
+  DMat embed_{}, head_{};
+  const float *fnorm_ = nullptr;
+  std::vector<Layer> layers_;
+  // device state
+  float *x_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr, *h_ = nullptr, *xn_ = nullptr;
+  float *logits_ = nullptr, *part_ = nullptr, *cos_ = nullptr, *sin_ = nullptr;
+  float2 *amax_ = nullptr;
+  Ctl *ctl_ = nullptr;
+  int *out_tok_ = nullptr;
+  uint16_t *kc_ = nullptr, *vc_ = nullptr;
+  // pinned host
+  Ctl *hctl_ = nullptr;
+  float *hout_ = nullptr;
+  int *htok_ = nullptr;
+  hipGraphExec_t g_state_ = nullptr, g_logits_ = nullptr, g_greedy_ = nullptr;
+
+  void *dalloc(size_t bytes);
+  DMat upload(const qph_tensor &t);
+  const float *upload_f32(const qph_tensor &t, int64_t n);
+  void enqueue_layers();
+  void enqueue_layer(int l);
+  void enqueue_head();
+  void build_graphs();
+  hipGraphExec_t capture(int parts);
+  void write_ctl(int tok, int pos);
+};
+
+}  // namespace qph

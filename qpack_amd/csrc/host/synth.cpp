@@ -1,0 +1,167 @@
+// Seeded synthetic Llama-family models written as QPACK2 files (random init: there are no checkpoints offline).
+//
+// Weights: N(0, std) from a counter-based generator, so every element is a pure function of (seed, tensor index,
+// element index) and the file is identical for any thread count:
+//   h = mix64(seed, tensor, pair index); u1 = (hi32(h) + 0.5) / 2^32, u2 = lo32(h) / 2^32;
+//   Box-Muller in double: r = sqrt(-2 ln u1), element 2p = r cos(2 pi u2), element 2p + 1 = r sin(2 pi u2); w = (float)(std * n).
+// Quantisation rules:
+//   q8 - per row s = max|w| / 127 (1 for an all-zero row), q = clamp(nearbyint(w / s), -127, 127): the rule of
+//        /root/reference/tools/qpack-quantize.cpp:327-339 and python/qpack/container.py:90-95;
+//   q4 - per 32-column group s = fp16(max|w| / 7), q = clamp(lrintf(w / s), -8, 7) stored as q + 8 in the QPACK2 q4 layout
+//        (byte j = column j low nibble, column j + 16 high nibble).  This absmax scale is this build's choice; the
+//        reference's own writer searches the scale by squared error (qpack-quantize.cpp:34-58).  Kernels read both alike.
+// Norm weights are 1.0; biases are N(0, std) f32.  Tensor names follow /root/reference/python/qpack/convert_llama.py:5-11.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "container.hpp"
+#include "synth.hpp"
+
+namespace qph {
+
+static inline uint64_t mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// elements [i0, i1) (i0 even) of tensor `tid` as float N(0, std)
+static void normals(uint64_t seed, uint64_t tid, int64_t i0, int64_t i1, float sd, float *out) {
+  const uint64_t key = mix64(seed ^ mix64(tid + 0x51ed270b27e3a1c5ull));
+  for (int64_t i = i0; i < i1; i += 2) {
+    const uint64_t h = mix64(key ^ (uint64_t)(i >> 1) * 0xd6e8feb86659fd93ull);
+    const double u1 = ((double)(h >> 32) + 0.5) * (1.0 / 4294967296.0), u2 = (double)(h & 0xffffffffull) * (1.0 / 4294967296.0);
+    const double r = std::sqrt(-2.0 * std::log(u1)), a = 6.283185307179586476925286766559 * u2;
+    out[i - i0] = (float)(sd * r * std::cos(a));
+    if (i + 1 < i1) out[i + 1 - i0] = (float)(sd * r * std::sin(a));
+  }
+}
+
+static void parallel_rows(int64_t rows, int threads, const std::function<void(int64_t, int64_t)> &f) {
+  if (threads <= 1 || rows < 64) { f(0, rows); return; }
+  std::vector<std::thread> th; const int64_t chunk = (rows + threads - 1) / threads;
+  for (int t = 0; t < threads; t++) {
+    const int64_t a = t * chunk, b = std::min(rows, a + chunk);
+    if (a < b) th.emplace_back([=, &f] { f(a, b); });
+  }
+  for (auto &t : th) t.join();
+}
+
+static uint16_t to_half(float f) { const _Float16 h = (_Float16)f; uint16_t u; memcpy(&u, &h, 2); return u; }
+static float from_half(uint16_t u) { _Float16 h; memcpy(&h, &u, 2); return (float)h; }
+
+enum class Q { F32, Q8, Q4 };
+struct Plan { std::string name; std::vector<int64_t> shape; Q q; bool ones; uint64_t tid; };
+
+void synth_write(const SynthSpec &s, const std::string &path, int threads) {
+  if (s.hidden <= 0 || s.layers <= 0 || s.heads <= 0 || s.kv_heads <= 0 || s.head_dim <= 0 || s.ffn <= 0 || s.vocab <= 0)
+    throw std::runtime_error("synth: all dimensions must be positive");
+  if (s.heads % s.kv_heads) throw std::runtime_error("synth: heads must be a multiple of kv_heads");
+  if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
+  const int64_t d = s.hidden, qd = (int64_t)s.heads * s.head_dim, kvd = (int64_t)s.kv_heads * s.head_dim, ff = s.ffn, V = s.vocab;
+  std::vector<Plan> ts; uint64_t tid = 0;
+  auto add = [&](const std::string &n, std::vector<int64_t> sh, Q q, bool ones = false) { ts.push_back({n, sh, q, ones, tid++}); };
+  const Q lq = s.q4 ? Q::Q4 : Q::Q8;
+  add("embed", {V, d}, Q::Q8);
+  if (!s.tied) add("lm_head", {V, d}, Q::Q8);
+  add("final_norm", {d}, Q::F32, true);
+  for (int l = 0; l < s.layers; l++) {
+    const std::string p = "layers." + std::to_string(l) + ".";
+    add(p + "attn_norm", {d}, Q::F32, true); add(p + "ffn_norm", {d}, Q::F32, true);
+    add(p + "wq", {qd, d}, lq); add(p + "wk", {kvd, d}, lq);
+    add(p + "wv", {kvd, d}, s.q4 && s.q4m_alt ? Q::Q8 : lq);
+    add(p + "wo", {d, qd}, lq);
+    if (s.qkv_bias) { add(p + "bq", {qd}, Q::F32); add(p + "bk", {kvd}, Q::F32); add(p + "bv", {kvd}, Q::F32); }
+    add(p + "w_gate", {ff, d}, lq); add(p + "w_up", {ff, d}, lq);
+    add(p + "w_down", {d, ff}, s.q4 && s.q4m_alt && l % 2 == 0 ? Q::Q8 : lq);
+  }
+  for (auto &t : ts) if (t.q == Q::Q4 && t.shape[1] % 32) throw std::runtime_error("synth: q4 tensor " + t.name + " needs cols % 32 == 0");
+
+  Json man = Json::object(), tl = Json::array();
+  std::vector<std::pair<std::string, uint64_t>> plan;
+  for (size_t k = 0; k < ts.size(); k++) {
+    const Plan &t = ts[k]; char bid[16]; snprintf(bid, sizeof bid, "w%04zu", k);
+    Json e = Json::object(); e.set("name", t.name);
+    Json sh = Json::array(); for (auto v : t.shape) sh.push(Json(v)); e.set("shape", sh); e.set("dtype", "float32");
+    const int64_t rows = t.shape[0], cols = t.shape.size() > 1 ? t.shape[1] : 1;
+    if (t.q == Q::F32) { e.set("kind", "f32"); e.set("blob", std::string(bid) + ".f32"); plan.push_back({std::string(bid) + ".f32", 4ull * rows * cols}); }
+    else if (t.q == Q::Q8) {
+      e.set("kind", "q8"); e.set("blob", std::string(bid) + ".q8"); e.set("scale", std::string(bid) + ".scale");
+      plan.push_back({std::string(bid) + ".q8", (uint64_t)(rows * cols)}); plan.push_back({std::string(bid) + ".scale", 4ull * rows});
+    } else {
+      e.set("kind", "q4"); e.set("blob", std::string(bid) + ".q4"); e.set("scale", std::string(bid) + ".scale"); e.set("group", 32);
+      plan.push_back({std::string(bid) + ".q4", (uint64_t)(rows * cols / 2)}); plan.push_back({std::string(bid) + ".scale", 2ull * rows * (cols / 32)});
+    }
+    tl.push(e);
+  }
+  man.set("format", "QPACK2"); man.set("quant", s.q4 ? (s.q4m_alt ? "q4m" : "q4") : "q8"); man.set("tensors", tl);
+  man.set("synthetic", Json::object()); man.obj.back().second.set("seed", Json((int64_t)s.seed)); man.obj.back().second.set("std", Json((double)s.std));
+  Json cfg = Json::object();
+  cfg.set("arch", "llama"); cfg.set("model_type", s.model_type[0] ? s.model_type : "llama");
+  cfg.set("hidden_size", Json(d)); cfg.set("num_hidden_layers", s.layers); cfg.set("num_attention_heads", s.heads);
+  cfg.set("num_key_value_heads", s.kv_heads); cfg.set("head_dim", s.head_dim); cfg.set("intermediate_size", Json(ff));
+  cfg.set("vocab_size", Json(V)); cfg.set("rope_theta", s.rope_theta); cfg.set("max_position_embeddings", s.max_pos);
+  cfg.set("rms_norm_eps", (double)s.rms_eps); cfg.set("tie_embeddings", (bool)s.tied); cfg.set("qkv_bias", (bool)s.qkv_bias);
+  const std::string mj = man.dump(), cj = cfg.dump();
+  plan.insert(plan.begin(), {"config.json", cj.size()});
+  plan.insert(plan.begin(), {"manifest.json", mj.size()});
+
+  ContainerWriter w(path, plan, "QPACK2\0\0");
+  w.write("manifest.json", mj.data(), mj.size());
+  w.write("config.json", cj.data(), cj.size());
+  size_t pi = 2;
+  for (const Plan &t : ts) {
+    const int64_t rows = t.shape[0], cols = t.shape.size() > 1 ? t.shape[1] : 1;
+    if (t.q == Q::F32) {
+      std::vector<float> v((size_t)(rows * cols));
+      if (t.ones) std::fill(v.begin(), v.end(), 1.f); else normals(s.seed, t.tid, 0, rows * cols, s.std, v.data());
+      w.write(plan[pi].first, v.data(), plan[pi].second); pi++;
+    } else if (t.q == Q::Q8) {
+      std::vector<int8_t> q((size_t)(rows * cols)); std::vector<float> sc((size_t)rows);
+      parallel_rows(rows, threads, [&](int64_t a, int64_t b) {
+        std::vector<float> row((size_t)cols);
+        for (int64_t r = a; r < b; r++) {
+          normals(s.seed, t.tid, r * cols, (r + 1) * cols, s.std, row.data());
+          float mx = 0; for (float v : row) mx = std::max(mx, std::fabs(v));
+          float sr = mx / 127.f; if (sr == 0) sr = 1.f;
+          for (int64_t c = 0; c < cols; c++) q[(size_t)(r * cols + c)] = (int8_t)std::max(-127, std::min(127, (int)std::nearbyint(row[(size_t)c] / sr)));
+          sc[(size_t)r] = sr;
+        }
+      });
+      w.write(plan[pi].first, q.data(), plan[pi].second); pi++;
+      w.write(plan[pi].first, sc.data(), plan[pi].second); pi++;
+    } else {
+      const int64_t G = cols / 32;
+      std::vector<uint8_t> q((size_t)(rows * cols / 2)); std::vector<uint16_t> sc((size_t)(rows * G));
+      parallel_rows(rows, threads, [&](int64_t a, int64_t b) {
+        std::vector<float> row((size_t)cols);
+        for (int64_t r = a; r < b; r++) {
+          normals(s.seed, t.tid, r * cols, (r + 1) * cols, s.std, row.data());
+          for (int64_t g = 0; g < G; g++) {
+            const float *wg = row.data() + 32 * g; float amax = 0; int qv[32];
+            for (int i = 0; i < 32; i++) amax = std::max(amax, std::fabs(wg[i]));
+            uint16_t h = 0;
+            if (amax > 0) {
+              h = to_half(amax / 7.f); const float sh = from_half(h);
+              for (int i = 0; i < 32; i++) qv[i] = std::max(-8, std::min(7, (int)std::lrintf(wg[i] / sh)));
+            } else for (int i = 0; i < 32; i++) qv[i] = 0;
+            uint8_t *o = q.data() + (size_t)(r * (cols / 2) + 16 * g);
+            for (int j = 0; j < 16; j++) o[j] = (uint8_t)((qv[j] + 8) | ((qv[j + 16] + 8) << 4));
+            sc[(size_t)(r * G + g)] = h;
+          }
+        }
+      });
+      w.write(plan[pi].first, q.data(), plan[pi].second); pi++;
+      w.write(plan[pi].first, sc.data(), plan[pi].second); pi++;
+    }
+  }
+  w.close();
+}
+
+}  // namespace qph

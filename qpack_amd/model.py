@@ -1,0 +1,148 @@
+"""HipLlama: the Python face of the C ABI, method for method the reference's qp::Model
+(/root/reference/include/qpack/qpack.h:128-171).  Used by the tests and bench.py; C++ callers use include/qpack_hip.h
+directly."""
+import ctypes as C
+
+import numpy as np
+
+from ._lib import Config, check, lib
+
+
+def _fptr(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _iptr(a):
+    return a.ctypes.data_as(C.POINTER(C.c_int))
+
+
+class HipLlama:
+    def __init__(self, handle):
+        self._h = C.c_void_p(handle)
+        cfg = Config()
+        check(lib().qph_config_of(self._h, C.byref(cfg)))
+        self.config = cfg
+
+    @classmethod
+    def load(cls, path, max_ctx=0):
+        """load_model(path, max_ctx) with QPACK_DEVICE selecting this backend (model_llama.cpp:221-235)"""
+        h = C.c_void_p()
+        check(lib().qph_load(str(path).encode(), int(max_ctx), C.byref(h)))
+        return cls(h.value)
+
+    def close(self):
+        if self._h:
+            lib().qph_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    # ---- queries (qpack.h:131-134)
+    def vocab(self):
+        return lib().qph_vocab(self._h)
+
+    def hidden(self):
+        return lib().qph_hidden(self._h)
+
+    def max_ctx(self):
+        return lib().qph_max_ctx(self._h)
+
+    def pos(self):
+        return lib().qph_pos(self._h)
+
+    # ---- token loop
+    def step(self, token, want=1):
+        """Model::step: want 0 -> None, 1 -> logits [vocab] float32, 2 -> final normed hidden [hidden]"""
+        out = None
+        if want == 1:
+            out = np.empty(self.vocab(), np.float32)
+        elif want == 2:
+            out = np.empty(self.hidden(), np.float32)
+        check(lib().qph_step(self._h, int(token), int(want), _fptr(out) if out is not None else None))
+        return out
+
+    def prefill(self, tokens, want=1):
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = None
+        if want == 1:
+            out = np.empty(self.vocab(), np.float32)
+        elif want == 2:
+            out = np.empty(self.hidden(), np.float32)
+        check(lib().qph_prefill(self._h, _iptr(toks), len(toks), int(want), _fptr(out) if out is not None else None))
+        return out
+
+    def greedy_run(self, token, n):
+        out = np.zeros(max(n, 1), np.int32)
+        got = C.c_int(0)
+        check(lib().qph_greedy_run(self._h, int(token), int(n), _iptr(out), C.byref(got)))
+        return out[:got.value]
+
+    def prefill_all(self, tokens):
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((len(toks), self.vocab()), np.float32)
+        check(lib().qph_prefill_all(self._h, _iptr(toks), len(toks), _fptr(out)))
+        return out
+
+    def reset(self):
+        check(lib().qph_reset(self._h))
+
+    def rewind(self, pos):
+        ok = C.c_int(0)
+        check(lib().qph_rewind(self._h, int(pos), C.byref(ok)))
+        return bool(ok.value)
+
+    def checkpoint(self):
+        return np.int32(self.pos()).tobytes()
+
+    def rollback(self, c):
+        check(lib().qph_set_pos(self._h, int(np.frombuffer(c, np.int32)[0])))
+
+    def snapshot(self):
+        n = C.c_int64(0)
+        check(lib().qph_snapshot_size(self._h, C.byref(n)))
+        buf = np.empty(n.value, np.uint8)
+        check(lib().qph_snapshot(self._h, buf.ctypes.data_as(C.c_void_p), n.value))
+        return buf.tobytes()
+
+    def restore(self, s):
+        buf = np.frombuffer(s, np.uint8)
+        check(lib().qph_restore(self._h, buf.ctypes.data_as(C.c_void_p), len(buf)))
+
+    # ---- measurement
+    def time_greedy(self, token, n):
+        ms = C.c_float(0)
+        check(lib().qph_time_greedy(self._h, int(token), int(n), C.byref(ms)))
+        return ms.value
+
+    def time_kernel(self, which, iters):
+        ms, b = C.c_float(0), C.c_double(0)
+        check(lib().qph_time_kernel(self._h, int(which), int(iters), C.byref(ms), C.byref(b)))
+        return ms.value, b.value
+
+
+def kernel_matvec(kind, q, scale, x):
+    """the product's matvec kernel on one matrix: returns (y, exact int32 sums, int16 activation, block scales)"""
+    from ._lib import QPH_Q8
+    q = np.ascontiguousarray(q)
+    scale = np.ascontiguousarray(scale)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows = q.shape[0]
+    cols = q.shape[1] if kind == QPH_Q8 else q.shape[1] * 2
+    y = np.empty(rows, np.float32)
+    sums = np.empty((rows, cols // 128 if kind == QPH_Q8 else cols // 32), np.int32)
+    xq = np.empty(cols, np.int16)
+    bs = np.empty(cols // 128, np.float32)
+    check(lib().qph_kernel_matvec(kind, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols, _fptr(x),
+                                  _fptr(y), sums.ctypes.data_as(C.POINTER(C.c_int32)), xq.ctypes.data_as(C.POINTER(C.c_int16)),
+                                  _fptr(bs)))
+    return y, sums, xq, bs
