@@ -233,42 +233,44 @@ __global__ __launch_bounds__(kThreads) void k_matvec(MvArgs a) {
   const int total = a.seg_tile0[a.nseg];
   float best_v = -INFINITY; int best_i = 0x7fffffff;
   for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    int seg = 0;
-    while (seg + 1 < a.nseg && tile >= a.seg_tile0[seg + 1]) seg++;
-    const DMat *mats[kMvSlots]; int rows_[kMvSlots];
+    // segment of this tile, chosen with selects (no dynamic indexing of the kernel-argument struct)
+    const int seg = (a.nseg > 1 && tile >= a.seg_tile0[1]) ? ((a.nseg > 2 && tile >= a.seg_tile0[2]) ? 2 : 1) : 0;
+    const DMat msel = seg == 0 ? a.m[0] : (seg == 1 ? a.m[1] : a.m[2]);
+    const int tile0 = seg == 0 ? a.seg_tile0[0] : (seg == 1 ? a.seg_tile0[1] : a.seg_tile0[2]);
+    DMat mats[kMvSlots]; int rows_[kMvSlots];
     if (EPI == EPI_SWIGLU) {
       const int r = (tile - a.seg_tile0[0]) * kMvWaves + wave;
-      mats[0] = &a.m[0]; mats[1] = &a.m[1]; rows_[0] = rows_[1] = r;
+      mats[0] = a.m[0]; mats[1] = a.m[1]; rows_[0] = rows_[1] = r;
     } else {
-      const int r0 = (tile - a.seg_tile0[seg]) * (kMvWaves * kMvSlots) + wave * kMvSlots;
+      const int r0 = (tile - tile0) * (kMvWaves * kMvSlots) + wave * kMvSlots;
 #pragma unroll
-      for (int s = 0; s < kMvSlots; s++) { mats[s] = &a.m[seg]; rows_[s] = r0 + s; }
+      for (int s = 0; s < kMvSlots; s++) { mats[s] = msel; rows_[s] = r0 + s; }
     }
     int rc[kMvSlots];   // clamped rows: out-of-range slots compute row rows-1 and store nothing
 #pragma unroll
-    for (int s = 0; s < kMvSlots; s++) rc[s] = rows_[s] < mats[s]->rows ? rows_[s] : mats[s]->rows - 1;
+    for (int s = 0; s < kMvSlots; s++) rc[s] = rows_[s] < mats[s].rows ? rows_[s] : mats[s].rows - 1;
     float val[kMvSlots];
-    const int kind = mats[0]->kind;
+    const int kind = mats[0].kind;
     if (kind == MK_Q8) {
       const int8_t *rp[kMvSlots];
 #pragma unroll
-      for (int s = 0; s < kMvSlots; s++) rp[s] = (const int8_t *)mats[s]->q + (size_t)rc[s] * cols;
+      for (int s = 0; s < kMvSlots; s++) rp[s] = (const int8_t *)mats[s].q + (size_t)rc[s] * cols;
       dot_q8<kMvSlots>(rp, cols, av, lane, sums);
       __syncthreads();
       float acc = 0.f;
       if (lane < kMvSlots) {
         const int *ss = sums + lane * av.nbp;
         for (int b = 0; b < nb; b++) acc = __builtin_fmaf(av.bs[b], (float)ss[b], acc);
-        int rl = rc[0]; const float *scl = (const float *)mats[0]->s;
+        int rl = rc[0]; const float *scl = (const float *)mats[0].s;
 #pragma unroll
-        for (int s = 1; s < kMvSlots; s++) if (lane == s) { rl = rc[s]; scl = (const float *)mats[s]->s; }
+        for (int s = 1; s < kMvSlots; s++) if (lane == s) { rl = rc[s]; scl = (const float *)mats[s].s; }
         acc = acc * scl[rl];
       }
 #pragma unroll
       for (int s = 0; s < kMvSlots; s++) val[s] = lane_bcast(acc, s);
       if (a.dbg_sums && seg == 0) {
         for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s]->rows)
+          if (rows_[s] < mats[s].rows)
             for (int b = lane; b < nb; b += kWave) a.dbg_sums[(size_t)rows_[s] * nb + b] = sums[s * av.nbp + b];
       }
       __syncthreads();
@@ -277,34 +279,36 @@ __global__ __launch_bounds__(kThreads) void k_matvec(MvArgs a) {
       const int G = cols / 32;
 #pragma unroll
       for (int s = 0; s < kMvSlots; s++) {
-        rq[s] = (const uint8_t *)mats[s]->q + (size_t)rc[s] * (cols / 2);
-        rs[s] = (const uint16_t *)mats[s]->s + (size_t)rc[s] * G;
-        dbg[s] = (a.dbg_sums && seg == 0 && rows_[s] < mats[s]->rows && EPI != EPI_SWIGLU) ? a.dbg_sums + (size_t)rows_[s] * G : nullptr;
+        rq[s] = (const uint8_t *)mats[s].q + (size_t)rc[s] * (cols / 2);
+        rs[s] = (const uint16_t *)mats[s].s + (size_t)rc[s] * G;
+        dbg[s] = (a.dbg_sums && seg == 0 && rows_[s] < mats[s].rows && EPI != EPI_SWIGLU) ? a.dbg_sums + (size_t)rows_[s] * G : nullptr;
       }
       dot_q4<kMvSlots>(rq, rs, cols, av, lane, val, dbg);
     }
+    float *const out_seg = seg == 0 ? a.out[0] : (seg == 1 ? a.out[1] : a.out[2]);
+    const float *const bias_seg = seg == 0 ? a.bias[0] : (seg == 1 ? a.bias[1] : a.bias[2]);
     if (lane == 0) {
       if (EPI == EPI_STORE) {
 #pragma unroll
         for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s]->rows) {
+          if (rows_[s] < mats[s].rows) {
             float y = val[s];
-            if (a.bias[seg]) y = y + a.bias[seg][rows_[s]];
-            a.out[seg][rows_[s]] = y;
+            if (bias_seg) y = y + bias_seg[rows_[s]];
+            out_seg[rows_[s]] = y;
           }
       } else if (EPI == EPI_RESID) {
 #pragma unroll
         for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s]->rows) a.out[0][rows_[s]] = a.out[0][rows_[s]] + val[s];
+          if (rows_[s] < mats[s].rows) a.out[0][rows_[s]] = a.out[0][rows_[s]] + val[s];
       } else if (EPI == EPI_SWIGLU) {
-        if (rows_[0] < mats[0]->rows) {
+        if (rows_[0] < mats[0].rows) {
           const float g = val[0], u = val[1];
           a.out[0][rows_[0]] = g / (1.f + exp_poly(0.f - g)) * u;   // silu_mul, kernels_x86.cpp:427-431
         }
       } else {
 #pragma unroll
         for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s]->rows) {
+          if (rows_[s] < mats[s].rows) {
             a.out[0][rows_[s]] = val[s];
             if (better(val[s], rows_[s], best_v, best_i)) { best_v = val[s]; best_i = rows_[s]; }
           }

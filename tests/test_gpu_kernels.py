@@ -1,0 +1,62 @@
+"""GPU parity of the matvec kernel (the decode hot path) against the oracle, through the C ABI.
+
+Bar: int16 activations, block scales and int32 accumulators bit-exact; q8 outputs bit-identical to rows_q8
+(/root/reference/src/kernels_x86.cpp:55-71); q4 outputs within 2e-6 relative to the sum of |group terms| (the q4
+float order is a per-lane chain + wave tree instead of rows_q4's 8-lane split).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import qpack_amd as qa
+
+pytestmark = pytest.mark.gpu
+
+
+def act_vector(rng, cols):
+    """N(0,1) activations with the cases quant_rows must get right: an all-zero block, outliers, a single spike"""
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    x[128:256] = 0                      # all-zero block -> scale 0
+    x[5] = 300.0                        # outlier coarsens only its own block
+    x[-128:] = 0; x[-60] = -7.25        # one non-zero value in a block
+    x[300:310] = 1e-30                  # tiny values
+    return x
+
+
+def q8_matrix(rng, rows, cols):
+    q = rng.integers(-127, 128, (rows, cols)).astype(np.int8)
+    q[0, :] = 127; q[min(1, rows - 1), :] = -127       # extreme rows
+    s = (rng.random(rows).astype(np.float32) * 0.01 + 1e-4).astype(np.float32)
+    return q, s
+
+
+@pytest.mark.parametrize("rows,cols", [(1000, 4096), (513, 896), (300, 14336), (64, 18944), (7, 128), (4864, 896)])
+def test_matvec_q8_bit_exact(rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    q, s = q8_matrix(rng, rows, cols)
+    x = act_vector(rng, cols)
+    print(f"q8 matvec rows={rows} cols={cols}", flush=True)
+    y, sums, xq, bs = qa.kernel_matvec(qa.QPH_Q8, q, s, x)
+    xq_o, bs_o = O.quant_act(x)
+    np.testing.assert_array_equal(xq, xq_o)
+    np.testing.assert_array_equal(bs, bs_o)
+    np.testing.assert_array_equal(sums, O.block_sums_q8(q, xq_o))
+    np.testing.assert_array_equal(y, O.rows_q8(q, s, xq_o, bs_o))
+
+
+@pytest.mark.parametrize("rows,cols", [(1000, 4096), (257, 896), (300, 18944), (9, 128), (3584, 3584)])
+def test_matvec_q4_exact_sums(rows, cols):
+    rng = np.random.default_rng(rows * 11 + cols)
+    q = rng.integers(0, 256, (rows, cols // 2)).astype(np.uint8)
+    s = (rng.random((rows, cols // 32)) * 0.01 + 1e-4).astype(np.float16).view(np.uint16)
+    x = act_vector(rng, cols)
+    print(f"q4 matvec rows={rows} cols={cols}", flush=True)
+    y, sums, xq, bs = qa.kernel_matvec(qa.QPH_Q4, q, s, x)
+    xq_o, bs_o = O.quant_act(x)
+    np.testing.assert_array_equal(xq, xq_o)
+    gs = O.group_sums_q4(q, xq_o)
+    np.testing.assert_array_equal(sums, gs)
+    y_o = O.rows_q4(q, s, xq_o, bs_o)
+    comb = s.view(np.float16).astype(np.float32) * np.repeat(bs_o, 4)[None, :]
+    mag = np.abs(comb * gs).sum(1)
+    assert np.all(np.abs(y - y_o) <= 2e-6 * mag + 1e-30), float(np.max(np.abs(y - y_o) / (mag + 1e-30)))
