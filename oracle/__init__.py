@@ -60,8 +60,12 @@ class QpackFile:
         raise ValueError(f"tensor kind {e['kind']} not handled by the oracle")
 
     def close(self):
+        """releases the file; the mapping itself closes once no numpy view of it is alive"""
         self.buf = None
-        self.mm.close()
+        try:
+            self.mm.close()
+        except BufferError:
+            pass
         self.f.close()
 
 

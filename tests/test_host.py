@@ -1,0 +1,107 @@
+"""Host-side checks (CPU only): the C ABI library loads and exports every declared symbol, the QPACK2 writer produces
+files the reference format readers accept, the synthetic generator is deterministic, and argument errors are reported
+through the error channel without touching a GPU."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as O
+import qpack_amd as qa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    txt = open(os.path.join(ROOT, "include", "qpack_hip.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(qph_[a-z_0-9]+)\s*\(", txt)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = qa.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 25
+    for s in syms:
+        assert hasattr(L, s), s
+    assert set(syms) == set(qa._lib.SIGNATURES), "ctypes signatures out of sync with include/qpack_hip.h"
+
+
+def test_device_count_without_gpu_is_not_an_error():
+    assert qa.device_count() >= 0
+
+
+def test_errors_without_gpu():
+    with pytest.raises(qa.QphError, match="cannot open"):
+        qa.HipLlama.load("/nonexistent/model.qpack")
+    q = np.zeros((4, 100), np.int8)
+    with pytest.raises(qa.QphError, match="multiple of 128"):
+        qa.kernel_matvec(qa.QPH_Q8, q, np.ones(4, np.float32), np.zeros(100, np.float32))
+
+
+def test_bad_container_is_rejected(tmp_path):
+    p = tmp_path / "bad.qpack"
+    p.write_bytes(b"NOTQPACK" + b"\0" * 64)
+    with pytest.raises(qa.QphError, match="not a QPACK"):
+        qa.HipLlama.load(str(p))
+    p.write_bytes(b"QPACK2\0\0" + np.uint32(1).tobytes() + b"\0" * 4 + b"x" * 56 + np.uint64(10 ** 9).tobytes() * 2)
+    with pytest.raises(qa.QphError, match="corrupt table of contents"):
+        qa.HipLlama.load(str(p))
+
+
+@pytest.mark.parametrize("name", ["mini", "mini_q4m"])
+def test_synthetic_file_layout(name, tmp_path):
+    p = str(tmp_path / "m.qpack")
+    qa.write_synthetic(name, p, seed=5)
+    f = O.QpackFile(p)
+    shape = qa.CONFIGS[name]
+    c = f.config
+    assert c["arch"] == "llama" and c["hidden_size"] == shape.hidden and c["tie_embeddings"] == shape.tied
+    for nm, (off, ln) in f.toc.items():
+        assert off % 64 == 0, nm
+    # q8 rule (/root/reference/tools/qpack-quantize.cpp:327-339): every row reaches |q| = 127, q in [-127, 127]
+    k, q, s, rows, cols = f.tensor("embed")
+    assert k == O.OR_Q8 and q.shape == (shape.vocab, shape.hidden)
+    assert np.all(np.abs(q.astype(np.int32)).max(1) == 127) and q.min() >= -127
+    assert np.all((s > 0.02 * 2 / 127) & (s < 0.02 * 6.5 / 127))   # row absmax of N(0, 0.02) over hundreds of columns
+    if shape.q4:
+        k, q4, s4, rows, cols = f.tensor("layers.0.wq")
+        assert k == O.OR_Q4
+        nib = np.concatenate([q4 & 15, q4 >> 4], axis=1)
+        assert nib.max() <= 15 and np.any(nib == 1)   # q = -7 present (absmax maps to +-7)
+        k2 = f.tensor("layers.0.wv")[0]
+        assert k2 == (O.OR_Q8 if shape.q4m_alt else O.OR_Q4)
+    n = f.tensor("final_norm")[1]
+    assert np.all(n == 1.0)
+    f.close()
+
+
+def test_synthetic_is_deterministic_across_threads(tmp_path):
+    a, b, c = (str(tmp_path / f"{i}.qpack") for i in range(3))
+    qa.write_synthetic("mini_q4m", a, seed=9, threads=1)
+    qa.write_synthetic("mini_q4m", b, seed=9, threads=7)
+    qa.write_synthetic("mini_q4m", c, seed=10, threads=7)
+    assert open(a, "rb").read() == open(b, "rb").read()
+    assert open(a, "rb").read() != open(c, "rb").read()
+
+
+def test_weights_are_normal(tmp_path):
+    p = str(tmp_path / "m.qpack")
+    qa.write_synthetic("mini128", p, seed=3, std=0.02)
+    f = O.QpackFile(p)
+    k, q, s, rows, cols = f.tensor("layers.1.w_up")
+    w = q.astype(np.float64) * s[:, None]
+    assert abs(w.mean()) < 1e-4 and abs(w.std() - 0.02) < 5e-4
+    kurt = ((w - w.mean()) ** 4).mean() / w.var() ** 2
+    assert abs(kurt - 3.0) < 0.1
+    f.close()
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_reference_reads_synthetic_files(tmp_path):
+    p = str(tmp_path / "m.qpack")
+    qa.write_synthetic("mini_q4m", p, seed=2)
+    r = O.Ref(p, 32)
+    assert r.vocab() == qa.CONFIGS["mini_q4m"].vocab and r.hidden() == qa.CONFIGS["mini_q4m"].hidden
+    r.close()
