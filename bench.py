@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""bench.py - batch-1 decode tokens/s (+ % of HBM peak) and prefill tokens/s of the 8B-shape q8 Llama on one MI355X.
+
+Workload (BASELINE.json configs[2] / [3]): Llama-3-8B shape (32 layers, hidden 4096, 32 / 8 heads, head_dim 128,
+SwiGLU 14336, vocab 128256, untied head), seeded N(0, 0.02) random-init weights in q8, fp16 KV cache.
+  decode  - 128-token prompt, `--warmup` untimed greedy tokens, then exactly `--steps` greedy tokens timed (device
+            argmax feeds the next step; HIP events on the model's stream, host clock around it)
+  prefill - one `--prefill-tokens` prompt (C4), host clock around qph_prefill
+Roofline: the dominant decode kernel (layer-0 fused RMSNorm + gate/up + SwiGLU matvec, ~47 % of the step's bytes),
+replayed alone and timed with HIP events on the model's stream; achieved = its algorithmic bytes / mean duration.
+CPU baseline: the reference engine compiled from its own sources (oracle/_ref/libqpref.so, AVX2) on the same file,
+on the host cores, qpack-bench protocol on a bounded sample.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "batch-1 decode tokens/s + % HBM peak; prefill tokens/s (8B-shape q8)"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def step_bytes(shape, T):
+    """algorithmic HBM bytes of one decode step at context T: every weight byte + scale once, norms / biases, the embedding
+    row, and the fp16 K and V rows of positions [0, T) in every layer"""
+    d, ff, V, L = shape.hidden, shape.ffn, shape.vocab, shape.layers
+    qd, kvd = shape.heads * shape.head_dim, shape.kv_heads * shape.head_dim
+
+    def mat(rows, cols, q4):
+        return rows * cols / 2 + 2 * rows * (cols // 32) if q4 else rows * cols + 4 * rows
+    q4 = shape.q4
+    layer = (mat(qd, d, q4) + mat(kvd, d, q4) + mat(kvd, d, q4 and not shape.q4m_alt) + mat(d, qd, q4)
+             + 2 * mat(ff, d, q4) + mat(d, ff, q4) + 2 * 4 * d + (4 * (qd + 2 * kvd) if shape.qkv_bias else 0))
+    if q4 and shape.q4m_alt:   # even layers keep w_down in q8
+        layer_down_q8 = mat(d, ff, False) - mat(d, ff, True)
+        weights = L * layer + (L + 1) // 2 * layer_down_q8
+    else:
+        weights = L * layer
+    head = mat(V, d, False) + 4 * d
+    kv = L * 2 * T * kvd * 2
+    return weights + head + d + kv
+
+
+def cpu_baseline(path, threads, n_prompt=16, n_gen=16, reps=2):
+    """qpack-bench --row protocol (tools/qpack-bench.cpp:35-47) on the reference engine: reset, prefill(np), ng x step,
+    best of reps"""
+    import oracle
+    L = oracle.rlib(threads)
+    ref = oracle.Ref(path, n_prompt + n_gen + 8)
+    toks = np.array([100 + (i * 37) % 5000 for i in range(n_prompt)], np.int32)
+    pp = tg = 0.0
+    for _ in range(reps):
+        ref.reset()
+        t0 = time.time()
+        ref.prefill(toks, 1)
+        t1 = time.time()
+        for i in range(n_gen):
+            ref.step(100 + (i * 53) % 5000, 1)
+        t2 = time.time()
+        pp, tg = max(pp, n_prompt / (t1 - t0)), max(tg, n_gen / (t2 - t1))
+    used = L.qpref_threads()
+    ref.close()
+    return dict(value=round(tg, 3), unit="tokens/s", cores=used, kind="reference",
+                sample=f"reference qp::Llama (AVX2, {used} threads) on the same C3 file: prefill {n_prompt} + {n_gen} decode steps "
+                       f"(qpack-bench protocol, best of {reps}); its prefill rate {pp:.2f} tok/s")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed greedy decode tokens")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed greedy decode tokens before the timed ones")
+    ap.add_argument("--config", default="c3", help="synthetic shape (qpack_amd.CONFIGS key)")
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--kernel-iters", type=int, default=100)
+    ap.add_argument("--model", help="use this .qpack instead of synthesising one")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); the multi-GPU sharding plan is "
+              "design-only (DESIGN.md, 'More than one GPU')", file=sys.stderr)
+        sys.exit(2)
+
+    import qpack_amd as qa
+    if qa.device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    shape = qa.CONFIGS[a.config]
+    tmpdir = None
+    path = a.model
+    if not path:
+        tmpdir = tempfile.mkdtemp(prefix="qpack_bench_")
+        path = os.path.join(tmpdir, f"{a.config}.qpack")
+        t = time.time()
+        qa.write_synthetic(a.config, path, seed=a.seed, threads=min(16, os.cpu_count() or 8))
+        log(f"synthesised {a.config} ({os.path.getsize(path) / 2**30:.2f} GiB) in {time.time() - t:.1f}s")
+    ctx = max(a.prompt + a.warmup + a.steps + 8, (0 if a.no_prefill else a.prefill_tokens) + 8)
+    t = time.time()
+    m = qa.HipLlama.load(path, max_ctx=ctx)
+    log(f"loaded into HBM in {time.time() - t:.1f}s (max_ctx {ctx})")
+
+    rng = np.random.default_rng(a.seed)
+    prompt = rng.integers(0, shape.vocab, a.prompt).astype(np.int32)
+    lg = m.prefill(prompt, 1)
+    tok = int(np.argmax(lg))
+    if a.warmup:
+        tok = int(m.greedy_run(tok, a.warmup)[-1])
+    T0 = m.pos()
+    t0 = time.perf_counter()
+    ms = m.time_greedy(tok, a.steps)
+    wall = time.perf_counter() - t0
+    T1 = m.pos()
+    tok_s = a.steps / (ms / 1e3)
+    mean_T = (T0 + 1 + T1) / 2
+    sb = step_bytes(shape, mean_T)
+    step_gbs = sb / (ms / 1e3 / a.steps) / 1e9
+    log(f"decode: {a.steps} tokens in {ms:.2f} ms (HIP events), wall {wall * 1e3:.2f} ms -> {tok_s:.1f} tok/s, "
+        f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / HBM_PEAK_GBS:.1f}% of peak)")
+
+    kms, kbytes = m.time_kernel(0, a.kernel_iters)
+    k_gbs = kbytes / (kms / 1e3) / 1e9
+    log(f"dominant kernel (layer-0 gate/up matvec): {kms * 1e3:.2f} us, {kbytes / 1e6:.1f} MB -> {k_gbs:.0f} GB/s")
+    others = {}
+    for which, name in [(1, "down"), (2, "qkv"), (3, "wo"), (4, "head"), (5, "attention")]:
+        ks, kb = m.time_kernel(which, a.kernel_iters)
+        others[name] = dict(us=round(ks * 1e3, 2), mbytes=round(kb / 1e6, 3), gbs=round(kb / (ks / 1e3) / 1e9, 1))
+        log(f"  {name}: {ks * 1e3:.2f} us, {kb / 1e6:.2f} MB -> {kb / (ks / 1e3) / 1e9:.0f} GB/s")
+
+    prefill = None
+    if not a.no_prefill:
+        m.reset()
+        p2 = rng.integers(0, shape.vocab, a.prefill_tokens).astype(np.int32)
+        t = time.perf_counter()
+        m.prefill(p2, 1)
+        pt = time.perf_counter() - t
+        prefill = dict(tokens=a.prefill_tokens, seconds=round(pt, 4), tokens_per_s=round(a.prefill_tokens / pt, 1),
+                       path="per-token decode steps (the batched MFMA prefill is not wired yet)")
+        log(f"prefill {a.prefill_tokens} tokens: {pt:.3f}s -> {a.prefill_tokens / pt:.1f} tok/s")
+    m.close()
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        import oracle
+        if oracle.ref_available():
+            t = time.time()
+            cpu = cpu_baseline(path, min(16, os.cpu_count() or 1))
+            log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads ({time.time() - t:.1f}s)")
+        else:
+            log("cpu baseline skipped: oracle/_ref/libqpref.so is not built")
+    if tmpdir:
+        os.remove(path)
+        os.rmdir(tmpdir)
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms / a.steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x int16 activations -> int32 (fp32 epilogue, fp16 KV)",
+        "data": f"synthetic: seeded N(0,0.02) random-init weights quantised to q8 (seed {a.seed}), uniform random prompt ids",
+        "config": {"workload": f"{a.config}: Llama-3-8B-shape q8 batch-1 decode, {a.prompt}-token prompt + {a.warmup} warm-up + "
+                               f"{a.steps} timed greedy tokens, fp16 KV (context {T0}..{T1})",
+                   "decode_tokens": a.steps, "prompt_tokens": a.prompt, "parallelism": "single GPU"},
+        "hbm_pct_of_peak": round(100 * step_gbs / HBM_PEAK_GBS, 2),
+        "step_roofline": {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(step_gbs / HBM_PEAK_GBS, 4), "bytes_per_token": round(sb)},
+        "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_matvec<PRO_NORM,EPI_SWIGLU> (layer-0 gate+up, 2 x 14336 x 4096 q8)",
+                     "bytes_per_launch": round(kbytes), "us_per_launch": round(kms * 1e3, 2)},
+        "kernels": others,
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
