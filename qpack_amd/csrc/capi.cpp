@@ -164,7 +164,7 @@ int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int 
       qph::MvArgs a{}; a.m[0].q = dq; a.m[0].s = ds; a.m[0].rows = rows; a.m[0].cols = cols; a.m[0].kind = kind == QPH_Q8 ? qph::MK_Q8 : qph::MK_Q4;
       a.nseg = 1; a.x = dx; a.out[0] = dy; a.dbg_sums = dsum; a.dbg_xq = dxq; a.dbg_bs = dbs;
       qph::mv_plan(a, qph::EPI_STORE);
-      hck(qph::launch_matvec(qph::PRO_QUANT, qph::EPI_STORE, a, 1024, nullptr), "launch matvec");
+      hck(qph::launch_matvec(qph::PRO_QUANT, qph::EPI_STORE, a, 256, nullptr), "launch matvec");
       hck(hipDeviceSynchronize(), "matvec");
       hck(hipMemcpy(y, dy, 4ull * rows, hipMemcpyDeviceToHost), "download y");
       if (sums) hck(hipMemcpy(sums, dsum, 4 * nsum, hipMemcpyDeviceToHost), "download sums");

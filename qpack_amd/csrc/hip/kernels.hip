@@ -15,6 +15,8 @@
 // The prologue optionally fuses RMSNorm (PRO_NORM); epilogues fuse bias, residual add, SwiGLU and the argmax partials.
 #include <math.h>
 
+#include <algorithm>
+
 #include "launch.hpp"
 
 namespace qph {
@@ -28,7 +30,7 @@ struct ActView {
   float *bs;     // [nb] block scales
   int *lsum;     // [nb] sum of the low bytes per 128-column block
   int *gsum;     // [cols / 32] sum of q per 32-column group
-  float *red;    // [16] reduction scratch
+  float *red;    // [32] reduction scratch (16 wave partials, argmax values and indices)
   int *sums;     // [waves][slots][nbp] q8 block sums
   int nbp;
 };
@@ -44,53 +46,85 @@ __device__ inline ActView act_view(char *smem, int cols) {
   v.lsum = (int *)(v.bs + v.nbp);
   v.gsum = v.lsum + v.nbp;
   v.red = (float *)(v.gsum + round_up(G, 4));
-  v.sums = (int *)(v.red + 16);
+  v.sums = (int *)(v.red + 32);
   return v;
 }
-size_t mv_lds_bytes(int cols) {
+size_t mv_lds_bytes(int cols, int waves) {
   const int nb = cols / kQB, G = cols / 32, nbp = round_up(nb, 4);
-  return (size_t)2 * cols + 4 * (size_t)nbp * 2 + 4 * (size_t)round_up(G, 4) + 16 * 4 + 4 * (size_t)kMvWaves * kMvSlots * nbp;
+  return (size_t)2 * cols + 4 * (size_t)nbp * 2 + 4 * (size_t)round_up(G, 4) + 32 * 4 + 4 * (size_t)waves * kMvSlots * nbp;
 }
 
-// 1 / sqrt(sum(x^2) / n + eps) over the workgroup: per-thread fma sums over a 256-stride, a butterfly per wave and the
-// four wave sums added in a fixed order.  (The reference sums sequentially, kernels.cpp:185; the order differs.)
-__device__ float block_rms_inv(const float *x, int n, float eps, float *red) {
-  float s = 0;
-  for (int i = threadIdx.x; i < n; i += kThreads) s = __builtin_fmaf(x[i], x[i], s);
-  s = wave_sum(s);
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[w] = s;
-  __syncthreads();
-  const float ss = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();
-  return 1.f / sqrtf(ss / (float)n + eps);
-}
-
-// builds the int16 activation of x (optionally RMSNorm(x) * w first) in LDS.  Eight lanes own a 128-column block,
-// 16 columns each.  Arithmetic of quant_rows: mx = max |v|, isx = mx > 0 ? 32767 / mx : 0, bs = mx / 32767,
-// q = rint(v * isx).
+// The activation prologue in two halves, so its global reads are issued before the weight prefetch (a wave's loads
+// return in order: a read issued after the prefetch would wait for all of it).
+//   act_load:   eight lanes own a 128-column block, 16 columns each (two passes cover up to 2 x blockDim.x / 8 blocks);
+//               x (and the RMSNorm weight) go to registers.
+//   act_build:  optional RMSNorm, then quant_rows' arithmetic (/root/reference/src/kernels.cpp:17-31): mx = max |v|,
+//               isx = mx > 0 ? 32767 / mx : 0, bs = mx / 32767, q = rint(v * isx); written to LDS as byte planes.
+// The sum of squares is taken per 128-column block (each lane fma-sums its 16 columns in order, the 8 lanes add with
+// DPP), then wave 0 adds the block sums in a fixed tree: the same value for every workgroup size.  (The reference sums
+// sequentially, kernels.cpp:185; the order differs.)
+struct ActRegs {
+  float4 x[2][4];
+  float4 w[2][4];
+};
 template <int PRO>
-__device__ void build_act(const float *x, const float *w, float eps, int cols, const ActView &a) {
+__device__ __forceinline__ void act_load(const float *x, const float *w, int cols, ActRegs &r) {
+  const int nb = cols / kQB, per = (int)blockDim.x / 8, sub = threadIdx.x & 7;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int b = p * per + (int)(threadIdx.x >> 3);
+    if (b < nb) {
+      const int c0 = b * kQB + sub * 16;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        r.x[p][k] = *(const float4 *)(x + c0 + 4 * k);
+        if (PRO == PRO_NORM) r.w[p][k] = *(const float4 *)(w + c0 + 4 * k);
+      }
+    }
+  }
+}
+__device__ __forceinline__ float f4get(const float4 &v, int j) { return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w)); }
+
+template <int PRO>
+__device__ void act_build(const ActRegs &r, float eps, int cols, const ActView &a) {
+  const int nb = cols / kQB, per = (int)blockDim.x / 8, sub = threadIdx.x & 7;
   float inv = 1.f;
-  if (PRO == PRO_NORM) inv = block_rms_inv(x, cols, eps, a.red);
-  const int nb = cols / kQB, tid = threadIdx.x, sub = tid & 7;
-  for (int b0 = 0; b0 < nb; b0 += kThreads / 8) {
-    const int b = b0 + (tid >> 3);
+  if (PRO == PRO_NORM) {
+    float *bss = (float *)a.sums;   // block sums of squares; the sums area is free until the main loop
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int b = p * per + (int)(threadIdx.x >> 3);
+      if (b < nb) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) { const float v = f4get(r.x[p][k >> 2], k & 3); s = __builtin_fmaf(v, v, s); }
+        s += dpp_f<kDppQuadXor1>(s);
+        s += dpp_f<kDppQuadXor2>(s);
+        s += dpp_f<kDppHalfMirror>(s);
+        if (sub == 0) bss[b] = s;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      float v[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) { const int b = (int)threadIdx.x + 64 * k; v[k] = b < nb ? bss[b] : 0.f; }
+      const float t = wave_sum((v[0] + v[1]) + (v[2] + v[3]));
+      if (threadIdx.x == 0) a.red[0] = 1.f / sqrtf(t / (float)cols + eps);
+    }
+    __syncthreads();
+    inv = a.red[0];
+  }
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int b = p * per + (int)(threadIdx.x >> 3);
     if (b < nb) {
       const int c0 = b * kQB + sub * 16;
       float v[16];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const float4 t = *(const float4 *)(x + c0 + 4 * k);
-        v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
-      }
-      if (PRO == PRO_NORM) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const float4 t = *(const float4 *)(w + c0 + 4 * k);
-          v[4 * k] = v[4 * k] * inv * t.x; v[4 * k + 1] = v[4 * k + 1] * inv * t.y;
-          v[4 * k + 2] = v[4 * k + 2] * inv * t.z; v[4 * k + 3] = v[4 * k + 3] * inv * t.w;
-        }
+      for (int k = 0; k < 16; k++) {
+        v[k] = f4get(r.x[p][k >> 2], k & 3);
+        if (PRO == PRO_NORM) v[k] = v[k] * inv * f4get(r.w[p][k >> 2], k & 3);
       }
       float m = 0;
 #pragma unroll
@@ -122,234 +156,278 @@ __device__ void build_act(const float *x, const float *w, float eps, int cols, c
   __syncthreads();
 }
 
-// ------------------------------------------------------------------ dot products of row slots
+// ------------------------------------------------------------------ streaming matvec
 // one 16-byte weight load (global_load_dwordx4)
 __device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
+__device__ __forceinline__ float lane_bcast(float v, int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane)); }
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-// q8: NS rows against the LDS activation; block sums (already corrected by -128 sum(l)) go to sums[s * nbp + b].
+// A unit is NS rows of one segment (EPI_SWIGLU: row r of the gate and of the up matrix).  Waves own units
+// round-robin and stream them chunk by chunk (1 KiB of every row of the unit per step: lane i reads bytes [16 i, 16 i + 16)).
 template <int NS>
-__device__ __forceinline__ void dot_q8(const int8_t *const rowp[NS], int cols, const ActView &a, int lane, int *sums) {
-  constexpr int U = 4;
-  const int nch = (cols + 1023) >> 10;
-  for (int c0 = 0; c0 < nch; c0 += U) {
-    uint4 w[U][NS];
+struct UnitGeo {
+  const uint8_t *p[NS];     // row bytes (clamped rows)
+  const uint16_t *sp[NS];   // q4 fp16 scale rows
+  const float *sc[NS];      // q8 row scale
+  int row[NS];              // output rows (may be >= rows: computed, not stored)
+  int rows, seg, kind, nch, rowbytes;
+};
+
+template <int EPI, int NS>
+__device__ __forceinline__ UnitGeo<NS> unit_geo(const MvArgs &a, int u, int cols) {
+  UnitGeo<NS> g;
+  int seg = 0;
+  if (EPI != EPI_SWIGLU && a.nseg > 1 && u >= a.seg_tile0[1]) seg = (a.nseg > 2 && u >= a.seg_tile0[2]) ? 2 : 1;
+  const DMat m0 = seg == 0 ? a.m[0] : (seg == 1 ? a.m[1] : a.m[2]);
+  const int u0 = seg == 0 ? a.seg_tile0[0] : (seg == 1 ? a.seg_tile0[1] : a.seg_tile0[2]);
+  g.seg = seg; g.kind = m0.kind; g.rows = m0.rows;
+  g.rowbytes = m0.kind == MK_Q8 ? cols : cols / 2;
+  g.nch = (g.rowbytes + 1023) >> 10;
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int col = (c0 + u) * 1024 + lane * 16;
-#pragma unroll
-      for (int s = 0; s < NS; s++)
-        w[u][s] = (c0 + u < nch && col < cols) ? ld16(rowp[s] + col) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int c = c0 + u;
-      if (c >= nch) break;
-      const int col = c * 1024 + lane * 16;
-      const bool act = col < cols;
-      const uint4 h = act ? *(const uint4 *)(a.xh + col) : make_uint4(0, 0, 0, 0);
-      const uint4 l = act ? *(const uint4 *)(a.xl + col) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int s = 0; s < NS; s++) {
-        const uint4 ww = w[u][s];
-        int A = __builtin_amdgcn_sdot4((int)ww.x, (int)h.x, 0, false);
-        A = __builtin_amdgcn_sdot4((int)ww.y, (int)h.y, A, false);
-        A = __builtin_amdgcn_sdot4((int)ww.z, (int)h.z, A, false);
-        A = __builtin_amdgcn_sdot4((int)ww.w, (int)h.w, A, false);
-        uint32_t B = __builtin_amdgcn_udot4(ww.x ^ 0x80808080u, l.x, 0u, false);
-        B = __builtin_amdgcn_udot4(ww.y ^ 0x80808080u, l.y, B, false);
-        B = __builtin_amdgcn_udot4(ww.z ^ 0x80808080u, l.z, B, false);
-        B = __builtin_amdgcn_udot4(ww.w ^ 0x80808080u, l.w, B, false);
-        const int p = sum8_i(A * 256 + (int)B);
-        if (act && (lane & 7) == 0) {
-          const int b = c * 8 + (lane >> 3);
-          sums[s * a.nbp + b] = p - 128 * a.lsum[b];
-        }
-      }
-    }
+  for (int s = 0; s < NS; s++) {
+    const DMat m = (EPI == EPI_SWIGLU && s == 1) ? a.m[1] : m0;
+    const int r = EPI == EPI_SWIGLU ? (u - u0) : (u - u0) * NS + s;
+    g.row[s] = r;
+    const int rc = r < m.rows ? r : m.rows - 1;
+    g.p[s] = (const uint8_t *)m.q + (size_t)rc * g.rowbytes;
+    g.sp[s] = (const uint16_t *)m.s + (size_t)rc * (cols / 32);
+    g.sc[s] = (const float *)m.s + rc;
   }
+  return g;
 }
 
-// q4: NS rows; returns each row's value (identical in every lane).  Optional exact group sums into dbg[s][g].
-template <int NS>
-__device__ __forceinline__ void dot_q4(const uint8_t *const rowq[NS], const uint16_t *const rows_s[NS], int cols, const ActView &a,
-                                       int lane, float out[NS], int32_t *const dbg[NS]) {
-  const int G = cols / 32, nch = (G + 63) >> 6;
+// the matvec kernel: prefetch ring of D steps per wave (issued before the activation prologue, so weight streaming
+// starts at launch), no workgroup barrier after the prologue.
+template <int PRO, int EPI, int NS>
+__global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
+  const int WAVES = (int)blockDim.x >> 6;
+  constexpr int D = NS == 1 ? 8 : 4;
+  extern __shared__ __align__(16) char smem[];
+  const int cols = a.m[0].cols, G = cols / 32, nb = cols / kQB;
+  const ActView av = act_view(smem, cols);
+  // wave-uniform bookkeeping lives in scalar registers (the compiler cannot prove threadIdx.x >> 6 uniform)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int W = gridDim.x * WAVES, gw = wave * gridDim.x + blockIdx.x;
+  const int U = a.seg_tile0[a.nseg];
+  const int nmine = gw < U ? (U - gw + W - 1) / W : 0;
+  int *sums = av.sums + wave * kMvSlots * av.nbp;
+
+  ActRegs ar;
+  act_load<PRO>(a.x, a.norm_w, cols, ar);
+  uint4 wr[D][NS];
+  uint16_t sr[D][NS];
+  int pi = 0, pc = 0;
+  UnitGeo<NS> pg = unit_geo<EPI, NS>(a, nmine ? gw : 0, cols);
+  auto issue = [&](uint4 (&w)[NS], uint16_t (&sv)[NS]) {
+    if (pi < nmine) {
+      const int off = pc * 1024 + lane * 16, grp = pc * 64 + lane;
+#pragma unroll
+      for (int s = 0; s < NS; s++) {
+        w[s] = off < pg.rowbytes ? ld16(pg.p[s] + off) : make_uint4(0, 0, 0, 0);
+        sv[s] = (pg.kind == MK_Q4 && grp < G) ? pg.sp[s][grp] : (uint16_t)0;
+      }
+      if (++pc == pg.nch) { pc = 0; if (++pi < nmine) pg = unit_geo<EPI, NS>(a, gw + pi * W, cols); }
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < D; k++) issue(wr[k], sr[k]);
+
+  act_build<PRO>(ar, a.eps, cols, av);
+  if (blockIdx.x == 0 && (a.dbg_xq || a.dbg_bs)) {
+    for (int c = threadIdx.x; c < cols; c += blockDim.x)
+      if (a.dbg_xq) a.dbg_xq[c] = (int16_t)(((int)av.xh[c] << 8) | av.xl[c]);
+    for (int b = threadIdx.x; b < nb; b += blockDim.x)
+      if (a.dbg_bs) a.dbg_bs[b] = av.bs[b];
+  }
+
+  float best_v = -INFINITY; int best_i = 0x7fffffff;
+  int ci = 0, cc = 0;
+  UnitGeo<NS> cg = pg;
+  if (nmine) cg = unit_geo<EPI, NS>(a, gw, cols);
   float acc[NS];
 #pragma unroll
   for (int s = 0; s < NS; s++) acc[s] = 0.f;
-  for (int c = 0; c < nch; c++) {
-    const int g = c * 64 + lane;
-    if (g < G) {
-      uint4 w[NS]; uint16_t sc[NS];
+  while (ci < nmine) {
 #pragma unroll
-      for (int s = 0; s < NS; s++) { w[s] = ld16(rowq[s] + 16 * g); sc[s] = rows_s[s][g]; }
-      const uint4 h0 = *(const uint4 *)(a.xh + 32 * g), h1 = *(const uint4 *)(a.xh + 32 * g + 16);
-      const uint4 l0 = *(const uint4 *)(a.xl + 32 * g), l1 = *(const uint4 *)(a.xl + 32 * g + 16);
-      const int hx[8] = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-      const uint32_t lx[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-      const int corr = 8 * a.gsum[g];
-      const float bsg = a.bs[g >> 2];
+    for (int k = 0; k < D; k++) {
+      if (ci < nmine) {
+        if (cg.kind == MK_Q8) {
+          const int col = cc * 1024 + lane * 16;
+          const bool act = col < cols;
+          const uint4 h = act ? *(const uint4 *)(av.xh + col) : make_uint4(0, 0, 0, 0);
+          const uint4 l = act ? *(const uint4 *)(av.xl + col) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int s = 0; s < NS; s++) {
-        const uint32_t wd[4] = {w[s].x, w[s].y, w[s].z, w[s].w};
-        int A = 0; uint32_t B = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const uint32_t lo = wd[k] & 0x0f0f0f0fu, hi = (wd[k] >> 4) & 0x0f0f0f0fu;
-          A = __builtin_amdgcn_sdot4((int)lo, hx[k], A, false);
-          A = __builtin_amdgcn_sdot4((int)hi, hx[4 + k], A, false);
-          B = __builtin_amdgcn_udot4(lo, lx[k], B, false);
-          B = __builtin_amdgcn_udot4(hi, lx[4 + k], B, false);
-        }
-        const int isum = A * 256 + (int)B - corr;
-        if (dbg[s]) dbg[s][g] = isum;
-        acc[s] = __builtin_fmaf(half_bits_to_float(sc[s]) * bsg, (float)isum, acc[s]);
-      }
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < NS; s++) out[s] = wave_sum(acc[s]);
-}
-
-__device__ __forceinline__ float lane_bcast(float v, int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane)); }
-
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
-
-// ------------------------------------------------------------------ the matvec kernel
-template <int PRO, int EPI>
-__global__ __launch_bounds__(kThreads) void k_matvec(MvArgs a) {
-  extern __shared__ __align__(16) char smem[];
-  const int cols = a.m[0].cols;
-  const ActView av = act_view(smem, cols);
-  build_act<PRO>(a.x, a.norm_w, a.eps, cols, av);
-  if (blockIdx.x == 0 && (a.dbg_xq || a.dbg_bs)) {
-    for (int c = threadIdx.x; c < cols; c += kThreads)
-      if (a.dbg_xq) a.dbg_xq[c] = (int16_t)(((int)av.xh[c] << 8) | av.xl[c]);
-    for (int b = threadIdx.x; b < cols / kQB; b += kThreads)
-      if (a.dbg_bs) a.dbg_bs[b] = av.bs[b];
-  }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nb = cols / kQB;
-  int *sums = av.sums + wave * kMvSlots * av.nbp;
-  const int total = a.seg_tile0[a.nseg];
-  float best_v = -INFINITY; int best_i = 0x7fffffff;
-  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    // segment of this tile, chosen with selects (no dynamic indexing of the kernel-argument struct)
-    const int seg = (a.nseg > 1 && tile >= a.seg_tile0[1]) ? ((a.nseg > 2 && tile >= a.seg_tile0[2]) ? 2 : 1) : 0;
-    const DMat msel = seg == 0 ? a.m[0] : (seg == 1 ? a.m[1] : a.m[2]);
-    const int tile0 = seg == 0 ? a.seg_tile0[0] : (seg == 1 ? a.seg_tile0[1] : a.seg_tile0[2]);
-    DMat mats[kMvSlots]; int rows_[kMvSlots];
-    if (EPI == EPI_SWIGLU) {
-      const int r = (tile - a.seg_tile0[0]) * kMvWaves + wave;
-      mats[0] = a.m[0]; mats[1] = a.m[1]; rows_[0] = rows_[1] = r;
-    } else {
-      const int r0 = (tile - tile0) * (kMvWaves * kMvSlots) + wave * kMvSlots;
-#pragma unroll
-      for (int s = 0; s < kMvSlots; s++) { mats[s] = msel; rows_[s] = r0 + s; }
-    }
-    int rc[kMvSlots];   // clamped rows: out-of-range slots compute row rows-1 and store nothing
-#pragma unroll
-    for (int s = 0; s < kMvSlots; s++) rc[s] = rows_[s] < mats[s].rows ? rows_[s] : mats[s].rows - 1;
-    float val[kMvSlots];
-    const int kind = mats[0].kind;
-    if (kind == MK_Q8) {
-      const int8_t *rp[kMvSlots];
-#pragma unroll
-      for (int s = 0; s < kMvSlots; s++) rp[s] = (const int8_t *)mats[s].q + (size_t)rc[s] * cols;
-      dot_q8<kMvSlots>(rp, cols, av, lane, sums);
-      __syncthreads();
-      float acc = 0.f;
-      if (lane < kMvSlots) {
-        const int *ss = sums + lane * av.nbp;
-        for (int b = 0; b < nb; b++) acc = __builtin_fmaf(av.bs[b], (float)ss[b], acc);
-        int rl = rc[0]; const float *scl = (const float *)mats[0].s;
-#pragma unroll
-        for (int s = 1; s < kMvSlots; s++) if (lane == s) { rl = rc[s]; scl = (const float *)mats[s].s; }
-        acc = acc * scl[rl];
-      }
-#pragma unroll
-      for (int s = 0; s < kMvSlots; s++) val[s] = lane_bcast(acc, s);
-      if (a.dbg_sums && seg == 0) {
-        for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s].rows)
-            for (int b = lane; b < nb; b += kWave) a.dbg_sums[(size_t)rows_[s] * nb + b] = sums[s * av.nbp + b];
-      }
-      __syncthreads();
-    } else {
-      const uint8_t *rq[kMvSlots]; const uint16_t *rs[kMvSlots]; int32_t *dbg[kMvSlots];
-      const int G = cols / 32;
-#pragma unroll
-      for (int s = 0; s < kMvSlots; s++) {
-        rq[s] = (const uint8_t *)mats[s].q + (size_t)rc[s] * (cols / 2);
-        rs[s] = (const uint16_t *)mats[s].s + (size_t)rc[s] * G;
-        dbg[s] = (a.dbg_sums && seg == 0 && rows_[s] < mats[s].rows && EPI != EPI_SWIGLU) ? a.dbg_sums + (size_t)rows_[s] * G : nullptr;
-      }
-      dot_q4<kMvSlots>(rq, rs, cols, av, lane, val, dbg);
-    }
-    float *const out_seg = seg == 0 ? a.out[0] : (seg == 1 ? a.out[1] : a.out[2]);
-    const float *const bias_seg = seg == 0 ? a.bias[0] : (seg == 1 ? a.bias[1] : a.bias[2]);
-    if (lane == 0) {
-      if (EPI == EPI_STORE) {
-#pragma unroll
-        for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s].rows) {
-            float y = val[s];
-            if (bias_seg) y = y + bias_seg[rows_[s]];
-            out_seg[rows_[s]] = y;
+          for (int s = 0; s < NS; s++) {
+            const uint4 ww = wr[k][s];
+            int A = __builtin_amdgcn_sdot4((int)ww.x, (int)h.x, 0, false);
+            A = __builtin_amdgcn_sdot4((int)ww.y, (int)h.y, A, false);
+            A = __builtin_amdgcn_sdot4((int)ww.z, (int)h.z, A, false);
+            A = __builtin_amdgcn_sdot4((int)ww.w, (int)h.w, A, false);
+            uint32_t B = __builtin_amdgcn_udot4(ww.x ^ 0x80808080u, l.x, 0u, false);
+            B = __builtin_amdgcn_udot4(ww.y ^ 0x80808080u, l.y, B, false);
+            B = __builtin_amdgcn_udot4(ww.z ^ 0x80808080u, l.z, B, false);
+            B = __builtin_amdgcn_udot4(ww.w ^ 0x80808080u, l.w, B, false);
+            const int p = sum8_i(A * 256 + (int)B);
+            if (act && (lane & 7) == 0) {
+              const int b = cc * 8 + (lane >> 3);
+              sums[s * av.nbp + b] = p - 128 * av.lsum[b];
+            }
           }
-      } else if (EPI == EPI_RESID) {
+        } else {
+          const int g = cc * 64 + lane;
+          if (g < G) {
+            const uint4 h0 = *(const uint4 *)(av.xh + 32 * g), h1 = *(const uint4 *)(av.xh + 32 * g + 16);
+            const uint4 l0 = *(const uint4 *)(av.xl + 32 * g), l1 = *(const uint4 *)(av.xl + 32 * g + 16);
+            const int hx[8] = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+            const uint32_t lx[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            const int corr = 8 * av.gsum[g];
+            const float bsg = av.bs[g >> 2];
 #pragma unroll
-        for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s].rows) a.out[0][rows_[s]] = a.out[0][rows_[s]] + val[s];
-      } else if (EPI == EPI_SWIGLU) {
-        if (rows_[0] < mats[0].rows) {
-          const float g = val[0], u = val[1];
-          a.out[0][rows_[0]] = g / (1.f + exp_poly(0.f - g)) * u;   // silu_mul, kernels_x86.cpp:427-431
-        }
-      } else {
+            for (int s = 0; s < NS; s++) {
+              const uint32_t wd[4] = {wr[k][s].x, wr[k][s].y, wr[k][s].z, wr[k][s].w};
+              int A = 0; uint32_t B = 0;
 #pragma unroll
-        for (int s = 0; s < kMvSlots; s++)
-          if (rows_[s] < mats[s].rows) {
-            a.out[0][rows_[s]] = val[s];
-            if (better(val[s], rows_[s], best_v, best_i)) { best_v = val[s]; best_i = rows_[s]; }
+              for (int j = 0; j < 4; j++) {
+                const uint32_t lo = wd[j] & 0x0f0f0f0fu, hi = (wd[j] >> 4) & 0x0f0f0f0fu;
+                A = __builtin_amdgcn_sdot4((int)lo, hx[j], A, false);
+                A = __builtin_amdgcn_sdot4((int)hi, hx[4 + j], A, false);
+                B = __builtin_amdgcn_udot4(lo, lx[j], B, false);
+                B = __builtin_amdgcn_udot4(hi, lx[4 + j], B, false);
+              }
+              const int isum = A * 256 + (int)B - corr;
+              if (a.dbg_sums && cg.seg == 0 && EPI != EPI_SWIGLU && cg.row[s] < cg.rows) a.dbg_sums[(size_t)cg.row[s] * G + g] = isum;
+              acc[s] = __builtin_fmaf(half_bits_to_float(sr[k][s]) * bsg, (float)isum, acc[s]);
+            }
           }
+        }
+        issue(wr[k], sr[k]);
+        if (++cc == cg.nch) {   // the unit is complete
+          float val[NS];
+          if (cg.kind == MK_Q8) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float ch = 0.f;
+            if (lane < NS) {
+              const int *ss = sums + lane * av.nbp;
+              for (int b = 0; b < nb; b++) ch = __builtin_fmaf(av.bs[b], (float)ss[b], ch);
+              const float *scl = cg.sc[0];
+#pragma unroll
+              for (int s = 1; s < NS; s++) if (lane == s) scl = cg.sc[s];
+              ch = ch * *scl;
+            }
+#pragma unroll
+            for (int s = 0; s < NS; s++) val[s] = lane_bcast(ch, s);
+            if (a.dbg_sums && cg.seg == 0) {
+#pragma unroll
+              for (int s = 0; s < NS; s++)
+                if (cg.row[s] < cg.rows)
+                  for (int b = lane; b < nb; b += kWave) a.dbg_sums[(size_t)cg.row[s] * nb + b] = sums[s * av.nbp + b];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          } else {
+#pragma unroll
+            for (int s = 0; s < NS; s++) { val[s] = wave_sum(acc[s]); acc[s] = 0.f; }
+          }
+          if (lane == 0) {
+            float *const out_seg = cg.seg == 0 ? a.out[0] : (cg.seg == 1 ? a.out[1] : a.out[2]);
+            const float *const bias_seg = cg.seg == 0 ? a.bias[0] : (cg.seg == 1 ? a.bias[1] : a.bias[2]);
+            if (EPI == EPI_STORE) {
+#pragma unroll
+              for (int s = 0; s < NS; s++)
+                if (cg.row[s] < cg.rows) { float y = val[s]; if (bias_seg) y = y + bias_seg[cg.row[s]]; out_seg[cg.row[s]] = y; }
+            } else if (EPI == EPI_RESID) {
+#pragma unroll
+              for (int s = 0; s < NS; s++)
+                if (cg.row[s] < cg.rows) a.out[0][cg.row[s]] = a.out[0][cg.row[s]] + val[s];
+            } else if (EPI == EPI_SWIGLU) {
+              if (cg.row[0] < cg.rows) {
+                const float gt = val[0], u = val[1];
+                a.out[0][cg.row[0]] = gt / (1.f + exp_poly(0.f - gt)) * u;   // silu_mul, kernels_x86.cpp:427-431
+              }
+            } else {
+#pragma unroll
+              for (int s = 0; s < NS; s++)
+                if (cg.row[s] < cg.rows) {
+                  a.out[0][cg.row[s]] = val[s];
+                  if (better(val[s], cg.row[s], best_v, best_i)) { best_v = val[s]; best_i = cg.row[s]; }
+                }
+            }
+          }
+          cc = 0;
+          if (++ci < nmine) cg = unit_geo<EPI, NS>(a, gw + ci * W, cols);
+        }
       }
     }
   }
   if (EPI == EPI_ARGMAX) {
     __syncthreads();
-    float *rv = av.red; int *ri = (int *)(av.red + 8);
+    float *rv = av.red; int *ri = (int *)(av.red + 16);
     if (lane == 0) { rv[wave] = best_v; ri[wave] = best_i; }
     __syncthreads();
     if (threadIdx.x == 0) {
       float bv = rv[0]; int bi = ri[0];
-      for (int w = 1; w < kMvWaves; w++) if (better(rv[w], ri[w], bv, bi)) { bv = rv[w]; bi = ri[w]; }
+      for (int w = 1; w < WAVES; w++) if (better(rv[w], ri[w], bv, bi)) { bv = rv[w]; bi = ri[w]; }
       a.amax[blockIdx.x] = make_float2(bv, __builtin_bit_cast(float, bi));
     }
   }
 }
 
-int mv_tile_rows(int epi) { return epi == EPI_SWIGLU ? kMvWaves : kMvWaves * kMvSlots; }
+// rows per unit: SwiGLU units are one gate/up row pair; large matrices stream 2 rows per unit (the activation LDS reads
+// serve both), small ones 1 row so every wave gets an equal share
+static int mv_ns(const MvArgs &a, int epi, int waves) {
+  if (epi == EPI_SWIGLU) return 2;
+  int rows = 0;
+  for (int s = 0; s < a.nseg; s++) rows += a.m[s].rows;
+  return rows >= 4 * waves ? 2 : 1;
+}
+int mv_tile_rows(int epi) { return epi == EPI_SWIGLU ? 1 : 2; }
 void mv_plan(MvArgs &a, int epi) {
-  const int tr = mv_tile_rows(epi); int t = 0;
+  // unit prefix per segment for 2-row units; launch_matvec re-plans when it picks 1-row units
+  const int ns = epi == EPI_SWIGLU ? 1 : 2; int t = 0;
   const int nseg = epi == EPI_SWIGLU ? 1 : a.nseg;
-  for (int s = 0; s < nseg; s++) { a.seg_tile0[s] = t; t += (a.m[s].rows + tr - 1) / tr; }
+  for (int s = 0; s < nseg; s++) { a.seg_tile0[s] = t; t += (a.m[s].rows + ns - 1) / ns; }
   a.seg_tile0[nseg] = t;
   if (epi == EPI_SWIGLU) a.nseg = 1;
 }
 
-template <int PRO, int EPI>
-static hipError_t launch_mv_t(const MvArgs &a, int grid_cap, hipStream_t st) {
-  const int tiles = a.seg_tile0[a.nseg];
-  const int grid = tiles < grid_cap ? tiles : grid_cap;
-  const size_t lds = mv_lds_bytes(a.m[0].cols);
-  hipLaunchKernelGGL((k_matvec<PRO, EPI>), dim3(grid), dim3(kThreads), lds, st, a);
+// Launch shape: every CU gets one workgroup of `w` waves and every wave the same number of units, where possible:
+// units per CU upc = ceil(U / cus); w = the largest divisor of upc in [4, 16] (16 when there is none).
+template <int PRO, int EPI, int NS>
+static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
+  if (EPI != EPI_SWIGLU) {
+    int t = 0;
+    for (int s = 0; s < a.nseg; s++) { a.seg_tile0[s] = t; t += (a.m[s].rows + NS - 1) / NS; }
+    a.seg_tile0[a.nseg] = t;
+  }
+  const int units = a.seg_tile0[a.nseg], cus = g_mv_config.cus;
+  const int upc = (units + cus - 1) / cus;
+  int w = upc <= 16 ? upc : 16;
+  if (upc > 16) for (int c = 16; c >= 4; c--) if (upc % c == 0) { w = c; break; }
+  const int u = (upc + w - 1) / w;                                  // units per wave
+  int grid = (units + w * u - 1) / (w * u);
+  if (grid > grid_cap) return hipErrorInvalidValue;
+  const int cols = a.m[0].cols;
+  if (cols / kQB > 2 * w * 8) {   // the prologue covers 2 x (threads / 8) blocks: widen the workgroup
+    w = 16; grid = (units + 16 * u - 1) / (16 * u);
+  }
+  hipLaunchKernelGGL((k_matvec<PRO, EPI, NS>), dim3(grid), dim3(w * 64), mv_lds_bytes(cols, w), st, a);
   return hipGetLastError();
 }
+MvConfig g_mv_config;
+// grid_cap: the most workgroups one launch may use (EPI_ARGMAX writes one (max, index) partial per workgroup)
 hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st) {
-#define QPH_MV(P, E) if (pro == P && epi == E) return launch_mv_t<P, E>(a, grid_cap, st);
-  QPH_MV(PRO_QUANT, EPI_STORE) QPH_MV(PRO_QUANT, EPI_RESID) QPH_MV(PRO_NORM, EPI_STORE) QPH_MV(PRO_NORM, EPI_SWIGLU)
-  QPH_MV(PRO_NORM, EPI_ARGMAX) QPH_MV(PRO_QUANT, EPI_ARGMAX)
+  const int cols = a.m[0].cols;
+  if (cols % kQB || cols > 32768) return hipErrorInvalidValue;
+  const int ns = mv_ns(a, epi, g_mv_config.cus * 16);
+#define QPH_MV(P, E) \
+  if (pro == P && epi == E) return ns == 2 ? launch_mv_t<P, E, 2>(a, grid_cap, st) : launch_mv_t<P, E, 1>(a, grid_cap, st);
+  QPH_MV(PRO_QUANT, EPI_STORE) QPH_MV(PRO_QUANT, EPI_RESID) QPH_MV(PRO_NORM, EPI_STORE) QPH_MV(PRO_NORM, EPI_ARGMAX)
+  QPH_MV(PRO_QUANT, EPI_ARGMAX)
 #undef QPH_MV
+  if (pro == PRO_NORM && epi == EPI_SWIGLU) return launch_mv_t<PRO_NORM, EPI_SWIGLU, 2>(a, grid_cap, st);
   return hipErrorInvalidValue;
 }
 
@@ -377,13 +455,18 @@ hipError_t launch_embed(const DMat &embed, const Ctl *ctl, float *x, hipStream_t
   return hipGetLastError();
 }
 
-__global__ __launch_bounds__(kThreads) void k_rmsnorm(const float *x, const float *w, int n, float eps, float *out) {
-  __shared__ float red[16];
-  const float inv = block_rms_inv(x, n, eps, red);
-  for (int i = threadIdx.x; i < n; i += kThreads) out[i] = x[i] * inv * w[i];
+// out = RMSNorm(x) * w with the PRO_NORM prologue's arithmetic (same inverse norm, same products)
+__global__ __launch_bounds__(1024) void k_rmsnorm(const float *x, const float *w, int n, float eps, float *out) {
+  extern __shared__ __align__(16) char smem[];
+  const ActView av = act_view(smem, n);
+  ActRegs ar;
+  act_load<PRO_NORM>(x, w, n, ar);
+  act_build<PRO_NORM>(ar, eps, n, av);
+  const float inv = av.red[0];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
 }
 hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, float *out, hipStream_t st) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, st, x, w, n, eps, out);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), mv_lds_bytes(n, 16), st, x, w, n, eps, out);
   return hipGetLastError();
 }
 
@@ -452,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void k_attention(AttnArgs a) {
     }
     __syncthreads();
     // scores: wave w takes heads w, w + 4; lane = position
-    for (int j = wave; j < rep; j += kMvWaves) {
+    for (int j = wave; j < rep; j += kThreads / kWave) {
       float s = -INFINITY;
       if (lane < n) {
         float acc = 0.f;

@@ -34,13 +34,19 @@ struct MvArgs {
   float *dbg_bs;          // optional: the activation block scales
 };
 
-// rows per workgroup tile for the matvec kernel (4 waves x 2 row slots; EPI_SWIGLU pairs gate/up rows: 4 rows)
-constexpr int kMvWaves = 4;
+// The matvec kernel runs one workgroup of up to 16 waves per CU; every wave streams its own units of 1 or 2 rows
+// (2 slots: EPI_SWIGLU pairs the gate and up rows).  `cus` is the device's CU count.
+struct MvConfig {
+  int cus = 256;
+};
+extern MvConfig g_mv_config;
+constexpr int kMvMaxWaves = 16;
 constexpr int kMvSlots = 2;
 int mv_tile_rows(int epi);
-size_t mv_lds_bytes(int cols);
+size_t mv_lds_bytes(int cols, int waves);
 // fills seg_tile0 from the segment row counts
 void mv_plan(MvArgs &a, int epi);
+// grid_cap: the most workgroups (EPI_ARGMAX writes one (max, index) partial per workgroup launched)
 hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st);
 
 // x[0..d) = row ctl->tok of the embedding (row_f32 semantics, /root/reference/src/kernels.cpp:146-162)

@@ -2,6 +2,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <stdexcept>
@@ -72,6 +73,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   int dev = 0;
   QPH_CK(hipGetDevice(&dev));
   QPH_CK(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
+  g_mv_config.cus = cus_;
   QPH_CK(hipStreamCreateWithFlags(&st_, hipStreamNonBlocking));
   embed_ = upload(need("embed")); shape(embed_, V, d, "embed");
   if (cfg.tied) head_ = embed_;
@@ -104,8 +106,12 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   k_ = (float *)dalloc(4ull * kvd_); v_ = (float *)dalloc(4ull * kvd_); att_ = (float *)dalloc(4ull * qd_);
   h_ = (float *)dalloc(4ull * ff); logits_ = (float *)dalloc(4ull * V);
   part_ = (float *)dalloc(4ull * nh * max_chunks_ * (hd + 2));
-  head_grid_ = std::min((V + mv_tile_rows(EPI_ARGMAX) - 1) / mv_tile_rows(EPI_ARGMAX), 4 * cus_);
+  head_grid_ = cus_ * 4;
   amax_ = (float2 *)dalloc(sizeof(float2) * head_grid_);
+  {  // partials of workgroups a smaller launch does not use must never win the pick
+    std::vector<float2> init((size_t)head_grid_, make_float2(-INFINITY, __builtin_bit_cast(float, 0x7fffffff)));
+    QPH_CK(hipMemcpy(amax_, init.data(), init.size() * sizeof(float2), hipMemcpyHostToDevice));
+  }
   ctl_ = (Ctl *)dalloc(sizeof(Ctl));
   out_tok_ = (int *)dalloc(4ull * (ctx_ + 1));
   // RoPE tables in the reference's precision: inv_i = 1 / theta^(2i/hd) and angle pos * inv_i in double, cos / sin
@@ -139,7 +145,7 @@ HipLlama::~HipLlama() {
 
 void HipLlama::enqueue_layer(int l) {
   const Layer &ly = layers_[l];
-  const int cap = 4 * cus_;
+  const int cap = 1 << 20;
   const float eps = cfg_.rms_eps;
   {  // RMSNorm + q/k/v (+ bias)
     MvArgs a{}; a.m[0] = ly.wq; a.m[1] = ly.wk; a.m[2] = ly.wv; a.nseg = 3; a.x = x_; a.norm_w = ly.an; a.eps = eps;
@@ -197,9 +203,22 @@ hipGraphExec_t HipLlama::capture(int parts) {
 }
 
 void HipLlama::build_graphs() {
+  const char *ng = getenv("QPH_NO_GRAPH");
+  if (ng && atoi(ng) > 0) { use_graphs_ = false; return; }
   g_state_ = capture(0);
   g_logits_ = capture(1);
   g_greedy_ = capture(2);
+}
+
+// one decode step: parts 0 = layers, 1 = + output head (logits), 2 = + greedy pick (ctl advances on the device)
+void HipLlama::run_step(int parts) {
+  if (use_graphs_) {
+    QPH_CK(hipGraphLaunch(parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_, st_));
+    return;
+  }
+  enqueue_layers();
+  if (parts >= 1) enqueue_head();
+  if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
 }
 
 void HipLlama::write_ctl(int tok, int pos) {
@@ -218,10 +237,10 @@ void HipLlama::step(int tok, int want, float *out) {
   if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
   write_ctl(tok, pos_);
   if (want == 1) {
-    QPH_CK(hipGraphLaunch(g_logits_, st_));
+    run_step(1);
     QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
   } else {
-    QPH_CK(hipGraphLaunch(g_state_, st_));
+    run_step(0);
     if (want == 2) {
       QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
       QPH_CK(hipMemcpyAsync(hout_, xn_, 4ull * cfg_.hidden, hipMemcpyDeviceToHost, st_));
@@ -247,7 +266,7 @@ int HipLlama::greedy_run(int tok, int n, int *out) {
   if (n <= 0) return 0;
   if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
   write_ctl(tok, pos_);
-  for (int i = 0; i < n; i++) QPH_CK(hipGraphLaunch(g_greedy_, st_));
+  for (int i = 0; i < n; i++) run_step(2);
   QPH_CK(hipMemcpyAsync(htok_, out_tok_, 4ull * n, hipMemcpyDeviceToHost, st_));
   QPH_CK(hipStreamSynchronize(st_));
   memcpy(out, htok_, 4ull * n);
@@ -293,7 +312,7 @@ float HipLlama::time_greedy(int tok, int n) {
   QPH_CK(hipEventCreate(&e0)); QPH_CK(hipEventCreate(&e1));
   write_ctl(tok, pos_);
   QPH_CK(hipEventRecord(e0, st_));
-  for (int i = 0; i < n; i++) QPH_CK(hipGraphLaunch(g_greedy_, st_));
+  for (int i = 0; i < n; i++) run_step(2);
   QPH_CK(hipEventRecord(e1, st_));
   QPH_CK(hipEventSynchronize(e1));
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
@@ -309,7 +328,7 @@ static double mat_bytes(const DMat &m) {
 float HipLlama::time_kernel(int which, int iters, double *bytes) {
   if (iters <= 0) iters = 1;
   const Layer &ly = layers_[0];
-  const int cap = 4 * cus_, d = cfg_.hidden;
+  const int cap = 1 << 20, d = cfg_.hidden;
   const float eps = cfg_.rms_eps;
   write_ctl(0, std::min(pos_, ctx_ - 1));
   auto launch = [&]() {

@@ -64,6 +64,8 @@ class HipLlama {
   float *hout_ = nullptr;
   int *htok_ = nullptr;
   hipGraphExec_t g_state_ = nullptr, g_logits_ = nullptr, g_greedy_ = nullptr;
+  bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
+  void run_step(int parts);
 
   void *dalloc(size_t bytes);
   DMat upload(const qph_tensor &t);
