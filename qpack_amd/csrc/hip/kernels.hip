@@ -49,9 +49,12 @@ __device__ inline ActView act_view(char *smem, int cols) {
   v.sums = (int *)(v.red + 32);
   return v;
 }
-size_t mv_lds_bytes(int cols, int waves) {
+// LDS of the matvec kernel: activation planes, block scales / low-byte sums, group sums, reduction scratch, and per wave
+// `per_wave` ints of block sums (q8) or unit values (q4) - at least nbp in total (the RMSNorm block sums use it first)
+size_t mv_lds_bytes(int cols, int waves, int per_wave) {
   const int nb = cols / kQB, G = cols / 32, nbp = round_up(nb, 4);
-  return (size_t)2 * cols + 4 * (size_t)nbp * 2 + 4 * (size_t)round_up(G, 4) + 32 * 4 + 4 * (size_t)waves * kMvSlots * nbp;
+  const size_t sums = std::max<size_t>((size_t)waves * per_wave, (size_t)nbp);
+  return (size_t)2 * cols + 4 * (size_t)nbp * 2 + 4 * (size_t)round_up(G, 4) + 32 * 4 + 4 * sums;
 }
 
 // The activation prologue in two halves, so its global reads are issued before the weight prefetch (a wave's loads
@@ -196,69 +199,95 @@ __device__ __forceinline__ UnitGeo<NS> unit_geo(const MvArgs &a, int u, int cols
   return g;
 }
 
-// the matvec kernel: prefetch ring of D steps per wave (issued before the activation prologue, so weight streaming
-// starts at launch), no workgroup barrier after the prologue.
-template <int PRO, int EPI, int NS>
+// row pointers of unit u (NS rows of one segment; EPI_SWIGLU: row u of the gate and of the up matrix)
+template <int EPI, int NS>
+__device__ __forceinline__ void unit_rows(const MvArgs &a, int u, int cols, const uint8_t *(&p)[NS], const uint16_t *(&sp)[NS]) {
+  const UnitGeo<NS> g = unit_geo<EPI, NS>(a, u, cols);
+#pragma unroll
+  for (int s = 0; s < NS; s++) { p[s] = g.p[s]; sp[s] = g.sp[s]; }
+}
+
+// The matvec kernel.  Per wave: a ring of D prefetched steps (one 1 KiB chunk of each of the unit's NS rows per step,
+// issued right after the activation reads so streaming starts at launch), and a main loop whose only vector memory
+// operations are those unconditional prefetch loads: a wave's loads return in order, and any other load or store in
+// the loop would make the compiler wait for the whole ring.  Block sums (q8) and unit results (q4) go to LDS; the
+// fp32 chains, scales and stores run after the loop, one lane per (unit, row).
+template <int PRO, int EPI, int NS, int KIND, bool DBG>
 __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
-  const int WAVES = (int)blockDim.x >> 6;
-  constexpr int D = NS == 1 ? 8 : 4;
+  constexpr int D = 8 / NS;
   extern __shared__ __align__(16) char smem[];
+  const int WAVES = (int)blockDim.x >> 6;
   const int cols = a.m[0].cols, G = cols / 32, nb = cols / kQB;
   const ActView av = act_view(smem, cols);
-  // wave-uniform bookkeeping lives in scalar registers (the compiler cannot prove threadIdx.x >> 6 uniform)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int W = gridDim.x * WAVES, gw = wave * gridDim.x + blockIdx.x;
   const int U = a.seg_tile0[a.nseg];
   const int nmine = gw < U ? (U - gw + W - 1) / W : 0;
-  int *sums = av.sums + wave * kMvSlots * av.nbp;
+  const int rowbytes = KIND == MK_Q8 ? cols : cols / 2;
+  const int nch = (rowbytes + 1023) >> 10;
+  const int total = nmine * nch;
+  // per-wave LDS: q8 block sums [upw][NS][nbp] ints, q4 unit values [upw][NS] floats
+  int *wsum = av.sums + wave * (a.upw * NS * (KIND == MK_Q8 ? av.nbp : 1));
+  float *wval = (float *)wsum;
 
   ActRegs ar;
-  act_load<PRO>(a.x, a.norm_w, cols, ar);
+  const int dm = a.dbg_mode;
+  if (!(dm & 2)) act_load<PRO>(a.x, a.norm_w, cols, ar);
+
   uint4 wr[D][NS];
   uint16_t sr[D][NS];
   int pi = 0, pc = 0;
-  UnitGeo<NS> pg = unit_geo<EPI, NS>(a, nmine ? gw : 0, cols);
+  const uint8_t *pp[NS]; const uint16_t *psp[NS];
+  unit_rows<EPI, NS>(a, nmine ? gw : 0, cols, pp, psp);
   auto issue = [&](uint4 (&w)[NS], uint16_t (&sv)[NS]) {
-    if (pi < nmine) {
-      const int off = pc * 1024 + lane * 16, grp = pc * 64 + lane;
+    // past the wave's last unit every lane re-reads the same 16 bytes (one cache line, no HBM traffic)
+    const bool live = pi < nmine;
+    const int off = pc * 1024 + lane * 16, grp = pc * 64 + lane;
+    const int offc = !live ? 0 : (off < rowbytes ? off : rowbytes - 16);
+    const int grpc = !live ? 0 : (grp < G ? grp : G - 1);
 #pragma unroll
-      for (int s = 0; s < NS; s++) {
-        w[s] = off < pg.rowbytes ? ld16(pg.p[s] + off) : make_uint4(0, 0, 0, 0);
-        sv[s] = (pg.kind == MK_Q4 && grp < G) ? pg.sp[s][grp] : (uint16_t)0;
-      }
-      if (++pc == pg.nch) { pc = 0; if (++pi < nmine) pg = unit_geo<EPI, NS>(a, gw + pi * W, cols); }
+    for (int s = 0; s < NS; s++) {
+      w[s] = ld16(pp[s] + offc);
+      if (KIND == MK_Q4) sv[s] = psp[s][grpc];
     }
+    if (live && ++pc == nch) { pc = 0; if (++pi < nmine) unit_rows<EPI, NS>(a, gw + pi * W, cols, pp, psp); }
   };
 #pragma unroll
   for (int k = 0; k < D; k++) issue(wr[k], sr[k]);
 
-  act_build<PRO>(ar, a.eps, cols, av);
-  if (blockIdx.x == 0 && (a.dbg_xq || a.dbg_bs)) {
+  if (!(dm & 2)) act_build<PRO>(ar, a.eps, cols, av);
+  else __syncthreads();
+  if (DBG && blockIdx.x == 0) {
     for (int c = threadIdx.x; c < cols; c += blockDim.x)
       if (a.dbg_xq) a.dbg_xq[c] = (int16_t)(((int)av.xh[c] << 8) | av.xl[c]);
     for (int b = threadIdx.x; b < nb; b += blockDim.x)
       if (a.dbg_bs) a.dbg_bs[b] = av.bs[b];
   }
 
-  float best_v = -INFINITY; int best_i = 0x7fffffff;
   int ci = 0, cc = 0;
-  UnitGeo<NS> cg = pg;
-  if (nmine) cg = unit_geo<EPI, NS>(a, gw, cols);
   float acc[NS];
 #pragma unroll
   for (int s = 0; s < NS; s++) acc[s] = 0.f;
-  while (ci < nmine) {
+  for (int t0 = 0; t0 < total; t0 += D) {
 #pragma unroll
     for (int k = 0; k < D; k++) {
-      if (ci < nmine) {
-        if (cg.kind == MK_Q8) {
+      uint4 cur[NS]; uint16_t curs[NS];
+#pragma unroll
+      for (int s = 0; s < NS; s++) { cur[s] = wr[k][s]; curs[s] = sr[k][s]; }
+      issue(wr[k], sr[k]);
+      if (t0 + k < total) {
+        if (dm & 1) {
+#pragma unroll
+          for (int s = 0; s < NS; s++) acc[s] += (float)(cur[s].x ^ cur[s].y ^ cur[s].z ^ cur[s].w);
+        } else if (KIND == MK_Q8) {
           const int col = cc * 1024 + lane * 16;
           const bool act = col < cols;
-          const uint4 h = act ? *(const uint4 *)(av.xh + col) : make_uint4(0, 0, 0, 0);
-          const uint4 l = act ? *(const uint4 *)(av.xl + col) : make_uint4(0, 0, 0, 0);
+          const int colc = act ? col : cols - 16;
+          const uint4 h = *(const uint4 *)(av.xh + colc);
+          const uint4 l = *(const uint4 *)(av.xl + colc);
 #pragma unroll
           for (int s = 0; s < NS; s++) {
-            const uint4 ww = wr[k][s];
+            const uint4 ww = cur[s];
             int A = __builtin_amdgcn_sdot4((int)ww.x, (int)h.x, 0, false);
             A = __builtin_amdgcn_sdot4((int)ww.y, (int)h.y, A, false);
             A = __builtin_amdgcn_sdot4((int)ww.z, (int)h.z, A, false);
@@ -270,99 +299,107 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
             const int p = sum8_i(A * 256 + (int)B);
             if (act && (lane & 7) == 0) {
               const int b = cc * 8 + (lane >> 3);
-              sums[s * av.nbp + b] = p - 128 * av.lsum[b];
+              wsum[(ci * NS + s) * av.nbp + b] = p - 128 * av.lsum[b];
             }
           }
         } else {
           const int g = cc * 64 + lane;
-          if (g < G) {
-            const uint4 h0 = *(const uint4 *)(av.xh + 32 * g), h1 = *(const uint4 *)(av.xh + 32 * g + 16);
-            const uint4 l0 = *(const uint4 *)(av.xl + 32 * g), l1 = *(const uint4 *)(av.xl + 32 * g + 16);
-            const int hx[8] = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-            const uint32_t lx[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-            const int corr = 8 * av.gsum[g];
-            const float bsg = av.bs[g >> 2];
+          const bool act = g < G;
+          const int gc = act ? g : G - 1;
+          const uint4 h0 = *(const uint4 *)(av.xh + 32 * gc), h1 = *(const uint4 *)(av.xh + 32 * gc + 16);
+          const uint4 l0 = *(const uint4 *)(av.xl + 32 * gc), l1 = *(const uint4 *)(av.xl + 32 * gc + 16);
+          const int hx[8] = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+          const uint32_t lx[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+          const int corr = 8 * av.gsum[gc];
+          const float bsg = av.bs[gc >> 2];
 #pragma unroll
-            for (int s = 0; s < NS; s++) {
-              const uint32_t wd[4] = {wr[k][s].x, wr[k][s].y, wr[k][s].z, wr[k][s].w};
-              int A = 0; uint32_t B = 0;
+          for (int s = 0; s < NS; s++) {
+            const uint32_t wd[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
+            int A = 0; uint32_t B = 0;
 #pragma unroll
-              for (int j = 0; j < 4; j++) {
-                const uint32_t lo = wd[j] & 0x0f0f0f0fu, hi = (wd[j] >> 4) & 0x0f0f0f0fu;
-                A = __builtin_amdgcn_sdot4((int)lo, hx[j], A, false);
-                A = __builtin_amdgcn_sdot4((int)hi, hx[4 + j], A, false);
-                B = __builtin_amdgcn_udot4(lo, lx[j], B, false);
-                B = __builtin_amdgcn_udot4(hi, lx[4 + j], B, false);
-              }
-              const int isum = A * 256 + (int)B - corr;
-              if (a.dbg_sums && cg.seg == 0 && EPI != EPI_SWIGLU && cg.row[s] < cg.rows) a.dbg_sums[(size_t)cg.row[s] * G + g] = isum;
-              acc[s] = __builtin_fmaf(half_bits_to_float(sr[k][s]) * bsg, (float)isum, acc[s]);
+            for (int j = 0; j < 4; j++) {
+              const uint32_t lo = wd[j] & 0x0f0f0f0fu, hi = (wd[j] >> 4) & 0x0f0f0f0fu;
+              A = __builtin_amdgcn_sdot4((int)lo, hx[j], A, false);
+              A = __builtin_amdgcn_sdot4((int)hi, hx[4 + j], A, false);
+              B = __builtin_amdgcn_udot4(lo, lx[j], B, false);
+              B = __builtin_amdgcn_udot4(hi, lx[4 + j], B, false);
             }
+            const int isum = A * 256 + (int)B - corr;
+            if (DBG && act && a.dbg_sums) {
+              const UnitGeo<NS> og = unit_geo<EPI, NS>(a, gw + ci * W, cols);
+              if (og.seg == 0 && og.row[s] < og.rows) a.dbg_sums[(size_t)og.row[s] * G + g] = isum;
+            }
+            if (act) acc[s] = __builtin_fmaf(half_bits_to_float(curs[s]) * bsg, (float)isum, acc[s]);
           }
         }
-        issue(wr[k], sr[k]);
-        if (++cc == cg.nch) {   // the unit is complete
-          float val[NS];
-          if (cg.kind == MK_Q8) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            float ch = 0.f;
-            if (lane < NS) {
-              const int *ss = sums + lane * av.nbp;
-              for (int b = 0; b < nb; b++) ch = __builtin_fmaf(av.bs[b], (float)ss[b], ch);
-              const float *scl = cg.sc[0];
+        if (++cc == nch) {   // unit complete: q4 values to LDS (LDS and cross-lane ops only inside the loop)
+          if (KIND == MK_Q4) {
 #pragma unroll
-              for (int s = 1; s < NS; s++) if (lane == s) scl = cg.sc[s];
-              ch = ch * *scl;
-            }
-#pragma unroll
-            for (int s = 0; s < NS; s++) val[s] = lane_bcast(ch, s);
-            if (a.dbg_sums && cg.seg == 0) {
-#pragma unroll
-              for (int s = 0; s < NS; s++)
-                if (cg.row[s] < cg.rows)
-                  for (int b = lane; b < nb; b += kWave) a.dbg_sums[(size_t)cg.row[s] * nb + b] = sums[s * av.nbp + b];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-          } else {
-#pragma unroll
-            for (int s = 0; s < NS; s++) { val[s] = wave_sum(acc[s]); acc[s] = 0.f; }
-          }
-          if (lane == 0) {
-            float *const out_seg = cg.seg == 0 ? a.out[0] : (cg.seg == 1 ? a.out[1] : a.out[2]);
-            const float *const bias_seg = cg.seg == 0 ? a.bias[0] : (cg.seg == 1 ? a.bias[1] : a.bias[2]);
-            if (EPI == EPI_STORE) {
-#pragma unroll
-              for (int s = 0; s < NS; s++)
-                if (cg.row[s] < cg.rows) { float y = val[s]; if (bias_seg) y = y + bias_seg[cg.row[s]]; out_seg[cg.row[s]] = y; }
-            } else if (EPI == EPI_RESID) {
-#pragma unroll
-              for (int s = 0; s < NS; s++)
-                if (cg.row[s] < cg.rows) a.out[0][cg.row[s]] = a.out[0][cg.row[s]] + val[s];
-            } else if (EPI == EPI_SWIGLU) {
-              if (cg.row[0] < cg.rows) {
-                const float gt = val[0], u = val[1];
-                a.out[0][cg.row[0]] = gt / (1.f + exp_poly(0.f - gt)) * u;   // silu_mul, kernels_x86.cpp:427-431
-              }
-            } else {
-#pragma unroll
-              for (int s = 0; s < NS; s++)
-                if (cg.row[s] < cg.rows) {
-                  a.out[0][cg.row[s]] = val[s];
-                  if (better(val[s], cg.row[s], best_v, best_i)) { best_v = val[s]; best_i = cg.row[s]; }
-                }
+            for (int s = 0; s < NS; s++) {
+              const float v = wave_sum(acc[s]);
+              if (lane == 0) wval[ci * NS + s] = v;
+              acc[s] = 0.f;
             }
           }
-          cc = 0;
-          if (++ci < nmine) cg = unit_geo<EPI, NS>(a, gw + ci * W, cols);
+          cc = 0; ci++;
         }
       }
     }
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // epilogue: lane j finishes (unit j / NS, row slot j % NS)
+  float best_v = -INFINITY; int best_i = 0x7fffffff;
+  for (int j0 = 0; j0 < nmine * NS; j0 += kWave) {
+    const int j = j0 + lane, u = j / NS, s = j % NS;
+    const bool live = j < nmine * NS;
+    const UnitGeo<NS> og = unit_geo<EPI, NS>(a, gw + (live ? u : 0) * W, cols);
+    int row = og.row[0]; const float *scl = og.sc[0];
+#pragma unroll
+    for (int t = 1; t < NS; t++) if (s == t) { row = og.row[t]; scl = og.sc[t]; }
+    float v = 0.f;
+    if (live) {
+      if (KIND == MK_Q8) {
+        const int *ss = wsum + (u * NS + s) * av.nbp;
+        float ch = 0.f;   // rows_q8's block order; LDS read 16 blocks at a time so the chain is not latency-bound
+        int b = 0;
+        for (; b + 16 <= nb; b += 16) {
+          int4 sv[4]; float4 bv[4];
+#pragma unroll
+          for (int q = 0; q < 4; q++) { sv[q] = *(const int4 *)(ss + b + 4 * q); bv[q] = *(const float4 *)(av.bs + b + 4 * q); }
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            ch = __builtin_fmaf(bv[q].x, (float)sv[q].x, ch); ch = __builtin_fmaf(bv[q].y, (float)sv[q].y, ch);
+            ch = __builtin_fmaf(bv[q].z, (float)sv[q].z, ch); ch = __builtin_fmaf(bv[q].w, (float)sv[q].w, ch);
+          }
+        }
+        for (; b < nb; b++) ch = __builtin_fmaf(av.bs[b], (float)ss[b], ch);
+        v = ch * *scl;
+        if (DBG && a.dbg_sums && og.seg == 0 && row < og.rows)
+          for (int b = 0; b < nb; b++) a.dbg_sums[(size_t)row * nb + b] = ss[b];
+      } else {
+        v = wval[u * NS + s];
+      }
+    }
+    const bool store = live && row < og.rows;
+    if (EPI == EPI_SWIGLU) {
+      const float up = __shfl_xor(v, 1, kWave);   // slot 1 (up) sits in the lane after slot 0 (gate)
+      if (store && s == 0) a.out[0][row] = v / (1.f + exp_poly(0.f - v)) * up;   // silu_mul, kernels_x86.cpp:427-431
+    } else if (store) {
+      float *const out_seg = og.seg == 0 ? a.out[0] : (og.seg == 1 ? a.out[1] : a.out[2]);
+      const float *const bias_seg = og.seg == 0 ? a.bias[0] : (og.seg == 1 ? a.bias[1] : a.bias[2]);
+      if (EPI == EPI_STORE) { float y = v; if (bias_seg) y = y + bias_seg[row]; out_seg[row] = y; }
+      else if (EPI == EPI_RESID) a.out[0][row] = a.out[0][row] + v;
+      else { a.out[0][row] = v; if (better(v, row, best_v, best_i)) { best_v = v; best_i = row; } }
+    }
+  }
   if (EPI == EPI_ARGMAX) {
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(best_v, o, kWave); const int oi = __shfl_xor(best_i, o, kWave);
+      if (better(ov, oi, best_v, best_i)) { best_v = ov; best_i = oi; }
+    }
     __syncthreads();
     float *rv = av.red; int *ri = (int *)(av.red + 16);
     if (lane == 0) { rv[wave] = best_v; ri[wave] = best_i; }
@@ -395,7 +432,7 @@ void mv_plan(MvArgs &a, int epi) {
 
 // Launch shape: every CU gets one workgroup of `w` waves and every wave the same number of units, where possible:
 // units per CU upc = ceil(U / cus); w = the largest divisor of upc in [4, 16] (16 when there is none).
-template <int PRO, int EPI, int NS>
+template <int PRO, int EPI, int NS, int KIND>
 static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
   if (EPI != EPI_SWIGLU) {
     int t = 0;
@@ -406,29 +443,55 @@ static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
   const int upc = (units + cus - 1) / cus;
   int w = upc <= 16 ? upc : 16;
   if (upc > 16) for (int c = 16; c >= 4; c--) if (upc % c == 0) { w = c; break; }
-  const int u = (upc + w - 1) / w;                                  // units per wave
-  int grid = (units + w * u - 1) / (w * u);
-  if (grid > grid_cap) return hipErrorInvalidValue;
+  int u = (upc + w - 1) / w;                                        // units per wave
   const int cols = a.m[0].cols;
-  if (cols / kQB > 2 * w * 8) {   // the prologue covers 2 x (threads / 8) blocks: widen the workgroup
-    w = 16; grid = (units + 16 * u - 1) / (16 * u);
+  if (cols / kQB > 2 * w * 8) { w = 16; u = (upc + 15) / 16; }     // the prologue covers 2 x (threads / 8) blocks
+  const int grid = (units + w * u - 1) / (w * u);
+  if (grid > grid_cap) return hipErrorInvalidValue;
+  // a wave may own one unit more than u when the grid rounds: size the per-wave LDS for ceil(units / waves)
+  const int waves = grid * w;
+  a.upw = (units + waves - 1) / waves;
+  const int nbp = ((cols / kQB) + 3) / 4 * 4;
+  const size_t lds = mv_lds_bytes(cols, w, a.upw * NS * (KIND == MK_Q8 ? nbp : 1));
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const bool dbg = a.dbg_sums || a.dbg_xq || a.dbg_bs;
+  if (dbg) {
+    if (PRO != PRO_QUANT || EPI != EPI_STORE) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_matvec<PRO_QUANT, EPI_STORE, NS, KIND, true>), dim3(grid), dim3(w * 64), lds, st, a);
+  } else {
+    hipLaunchKernelGGL((k_matvec<PRO, EPI, NS, KIND, false>), dim3(grid), dim3(w * 64), lds, st, a);
   }
-  hipLaunchKernelGGL((k_matvec<PRO, EPI, NS>), dim3(grid), dim3(w * 64), mv_lds_bytes(cols, w), st, a);
   return hipGetLastError();
 }
-MvConfig g_mv_config;
-// grid_cap: the most workgroups one launch may use (EPI_ARGMAX writes one (max, index) partial per workgroup)
-hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st) {
-  const int cols = a.m[0].cols;
-  if (cols % kQB || cols > 32768) return hipErrorInvalidValue;
-  const int ns = mv_ns(a, epi, g_mv_config.cus * 16);
+template <int KIND>
+static hipError_t launch_mv_k(int pro, int epi, const MvArgs &a, int ns, int grid_cap, hipStream_t st) {
 #define QPH_MV(P, E) \
-  if (pro == P && epi == E) return ns == 2 ? launch_mv_t<P, E, 2>(a, grid_cap, st) : launch_mv_t<P, E, 1>(a, grid_cap, st);
+  if (pro == P && epi == E) return ns == 2 ? launch_mv_t<P, E, 2, KIND>(a, grid_cap, st) : launch_mv_t<P, E, 1, KIND>(a, grid_cap, st);
   QPH_MV(PRO_QUANT, EPI_STORE) QPH_MV(PRO_QUANT, EPI_RESID) QPH_MV(PRO_NORM, EPI_STORE) QPH_MV(PRO_NORM, EPI_ARGMAX)
   QPH_MV(PRO_QUANT, EPI_ARGMAX)
 #undef QPH_MV
-  if (pro == PRO_NORM && epi == EPI_SWIGLU) return launch_mv_t<PRO_NORM, EPI_SWIGLU, 2>(a, grid_cap, st);
+  if (pro == PRO_NORM && epi == EPI_SWIGLU) return launch_mv_t<PRO_NORM, EPI_SWIGLU, 2, KIND>(a, grid_cap, st);
   return hipErrorInvalidValue;
+}
+MvConfig g_mv_config;
+// grid_cap: the most workgroups one launch may use (EPI_ARGMAX writes one (max, index) partial per workgroup).
+// Segments of different kinds (q4m: q4 wq / wk with a q8 wv) go out as one launch per kind.
+hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st) {
+  const int cols = a.m[0].cols;
+  if (cols % kQB || cols > 32768) return hipErrorInvalidValue;
+  const int nseg = epi == EPI_SWIGLU ? 1 : a.nseg;
+  for (int k : {(int)MK_Q8, (int)MK_Q4}) {
+    MvArgs b = a; b.nseg = 0;
+    for (int s = 0; s < nseg; s++)
+      if (a.m[s].kind == k) { b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s]; b.nseg++; }
+    if (!b.nseg) continue;
+    if (epi == EPI_SWIGLU) { b.m[1] = a.m[1]; b.nseg = 1; b.seg_tile0[0] = 0; b.seg_tile0[1] = a.m[0].rows; }
+    if (b.nseg != nseg && (b.dbg_sums || epi == EPI_ARGMAX)) return hipErrorInvalidValue;
+    const int ns = mv_ns(b, epi, g_mv_config.cus * 16);
+    const hipError_t e = k == MK_Q8 ? launch_mv_k<MK_Q8>(pro, epi, b, ns, grid_cap, st) : launch_mv_k<MK_Q4>(pro, epi, b, ns, grid_cap, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // ------------------------------------------------------------------ embedding, norm
@@ -466,7 +529,7 @@ __global__ __launch_bounds__(1024) void k_rmsnorm(const float *x, const float *w
   for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
 }
 hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, float *out, hipStream_t st) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), mv_lds_bytes(n, 16), st, x, w, n, eps, out);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), mv_lds_bytes(n, 16, 0), st, x, w, n, eps, out);
   return hipGetLastError();
 }
 

@@ -32,6 +32,8 @@ struct MvArgs {
   int32_t *dbg_sums;      // optional: exact int32 accumulators [rows, cols/128] (q8) or [rows, cols/32] (q4), segment 0
   int16_t *dbg_xq;        // optional: the quantised activation (workgroup 0 writes it)
   float *dbg_bs;          // optional: the activation block scales
+  int dbg_mode;           // measurement only: bit 0 skips the dot products, bit 1 skips the activation prologue
+  int upw;                // set by the launcher: the most units one wave owns (sizes the per-wave LDS)
 };
 
 // The matvec kernel runs one workgroup of up to 16 waves per CU; every wave streams its own units of 1 or 2 rows
@@ -43,7 +45,7 @@ extern MvConfig g_mv_config;
 constexpr int kMvMaxWaves = 16;
 constexpr int kMvSlots = 2;
 int mv_tile_rows(int epi);
-size_t mv_lds_bytes(int cols, int waves);
+size_t mv_lds_bytes(int cols, int waves, int per_wave);
 // fills seg_tile0 from the segment row counts
 void mv_plan(MvArgs &a, int epi);
 // grid_cap: the most workgroups (EPI_ARGMAX writes one (max, index) partial per workgroup launched)

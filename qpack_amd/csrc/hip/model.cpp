@@ -331,8 +331,11 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   const int cap = 1 << 20, d = cfg_.hidden;
   const float eps = cfg_.rms_eps;
   write_ctl(0, std::min(pos_, ctx_ - 1));
+  const char *dme = getenv("QPH_MV_DBG");
+  const int dmode = dme ? atoi(dme) : 0;
   auto launch = [&]() {
     MvArgs a{};
+    a.dbg_mode = dmode;
     switch (which) {
       case 0:
         a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
