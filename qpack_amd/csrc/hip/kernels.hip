@@ -534,142 +534,243 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 }
 
 // ------------------------------------------------------------------ decode attention (split-K over the context)
-// grid (kv group g, chunk c of `chunk` positions).  The workgroup applies RoPE to its rep query heads (rotate-half with
-// the reference's contraction: a' = fma(a, cos, -(b sin)), b' = fma(b, cos, a sin), model_llama.cpp:176), and the
-// workgroup owning the current position writes the rotated k and v as fp16 into the cache.  Positions are staged in LDS
-// 64 at a time; online softmax per head; partials [m, l, o] per (head, chunk) are merged by k_attn_merge.
+// grid (kv group g, split s), 16 waves (8 for wide GQA groups).  The number of active splits follows the context, S_eff = ceil(T / 1024)
+// (at most grid.y): below 1024 positions one workgroup per kv group does everything and no cross-workgroup merge is
+// needed.  Split s takes positions [s T / S_eff, (s + 1) T / S_eff); each wave a contiguous sub-range, streamed straight
+// from HBM 16 positions at a time with the next block's K and V loads in flight (double-buffered registers).
+// The workgroup applies RoPE to its rep query heads (rotate-half with the reference's contraction
+// a' = fma(a, cos, -(b sin)), b' = fma(b, cos, a sin), model_llama.cpp:176); the workgroup owning the current position
+// writes the rotated k and the v row into the cache as fp16 (round to nearest even, to_f16).
+//   scores: LPP = HD / 8 lanes share a position, each holding 8 dims of K and of every query head; DPP sums the LPP
+//           partial dots; scale 1/sqrt(hd) as in attend() (model_llama.cpp:137-146).
+//   online softmax per wave and head (max and sum over rows of 16 lanes, one head per row); values: lane owns HD / 64 dims.
+// The 16 wave partials merge in LDS; with several splits the last one to finish (release / acquire on a per-group
+// counter, which that workgroup resets) merges the split partials in split order - the merge of model_llama.cpp:160-165:
+// M = max m, L = sum l e^(m - M), out = sum o e^(m - M) * (1 / L).
+constexpr int kAttnMaxSplits = 256;
+constexpr int kSplitPos = 1024;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// sum / max over aligned rows of 16 lanes (every lane of the row gets the result)
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<kDppQuadXor1>(v); v += dpp_f<kDppQuadXor2>(v); v += dpp_f<kDppHalfMirror>(v); v += dpp_f<0x140>(v);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v)); v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v)); v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+// one 16-position block of one wave: K pieces (lane = position-in-pass x 8-dim slice) and V dims (lane owns VD dims)
 template <int HD>
-__global__ __launch_bounds__(kThreads) void k_attention(AttnArgs a) {
-  constexpr int TP = 64, KS = HD + 2, HALF = HD / 2, JMAX = 8;
-  constexpr int TPI = kThreads / HD;   // head groups of the output accumulation
-  constexpr int JPT = (JMAX + TPI - 1) / TPI;
-  __shared__ float qs[JMAX][HD];
-  __shared__ uint16_t ks[TP][KS];
-  __shared__ uint16_t vs[TP][HD];
-  __shared__ float ps[JMAX][TP];
-  __shared__ float m_run[JMAX], l_run[JMAX], corr[JMAX];
-  __shared__ uint16_t knew[HD], vnew[HD];
-  const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, c = blockIdx.y, rep = a.nh / a.nkv, kvd = a.nkv * HD;
-  const int t0 = c * a.chunk;
-  if (t0 >= T) return;
-  const int t1 = t0 + a.chunk < T ? t0 + a.chunk : T;
+struct KvBlock {
+  static constexpr int LPP = HD / 8, PPI = kWave / LPP, KP = 16 / PPI, VD = HD / kWave;
+  u32x4 k[KP];
+  uint32_t v[16];
+};
+template <int HD>
+__device__ __forceinline__ void kv_load(const uint16_t *kc, const uint16_t *vc, int kvd, int g, int tb, int te, int lane, KvBlock<HD> &b) {
+  using B = KvBlock<HD>;
+  const int psub = lane / B::LPP, dsl = lane % B::LPP;
+#pragma unroll
+  for (int i = 0; i < B::KP; i++) {
+    const int t = tb + i * B::PPI + psub;
+    b.k[i] = *(const u32x4 *)(kc + (size_t)(t < te ? t : tb) * kvd + g * HD + dsl * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int t = tb + i < te ? tb + i : tb;
+    if (B::VD == 2) b.v[i] = *(const uint32_t *)(vc + (size_t)t * kvd + g * HD + 2 * lane);
+    else b.v[i] = vc[(size_t)t * kvd + g * HD + lane];
+  }
+}
+
+// waves per attention workgroup: 16, or 8 where 16 would not fit the registers (wide GQA groups)
+constexpr int attn_waves(int hd, int rep) { return (hd == 64 && rep >= 7) || (hd == 128 && rep >= 5) ? 8 : 16; }
+template <int HD, int REP>
+__global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs a) {
+  using B = KvBlock<HD>;
+  constexpr int NW = attn_waves(HD, REP), HALF = HD / 2, LPP = B::LPP, PPI = B::PPI, VD = B::VD;
+  __shared__ __align__(16) float qs[REP][HD];
+  __shared__ float sc[NW][REP][16];
+  __shared__ float wm[NW][REP], wl[NW][REP];
+  __shared__ float ored[NW][REP][HD];
+  __shared__ __align__(16) uint16_t knew[HD];
+  __shared__ __align__(16) uint16_t vnew[HD];
+  __shared__ int last;
+  const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
+  const int S = min((int)gridDim.y, (T + kSplitPos - 1) / kSplitPos);
+  if (s >= S) return;
+  const int kvd = a.nkv * HD;
+  const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int n = t1 - t0, wt0 = t0 + (int)((int64_t)wave * n / NW), wt1 = t0 + (int)((int64_t)(wave + 1) * n / NW);
+  // this wave's first block goes out before anything else
+  KvBlock<HD> cur, nxt;
+  if (wt0 < wt1) kv_load<HD>(a.kc, a.vc, kvd, g, wt0, wt1, lane, cur);
   const float *cs = a.cos_t + (size_t)pos * HALF, *sn = a.sin_t + (size_t)pos * HALF;
-  for (int e = threadIdx.x; e < rep * HALF; e += kThreads) {
-    const int j = e / HALF, i = e % HALF; const float *qh = a.q + (size_t)(g * rep + j) * HD;
+  for (int e = threadIdx.x; e < REP * HALF; e += blockDim.x) {
+    const int j = e / HALF, i = e % HALF; const float *qh = a.q + (size_t)(g * REP + j) * HD;
     const float x0 = qh[i], x1 = qh[i + HALF];
     qs[j][i] = __builtin_fmaf(x0, cs[i], -(x1 * sn[i]));
     qs[j][i + HALF] = __builtin_fmaf(x1, cs[i], x0 * sn[i]);
   }
-  const bool own = t0 <= pos && pos < t1;
-  if (own) {
-    for (int i = threadIdx.x; i < HALF; i += kThreads) {
+  if (t0 <= pos && pos < t1) {
+    for (int i = threadIdx.x; i < HALF; i += blockDim.x) {
       const float *kh = a.k + (size_t)g * HD; const float x0 = kh[i], x1 = kh[i + HALF];
       const uint16_t k0 = float_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
       const uint16_t k1 = float_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
       knew[i] = k0; knew[i + HALF] = k1;
       a.kc[(size_t)pos * kvd + g * HD + i] = k0; a.kc[(size_t)pos * kvd + g * HD + i + HALF] = k1;
     }
-    for (int i = threadIdx.x; i < HD; i += kThreads) {
+    for (int i = threadIdx.x; i < HD; i += blockDim.x) {
       const uint16_t v = float_to_half_bits(a.v[(size_t)g * HD + i]);
       vnew[i] = v; a.vc[(size_t)pos * kvd + g * HD + i] = v;
     }
   }
-  if (threadIdx.x < JMAX) { m_run[threadIdx.x] = -INFINITY; l_run[threadIdx.x] = 0.f; }
-  const float scl = 1.f / sqrtf((float)HD);
-  float o[JPT];
-#pragma unroll
-  for (int jj = 0; jj < JPT; jj++) o[jj] = 0.f;
-  const int oi = threadIdx.x % HD, oj0 = threadIdx.x / HD;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   __syncthreads();
-  for (int ts = t0; ts < t1; ts += TP) {
-    const int n = t1 - ts < TP ? t1 - ts : TP;
-    // stage K (padded rows) and V
-    for (int e = threadIdx.x; e < n * (HD / 2); e += kThreads) {
-      const int t = e / (HD / 2), i2 = e % (HD / 2), tp = ts + t;
-      uint32_t kw, vw;
-      if (tp == pos) { kw = knew[2 * i2] | ((uint32_t)knew[2 * i2 + 1] << 16); vw = vnew[2 * i2] | ((uint32_t)vnew[2 * i2 + 1] << 16); }
-      else {
-        kw = *(const uint32_t *)(a.kc + (size_t)tp * kvd + g * HD + 2 * i2);
-        vw = *(const uint32_t *)(a.vc + (size_t)tp * kvd + g * HD + 2 * i2);
+  const float scl = 1.f / sqrtf((float)HD);
+  const int psub = lane / LPP, dsl = lane % LPP;
+  float o[REP][VD];
+#pragma unroll
+  for (int j = 0; j < REP; j++)
+#pragma unroll
+    for (int d = 0; d < VD; d++) o[j][d] = 0.f;
+  if (lane < REP) { wm[wave][lane] = -INFINITY; wl[wave][lane] = 0.f; }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int tb = wt0; tb < wt1; tb += 16) {
+    const int np = wt1 - tb < 16 ? wt1 - tb : 16;
+    if (tb + 16 < wt1) kv_load<HD>(a.kc, a.vc, kvd, g, tb + 16, wt1, lane, nxt);   // next block in flight
+    // the current position's row comes from LDS (this workgroup wrote it)
+    const bool has_pos = tb <= pos && pos < tb + np;
+    // scores
+#pragma unroll
+    for (int i = 0; i < B::KP; i++) {
+      const int p = i * PPI + psub, t = tb + p;
+      const u32x4 kw = (has_pos && t == pos) ? *(const u32x4 *)(knew + dsl * 8) : cur.k[i];
+      float kf[8];
+#pragma unroll
+      for (int q = 0; q < 4; q++) { kf[2 * q] = half_bits_to_float((uint16_t)(kw[q] & 0xffff)); kf[2 * q + 1] = half_bits_to_float((uint16_t)(kw[q] >> 16)); }
+#pragma unroll
+      for (int j = 0; j < REP; j++) {
+        const float4 qa = *(const float4 *)&qs[j][dsl * 8], qb = *(const float4 *)&qs[j][dsl * 8 + 4];
+        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        float d = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) d = __builtin_fmaf(qv[q], kf[q], d);
+        d += dpp_f<kDppQuadXor1>(d);
+        d += dpp_f<kDppQuadXor2>(d);
+        d += dpp_f<kDppHalfMirror>(d);
+        if (LPP == 16) d += dpp_f<0x140>(d);   // row_mirror: lane i <-> 15 - i
+        if (dsl == 0 && p < np) sc[wave][j][p] = d * scl;
       }
-      *(uint32_t *)&ks[t][2 * i2] = kw;
-      *(uint32_t *)&vs[t][2 * i2] = vw;
     }
-    __syncthreads();
-    // scores: wave w takes heads w, w + 4; lane = position
-    for (int j = wave; j < rep; j += kThreads / kWave) {
-      float s = -INFINITY;
-      if (lane < n) {
-        float acc = 0.f;
-#pragma unroll 8
-        for (int i = 0; i < HD; i += 2) {
-          const uint32_t kw = *(const uint32_t *)&ks[lane][i];
-          acc = __builtin_fmaf(qs[j][i], half_bits_to_float((uint16_t)(kw & 0xffff)), acc);
-          acc = __builtin_fmaf(qs[j][i + 1], half_bits_to_float((uint16_t)(kw >> 16)), acc);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // online softmax: lane -> (head jp + lane / 16, position lane % 16)
+    float cfr[REP];
+#pragma unroll
+    for (int jp = 0; jp < REP; jp += 4) {
+      const int j = jp + (lane >> 4), p = lane & 15;
+      const bool hj = j < REP, ok = hj && p < np;
+      const float sv = ok ? sc[wave][hj ? j : 0][p] : -INFINITY;
+      const float mt = row16_max(sv);
+      const float mo = hj ? wm[wave][j] : 0.f, mn = fmaxf(mo, mt);
+      const float cf = mo == -INFINITY ? 0.f : expf(mo - mn);
+      const float pv = ok ? expf(sv - mn) : 0.f;
+      const float ls = row16_sum(pv);
+      if (ok) sc[wave][j][p] = pv;
+      if (hj && p == 0) { wl[wave][j] = wl[wave][j] * cf + ls; wm[wave][j] = mn; }
+#pragma unroll
+      for (int jj = jp; jj < jp + 4 && jj < REP; jj++) cfr[jj] = lane_bcast(cf, (jj - jp) * 16);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < REP; j++)
+#pragma unroll
+      for (int d = 0; d < VD; d++) o[j][d] *= cfr[j];
+    // values
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+      if (t < np) {
+        uint32_t vw = cur.v[t];
+        if (has_pos && tb + t == pos) vw = VD == 2 ? ((uint32_t)vnew[2 * lane] | ((uint32_t)vnew[2 * lane + 1] << 16)) : vnew[lane];
+        float vf[VD];
+        vf[0] = half_bits_to_float((uint16_t)(vw & 0xffff));
+        if (VD == 2) vf[VD - 1] = half_bits_to_float((uint16_t)(vw >> 16));
+#pragma unroll
+        for (int j = 0; j < REP; j++) {
+          const float p = sc[wave][j][t];
+#pragma unroll
+          for (int d = 0; d < VD; d++) o[j][d] = __builtin_fmaf(p, vf[d], o[j][d]);
         }
-        s = acc * scl;
-      }
-      const float mt = wave_max(s);
-      const float mo = m_run[j], mn = fmaxf(mo, mt);
-      const float p = lane < n ? expf(s - mn) : 0.f;
-      const float sum = wave_sum(p);
-      ps[j][lane] = p;
-      if (lane == 0) {
-        const float cf = expf(mo - mn);   // 0 on the first tile (mo = -inf)
-        corr[j] = cf; m_run[j] = mn; l_run[j] = l_run[j] * cf + sum;
       }
     }
-    __syncthreads();
+    cur = nxt;
+  }
+  // the 16 waves -> this split's [m, l, o]
 #pragma unroll
-    for (int jj = 0; jj < JPT; jj++) {
-      const int j = oj0 + jj * TPI;
-      if (j < rep) {
-        float acc = o[jj] * corr[j];
-        for (int t = 0; t < n; t++) acc = __builtin_fmaf(ps[j][t], half_bits_to_float(vs[t][oi]), acc);
-        o[jj] = acc;
-      }
-    }
-    __syncthreads();
-  }
+  for (int j = 0; j < REP; j++)
 #pragma unroll
-  for (int jj = 0; jj < JPT; jj++) {
-    const int j = oj0 + jj * TPI;
-    if (j < rep) {
-      float *pp = a.part + ((size_t)(g * rep + j) * a.max_chunks + c) * (HD + 2);
-      if (oi == 0) { pp[0] = m_run[j]; pp[1] = l_run[j]; }
-      pp[2 + oi] = o[jj];
+    for (int d = 0; d < VD; d++) ored[wave][j][lane * VD + d] = o[j][d];
+  __syncthreads();
+  for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
+    const int j = e / HD, i = e % HD;
+    float M = wm[0][j];
+    for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w][j]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < NW; w++) {
+      const float f = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);
+      L = __builtin_fmaf(wl[w][j], f, L); O = __builtin_fmaf(f, ored[w][j][i], O);
+    }
+    if (S == 1) a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
+    else {
+      float *pp = a.part + ((size_t)(g * REP + j) * gridDim.y + s) * (HD + 2);
+      if (i == 0) { pp[0] = M; pp[1] = L; }
+      pp[2 + i] = O;
     }
   }
-}
-
-// merge of the chunk partials per head (the fixed-order merge of model_llama.cpp:160-165): M = max m_c,
-// L = sum l_c e^(m_c - M), out = (sum o_c e^(m_c - M)) * (1 / L)
-template <int HD>
-__global__ void k_attn_merge(AttnArgs a) {
-  const int h = blockIdx.x, i = threadIdx.x, T = a.ctl->pos + 1, nc = (T + a.chunk - 1) / a.chunk;
-  const float *ph = a.part + (size_t)h * a.max_chunks * (HD + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < nc; c++) M = fmaxf(M, ph[(size_t)c * (HD + 2)]);
-  float L = 0.f, o = 0.f;
-  for (int c = 0; c < nc; c++) {
-    const float *pc = ph + (size_t)c * (HD + 2); const float f = expf(pc[0] - M);
-    L = __builtin_fmaf(pc[1], f, L); o = __builtin_fmaf(f, pc[2 + i], o);
+  if (S == 1) return;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // every wave's partial stores before the counter bump
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(a.counters + g, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == S - 1;
+    if (last) __hip_atomic_store(a.counters + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  a.att[(size_t)h * HD + i] = o * (1.f / L);
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
+    const int j = e / HD, i = e % HD;
+    const float *ph = a.part + (size_t)(g * REP + j) * gridDim.y * (HD + 2);
+    float M = -INFINITY;
+    for (int c = 0; c < S; c++) M = fmaxf(M, ph[(size_t)c * (HD + 2)]);
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < S; c++) {
+      const float *pc = ph + (size_t)c * (HD + 2);
+      const float f = pc[0] == -INFINITY ? 0.f : expf(pc[0] - M);
+      L = __builtin_fmaf(pc[1], f, L); O = __builtin_fmaf(f, pc[2 + i], O);
+    }
+    a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
+  }
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
-  if (a.nh / a.nkv > 8) return hipErrorInvalidValue;
+  if (a.nh % a.nkv || a.nh / a.nkv > 8 || a.max_chunks < 1 || a.max_chunks > kAttnMaxSplits) return hipErrorInvalidValue;
   const dim3 grid(a.nkv, a.max_chunks);
-  if (a.hd == 64) {
-    hipLaunchKernelGGL(k_attention<64>, grid, dim3(kThreads), 0, st, a);
-    hipLaunchKernelGGL(k_attn_merge<64>, dim3(a.nh), dim3(64), 0, st, a);
-  } else if (a.hd == 128) {
-    hipLaunchKernelGGL(k_attention<128>, grid, dim3(kThreads), 0, st, a);
-    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.nh), dim3(128), 0, st, a);
-  } else return hipErrorInvalidValue;
-  return hipGetLastError();
+  const int rep = a.nh / a.nkv;
+#define QPH_ATT(HD, R) if (a.hd == HD && rep == R) { const int nw = attn_waves(HD, R); hipLaunchKernelGGL((k_attention<HD, R>), grid, dim3(nw * 64), 0, st, a); return hipGetLastError(); }
+  QPH_ATT(64, 1) QPH_ATT(64, 2) QPH_ATT(64, 3) QPH_ATT(64, 4) QPH_ATT(64, 5) QPH_ATT(64, 6) QPH_ATT(64, 7) QPH_ATT(64, 8)
+  QPH_ATT(128, 1) QPH_ATT(128, 2) QPH_ATT(128, 3) QPH_ATT(128, 4) QPH_ATT(128, 5) QPH_ATT(128, 6) QPH_ATT(128, 7) QPH_ATT(128, 8)
+#undef QPH_ATT
+  return hipErrorInvalidValue;
 }
 
 // ------------------------------------------------------------------ greedy pick

@@ -61,9 +61,11 @@ struct AttnArgs {
   uint16_t *kc, *vc;           // this layer's fp16 caches [ctx][kvd]
   const float *cos_t, *sin_t;  // RoPE tables [ctx][hd / 2]
   const Ctl *ctl;
-  float *part;                 // [nh][max_chunks][hd + 2]: running max, sum, unnormalised output
-  float *att;                  // merged output [nh * hd]
-  int nh, nkv, hd, chunk, max_chunks;
+  float *part;                 // [nh][splits][hd + 2]: max, sum, unnormalised output of every split
+  int *counters;               // [nkv] zero; each group's last split resets its counter
+  float *att;                  // output [nh * hd]
+  int nh, nkv, hd;
+  int max_chunks;              // splits S of the context per kv group (grid.y)
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 

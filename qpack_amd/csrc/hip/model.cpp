@@ -96,9 +96,11 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     layers_.push_back(ly);
   }
   // attention split: enough (group, chunk) workgroups to cover the chip at full context
-  chunk_ = 64;
-  while ((int64_t)nkv * ((ctx_ + chunk_ - 1) / chunk_) > 4ll * cus_ && chunk_ < 1024) chunk_ *= 2;
-  max_chunks_ = (ctx_ + chunk_ - 1) / chunk_;
+  // splits of the context per kv group: the kernel activates ceil(T / 1024) of them (one workgroup per group below
+  // 1024 positions, no merge); the grid covers the full context
+  max_chunks_ = std::max(1, std::min(256, (ctx_ + 1023) / 1024));
+  if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(256, atoi(e)));
+  counters_ = (int *)dalloc(4ull * nkv);
   const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
   kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
   QPH_CK(hipMemset(kc_, 0, kvn * 2)); QPH_CK(hipMemset(vc_, 0, kvn * 2));
@@ -106,6 +108,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   k_ = (float *)dalloc(4ull * kvd_); v_ = (float *)dalloc(4ull * kvd_); att_ = (float *)dalloc(4ull * qd_);
   h_ = (float *)dalloc(4ull * ff); logits_ = (float *)dalloc(4ull * V);
   part_ = (float *)dalloc(4ull * nh * max_chunks_ * (hd + 2));
+  QPH_CK(hipMemset(counters_, 0, 4ull * nkv));
   head_grid_ = cus_ * 4;
   amax_ = (float2 *)dalloc(sizeof(float2) * head_grid_);
   {  // partials of workgroups a smaller launch does not use must never win the pick
@@ -156,7 +159,7 @@ void HipLlama::enqueue_layer(int l) {
     AttnArgs a{}; a.q = q_; a.k = k_; a.v = v_;
     a.kc = kc_ + (size_t)l * ctx_ * kvd_; a.vc = vc_ + (size_t)l * ctx_ * kvd_;
     a.cos_t = cos_; a.sin_t = sin_; a.ctl = ctl_; a.part = part_; a.att = att_;
-    a.nh = cfg_.heads; a.nkv = cfg_.kv_heads; a.hd = cfg_.head_dim; a.chunk = chunk_; a.max_chunks = max_chunks_;
+    a.nh = cfg_.heads; a.nkv = cfg_.kv_heads; a.hd = cfg_.head_dim; a.max_chunks = max_chunks_; a.counters = counters_;
     QPH_CK(launch_attention(a, st_));
   }
   {  // wo + residual
@@ -353,8 +356,8 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
       case 4: enqueue_head(); break;
       case 5: {
         AttnArgs t{}; t.q = q_; t.k = k_; t.v = v_; t.kc = kc_; t.vc = vc_; t.cos_t = cos_; t.sin_t = sin_; t.ctl = ctl_;
-        t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim; t.chunk = chunk_;
-        t.max_chunks = max_chunks_;
+        t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
+        t.max_chunks = max_chunks_; t.counters = counters_;
         QPH_CK(launch_attention(t, st_)); break;
       }
       default: throw std::runtime_error("time_kernel: unknown kernel id");

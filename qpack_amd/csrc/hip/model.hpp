@@ -44,7 +44,8 @@ class HipLlama {
     const float *an = nullptr, *fn = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
   };
   qph_config cfg_;
-  int ctx_ = 0, kvd_ = 0, qd_ = 0, chunk_ = 64, max_chunks_ = 1, cus_ = 256, head_grid_ = 0;
+  int ctx_ = 0, kvd_ = 0, qd_ = 0, max_chunks_ = 1, cus_ = 256, head_grid_ = 0;
+  int *counters_ = nullptr;
   int pos_ = 0;
   unsigned slot_ = 0;
   hipStream_t st_ = nullptr;
