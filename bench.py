@@ -6,8 +6,10 @@ SwiGLU 14336, vocab 128256, untied head), seeded N(0, 0.02) random-init weights 
   decode  - 128-token prompt, `--warmup` untimed greedy tokens, then exactly `--steps` greedy tokens timed (device
             argmax feeds the next step; HIP events on the model's stream, host clock around it)
   prefill - one `--prefill-tokens` prompt (C4), host clock around qph_prefill
-Roofline: the dominant decode kernel (layer-0 fused RMSNorm + gate/up + SwiGLU matvec, ~47 % of the step's bytes),
-replayed alone and timed with HIP events on the model's stream; achieved = its algorithmic bytes / mean duration.
+Roofline: the dominant decode kernel (fused RMSNorm + gate/up + SwiGLU matvec, ~47 % of the step's bytes), launched
+alone over the 32 layers in turn and timed with HIP events on the model's stream; achieved = its algorithmic bytes /
+mean duration.  traffic = its HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (committed summary under
+profiles/, produced by --profile runs and --pmc-summary).
 CPU baseline: the reference engine compiled from its own sources (oracle/_ref/libqpref.so, AVX2) on the same file,
 on the host cores, qpack-bench protocol on a bounded sample.
 
@@ -26,6 +28,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+DOMINANT = "k_matvec<1, 2, 2, 1, false>"   # PRO_NORM, EPI_SWIGLU, 2 rows per unit, q8
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_matvec_norm_swiglu_q8_c3_traffic.md")
+COPY_BYTES = 1 << 29                         # calibration copy: 512 MiB read + 512 MiB written
 METRIC = "batch-1 decode tokens/s + % HBM peak; prefill tokens/s (8B-shape q8)"
 
 
@@ -52,6 +57,42 @@ def step_bytes(shape, T):
     head = mat(V, d, False) + 4 * d
     kv = L * 2 * T * kvd * 2
     return weights + head + d + kv
+
+
+def calibration_copy(reps=4):
+    """the library's plain copy kernel k_copy over COPY_BYTES (read once, written once) for scaling the byte counters"""
+    import qpack_amd as qa
+    ms = qa.time_copy(COPY_BYTES, reps)
+    log(f"calibration copy: {COPY_BYTES >> 20} MiB in {ms * 1e3:.1f} us -> {2 * COPY_BYTES / (ms / 1e3) / 1e9:.0f} GB/s (read + write)")
+
+
+def pmc_summary(csv_path, kernel_sub, copy_sub="k_copy"):
+    """per-dispatch averages of each counter in a rocprofv3 counter_collection.csv, for the dominant kernel and for the
+    calibration copy; returns {counter: (kernel_mean, copy_mean, n_kernel, n_copy)}"""
+    import csv
+    acc = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            name, ctr, val = r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])
+            which = 0 if kernel_sub in name else (1 if copy_sub in name else None)
+            if which is None:
+                continue
+            e = acc.setdefault(ctr, [[], []])
+            e[which].append(val)
+    return {c: (float(np.mean(k)) if k else None, float(np.mean(cp)) if cp else None, len(k), len(cp))
+            for c, (k, cp) in acc.items()}
+
+
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed counter summary (line 'traffic_bytes: N')"""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(path, threads, n_prompt=16, n_gen=16, reps=2):
@@ -91,10 +132,30 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="launch kernels one by one (no HIP graphs) so a profiler sees every dispatch, and run a "
+                         "calibration copy of known size for the byte counters")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the dominant kernel's per-launch HBM traffic from two rocprofv3 --pmc runs "
+                         "(FETCH_SIZE, WRITE_SIZE) of --profile, scaled by the calibration copy; no GPU work")
     a = ap.parse_args()
+    if a.pmc_summary:
+        scale_note = []
+        total = 0.0
+        for path, ctr in zip(a.pmc_summary, ("FETCH_SIZE", "WRITE_SIZE")):
+            k, cp, nk, ncp = pmc_summary(path, DOMINANT)[ctr]
+            f = (COPY_BYTES / 1024) / cp            # counter reads KiB; the copy moves COPY_BYTES each way
+            total += k * 1024 * f
+            scale_note.append(f"{ctr}: kernel {k:.1f} KiB/dispatch over {nk} dispatches; copy {cp:.1f} KiB/dispatch "
+                              f"over {ncp} (expected {COPY_BYTES // 1024}) -> scale {f:.4f} -> {k * 1024 * f:.0f} B")
+        print("\n".join(scale_note))
+        print(f"traffic_bytes: {total:.0f}")
+        return
+    if a.profile:
+        os.environ["QPH_NO_GRAPH"] = "1"
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); the multi-GPU sharding plan is "
-              "design-only (DESIGN.md, 'More than one GPU')", file=sys.stderr)
+              "documented as a design, not built", file=sys.stderr)
         sys.exit(2)
 
     import qpack_amd as qa
@@ -133,6 +194,8 @@ def main():
     log(f"decode: {a.steps} tokens in {ms:.2f} ms (HIP events), wall {wall * 1e3:.2f} ms -> {tok_s:.1f} tok/s, "
         f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / HBM_PEAK_GBS:.1f}% of peak)")
 
+    if a.profile:
+        calibration_copy()
     kms, kbytes = m.time_kernel(0, a.kernel_iters)
     k_gbs = kbytes / (kms / 1e3) / 1e9
     log(f"dominant kernel (layer-0 gate/up matvec): {kms * 1e3:.2f} us, {kbytes / 1e6:.1f} MB -> {k_gbs:.0f} GB/s")
@@ -179,8 +242,9 @@ def main():
         "step_roofline": {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4), "bytes_per_token": round(sb)},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_matvec<PRO_NORM,EPI_SWIGLU> (layer-0 gate+up, 2 x 14336 x 4096 q8)",
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "kernel": "k_matvec<PRO_NORM,EPI_SWIGLU> (fused RMSNorm + gate/up + SwiGLU, 2 x 14336 x 4096 q8; "
+                               "launches walk the 32 layers)",
                      "bytes_per_launch": round(kbytes), "us_per_launch": round(kms * 1e3, 2)},
         "kernels": others,
         "prefill": prefill,

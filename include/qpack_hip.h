@@ -93,10 +93,15 @@ int qph_restore(qph_model *m, const uint8_t *buf, int64_t n);
 /* Runs n greedy decode steps from token/position as greedy_run does and reports the HIP-event time of the whole run
  * on the model's stream (*ms). */
 int qph_time_greedy(qph_model *m, int token, int n, float *ms);
-/* Replays one decode-step kernel `iters` times on the model's stream and reports its mean HIP-event duration and its
- * algorithmic HBM bytes per launch.  which: 0 = layer-0 fused gate/up matvec, 1 = layer-0 down matvec, 2 = layer-0 qkv
- * matvec, 3 = layer-0 wo matvec, 4 = output head matvec, 5 = layer-0 attention at the current position. */
+/* Launches one decode-step kernel `iters` times on the model's stream, walking the layers in turn as the token loop
+ * does, and reports its mean HIP-event duration and its algorithmic HBM bytes per launch (mean over the layers).
+ * which: 0 = fused RMSNorm + gate/up + SwiGLU matvec, 1 = down matvec, 2 = fused RMSNorm + qkv matvec, 3 = wo matvec,
+ * 4 = output head matvec + argmax partials, 5 = attention at the current position. */
 int qph_time_kernel(qph_model *m, int which, int iters, float *ms, double *bytes);
+/* A plain device-to-device copy of `bytes` (a multiple of 16) through the kernel k_copy, `iters` times on a stream of
+ * its own, with the buffers allocated and freed inside; *ms = mean HIP-event duration.  Calibrates hardware byte
+ * counters (a profiler's FETCH_SIZE / WRITE_SIZE of k_copy should read `bytes` each). */
+int qph_time_copy(int64_t bytes, int iters, float *ms);
 
 /* ---- parity hooks (no reference counterpart; the int32 contract of rows_q8 / rows_q4, kernels_x86.cpp:55-106) */
 /* Runs the product's matvec kernel on one matrix (host buffers in, host buffers out): activation quantisation of x,

@@ -5,8 +5,8 @@
   kernel_matvec(...)    - the product's matvec kernel on one matrix, with its exact int32 accumulators (parity hook)
 """
 from ._lib import LIB_PATH, QPH_F32, QPH_Q4, QPH_Q8, QphError, device_count, lib
-from .model import HipLlama, kernel_matvec
+from .model import HipLlama, kernel_matvec, time_copy
 from .synth import CONFIGS, Shape, write_synthetic
 
-__all__ = ["HipLlama", "kernel_matvec", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
+__all__ = ["HipLlama", "kernel_matvec", "time_copy", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
            "QPH_F32", "QPH_Q8", "QPH_Q4"]

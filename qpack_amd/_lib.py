@@ -63,6 +63,7 @@ SIGNATURES = {
     "qph_restore": (_I, [_P, C.c_void_p, C.c_int64]),
     "qph_time_greedy": (_I, [_P, _I, _I, _FP]),
     "qph_time_kernel": (_I, [_P, _I, _I, _FP, C.POINTER(C.c_double)]),
+    "qph_time_copy": (_I, [C.c_int64, _I, _FP]),
     "qph_kernel_matvec": (_I, [_I, _P, _P, _I, _I, _FP, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int16), _FP]),
     "qph_kernel_matmul": (_I, [_I, _P, _P, _I, _I, _FP, _I, _FP]),
     "qph_synth_write": (_I, [C.POINTER(SynthSpecC), C.c_char_p, _I]),

@@ -142,6 +142,38 @@ int qph_time_kernel(qph_model *m, int which, int iters, float *ms, double *bytes
   QPH_API_TRY({ need(m, "model"); need(ms, "ms"); need(bytes, "bytes"); *ms = m->m->time_kernel(which, iters, bytes); });
 }
 
+int qph_time_copy(int64_t bytes, int iters, float *ms) {
+  QPH_API_TRY({
+    need(ms, "ms");
+    if (bytes <= 0 || bytes % 16) throw std::invalid_argument("time_copy: bytes must be a positive multiple of 16");
+    if (iters <= 0) iters = 1;
+    void *src = nullptr, *dst = nullptr;
+    hipStream_t st = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto cleanup = [&]() {
+      if (e0) (void)hipEventDestroy(e0);
+      if (e1) (void)hipEventDestroy(e1);
+      if (st) (void)hipStreamDestroy(st);
+      if (src) (void)hipFree(src);
+      if (dst) (void)hipFree(dst);
+    };
+    try {
+      QPH_CK(hipMalloc(&src, bytes)); QPH_CK(hipMalloc(&dst, bytes));
+      QPH_CK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+      QPH_CK(hipMemsetAsync(src, 1, bytes, st));
+      QPH_CK(hipEventCreate(&e0)); QPH_CK(hipEventCreate(&e1));
+      QPH_CK(qph::launch_copy(src, dst, bytes / 16, st));   // warm-up
+      QPH_CK(hipEventRecord(e0, st));
+      for (int i = 0; i < iters; i++) QPH_CK(qph::launch_copy(src, dst, bytes / 16, st));
+      QPH_CK(hipEventRecord(e1, st));
+      QPH_CK(hipEventSynchronize(e1));
+      QPH_CK(hipEventElapsedTime(ms, e0, e1));
+      *ms /= iters;
+    } catch (...) { cleanup(); throw; }
+    cleanup();
+  });
+}
+
 int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int cols, const float *x, float *y,
                       int32_t *sums, int16_t *xq, float *bs) {
   QPH_API_TRY({

@@ -800,4 +800,14 @@ hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_to
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ calibration copy
+__global__ __launch_bounds__(256) void k_copy(const u32x4 *src, u32x4 *dst, size_t n16) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+hipError_t launch_copy(const void *src, void *dst, size_t n16, hipStream_t st) {
+  hipLaunchKernelGGL(k_copy, dim3(4096), dim3(256), 0, st, (const u32x4 *)src, (u32x4 *)dst, n16);
+  return hipGetLastError();
+}
+
 }  // namespace qph

@@ -2,7 +2,17 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <stdexcept>
+#include <string>
+
 #include "common.hpp"
+
+// host code: throw on a failed HIP call
+#define QPH_CK(x)                                                                                           \
+  do {                                                                                                      \
+    hipError_t e_ = (x);                                                                                    \
+    if (e_ != hipSuccess) throw std::runtime_error(std::string("hip: ") + hipGetErrorString(e_) + " at " + #x); \
+  } while (0)
 
 namespace qph {
 
@@ -71,6 +81,9 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 
 // greedy pick over the head's per-workgroup (max, index) pairs; advances ctl (tok = pick, pos += 1, n_out += 1) and
 // writes the pick to out_tokens[ctl->n_out]
+// dst[0..n16) = src[0..n16) in 16-byte words (counter calibration)
+hipError_t launch_copy(const void *src, void *dst, size_t n16, hipStream_t st);
+
 hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st);
 
 }  // namespace qph

@@ -11,12 +11,6 @@
 
 namespace qph {
 
-#define QPH_CK(x)                                                                                           \
-  do {                                                                                                      \
-    hipError_t e_ = (x);                                                                                    \
-    if (e_ != hipSuccess) throw std::runtime_error(std::string("hip: ") + hipGetErrorString(e_) + " at " + #x); \
-  } while (0)
-
 static constexpr unsigned kRing = 256;   // pinned control slots (one per host-driven step in flight)
 
 void *HipLlama::dalloc(size_t bytes) {
@@ -330,13 +324,17 @@ static double mat_bytes(const DMat &m) {
 
 float HipLlama::time_kernel(int which, int iters, double *bytes) {
   if (iters <= 0) iters = 1;
-  const Layer &ly = layers_[0];
-  const int cap = 1 << 20, d = cfg_.hidden;
+  // consecutive launches walk the layers, as the token loop does, so no launch finds its weights in the
+  // 256 MiB last-level cache from the previous one
+  const int L = cfg_.layers, d = cfg_.hidden, cap = 1 << 20;
+  int li = 0;
   const float eps = cfg_.rms_eps;
   write_ctl(0, std::min(pos_, ctx_ - 1));
   const char *dme = getenv("QPH_MV_DBG");
   const int dmode = dme ? atoi(dme) : 0;
   auto launch = [&]() {
+    const Layer &ly = layers_[li];
+    li = li + 1 == L ? 0 : li + 1;
     MvArgs a{};
     a.dbg_mode = dmode;
     switch (which) {
@@ -363,15 +361,20 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
       default: throw std::runtime_error("time_kernel: unknown kernel id");
     }
   };
-  switch (which) {
-    case 0: *bytes = mat_bytes(ly.wg) + mat_bytes(ly.wu) + 4.0 * d; break;
-    case 1: *bytes = mat_bytes(ly.wd); break;
-    case 2: *bytes = mat_bytes(ly.wq) + mat_bytes(ly.wk) + mat_bytes(ly.wv) + 4.0 * d; break;
-    case 3: *bytes = mat_bytes(ly.wo); break;
-    case 4: *bytes = mat_bytes(head_) + 4.0 * d + 4.0 * cfg_.vocab; break;
-    case 5: *bytes = 4.0 * (double)(pos_ + 1) * kvd_; break;
-    default: throw std::runtime_error("time_kernel: unknown kernel id");
+  // algorithmic bytes per launch, averaged over the layers (q4 mixes differ by layer)
+  double sum = 0;
+  for (const Layer &ly : layers_) {
+    switch (which) {
+      case 0: sum += mat_bytes(ly.wg) + mat_bytes(ly.wu) + 4.0 * d; break;
+      case 1: sum += mat_bytes(ly.wd); break;
+      case 2: sum += mat_bytes(ly.wq) + mat_bytes(ly.wk) + mat_bytes(ly.wv) + 4.0 * d; break;
+      case 3: sum += mat_bytes(ly.wo); break;
+      case 4: sum += mat_bytes(head_) + 4.0 * d + 4.0 * cfg_.vocab; break;
+      case 5: sum += 4.0 * (double)(pos_ + 1) * kvd_; break;
+      default: throw std::runtime_error("time_kernel: unknown kernel id");
+    }
   }
+  *bytes = sum / L;
   launch();   // warm-up
   hipEvent_t e0, e1;
   QPH_CK(hipEventCreate(&e0)); QPH_CK(hipEventCreate(&e1));

@@ -130,6 +130,13 @@ class HipLlama:
         return ms.value, b.value
 
 
+def time_copy(nbytes, iters=4):
+    """mean duration (ms) of the library's plain device copy kernel k_copy over nbytes (qph_time_copy)"""
+    ms = C.c_float()
+    check(lib().qph_time_copy(int(nbytes), int(iters), C.byref(ms)))
+    return ms.value
+
+
 def kernel_matvec(kind, q, scale, x):
     """the product's matvec kernel on one matrix: returns (y, exact int32 sums, int16 activation, block scales)"""
     from ._lib import QPH_Q8
