@@ -534,9 +534,10 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 }
 
 // ------------------------------------------------------------------ decode attention (split-K over the context)
-// grid (kv group g, split s), 16 waves (8 for wide GQA groups).  The number of active splits follows the context, S_eff = ceil(T / 1024)
-// (at most grid.y): below 1024 positions one workgroup per kv group does everything and no cross-workgroup merge is
-// needed.  Split s takes positions [s T / S_eff, (s + 1) T / S_eff); each wave a contiguous sub-range, streamed straight
+// grid (kv group g, split s), 4 waves (one per SIMD).  The number of active splits follows the context,
+// S_eff = min(grid.y, ceil(T / 64)): the work of a token's attention is small, so it is spread over as many CUs as the
+// context allows instead of queueing 16 waves on one CU's SIMDs; below 65 positions one workgroup per kv group does
+// everything and no cross-workgroup merge is needed.  Split s takes positions [s T / S_eff, (s + 1) T / S_eff); each wave a contiguous sub-range, streamed straight
 // from HBM 16 positions at a time with the next block's K and V loads in flight (double-buffered registers).
 // The workgroup applies RoPE to its rep query heads (rotate-half with the reference's contraction
 // a' = fma(a, cos, -(b sin)), b' = fma(b, cos, a sin), model_llama.cpp:176); the workgroup owning the current position
@@ -544,11 +545,11 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 //   scores: LPP = HD / 8 lanes share a position, each holding 8 dims of K and of every query head; DPP sums the LPP
 //           partial dots; scale 1/sqrt(hd) as in attend() (model_llama.cpp:137-146).
 //   online softmax per wave and head (max and sum over rows of 16 lanes, one head per row); values: lane owns HD / 64 dims.
-// The 16 wave partials merge in LDS; with several splits the last one to finish (release / acquire on a per-group
+// The wave partials merge in LDS; with several splits the last one to finish (release / acquire on a per-group
 // counter, which that workgroup resets) merges the split partials in split order - the merge of model_llama.cpp:160-165:
 // M = max m, L = sum l e^(m - M), out = sum o e^(m - M) * (1 / L).
-constexpr int kAttnMaxSplits = 256;
-constexpr int kSplitPos = 1024;
+constexpr int kAttnMaxSplits = 64;
+constexpr int kSplitPos = 64;   // fewest positions per context split (4 waves x one 16-position block)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // sum / max over aligned rows of 16 lanes (every lane of the row gets the result)
@@ -586,8 +587,9 @@ __device__ __forceinline__ void kv_load(const uint16_t *kc, const uint16_t *vc, 
   }
 }
 
-// waves per attention workgroup: 16, or 8 where 16 would not fit the registers (wide GQA groups)
-constexpr int attn_waves(int hd, int rep) { return (hd == 64 && rep >= 7) || (hd == 128 && rep >= 5) ? 8 : 16; }
+// waves per attention workgroup: one per SIMD, so a workgroup's waves never queue behind each other on one SIMD;
+// the context is split over workgroups instead
+constexpr int attn_waves(int, int) { return 4; }
 template <int HD, int REP>
 __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs a) {
   using B = KvBlock<HD>;
@@ -714,7 +716,7 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
     }
     cur = nxt;
   }
-  // the 16 waves -> this split's [m, l, o]
+  // the waves -> this split's [m, l, o]
 #pragma unroll
   for (int j = 0; j < REP; j++)
 #pragma unroll
@@ -731,34 +733,64 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
     }
     if (S == 1) a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
     else {
+      // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback
       float *pp = a.part + ((size_t)(g * REP + j) * gridDim.y + s) * (HD + 2);
-      if (i == 0) { pp[0] = M; pp[1] = L; }
-      pp[2 + i] = O;
+      if (i == 0) {
+        __hip_atomic_store(pp, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(pp + 2 + i, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (S == 1) return;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // every wave's partial stores before the counter bump
+  // this thread's coherent stores have completed before the workgroup's counter bump
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(a.counters + g, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = __hip_atomic_fetch_add(a.counters + g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == S - 1;
     if (last) __hip_atomic_store(a.counters + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // the last split merges, in split order (model_llama.cpp:160-165): per head the max M, the weights
+  // f_c = exp(m_c - M) and L = sum_c l_c f_c, then O = sum_c f_c o_c; partials read with coherent (sc1) loads
+  __shared__ float fw[REP][kAttnMaxSplits], lw[REP][kAttnMaxSplits], linv[REP];
+  const float *pg = a.part + (size_t)g * REP * gridDim.y * (HD + 2);
+  for (int e = threadIdx.x; e < REP * S; e += blockDim.x) {
+    const int j = e / S, c = e % S;
+    const float *pc = pg + ((size_t)j * gridDim.y + c) * (HD + 2);
+    fw[j][c] = __hip_atomic_load(pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lw[j][c] = __hip_atomic_load(pc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (threadIdx.x < REP) {
+    const int j = threadIdx.x;
+    float M = -INFINITY;
+    for (int c = 0; c < S; c++) M = fmaxf(M, fw[j][c]);
+    float L = 0.f;
+    for (int c = 0; c < S; c++) {
+      const float f = fw[j][c] == -INFINITY ? 0.f : expf(fw[j][c] - M);
+      L = __builtin_fmaf(lw[j][c], f, L);
+      fw[j][c] = f;
+    }
+    linv[j] = 1.f / L;
+  }
+  __syncthreads();
   for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
     const int j = e / HD, i = e % HD;
-    const float *ph = a.part + (size_t)(g * REP + j) * gridDim.y * (HD + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < S; c++) M = fmaxf(M, ph[(size_t)c * (HD + 2)]);
-    float L = 0.f, O = 0.f;
-    for (int c = 0; c < S; c++) {
-      const float *pc = ph + (size_t)c * (HD + 2);
-      const float f = pc[0] == -INFINITY ? 0.f : expf(pc[0] - M);
-      L = __builtin_fmaf(pc[1], f, L); O = __builtin_fmaf(f, pc[2 + i], O);
+    const float *ph = pg + (size_t)j * gridDim.y * (HD + 2) + 2 + i;
+    float O = 0.f;
+    for (int c0 = 0; c0 < S; c0 += 8) {   // 8 independent loads in flight, then the ordered fma chain
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        v[k] = c0 + k < S ? __hip_atomic_load(ph + (size_t)(c0 + k) * (HD + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        if (c0 + k < S) O = __builtin_fmaf(fw[j][c0 + k], v[k], O);
     }
-    a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
+    a.att[(size_t)(g * REP + j) * HD + i] = O * linv[j];
   }
 }
 

@@ -92,8 +92,9 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   // attention split: enough (group, chunk) workgroups to cover the chip at full context
   // splits of the context per kv group: the kernel activates ceil(T / 1024) of them (one workgroup per group below
   // 1024 positions, no merge); the grid covers the full context
-  max_chunks_ = std::max(1, std::min(256, (ctx_ + 1023) / 1024));
-  if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(256, atoi(e)));
+  // context splits per kv group: one per 64 positions, at most 64 (the kernel uses min(this, ceil(T / 64)))
+  max_chunks_ = std::max(1, std::min(64, (ctx_ + 63) / 64));
+  if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(64, atoi(e)));
   counters_ = (int *)dalloc(4ull * nkv);
   const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
   kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
