@@ -208,8 +208,30 @@ int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int 
 }
 
 int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y) {
-  QPH_API_TRY({ (void)kind; (void)q; (void)scale; (void)rows; (void)cols; (void)X; (void)B; (void)Y;
-                throw std::runtime_error("qph_kernel_matmul: the batched prefill kernel is not built yet"); });
+  QPH_API_TRY({
+    need(q, "q"); need(scale, "scale"); need(X, "X"); need(Y, "Y");
+    if (rows <= 0 || B <= 0 || cols <= 0 || cols % 128) throw std::invalid_argument("matmul: rows, B > 0 and cols a positive multiple of 128 required");
+    if (kind != QPH_Q8) throw std::invalid_argument("matmul: the batched kernel takes q8 weights (QPH_Q8)");
+    const int nb = cols / 128;
+    std::vector<void *> bufs;
+    auto alloc = [&](size_t n) { void *p = nullptr; hck(hipMalloc(&p, n), "hipMalloc"); bufs.push_back(p); return p; };
+    try {
+      void *dq = alloc((size_t)rows * cols), *ds = alloc(4ull * rows);
+      float *dx = (float *)alloc(4ull * B * cols), *dy = (float *)alloc(4ull * B * rows), *dxb = (float *)alloc(4ull * B * nb);
+      int8_t *dxh = (int8_t *)alloc((size_t)B * cols), *dxl = (int8_t *)alloc((size_t)B * cols);
+      hck(hipMemcpy(dq, q, (size_t)rows * cols, hipMemcpyHostToDevice), "upload q");
+      hck(hipMemcpy(ds, scale, 4ull * rows, hipMemcpyHostToDevice), "upload scale");
+      hck(hipMemcpy(dx, X, 4ull * B * cols, hipMemcpyHostToDevice), "upload X");
+      qph::PfQuantArgs qa{}; qa.x = dx; qa.ldx = cols; qa.cols = cols; qa.xh = dxh; qa.xl = dxl; qa.ldq = cols; qa.xb = dxb; qa.ldb = nb;
+      hck(qph::launch_pf_quant(qph::PRO_QUANT, qa, B, nullptr), "launch quant");
+      qph::GemmArgs ga{}; ga.w = (const int8_t *)dq; ga.scale = (const float *)ds; ga.rows = rows; ga.cols = cols;
+      ga.xh = dxh; ga.xl = dxl; ga.xb = dxb; ga.ntok = B; ga.ldq = cols; ga.ldb = nb; ga.y = dy; ga.ldy = rows;
+      hck(qph::launch_gemm(ga, nullptr), "launch gemm");
+      hck(hipDeviceSynchronize(), "matmul");
+      hck(hipMemcpy(Y, dy, 4ull * B * rows, hipMemcpyDeviceToHost), "download Y");
+    } catch (...) { for (void *p : bufs) (void)hipFree(p); throw; }
+    for (void *p : bufs) (void)hipFree(p);
+  });
 }
 
 int qph_synth_write(const qph_synth_spec *spec, const char *path, int threads) {

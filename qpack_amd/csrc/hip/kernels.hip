@@ -17,38 +17,13 @@
 
 #include <algorithm>
 
+#include "act.hpp"
 #include "launch.hpp"
 
 namespace qph {
 
 constexpr int kThreads = 256;
 
-// ------------------------------------------------------------------ LDS activation layout
-struct ActView {
-  int8_t *xh;    // [cols] high bytes (signed)
-  uint8_t *xl;   // [cols] low bytes (unsigned)
-  float *bs;     // [nb] block scales
-  int *lsum;     // [nb] sum of the low bytes per 128-column block
-  int *gsum;     // [cols / 32] sum of q per 32-column group
-  float *red;    // [32] reduction scratch (16 wave partials, argmax values and indices)
-  int *sums;     // [waves][slots][nbp] q8 block sums
-  int nbp;
-};
-
-__host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
-
-__device__ inline ActView act_view(char *smem, int cols) {
-  ActView v; const int nb = cols / kQB, G = cols / 32;
-  v.nbp = round_up(nb, 4);
-  v.xh = (int8_t *)smem;
-  v.xl = (uint8_t *)(smem + cols);
-  v.bs = (float *)(smem + 2 * cols);
-  v.lsum = (int *)(v.bs + v.nbp);
-  v.gsum = v.lsum + v.nbp;
-  v.red = (float *)(v.gsum + round_up(G, 4));
-  v.sums = (int *)(v.red + 32);
-  return v;
-}
 // LDS of the matvec kernel: activation planes, block scales / low-byte sums, group sums, reduction scratch, and per wave
 // `per_wave` ints of block sums (q8) or unit values (q4) - at least nbp in total (the RMSNorm block sums use it first)
 size_t mv_lds_bytes(int cols, int waves, int per_wave) {
@@ -57,107 +32,6 @@ size_t mv_lds_bytes(int cols, int waves, int per_wave) {
   return (size_t)2 * cols + 4 * (size_t)nbp * 2 + 4 * (size_t)round_up(G, 4) + 32 * 4 + 4 * sums;
 }
 
-// The activation prologue in two halves, so its global reads are issued before the weight prefetch (a wave's loads
-// return in order: a read issued after the prefetch would wait for all of it).
-//   act_load:   eight lanes own a 128-column block, 16 columns each (two passes cover up to 2 x blockDim.x / 8 blocks);
-//               x (and the RMSNorm weight) go to registers.
-//   act_build:  optional RMSNorm, then quant_rows' arithmetic (/root/reference/src/kernels.cpp:17-31): mx = max |v|,
-//               isx = mx > 0 ? 32767 / mx : 0, bs = mx / 32767, q = rint(v * isx); written to LDS as byte planes.
-// The sum of squares is taken per 128-column block (each lane fma-sums its 16 columns in order, the 8 lanes add with
-// DPP), then wave 0 adds the block sums in a fixed tree: the same value for every workgroup size.  (The reference sums
-// sequentially, kernels.cpp:185; the order differs.)
-struct ActRegs {
-  float4 x[2][4];
-  float4 w[2][4];
-};
-template <int PRO>
-__device__ __forceinline__ void act_load(const float *x, const float *w, int cols, ActRegs &r) {
-  const int nb = cols / kQB, per = (int)blockDim.x / 8, sub = threadIdx.x & 7;
-#pragma unroll
-  for (int p = 0; p < 2; p++) {
-    const int b = p * per + (int)(threadIdx.x >> 3);
-    if (b < nb) {
-      const int c0 = b * kQB + sub * 16;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        r.x[p][k] = *(const float4 *)(x + c0 + 4 * k);
-        if (PRO == PRO_NORM) r.w[p][k] = *(const float4 *)(w + c0 + 4 * k);
-      }
-    }
-  }
-}
-__device__ __forceinline__ float f4get(const float4 &v, int j) { return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w)); }
-
-template <int PRO>
-__device__ void act_build(const ActRegs &r, float eps, int cols, const ActView &a) {
-  const int nb = cols / kQB, per = (int)blockDim.x / 8, sub = threadIdx.x & 7;
-  float inv = 1.f;
-  if (PRO == PRO_NORM) {
-    float *bss = (float *)a.sums;   // block sums of squares; the sums area is free until the main loop
-#pragma unroll
-    for (int p = 0; p < 2; p++) {
-      const int b = p * per + (int)(threadIdx.x >> 3);
-      if (b < nb) {
-        float s = 0.f;
-#pragma unroll
-        for (int k = 0; k < 16; k++) { const float v = f4get(r.x[p][k >> 2], k & 3); s = __builtin_fmaf(v, v, s); }
-        s += dpp_f<kDppQuadXor1>(s);
-        s += dpp_f<kDppQuadXor2>(s);
-        s += dpp_f<kDppHalfMirror>(s);
-        if (sub == 0) bss[b] = s;
-      }
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-      float v[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) { const int b = (int)threadIdx.x + 64 * k; v[k] = b < nb ? bss[b] : 0.f; }
-      const float t = wave_sum((v[0] + v[1]) + (v[2] + v[3]));
-      if (threadIdx.x == 0) a.red[0] = 1.f / sqrtf(t / (float)cols + eps);
-    }
-    __syncthreads();
-    inv = a.red[0];
-  }
-#pragma unroll
-  for (int p = 0; p < 2; p++) {
-    const int b = p * per + (int)(threadIdx.x >> 3);
-    if (b < nb) {
-      const int c0 = b * kQB + sub * 16;
-      float v[16];
-#pragma unroll
-      for (int k = 0; k < 16; k++) {
-        v[k] = f4get(r.x[p][k >> 2], k & 3);
-        if (PRO == PRO_NORM) v[k] = v[k] * inv * f4get(r.w[p][k >> 2], k & 3);
-      }
-      float m = 0;
-#pragma unroll
-      for (int k = 0; k < 16; k++) m = fmaxf(m, fabsf(v[k]));
-      m = max8_f(m);
-      const float isx = m > 0 ? kActMax / m : 0.f;
-      if (sub == 0) a.bs[b] = m / kActMax;
-      uint32_t hw[4], lw[4]; int ls = 0, gs = 0;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        uint32_t hh = 0, ll = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const int q = (int)__builtin_rintf(v[4 * k + j] * isx);
-          hh |= (uint32_t)((q >> 8) & 0xff) << (8 * j);
-          ll |= (uint32_t)(q & 0xff) << (8 * j);
-          ls += q & 0xff; gs += q;
-        }
-        hw[k] = hh; lw[k] = ll;
-      }
-      *(uint4 *)(a.xh + c0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      *(uint4 *)(a.xl + c0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-      ls = sum8_i(ls);
-      if (sub == 0) a.lsum[b] = ls;
-      gs += dpp_i<kDppQuadXor1>(gs);
-      if ((sub & 1) == 0) a.gsum[c0 / 32] = gs;
-    }
-  }
-  __syncthreads();
-}
 
 // ------------------------------------------------------------------ streaming matvec
 // one 16-byte weight load (global_load_dwordx4)
@@ -495,24 +369,7 @@ hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStr
 }
 
 // ------------------------------------------------------------------ embedding, norm
-__global__ __launch_bounds__(kThreads) void k_embed(DMat e, const Ctl *ctl, float *x) {
-  int tok = ctl->tok;
-  tok = tok < 0 ? 0 : (tok >= e.rows ? e.rows - 1 : tok);
-  const int n = e.cols;
-  if (e.kind == MK_Q8) {
-    const int8_t *q = (const int8_t *)e.q + (size_t)tok * n; const float s = ((const float *)e.s)[tok];
-    for (int i = threadIdx.x; i < n; i += kThreads) x[i] = (float)q[i] * s;
-  } else if (e.kind == MK_Q4) {
-    const uint8_t *q = (const uint8_t *)e.q + (size_t)tok * (n / 2); const uint16_t *s = (const uint16_t *)e.s + (size_t)tok * (n / 32);
-    for (int i = threadIdx.x; i < n / 2; i += kThreads) {
-      const int g = i / 16, j = i % 16; const float sc = half_bits_to_float(s[g]); const uint8_t b = q[i];
-      x[32 * g + j] = (float)((int)(b & 15) - 8) * sc; x[32 * g + j + 16] = (float)((int)(b >> 4) - 8) * sc;
-    }
-  } else {
-    const float *q = (const float *)e.q + (size_t)tok * n;
-    for (int i = threadIdx.x; i < n; i += kThreads) x[i] = q[i];
-  }
-}
+__global__ __launch_bounds__(kThreads) void k_embed(DMat e, const Ctl *ctl, float *x) { embed_row(e, ctl->tok, x, threadIdx.x, kThreads); }
 hipError_t launch_embed(const DMat &embed, const Ctl *ctl, float *x, hipStream_t st) {
   hipLaunchKernelGGL(k_embed, dim3(1), dim3(kThreads), 0, st, embed, ctl, x);
   return hipGetLastError();

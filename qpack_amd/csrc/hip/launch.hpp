@@ -86,4 +86,28 @@ hipError_t launch_copy(const void *src, void *dst, size_t n16, hipStream_t st);
 
 hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st);
 
+// ---- batched prompt path (prefill.hip)
+// embeddings of B token ids (device array) into X[B][ldx]
+hipError_t launch_pf_embed(const DMat &embed, const int *toks, int B, float *X, int ldx, hipStream_t st);
+// per-token quantisation: X[t] (optionally RMSNorm(X[t]) * norm_w) -> int8 planes xh = q >> 8, xl = (q & 255) - 128
+// [B][ldq] and block scales xb [B][ldb]; the decode prologue's arithmetic
+struct PfQuantArgs {
+  const float *x; int ldx;
+  const float *norm_w; float eps;
+  int cols;
+  int8_t *xh, *xl; int ldq;
+  float *xb; int ldb;
+};
+hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st);
+// Y[t][r] = scale[r] * sum_b bs[t][b] * isum(r, t, b) (+ bias[r]), or Y[t][r] += that when resid; q8 weights
+struct GemmArgs {
+  const int8_t *w; const float *scale; int rows, cols;
+  const int8_t *xh, *xl; const float *xb; int ntok, ldq, ldb;
+  float *y; int ldy;
+  const float *bias;
+  int resid;
+};
+size_t gemm_lds_bytes();
+hipError_t launch_gemm(const GemmArgs &a, hipStream_t st);
+
 }  // namespace qph

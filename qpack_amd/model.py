@@ -153,3 +153,18 @@ def kernel_matvec(kind, q, scale, x):
                                   _fptr(y), sums.ctypes.data_as(C.POINTER(C.c_int32)), xq.ctypes.data_as(C.POINTER(C.c_int16)),
                                   _fptr(bs)))
     return y, sums, xq, bs
+
+
+def kernel_matmul(q, scale, X):
+    """the product's batched prefill kernels on one q8 matrix: Y[B, rows] = X[B, cols] W^T (qph_kernel_matmul)"""
+    from ._lib import QPH_Q8
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    scale = np.ascontiguousarray(scale, dtype=np.float32)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    rows, cols = q.shape
+    B = X.shape[0]
+    assert X.shape[1] == cols
+    Y = np.empty((B, rows), np.float32)
+    check(lib().qph_kernel_matmul(QPH_Q8, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols,
+                                  _fptr(X), B, _fptr(Y)))
+    return Y

@@ -60,3 +60,19 @@ def test_matvec_q4_exact_sums(rows, cols):
     comb = s.view(np.float16).astype(np.float32) * np.repeat(bs_o, 4)[None, :]
     mag = np.abs(comb * gs).sum(1)
     assert np.all(np.abs(y - y_o) <= 2e-6 * mag + 1e-30), float(np.max(np.abs(y - y_o) / (mag + 1e-30)))
+
+
+@pytest.mark.parametrize("rows,cols,B", [(1000, 4096, 200), (256, 896, 129), (300, 14336, 17), (7, 128, 1), (4864, 896, 64),
+                                         (130, 512, 300)])
+def test_matmul_q8_rows_equal_decode_arithmetic(rows, cols, B):
+    """batched prefill product (int8 MFMA, two activation planes): every token's row bit-identical to rows_q8 on that
+    token's quantised activation - the decode step's arithmetic; ragged row / token counts exercise the tile edges"""
+    rng = np.random.default_rng(rows * 13 + cols + B)
+    q, s = q8_matrix(rng, rows, cols)
+    X = np.stack([act_vector(rng, cols) * rng.uniform(0.1, 10) for _ in range(B)]).astype(np.float32)
+    X[B // 2] = 0                                   # an all-zero token
+    print(f"q8 matmul rows={rows} cols={cols} B={B}", flush=True)
+    Y = qa.kernel_matmul(q, s, X)
+    for b in range(B):
+        xq, bs = O.quant_act(X[b])
+        np.testing.assert_array_equal(Y[b], O.rows_q8(q, s, xq, bs), err_msg=f"token {b}")
