@@ -109,5 +109,24 @@ struct GemmArgs {
 };
 size_t gemm_lds_bytes();
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st);
+// token t of the batch at position p0 + t: RoPE on q [t][ldq] (in place) and k, fp16 k / v rows into the caches
+struct PfRopeArgs {
+  float *q; int ldq;
+  const float *k, *v; int ldk;
+  const float *cos_t, *sin_t;
+  uint16_t *kc, *vc;
+  int p0, nh, nkv, hd;
+};
+hipError_t launch_pf_rope(const PfRopeArgs &a, int B, hipStream_t st);
+// causal attention of the batch's (rotated) queries over cache positions [0, p0 + t] -> att [t][lda]
+struct PfAttnArgs {
+  const float *q; int ldq;
+  const uint16_t *kc, *vc;
+  float *att; int lda;
+  int ntok, p0, nh, nkv, hd;
+};
+hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st);
+// g = silu(g) * u over n floats
+hipError_t launch_pf_swiglu(float *g, const float *u, size_t n, hipStream_t st);
 
 }  // namespace qph

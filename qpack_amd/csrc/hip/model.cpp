@@ -89,9 +89,6 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     if (bq) { ly.bq = upload_f32(*bq, qd_); ly.bk = upload_f32(need(p + "bk"), kvd_); ly.bv = upload_f32(need(p + "bv"), kvd_); }
     layers_.push_back(ly);
   }
-  // attention split: enough (group, chunk) workgroups to cover the chip at full context
-  // splits of the context per kv group: the kernel activates ceil(T / 1024) of them (one workgroup per group below
-  // 1024 positions, no merge); the grid covers the full context
   // context splits per kv group: one per 64 positions, at most 64 (the kernel uses min(this, ceil(T / 64)))
   max_chunks_ = std::max(1, std::min(64, (ctx_ + 63) / 64));
   if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(64, atoi(e)));
@@ -112,6 +109,22 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   }
   ctl_ = (Ctl *)dalloc(sizeof(Ctl));
   out_tok_ = (int *)dalloc(4ull * (ctx_ + 1));
+  // batched prompt path: every layer matrix q8 (the int8 MFMA product); chunks of up to pf_cap_ tokens
+  pf_ok_ = true;
+  for (const Layer &ly : layers_)
+    for (const DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd}) pf_ok_ = pf_ok_ && m->kind == MK_Q8;
+  if (pf_ok_) {
+    pf_cap_ = std::min(kPfChunk, ctx_);
+    if (const char *e = getenv("QPH_PF_CHUNK")) pf_cap_ = std::max(1, std::min(pf_cap_, atoi(e)));   // test hook
+    const size_t B = pf_cap_, wide = std::max({d, qd_, ff});
+    pf_ldq_ = (int)(wide + 15) / 16 * 16;
+    pf_x_ = (float *)dalloc(4 * B * d); pf_q_ = (float *)dalloc(4 * B * qd_); pf_att_ = (float *)dalloc(4 * B * qd_);
+    pf_k_ = (float *)dalloc(4 * B * kvd_); pf_v_ = (float *)dalloc(4 * B * kvd_);
+    pf_g_ = (float *)dalloc(4 * B * ff); pf_u_ = (float *)dalloc(4 * B * ff);
+    pf_xh_ = (int8_t *)dalloc(B * pf_ldq_); pf_xl_ = (int8_t *)dalloc(B * pf_ldq_);
+    pf_xb_ = (float *)dalloc(4 * B * (pf_ldq_ / 128 + 1));
+    pf_tok_ = (int *)dalloc(4 * B);
+  }
   // RoPE tables in the reference's precision: inv_i = 1 / theta^(2i/hd) and angle pos * inv_i in double, cos / sin
   // rounded to float (model_llama.cpp:39, :173-175)
   const int half = hd / 2;
@@ -255,8 +268,73 @@ void HipLlama::prefill(const int *toks, int n, int want, float *out) {
   if (n <= 0) return;
   if (pos_ + n > ctx_) throw std::runtime_error("context window full (" + std::to_string(ctx_) + " tokens)");
   for (int i = 0; i < n; i++) if (toks[i] < 0 || toks[i] >= cfg_.vocab) throw std::runtime_error("token id out of range");
-  for (int i = 0; i < n; i++) step(toks[i], i + 1 == n ? want : 0, i + 1 == n ? out : nullptr);
-  if (!want) QPH_CK(hipStreamSynchronize(st_));
+  const bool force_steps = getenv("QPH_PREFILL_STEPS") != nullptr;   // test hook: the decode-step path
+  if (n == 1 || !pf_ok_ || force_steps) {   // one token (the reference's n == 1 case) or q4 layers: decode steps
+    for (int i = 0; i < n; i++) step(toks[i], i + 1 == n ? want : 0, i + 1 == n ? out : nullptr);
+    if (!want) QPH_CK(hipStreamSynchronize(st_));
+    return;
+  }
+  prefill_batched(toks, n);
+  if (want == 1) {
+    enqueue_head();
+    QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
+  } else if (want == 2) {
+    QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
+    QPH_CK(hipMemcpyAsync(hout_, xn_, 4ull * cfg_.hidden, hipMemcpyDeviceToHost, st_));
+  }
+  QPH_CK(hipStreamSynchronize(st_));
+  if (want && out) memcpy(out, hout_, 4ull * (want == 1 ? cfg_.vocab : cfg_.hidden));
+}
+
+// The prompt in chunks of up to pf_cap_ tokens, each layer as matrix products (model_llama.cpp:66-130): per chunk the
+// embeddings, then per layer RMSNorm + quantise -> q / k / v products (+ bias) -> RoPE and the fp16 cache rows ->
+// causal attention -> quantise -> wo product into the residual -> RMSNorm + quantise -> gate and up products ->
+// SwiGLU -> quantise -> down product into the residual.  Leaves the last token's hidden state in x_.
+void HipLlama::prefill_batched(const int *toks, int n) {
+  const int d = cfg_.hidden, ff = cfg_.ffn, nb_ld = pf_ldq_ / 128 + 1;
+  const float eps = cfg_.rms_eps;
+  auto quant = [&](int pro, const float *x, int ldx, const float *w, int cols, int B) {
+    PfQuantArgs a{}; a.x = x; a.ldx = ldx; a.norm_w = w; a.eps = eps; a.cols = cols;
+    a.xh = pf_xh_; a.xl = pf_xl_; a.ldq = pf_ldq_; a.xb = pf_xb_; a.ldb = nb_ld;
+    QPH_CK(launch_pf_quant(pro, a, B, st_));
+  };
+  auto gemm = [&](const DMat &m, float *y, int ldy, const float *bias, bool resid, int B) {
+    GemmArgs a{}; a.w = (const int8_t *)m.q; a.scale = (const float *)m.s; a.rows = m.rows; a.cols = m.cols;
+    a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld;
+    a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0;
+    QPH_CK(launch_gemm(a, st_));
+  };
+  int B = 0;
+  for (int s0 = 0; s0 < n; s0 += B) {
+    B = std::min(pf_cap_, n - s0);
+    const int p0 = pos_;
+    QPH_CK(hipMemcpyAsync(pf_tok_, toks + s0, 4ull * B, hipMemcpyHostToDevice, st_));
+    QPH_CK(launch_pf_embed(embed_, pf_tok_, B, pf_x_, d, st_));
+    for (int l = 0; l < cfg_.layers; l++) {
+      const Layer &ly = layers_[l];
+      uint16_t *kc = kc_ + (size_t)l * ctx_ * kvd_, *vc = vc_ + (size_t)l * ctx_ * kvd_;
+      quant(PRO_NORM, pf_x_, d, ly.an, d, B);
+      gemm(ly.wq, pf_q_, qd_, ly.bq, false, B);
+      gemm(ly.wk, pf_k_, kvd_, ly.bk, false, B);
+      gemm(ly.wv, pf_v_, kvd_, ly.bv, false, B);
+      PfRopeArgs r{}; r.q = pf_q_; r.ldq = qd_; r.k = pf_k_; r.v = pf_v_; r.ldk = kvd_; r.cos_t = cos_; r.sin_t = sin_;
+      r.kc = kc; r.vc = vc; r.p0 = p0; r.nh = cfg_.heads; r.nkv = cfg_.kv_heads; r.hd = cfg_.head_dim;
+      QPH_CK(launch_pf_rope(r, B, st_));
+      PfAttnArgs t{}; t.q = pf_q_; t.ldq = qd_; t.kc = kc; t.vc = vc; t.att = pf_att_; t.lda = qd_;
+      t.ntok = B; t.p0 = p0; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
+      QPH_CK(launch_pf_attn(t, st_));
+      quant(PRO_QUANT, pf_att_, qd_, nullptr, qd_, B);
+      gemm(ly.wo, pf_x_, d, nullptr, true, B);
+      quant(PRO_NORM, pf_x_, d, ly.fn, d, B);
+      gemm(ly.wg, pf_g_, ff, nullptr, false, B);
+      gemm(ly.wu, pf_u_, ff, nullptr, false, B);
+      QPH_CK(launch_pf_swiglu(pf_g_, pf_u_, (size_t)B * ff, st_));
+      quant(PRO_QUANT, pf_g_, ff, nullptr, ff, B);
+      gemm(ly.wd, pf_x_, d, nullptr, true, B);
+    }
+    pos_ += B;
+  }
+  QPH_CK(hipMemcpyAsync(x_, pf_x_ + (size_t)(B - 1) * d, 4ull * d, hipMemcpyDeviceToDevice, st_));
 }
 
 int HipLlama::greedy_run(int tok, int n, int *out) {

@@ -11,6 +11,10 @@
 //   - the float epilogue replays rows_q8's order per (row, token): acc = fma(bs[token][b], (float)isum_b, acc) over
 //     blocks in order, y = acc * scale[row]; every prompt token's projection is therefore bit-identical to a decode
 //     step's (the reference's own batched mm_q8 sums lane partials in another float order, within the logit tolerance).
+#include <math.h>
+
+#include <algorithm>
+
 #include "act.hpp"
 #include "launch.hpp"
 
@@ -191,6 +195,193 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t st) {
   if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
   const dim3 grid((a.ntok + kGN - 1) / kGN, (a.rows + kGM - 1) / kGM);
   hipLaunchKernelGGL(k_gemm_q8, grid, dim3(256), gemm_lds_bytes(), st, a);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ RoPE and the fp16 cache rows of a token batch
+// token t sits at position p0 + t: q heads and k groups rotate (rotate-half with the reference's contraction,
+// model_llama.cpp:86-90), k and v go to the layer's caches as fp16 (to_f16, kernels_x86.cpp:449-452)
+__global__ __launch_bounds__(256) void k_pf_rope(PfRopeArgs a) {
+  const int t = blockIdx.x, pos = a.p0 + t, half = a.hd / 2, kvd = a.nkv * a.hd;
+  const float *cs = a.cos_t + (size_t)pos * half, *sn = a.sin_t + (size_t)pos * half;
+  float *q = a.q + (size_t)t * a.ldq;
+  for (int e = threadIdx.x; e < a.nh * half; e += blockDim.x) {
+    const int h = e / half, i = e % half;
+    float *qh = q + h * a.hd; const float x0 = qh[i], x1 = qh[i + half];
+    qh[i] = __builtin_fmaf(x0, cs[i], -(x1 * sn[i]));
+    qh[i + half] = __builtin_fmaf(x1, cs[i], x0 * sn[i]);
+  }
+  const float *k = a.k + (size_t)t * a.ldk, *v = a.v + (size_t)t * a.ldk;
+  uint16_t *kr = a.kc + (size_t)pos * kvd, *vr = a.vc + (size_t)pos * kvd;
+  for (int e = threadIdx.x; e < a.nkv * half; e += blockDim.x) {
+    const int g = e / half, i = e % half;
+    const float x0 = k[g * a.hd + i], x1 = k[g * a.hd + i + half];
+    kr[g * a.hd + i] = float_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
+    kr[g * a.hd + i + half] = float_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
+  }
+  for (int e = threadIdx.x; e < kvd; e += blockDim.x) vr[e] = float_to_half_bits(v[e]);
+}
+hipError_t launch_pf_rope(const PfRopeArgs &a, int B, hipStream_t st) {
+  if (B <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_pf_rope, dim3(B), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ causal attention of a token batch (f16 MFMA)
+// Token t (position P = p0 + t) attends to cache positions [0, P] - the prompt path of model_llama.cpp:95-105.
+// A wave owns one unit = (16-token tile, query head); a workgroup's 4 waves share the kv group and stream its cache in
+// 32-position blocks through LDS (K as stored, V transposed), with an online softmax per token:
+//   scores  S^T[p][t] = K[p] . q[t] on v_mfma_f32_16x16x32_f16: A = K rows (exact fp16), B = q^T; q is fp32, so it
+//           enters as hi + lo halves (hi = f16(q), lo = f16(q - hi)) - two MFMAs, products exact, fp32 accumulation;
+//           scaled by 1/sqrt(hd) like the reference;
+//   values  O^T[d][t] += V^T[d][p] P^T[p][t], P split into hi + lo halves the same way; the C layout of S^T
+//           (lane l: token l % 16, positions 4 (l / 16) + i of each 16-block) is the B layout the value MFMA needs once
+//           its k index runs over those 8 positions, so P never leaves the registers;
+//   softmax each lane keeps its token's running max and sum (reduced over the 4 lanes holding that token).
+constexpr int kPfKB = 32;   // cache positions per block
+template <int HD>
+__global__ __launch_bounds__(256) void k_pf_attn(PfAttnArgs a) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int KS = HD + 8, VS = kPfKB + 8, DT = HD / 16;
+  __shared__ __align__(16) uint16_t ks[kPfKB * KS];
+  __shared__ __align__(16) uint16_t vt[HD * VS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+  const int g = blockIdx.y, rep = a.nh / a.nkv, kvd = a.nkv * HD;
+  const int ntiles = (a.ntok + 15) / 16, nunits = ntiles * rep;
+  const int u = blockIdx.x * 4 + wave;
+  const bool live = u < nunits;
+  const int tile = live ? u / rep : 0, head = g * rep + (live ? u % rep : 0);
+  const int t = tile * 16 + lr;                        // this lane's token
+  const bool tok_ok = live && t < a.ntok;
+  const int ptok = a.p0 + t;                           // its position: attends to [0, ptok]
+  const int wave_last = live ? a.p0 + min(tile * 16 + 15, a.ntok - 1) : -1;
+  // the workgroup streams up to its last live unit's last token
+  const int ulast = min(blockIdx.x * 4 + 3, nunits - 1);
+  const int wg_last = a.p0 + min((ulast / rep) * 16 + 15, a.ntok - 1);
+  const int nkb = wg_last / kPfKB + 1;
+
+  // q^T fragments: lane holds q[t][32 s + 8 lg + 0..7] as hi / lo halves
+  h8 qh[HD / 32], ql[HD / 32];
+  {
+    const float *qt = a.q + (size_t)(tok_ok ? t : 0) * a.ldq + head * HD;
+#pragma unroll
+    for (int s = 0; s < HD / 32; s++) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float x = tok_ok ? qt[32 * s + 8 * lg + j] : 0.f;
+        const _Float16 h = (_Float16)x;
+        qh[s][j] = h; ql[s][j] = (_Float16)(x - (float)h);
+      }
+    }
+  }
+  f4 o[DT];
+#pragma unroll
+  for (int d = 0; d < DT; d++) o[d] = (f4){0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  const float scl = 1.f / sqrtf((float)HD);
+  const uint16_t *kg = a.kc + g * HD, *vg = a.vc + g * HD;
+
+  for (int kb = 0; kb < nkb; kb++) {
+    const int pb = kb * kPfKB;
+    __syncthreads();   // the previous block's LDS reads are done
+    for (int c = tid; c < kPfKB * (HD / 8); c += 256) {
+      const int p = c / (HD / 8), d0 = (c % (HD / 8)) * 8, pos = pb + p;
+      uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
+      if (pos <= wg_last) {
+        kw = *(const uint4 *)(kg + (size_t)pos * kvd + d0);
+        vw = *(const uint4 *)(vg + (size_t)pos * kvd + d0);
+      }
+      *(uint4 *)(ks + p * KS + d0) = kw;
+      const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        vt[(d0 + 2 * j) * VS + p] = (uint16_t)(vv[j] & 0xffff);
+        vt[(d0 + 2 * j + 1) * VS + p] = (uint16_t)(vv[j] >> 16);
+      }
+    }
+    __syncthreads();
+    if (!live || pb > wave_last) continue;
+    // scores of the two 16-position halves
+    f4 sc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+      sc[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < HD / 32; s++) {
+        const h8 kf = *(const h8 *)(ks + (mt * 16 + lr) * KS + 32 * s + 8 * lg);
+        sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sc[mt], 0, 0, 0);
+        sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sc[mt], 0, 0, 0);
+      }
+    }
+    // online softmax for token t over positions pb + 16 mt + 4 lg + i
+    float sv[8], bm = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int p = pb + 16 * mt + 4 * lg + i;
+        const float x = (tok_ok && p <= ptok) ? sc[mt][i] * scl : -INFINITY;
+        sv[4 * mt + i] = x; bm = fmaxf(bm, x);
+      }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    const float corr = m == -INFINITY ? 0.f : exp_poly(m - mn);
+    float rs = 0.f;
+    h8 ph, pl;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float pv = sv[j] == -INFINITY ? 0.f : exp_poly(sv[j] - mn);
+      rs += pv;
+      const _Float16 h = (_Float16)pv;
+      ph[j] = h; pl[j] = (_Float16)(pv - (float)h);
+    }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    l = l * corr + rs;
+    m = mn;
+#pragma unroll
+    for (int d = 0; d < DT; d++) {
+      o[d] *= corr;
+      // V^T fragment: dim 16 d + lr, positions 4 lg + 0..3 and 16 + 4 lg + 0..3 (the k order of ph / pl)
+      const uint16_t *vr = vt + (16 * d + lr) * VS;
+      const uint2 v0 = *(const uint2 *)(vr + 4 * lg), v1 = *(const uint2 *)(vr + 16 + 4 * lg);
+      const uint4 vv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+      const h8 vf = __builtin_bit_cast(h8, vv);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
+    }
+  }
+  if (!tok_ok) return;
+  const float inv = 1.f / l;
+  float *out = a.att + (size_t)t * a.lda + head * HD;
+#pragma unroll
+  for (int d = 0; d < DT; d++)
+    *(float4 *)(out + 16 * d + 4 * lg) = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
+}
+hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st) {
+  if (a.ntok <= 0) return hipSuccess;
+  if (a.nh % a.nkv || (a.hd != 64 && a.hd != 128) || a.lda % 4) return hipErrorInvalidValue;
+  const int units = (a.ntok + 15) / 16 * (a.nh / a.nkv);
+  const dim3 grid((units + 3) / 4, a.nkv);
+  if (a.hd == 128) hipLaunchKernelGGL(k_pf_attn<128>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(k_pf_attn<64>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ SwiGLU of a token batch
+// g = silu(g) * u in place (silu_mul with exp256, kernels_x86.cpp:427-431, the decode epilogue's arithmetic)
+__global__ __launch_bounds__(256) void k_pf_swiglu(float *g, const float *u, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const float v = g[i];
+    g[i] = v / (1.f + exp_poly(0.f - v)) * u[i];
+  }
+}
+hipError_t launch_pf_swiglu(float *g, const float *u, size_t n, hipStream_t st) {
+  if (!n) return hipSuccess;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)blocks), dim3(256), 0, st, g, u, n);
   return hipGetLastError();
 }
 

@@ -81,3 +81,66 @@ def test_errors_are_reported(synth):
     assert len(gpu.greedy_run(1, 4)) == 0
     with pytest.raises(qa.QphError):
         qa.HipLlama.load("/nonexistent.qpack")
+
+
+def split_snapshot(snap, layers, kvd):
+    """the reference snapshot layout (model_llama.cpp:55-63): int32 pos, then per layer K rows then V rows (fp16)"""
+    pos = int(np.frombuffer(snap[:4], np.int32)[0])
+    body = np.frombuffer(snap[4:], np.float16).reshape(layers, 2, pos, kvd)
+    return pos, body[:, 0], body[:, 1]
+
+
+@pytest.mark.parametrize("cfg,chunk", [("mini", 48), ("mini128", 0), ("mini128", 37)])
+def test_batched_prefill(cfg, chunk, synth, monkeypatch):
+    """the int8-MFMA prompt path: chunked (ragged last chunk), a second prompt continuing at p0 > 0; logits and every
+    cache row against the oracle (within the tolerance / fp16 rounding), the greedy continuation identical, and the
+    layer-0 cache rows bit-identical to the GPU's own decode-step path (exact products, same quantised activations,
+    same RoPE and fp16 rounding; the decode path differs from the reference only by its RMSNorm summation order)"""
+    if chunk:
+        monkeypatch.setenv("QPH_PF_CHUNK", str(chunk))
+    path = synth(cfg)
+    gpu = qa.HipLlama.load(path, max_ctx=256)
+    orc = O.Oracle(path, max_ctx=256)
+    rng = np.random.default_rng(11)
+    toks = rng.integers(0, gpu.vocab(), 150).astype(np.int32)
+    prompts = ((0, 100), (100, 150))
+    for a, b in prompts:
+        print(f"{cfg} chunk {chunk}: prefill [{a}, {b})", flush=True)
+        lg = gpu.prefill(toks[a:b], 1)
+        for t in toks[a:b]:
+            lo = orc.step(int(t), 1)
+        err, ok = close(lg, lo)
+        assert ok, f"prefill [{a}, {b}) logits max|d| {err}"
+    shape = qa.CONFIGS[cfg]
+    kvd = shape.kv_heads * shape.head_dim
+    pos, kb, vb = split_snapshot(gpu.snapshot(), shape.layers, kvd)
+    assert pos == 150
+    ko, vo = orc.kv_cache()
+    for a, b in ((kb, ko[:, :150].view(np.float16)), (vb, vo[:, :150].view(np.float16))):
+        d = np.abs(a.astype(np.float32) - b.astype(np.float32))
+        assert d.max() <= 1e-2 + 2e-3 * np.abs(b.astype(np.float32)).max(), float(d.max())
+    g, o = gpu.greedy_run(int(np.argmax(lg)), 32), orc.greedy_run(int(np.argmax(lo)), 32)
+    np.testing.assert_array_equal(g, o)
+    gpu.reset()
+    monkeypatch.setenv("QPH_PREFILL_STEPS", "1")
+    for a, b in prompts:
+        gpu.prefill(toks[a:b], 0)
+    _, ks, vs = split_snapshot(gpu.snapshot(), shape.layers, kvd)
+    np.testing.assert_array_equal(kb[0].view(np.uint16), ks[0].view(np.uint16))
+    np.testing.assert_array_equal(vb[0].view(np.uint16), vs[0].view(np.uint16))
+    gpu.close(); orc.close()
+
+
+def test_batched_prefill_equals_step_path(synth, monkeypatch):
+    """the batched prompt path and the decode-step path agree (logits within the tolerance, same greedy pick)"""
+    path = synth("mini128")
+    toks = np.random.default_rng(5).integers(0, 2048, 90).astype(np.int32)
+    gpu = qa.HipLlama.load(path, max_ctx=128)
+    lb = gpu.prefill(toks, 1)
+    gpu.reset()
+    monkeypatch.setenv("QPH_PREFILL_STEPS", "1")
+    ls = gpu.prefill(toks, 1)
+    gpu.close()
+    err, ok = close(lb, ls)
+    assert ok, err
+    assert int(np.argmax(lb)) == int(np.argmax(ls))
