@@ -62,58 +62,83 @@ hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st)
 
 // ------------------------------------------------------------------ int8 MFMA matrix product (q8 weights)
 // Workgroup tile: 128 weight rows x 128 tokens, 4 waves in a 2 x 2 grid of 64 x 64, each a 4 x 4 grid of 16 x 16
-// MFMA tiles.  K advances one 128-column block at a time (two 64-deep MFMA steps per plane) through double-buffered
-// LDS: weight rows [128][144 B] (16 B padding per row keeps 16-lane fragment reads conflict-free), the two activation
-// planes [128][144 B] each, the block's row sums of W and the tokens' block scales.
+// MFMA tiles.  K advances one 128-column block at a time (two 64-deep MFMA steps per plane).  Operands reach LDS by
+// direct global->LDS loads (global_load_lds_dwordx4: a wave instruction lands 64 x 16 B contiguously) in a 3-stage
+// ring, so two blocks are always in flight while one is multiplied; no operand passes through registers.
+//   stage layout: weights, hi plane, lo plane, each [128 rows][128 B] with the 16-byte segments XOR-swizzled
+//   (physical segment = segment ^ (row & 7)) so 16-lane fragment reads hit distinct banks; then 128 block scales.
 //   fragments (v_mfma_i32_16x16x64_i8): lane l reads A = W[row l % 16][16 (l / 16) + 0..15] and B = plane[token l % 16]
 //   [16 (l / 16) + 0..15] - the same k set for A and B; C lane l holds rows 4 (l / 16) + 0..3 of token l % 16.
-constexpr int kGM = 128, kGN = 128, kGS = 144;
-size_t gemm_lds_bytes() { return (size_t)2 * (kGM + 2 * kGN) * kGS + 2 * kGM * 4 + 2 * kGN * 4; }
+//   sum(W) of each row over the block comes from one more MFMA against an all-ones B, landing in the C layout.
+// Rows or tokens past the end load a clamped (valid) address; their results are never stored.
+constexpr int kGM = 128, kGN = 128, kGStages = 3;
+constexpr int kGStage = 3 * 128 * 128 + 128 * 4;   // bytes per stage
+size_t gemm_lds_bytes() { return (size_t)kGStages * kGStage; }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+__device__ __forceinline__ void dma16(const void *g, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glb_void_t *)g, (lds_void_t *)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glb_void_t *)g, (lds_void_t *)lds_wave_base, 4, 0, 0);
+}
+// LDS reads of DMA-filled stages, kept out of the compiler's sight: it cannot tell which stage a DMA fills and would
+// otherwise wait for every load in flight before each read.  The results are only valid after lds_wait(), which takes
+// them as operands so no use can be scheduled before it.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const lds_void_t *)p; }
+__device__ __forceinline__ v4i lds_read16(uint32_t addr) {
+  v4i r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+__device__ __forceinline__ float lds_read4(uint32_t addr) {
+  float r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
 
 __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
   extern __shared__ __align__(16) char smem[];
-  int8_t *sw = (int8_t *)smem;                        // [2][kGM][kGS]
-  int8_t *sh = sw + 2 * kGM * kGS;                     // [2][kGN][kGS]
-  int8_t *sl = sh + 2 * kGN * kGS;                     // [2][kGN][kGS]
-  int *ssum = (int *)(sl + 2 * kGN * kGS);             // [2][kGM] row sums of W over the block
-  float *sbs = (float *)(ssum + 2 * kGM);              // [2][kGN] block scale of each token
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 1, wc = wave & 1, lr = lane & 15, lg = lane >> 4;
-  const int r0 = blockIdx.y * kGM, t0 = blockIdx.x * kGN;
+  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin (linear id % 8), so XCD x is given the
+  // contiguous x-th eighth of the tiles in row-major order (token tile fastest): a weight tile is reused from that
+  // XCD's L2 by the token tiles that need it
+  int r0, t0;
+  {
+    const int ntt = gridDim.x, n = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+    const int xcd = lin & 7, k = lin >> 3, base = n >> 3, rem = n & 7;
+    const int tile = xcd * base + min(xcd, rem) + k;
+    r0 = (tile / ntt) * kGM; t0 = (tile % ntt) * kGN;
+  }
   const int nb = a.cols / kQB;
 
-  // global -> registers: 4 x 16 B of weights, 4 x 16 B of each plane per thread (row / token tid / 8 + 32 j,
-  // 16-byte segment tid % 8), and one block scale (tid < 128)
-  v4i gw[4], gh[4], gl[4];
-  float gb = 0.f;
-  const int seg = tid & 7;
-  auto gload = [&](int kb) {
+  // this lane's DMA sources: instruction j of the wave covers tile rows 8 (4 wave + j) + lane / 8; the lane fetches the
+  // segment that belongs at physical position lane % 8 of that row
+  const int drow = lane >> 3, dseg = (lane & 7) ^ drow;
+  const int8_t *wsrc[4], *hsrc[4], *lsrc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int row = 8 * (4 * wave + j) + drow;
+    const int r = min(r0 + row, a.rows - 1), t = min(t0 + row, a.ntok - 1);
+    wsrc[j] = a.w + (size_t)r * a.cols + dseg * 16;
+    hsrc[j] = a.xh + (size_t)t * a.ldq + dseg * 16;
+    lsrc[j] = a.xl + (size_t)t * a.ldq + dseg * 16;
+  }
+  // block scales: waves w and w + 2 both fetch tokens 64 (w & 1) + lane (identical bytes to the same LDS slot), so
+  // every wave issues the same number of loads per stage
+  const float *bsrc = a.xb + (size_t)min(t0 + 64 * (wave & 1) + lane, a.ntok - 1) * a.ldb;
+  auto issue = [&](int kb) {
+    char *st = smem + (size_t)(kb % kGStages) * kGStage;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int row = (tid >> 3) + 32 * j;
-      const int r = r0 + row, t = t0 + row;
-      const v4i z = {0, 0, 0, 0};
-      gw[j] = r < a.rows ? *(const v4i *)(a.w + (size_t)r * a.cols + kb * kQB + seg * 16) : z;
-      gh[j] = t < a.ntok ? *(const v4i *)(a.xh + (size_t)t * a.ldq + kb * kQB + seg * 16) : z;
-      gl[j] = t < a.ntok ? *(const v4i *)(a.xl + (size_t)t * a.ldq + kb * kQB + seg * 16) : z;
+      const int rb = 8 * (4 * wave + j) * 128;
+      dma16(wsrc[j] + kb * kQB, st + rb);
+      dma16(hsrc[j] + kb * kQB, st + 128 * 128 + rb);
+      dma16(lsrc[j] + kb * kQB, st + 2 * 128 * 128 + rb);
     }
-    if (tid < kGN) gb = t0 + tid < a.ntok ? a.xb[(size_t)(t0 + tid) * a.ldb + kb] : 0.f;
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int row = (tid >> 3) + 32 * j;
-      *(v4i *)(sw + ((size_t)buf * kGM + row) * kGS + seg * 16) = gw[j];
-      *(v4i *)(sh + ((size_t)buf * kGN + row) * kGS + seg * 16) = gh[j];
-      *(v4i *)(sl + ((size_t)buf * kGN + row) * kGS + seg * 16) = gl[j];
-      int s = __builtin_amdgcn_sdot4(gw[j].x, 0x01010101, 0, false);
-      s = __builtin_amdgcn_sdot4(gw[j].y, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(gw[j].z, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(gw[j].w, 0x01010101, s, false);
-      s = sum8_i(s);   // the 8 segments of the row sit in 8 consecutive lanes
-      if (seg == 0) ssum[buf * kGM + row] = s;
-    }
-    if (tid < kGN) sbs[buf * kGN + tid] = gb;
+    dma4(bsrc + kb, st + 3 * 128 * 128 + 64 * 4 * (wave & 1));
   };
 
   float acc[4][4][4];
@@ -123,53 +148,72 @@ __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
     for (int ni = 0; ni < 4; ni++)
 #pragma unroll
       for (int i = 0; i < 4; i++) acc[mi][ni][i] = 0.f;
+  const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  issue(0);
+  if (nb > 1) issue(1);
   for (int kb = 0; kb < nb; kb++) {
-    const int buf = kb & 1;
-    if (kb + 1 < nb) gload(kb + 1);
-    v4i ch[4][4], cl[4][4];
+    // this wave's loads of block kb have landed (block kb + 1's 13 may still be in flight), then everyone's
+    if (kb + 1 < nb) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (kb + 2 < nb) issue(kb + 2);   // into the stage everyone finished reading in the previous iteration
+    const uint32_t st = lds_addr(smem + (size_t)(kb % kGStages) * kGStage);
+    const uint32_t sw = st, sh = st + 128 * 128, sl = st + 2 * 128 * 128, sbs = st + 3 * 128 * 128;
+    v4i ch[4][4], cl[4][4], cw[4];
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int mi = 0; mi < 4; mi++) {
+      cw[mi] = (v4i){0, 0, 0, 0};
 #pragma unroll
       for (int ni = 0; ni < 4; ni++) { ch[mi][ni] = (v4i){0, 0, 0, 0}; cl[mi][ni] = (v4i){0, 0, 0, 0}; }
+    }
+    float bsc[4];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      v4i A[4];
+      const int seg = ks * 4 + lg;
+      v4i A[4], BH[4], BL[4];
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-        A[mi] = *(const v4i *)(sw + ((size_t)buf * kGM + wr * 64 + mi * 16 + lr) * kGS + ks * 64 + lg * 16);
+      for (int mi = 0; mi < 4; mi++) {
+        const int row = wr * 64 + mi * 16 + lr;
+        A[mi] = lds_read16(sw + row * 128 + ((seg ^ (row & 7)) << 4));
+      }
 #pragma unroll
       for (int ni = 0; ni < 4; ni++) {
-        const size_t o = ((size_t)buf * kGN + wc * 64 + ni * 16 + lr) * kGS + ks * 64 + lg * 16;
-        const v4i bh = *(const v4i *)(sh + o), bl = *(const v4i *)(sl + o);
+        const int tok = wc * 64 + ni * 16 + lr;
+        const uint32_t o = tok * 128 + ((seg ^ (tok & 7)) << 4);
+        BH[ni] = lds_read16(sh + o); BL[ni] = lds_read16(sl + o);
+      }
+      if (ks == 1) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ni++) bsc[ni] = lds_read4(sbs + 4 * (wc * 64 + ni * 16 + lr));
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BH[2]), "+v"(BH[3]),
+                       "+v"(BL[0]), "+v"(BL[1]), "+v"(BL[2]), "+v"(BL[3]), "+v"(bsc[0]), "+v"(bsc[1]), "+v"(bsc[2]), "+v"(bsc[3]));
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BH[2]), "+v"(BH[3]),
+                       "+v"(BL[0]), "+v"(BL[1]), "+v"(BL[2]), "+v"(BL[3]));
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++) cw[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], ones, cw[mi], 0, 0, 0);
+#pragma unroll
+      for (int ni = 0; ni < 4; ni++)
 #pragma unroll
         for (int mi = 0; mi < 4; mi++) {
-          ch[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], bh, ch[mi][ni], 0, 0, 0);
-          cl[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], bl, cl[mi][ni], 0, 0, 0);
+          ch[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BH[ni], ch[mi][ni], 0, 0, 0);
+          cl[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BL[ni], cl[mi][ni], 0, 0, 0);
         }
-      }
     }
     // the block's exact int32 sums, then rows_q8's fma step
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++) {
-      int ws[4];
+    for (int ni = 0; ni < 4; ni++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) ws[i] = 128 * ssum[buf * kGM + wr * 64 + mi * 16 + 4 * lg + i];
-#pragma unroll
-      for (int ni = 0; ni < 4; ni++) {
-        const float b = sbs[buf * kGN + wc * 64 + ni * 16 + lr];
+      for (int mi = 0; mi < 4; mi++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int isum = ch[mi][ni][i] * 256 + cl[mi][ni][i] + ws[i];
-          acc[mi][ni][i] = __builtin_fmaf(b, (float)isum, acc[mi][ni][i]);
+          const int isum = ch[mi][ni][i] * 256 + cl[mi][ni][i] + 128 * cw[mi][i];
+          acc[mi][ni][i] = __builtin_fmaf(bsc[ni], (float)isum, acc[mi][ni][i]);
         }
-      }
-    }
-    if (kb + 1 < nb) sstore(buf ^ 1);
-    __syncthreads();
   }
   // y = acc * scale (+ bias), or y += (residual stream)
 #pragma unroll
