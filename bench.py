@@ -95,6 +95,61 @@ def read_traffic():
     return None
 
 
+def kv_fill_snapshot(shape, T, seed):
+    """a snapshot in the reference layout (model_llama.cpp:55-63) whose fp16 K / V rows are N(0, 1), as BASELINE's C5
+    fills its 16K context"""
+    kvd = shape.kv_heads * shape.head_dim
+    rng = np.random.default_rng(seed)
+    parts = [np.int32(T).tobytes()]
+    for _ in range(shape.layers):
+        for _ in range(2):
+            parts.append(rng.standard_normal((T, kvd), dtype=np.float32).astype(np.float16).tobytes())
+    return b"".join(parts)
+
+
+def other_config(name, seed, steps_override=None):
+    """decode tokens/s of another BASELINE config on its own workload: C1 / C2 prompt + greedy tokens (prompt through
+    the product's prefill), C5 greedy tokens after restoring a 16384-position N(0, 1) context"""
+    import qpack_amd as qa
+    shape = qa.CONFIGS[name]
+    runs = {"c1": (32, 128, None), "c2": (512, 256, None), "c5": (0, 128, 16384)}
+    prompt, steps, restore = runs[name]
+    steps = steps_override or steps
+    tmpdir = tempfile.mkdtemp(prefix="qpack_bench_")
+    path = os.path.join(tmpdir, name + ".qpack")
+    try:
+        qa.write_synthetic(name, path, seed=seed, threads=min(16, os.cpu_count() or 8))
+        ctx = max(prompt, restore or 0) + steps + 16
+        m = qa.HipLlama.load(path, max_ctx=ctx)
+        rng = np.random.default_rng(seed)
+        if restore:
+            m.restore(kv_fill_snapshot(shape, restore, seed))
+            tok = 1
+        else:
+            lg = m.prefill(rng.integers(0, shape.vocab, prompt).astype(np.int32), 1)
+            tok = int(np.argmax(lg))
+        T0 = m.pos()
+        tok = int(m.greedy_run(tok, 4)[-1])   # warm-up
+        T1 = m.pos()
+        ms = m.time_greedy(tok, steps)
+        att_ms, att_b = m.time_kernel(5, 50)
+        m.close()
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+        os.rmdir(tmpdir)
+    T2 = T1 + steps
+    sb = step_bytes(shape, (T1 + 1 + T2) / 2)
+    gbs = sb / (ms / 1e3 / steps) / 1e9
+    kind = "q4m" if shape.q4m_alt else ("q4" if shape.q4 else "q8")
+    ctx_desc = f"restored N(0,1) fp16 context of {restore}" if restore else f"{prompt}-token prompt"
+    return dict(tokens_per_s=round(steps / (ms / 1e3), 1), ms_per_token=round(ms / steps, 4),
+                hbm_pct_of_peak=round(100 * gbs / HBM_PEAK_GBS, 2), bytes_per_token=round(sb),
+                attention_us=round(att_ms * 1e3, 2),
+                workload=f"{name} ({kind}, {shape.layers} layers, hidden {shape.hidden}): {ctx_desc}, 4 warm-up + {steps} "
+                         f"timed greedy tokens (context {T1}..{T2})")
+
+
 def cpu_baseline(path, threads, n_prompt=16, n_gen=16, reps=2):
     """qpack-bench --row protocol (tools/qpack-bench.cpp:35-47) on the reference engine: reset, prefill(np), ng x step,
     best of reps"""
@@ -132,6 +187,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--configs", default="c1,c2,c5",
+                    help="other BASELINE configs whose decode rate is added to the line ('' for none)")
     ap.add_argument("--profile", action="store_true",
                     help="launch kernels one by one (no HIP graphs) so a profiler sees every dispatch, and run a "
                          "calibration copy of known size for the byte counters")
@@ -229,6 +286,13 @@ def main():
         log(f"prefill {T} tokens: {pt * 1e3:.1f} ms -> {T / pt:.0f} tok/s, {gemm_ops / pt / 1e12:.1f} algorithmic int8 TOP/s")
     m.close()
 
+    others_cfg = {}
+    for name in [c for c in a.configs.split(",") if c]:
+        t = time.time()
+        others_cfg[name] = other_config(name, a.seed)
+        log(f"{name}: {others_cfg[name]['tokens_per_s']} tok/s, {others_cfg[name]['hbm_pct_of_peak']}% of HBM peak "
+            f"({time.time() - t:.1f}s)")
+
     cpu = None
     if not a.no_cpu_baseline:
         import oracle
@@ -260,6 +324,7 @@ def main():
                      "bytes_per_launch": round(kbytes), "us_per_launch": round(kms * 1e3, 2)},
         "kernels": others,
         "prefill": prefill,
+        "other_configs": others_cfg,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -269,6 +269,10 @@ class Oracle:
     def reset(self):
         olib().or_reset(self.m)
 
+    def set_pos(self, pos):
+        if olib().or_set_pos(self.m, int(pos)):
+            raise RuntimeError("oracle set_pos: out of range")
+
     def step(self, tok, want=1):
         out = np.empty(self.cfg.V if want == 1 else self.cfg.d, np.float32) if want else None
         if olib().or_step(self.m, int(tok), want, _f(out) if out is not None else None):

@@ -590,13 +590,15 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
     }
     if (S == 1) a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
     else {
-      // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback
-      float *pp = a.part + ((size_t)(g * REP + j) * gridDim.y + s) * (HD + 2);
+      // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback.
+      // Layout: unnormalised outputs [nh][splits][HD], then (max, sum) pairs [nh][splits][2]
+      const size_t hs = (size_t)(g * REP + j) * gridDim.y + s;
       if (i == 0) {
-        __hip_atomic_store(pp, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(pp + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float *ml = a.part + (size_t)a.nh * gridDim.y * HD + 2 * hs;
+        __hip_atomic_store(ml, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ml + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __hip_atomic_store(pp + 2 + i, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.part + hs * HD + i, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (S == 1) return;
@@ -611,14 +613,15 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   __syncthreads();
   if (!last) return;
   // the last split merges, in split order (model_llama.cpp:160-165): per head the max M, the weights
-  // f_c = exp(m_c - M) and L = sum_c l_c f_c, then O = sum_c f_c o_c; partials read with coherent (sc1) loads
-  __shared__ float fw[REP][kAttnMaxSplits], lw[REP][kAttnMaxSplits], linv[REP];
-  const float *pg = a.part + (size_t)g * REP * gridDim.y * (HD + 2);
+  // f_c = exp(m_c - M) and L = sum_c l_c f_c, then O = sum_c f_c o_c.  One agent-scope acquire (an L2 invalidate: the
+  // partials were written through by other workgroups), then one thread per (head, 4 dims) streams its column of
+  // partials 16 splits at a time.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __shared__ float fw[REP][kAttnMaxSplits], linv[REP];
+  const float *ml = a.part + (size_t)a.nh * gridDim.y * HD + 2 * (size_t)g * REP * gridDim.y;
   for (int e = threadIdx.x; e < REP * S; e += blockDim.x) {
     const int j = e / S, c = e % S;
-    const float *pc = pg + ((size_t)j * gridDim.y + c) * (HD + 2);
-    fw[j][c] = __hip_atomic_load(pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    lw[j][c] = __hip_atomic_load(pc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    fw[j][c] = ml[2 * ((size_t)j * gridDim.y + c)];
   }
   __syncthreads();
   if (threadIdx.x < REP) {
@@ -628,26 +631,30 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
     float L = 0.f;
     for (int c = 0; c < S; c++) {
       const float f = fw[j][c] == -INFINITY ? 0.f : expf(fw[j][c] - M);
-      L = __builtin_fmaf(lw[j][c], f, L);
+      L = __builtin_fmaf(ml[2 * ((size_t)j * gridDim.y + c) + 1], f, L);
       fw[j][c] = f;
     }
     linv[j] = 1.f / L;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
-    const int j = e / HD, i = e % HD;
-    const float *ph = pg + (size_t)j * gridDim.y * (HD + 2) + 2 + i;
-    float O = 0.f;
-    for (int c0 = 0; c0 < S; c0 += 8) {   // 8 independent loads in flight, then the ordered fma chain
-      float v[8];
+  for (int e = threadIdx.x; e < REP * HD / 4; e += blockDim.x) {
+    const int j = e / (HD / 4), i4 = e % (HD / 4);
+    const float4 *ph = (const float4 *)(a.part + ((size_t)(g * REP + j) * gridDim.y) * HD) + i4;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = 0; c0 < S; c0 += 16) {   // 16 independent loads in flight, then the ordered fma chains
+      float4 v[16];
 #pragma unroll
-      for (int k = 0; k < 8; k++)
-        v[k] = c0 + k < S ? __hip_atomic_load(ph + (size_t)(c0 + k) * (HD + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      for (int k = 0; k < 16; k++) v[k] = c0 + k < S ? ph[(size_t)(c0 + k) * (HD / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int k = 0; k < 8; k++)
-        if (c0 + k < S) O = __builtin_fmaf(fw[j][c0 + k], v[k], O);
+      for (int k = 0; k < 16; k++)
+        if (c0 + k < S) {
+          const float f = fw[j][c0 + k];
+          O.x = __builtin_fmaf(f, v[k].x, O.x); O.y = __builtin_fmaf(f, v[k].y, O.y);
+          O.z = __builtin_fmaf(f, v[k].z, O.z); O.w = __builtin_fmaf(f, v[k].w, O.w);
+        }
     }
-    a.att[(size_t)(g * REP + j) * HD + i] = O * linv[j];
+    const float li = linv[j];
+    *(float4 *)(a.att + (size_t)(g * REP + j) * HD + 4 * i4) = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
   }
 }
 

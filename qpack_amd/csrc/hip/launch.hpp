@@ -71,7 +71,7 @@ struct AttnArgs {
   uint16_t *kc, *vc;           // this layer's fp16 caches [ctx][kvd]
   const float *cos_t, *sin_t;  // RoPE tables [ctx][hd / 2]
   const Ctl *ctl;
-  float *part;                 // [nh][splits][hd + 2]: max, sum, unnormalised output of every split
+  float *part;                 // unnormalised outputs [nh][splits][hd], then (max, sum) [nh][splits][2]
   int *counters;               // [nkv] zero; each group's last split resets its counter
   float *att;                  // output [nh * hd]
   int nh, nkv, hd;

@@ -144,3 +144,39 @@ def test_batched_prefill_equals_step_path(synth, monkeypatch):
     err, ok = close(lb, ls)
     assert ok, err
     assert int(np.argmax(lb)) == int(np.argmax(ls))
+
+
+def kv_snapshot(k, v):
+    """a snapshot in the reference layout (model_llama.cpp:55-63) from per-layer fp16 K / V rows [L][pos][kvd]"""
+    pos = k.shape[1]
+    parts = [np.int32(pos).tobytes()]
+    for layer in range(k.shape[0]):
+        parts += [np.ascontiguousarray(k[layer]).tobytes(), np.ascontiguousarray(v[layer]).tobytes()]
+    return b"".join(parts)
+
+
+@pytest.mark.parametrize("cfg,T", [("mini_q4m", 3000), ("mini128", 2500)])
+def test_long_context_restore(cfg, T, synth):
+    """decode at a long restored context (N(0,1) fp16 keys / values, as BASELINE's C5 fills its 16K cache): many
+    context splits per kv group and their merge; logits against the oracle holding the same cache, then greedy"""
+    path = synth(cfg)
+    shape = qa.CONFIGS[cfg]
+    kvd = shape.kv_heads * shape.head_dim
+    rng = np.random.default_rng(T)
+    k = rng.standard_normal((shape.layers, T, kvd)).astype(np.float16)
+    v = rng.standard_normal((shape.layers, T, kvd)).astype(np.float16)
+    gpu = qa.HipLlama.load(path, max_ctx=T + 64)
+    gpu.restore(kv_snapshot(k, v))
+    assert gpu.pos() == T
+    orc = O.Oracle(path, max_ctx=T + 64)
+    ko, vo = orc.kv_cache()
+    ko[:, :T] = k.view(np.uint16); vo[:, :T] = v.view(np.uint16)
+    orc.set_pos(T)
+    print(f"{cfg}: context {T}", flush=True)
+    for t in (5, 17, 230):
+        lg, lo = gpu.step(t, 1), orc.step(t, 1)
+        err, ok = close(lg, lo)
+        assert ok, f"step logits max|d| {err}"
+    g, o = gpu.greedy_run(int(np.argmax(lg)), 16), orc.greedy_run(int(np.argmax(lo)), 16)
+    np.testing.assert_array_equal(g, o)
+    gpu.close(); orc.close()
