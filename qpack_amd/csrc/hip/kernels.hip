@@ -391,11 +391,12 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 }
 
 // ------------------------------------------------------------------ decode attention (split-K over the context)
-// grid (kv group g, split s), 4 waves (one per SIMD).  The number of active splits follows the context,
-// S_eff = min(grid.y, ceil(T / 64)): the work of a token's attention is small, so it is spread over as many CUs as the
-// context allows instead of queueing 16 waves on one CU's SIMDs; below 65 positions one workgroup per kv group does
-// everything and no cross-workgroup merge is needed.  Split s takes positions [s T / S_eff, (s + 1) T / S_eff); each wave a contiguous sub-range, streamed straight
-// from HBM 16 positions at a time with the next block's K and V loads in flight (double-buffered registers).
+// grid (kv group g, split s), 16 waves (8 for wide GQA groups).  The number of active splits follows the context: while
+// every wave needs at most one 16-position block (T <= 16 x waves) one workgroup per kv group does everything and no
+// cross-workgroup merge is needed; beyond that S_eff = min(grid.y, ceil(T / 64)) splits, the waves of a split taking
+// contiguous runs of whole blocks - a mid-size context spreads over many CUs, a 16K context keeps all 16 waves busy.  Split s takes positions [s T / S_eff,
+// (s + 1) T / S_eff); each wave a contiguous sub-range, streamed straight from HBM 16 positions at a time with the next
+// block's K and V loads in flight (double-buffered registers).
 // The workgroup applies RoPE to its rep query heads (rotate-half with the reference's contraction
 // a' = fma(a, cos, -(b sin)), b' = fma(b, cos, a sin), model_llama.cpp:176); the workgroup owning the current position
 // writes the rotated k and the v row into the cache as fp16 (round to nearest even, to_f16).
@@ -406,7 +407,7 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 // counter, which that workgroup resets) merges the split partials in split order - the merge of model_llama.cpp:160-165:
 // M = max m, L = sum l e^(m - M), out = sum o e^(m - M) * (1 / L).
 constexpr int kAttnMaxSplits = 64;
-constexpr int kSplitPos = 64;   // fewest positions per context split (4 waves x one 16-position block)
+// positions per context split: one 16-position block per wave of the workgroup
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // sum / max over aligned rows of 16 lanes (every lane of the row gets the result)
@@ -444,9 +445,9 @@ __device__ __forceinline__ void kv_load(const uint16_t *kc, const uint16_t *vc, 
   }
 }
 
-// waves per attention workgroup: one per SIMD, so a workgroup's waves never queue behind each other on one SIMD;
-// the context is split over workgroups instead
-constexpr int attn_waves(int, int) { return 4; }
+// waves per attention workgroup: 16 (four per SIMD, so the latency of one wave's LDS / DPP / exp chains is covered by
+// the others), 8 where 16 would not fit the registers (wide GQA groups)
+constexpr int attn_waves(int hd, int rep) { return (hd == 64 && rep >= 7) || (hd == 128 && rep >= 5) ? 8 : 16; }
 template <int HD, int REP>
 __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs a) {
   using B = KvBlock<HD>;
@@ -459,12 +460,16 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   __shared__ __align__(16) uint16_t vnew[HD];
   __shared__ int last;
   const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
-  const int S = min((int)gridDim.y, (T + kSplitPos - 1) / kSplitPos);
+  // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
+  const int S = T <= 16 * NW ? 1 : min((int)gridDim.y, (T + 63) / 64);
   if (s >= S) return;
   const int kvd = a.nkv * HD;
   const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int n = t1 - t0, wt0 = t0 + (int)((int64_t)wave * n / NW), wt1 = t0 + (int)((int64_t)(wave + 1) * n / NW);
+  // waves take contiguous runs of whole 16-position blocks (waves without a block idle)
+  const int nblk = (t1 - t0 + 15) / 16, bpw = (nblk + NW - 1) / NW;
+  const int wt0 = min(t1, t0 + 16 * wave * bpw), wt1 = min(t1, t0 + 16 * (wave + 1) * bpw);
+  const int nact = (nblk + bpw - 1) / bpw;   // waves holding positions (the wave merge reads only theirs)
   // this wave's first block goes out before anything else
   KvBlock<HD> cur, nxt;
   if (wt0 < wt1) kv_load<HD>(a.kc, a.vc, kvd, g, wt0, wt1, lane, cur);
@@ -582,9 +587,9 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
     const int j = e / HD, i = e % HD;
     float M = wm[0][j];
-    for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w][j]);
+    for (int w = 1; w < nact; w++) M = fmaxf(M, wm[w][j]);
     float L = 0.f, O = 0.f;
-    for (int w = 0; w < NW; w++) {
+    for (int w = 0; w < nact; w++) {
       const float f = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);
       L = __builtin_fmaf(wl[w][j], f, L); O = __builtin_fmaf(f, ored[w][j][i], O);
     }
@@ -612,46 +617,52 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   }
   __syncthreads();
   if (!last) return;
-  // the last split merges, in split order (model_llama.cpp:160-165): per head the max M, the weights
-  // f_c = exp(m_c - M) and L = sum_c l_c f_c, then O = sum_c f_c o_c.  One agent-scope acquire (an L2 invalidate: the
-  // partials were written through by other workgroups), then one thread per (head, 4 dims) streams its column of
-  // partials 16 splits at a time.
+  // the last split merges the S partials (model_llama.cpp:160-165: M = max m_c, f_c = exp(m_c - M),
+  // L = sum l_c f_c, O = sum f_c o_c / L).  One agent-scope acquire (an L2 invalidate: the partials were written
+  // through by other workgroups); wave j reduces head j's (m, l) over the splits, one per lane; then P threads share
+  // each (head, 4 dims) column of partials, split c going to thread c mod P, and add their sums in LDS.
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   __shared__ float fw[REP][kAttnMaxSplits], linv[REP];
+  __shared__ float4 opart[NW * 64];
   const float *ml = a.part + (size_t)a.nh * gridDim.y * HD + 2 * (size_t)g * REP * gridDim.y;
-  for (int e = threadIdx.x; e < REP * S; e += blockDim.x) {
-    const int j = e / S, c = e % S;
-    fw[j][c] = ml[2 * ((size_t)j * gridDim.y + c)];
+  if (wave < REP) {
+    const int j = wave;
+    const bool on = lane < S;
+    const float2 v = on ? *(const float2 *)(ml + 2 * ((size_t)j * gridDim.y + lane)) : make_float2(-INFINITY, 0.f);
+    const float M = wave_max(v.x);
+    const float f = on && v.x != -INFINITY ? expf(v.x - M) : 0.f;
+    const float L = wave_sum(v.y * f);
+    if (on) fw[j][lane] = f;
+    if (lane == 0) linv[j] = 1.f / L;
   }
   __syncthreads();
-  if (threadIdx.x < REP) {
-    const int j = threadIdx.x;
-    float M = -INFINITY;
-    for (int c = 0; c < S; c++) M = fmaxf(M, fw[j][c]);
-    float L = 0.f;
-    for (int c = 0; c < S; c++) {
-      const float f = fw[j][c] == -INFINITY ? 0.f : expf(fw[j][c] - M);
-      L = __builtin_fmaf(ml[2 * ((size_t)j * gridDim.y + c) + 1], f, L);
-      fw[j][c] = f;
-    }
-    linv[j] = 1.f / L;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < REP * HD / 4; e += blockDim.x) {
+  constexpr int NC = REP * HD / 4;                            // output columns of 4 dims
+  constexpr int P = NW * 64 / NC >= 4 ? 4 : (NW * 64 / NC >= 2 ? 2 : 1);
+  const int e = threadIdx.x % NC, part = threadIdx.x / NC;
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (part < P) {
     const int j = e / (HD / 4), i4 = e % (HD / 4);
     const float4 *ph = (const float4 *)(a.part + ((size_t)(g * REP + j) * gridDim.y) * HD) + i4;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c0 = 0; c0 < S; c0 += 16) {   // 16 independent loads in flight, then the ordered fma chains
-      float4 v[16];
+    for (int c0 = part; c0 < S; c0 += 8 * P) {   // 8 independent loads in flight
+      float4 v[8];
 #pragma unroll
-      for (int k = 0; k < 16; k++) v[k] = c0 + k < S ? ph[(size_t)(c0 + k) * (HD / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int k = 0; k < 8; k++) v[k] = c0 + k * P < S ? ph[(size_t)(c0 + k * P) * (HD / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int k = 0; k < 16; k++)
-        if (c0 + k < S) {
-          const float f = fw[j][c0 + k];
+      for (int k = 0; k < 8; k++)
+        if (c0 + k * P < S) {
+          const float f = fw[j][c0 + k * P];
           O.x = __builtin_fmaf(f, v[k].x, O.x); O.y = __builtin_fmaf(f, v[k].y, O.y);
           O.z = __builtin_fmaf(f, v[k].z, O.z); O.w = __builtin_fmaf(f, v[k].w, O.w);
         }
+    }
+    opart[threadIdx.x] = O;
+  }
+  __syncthreads();
+  if (threadIdx.x < NC) {
+    const int j = e / (HD / 4), i4 = e % (HD / 4);
+    for (int q = 1; q < P; q++) {
+      const float4 t = opart[q * NC + threadIdx.x];
+      O.x += t.x; O.y += t.y; O.z += t.z; O.w += t.w;
     }
     const float li = linv[j];
     *(float4 *)(a.att + (size_t)(g * REP + j) * HD + 4 * i4) = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);

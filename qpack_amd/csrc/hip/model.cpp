@@ -89,7 +89,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     if (bq) { ly.bq = upload_f32(*bq, qd_); ly.bk = upload_f32(need(p + "bk"), kvd_); ly.bv = upload_f32(need(p + "bv"), kvd_); }
     layers_.push_back(ly);
   }
-  // context splits per kv group: one per 64 positions, at most 64 (the kernel uses min(this, ceil(T / 64)))
+  // context splits per kv group: one per 64 positions of the full context, at most 64 (the kernel activates
+  // min(this, ceil(T / 64)) of them beyond one workgroup's reach)
   max_chunks_ = std::max(1, std::min(64, (ctx_ + 63) / 64));
   if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(64, atoi(e)));
   counters_ = (int *)dalloc(4ull * nkv);
