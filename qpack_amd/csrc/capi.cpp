@@ -224,7 +224,10 @@ int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int 
       hck(hipMemcpy(dx, X, 4ull * B * cols, hipMemcpyHostToDevice), "upload X");
       qph::PfQuantArgs qa{}; qa.x = dx; qa.ldx = cols; qa.cols = cols; qa.xh = dxh; qa.xl = dxl; qa.ldq = cols; qa.xb = dxb; qa.ldb = nb;
       hck(qph::launch_pf_quant(qph::PRO_QUANT, qa, B, nullptr), "launch quant");
+      int *dws = (int *)alloc(4ull * rows * nb);
+      hck(qph::launch_rowsum_q8((const int8_t *)dq, rows, cols, dws, nullptr), "launch rowsum");
       qph::GemmArgs ga{}; ga.w = (const int8_t *)dq; ga.scale = (const float *)ds; ga.rows = rows; ga.cols = cols;
+      ga.wsum = dws; ga.ldw = nb;
       ga.xh = dxh; ga.xl = dxl; ga.xb = dxb; ga.ntok = B; ga.ldq = cols; ga.ldb = nb; ga.y = dy; ga.ldy = rows;
       hck(qph::launch_gemm(ga, nullptr), "launch gemm");
       hck(hipDeviceSynchronize(), "matmul");

@@ -99,15 +99,19 @@ struct PfQuantArgs {
   float *xb; int ldb;
 };
 hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st);
-// Y[t][r] = scale[r] * sum_b bs[t][b] * isum(r, t, b) (+ bias[r]), or Y[t][r] += that when resid; q8 weights
+// Y[t][r] = scale[r] * sum_b bs[t][b] * isum(r, t, b) (+ bias[r]), or Y[t][r] += that when resid; q8 weights with
+// their row block sums wsum [rows][ldw] (launch_rowsum_q8)
 struct GemmArgs {
   const int8_t *w; const float *scale; int rows, cols;
+  const int *wsum; int ldw;
   const int8_t *xh, *xl; const float *xb; int ntok, ldq, ldb;
   float *y; int ldy;
   const float *bias;
   int resid;
 };
 size_t gemm_lds_bytes();
+// out[row][block] = sum of W[row] over each 128-column block
+hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipStream_t st);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st);
 // token t of the batch at position p0 + t: RoPE on q [t][ldq] (in place) and k, fp16 k / v rows into the caches
 struct PfRopeArgs {

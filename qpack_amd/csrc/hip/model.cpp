@@ -115,6 +115,13 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   for (const Layer &ly : layers_)
     for (const DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd}) pf_ok_ = pf_ok_ && m->kind == MK_Q8;
   if (pf_ok_) {
+    for (Layer &ly : layers_)
+      for (DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd}) {
+        int *rs = (int *)dalloc(4ull * m->rows * (m->cols / 128));
+        QPH_CK(launch_rowsum_q8((const int8_t *)m->q, m->rows, m->cols, rs, st_));
+        m->rs = rs;
+      }
+    QPH_CK(hipStreamSynchronize(st_));
     pf_cap_ = std::min(kPfChunk, ctx_);
     if (const char *e = getenv("QPH_PF_CHUNK")) pf_cap_ = std::max(1, std::min(pf_cap_, atoi(e)));   // test hook
     const size_t B = pf_cap_, wide = std::max({d, qd_, ff});
@@ -301,6 +308,7 @@ void HipLlama::prefill_batched(const int *toks, int n) {
   };
   auto gemm = [&](const DMat &m, float *y, int ldy, const float *bias, bool resid, int B) {
     GemmArgs a{}; a.w = (const int8_t *)m.q; a.scale = (const float *)m.s; a.rows = m.rows; a.cols = m.cols;
+    a.wsum = m.rs; a.ldw = m.cols / 128;
     a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld;
     a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0;
     QPH_CK(launch_gemm(a, st_));

@@ -61,18 +61,19 @@ hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st)
 }
 
 // ------------------------------------------------------------------ int8 MFMA matrix product (q8 weights)
-// Workgroup tile: 128 weight rows x 128 tokens, 4 waves in a 2 x 2 grid of 64 x 64, each a 4 x 4 grid of 16 x 16
-// MFMA tiles.  K advances one 128-column block at a time (two 64-deep MFMA steps per plane).  Operands reach LDS by
-// direct global->LDS loads (global_load_lds_dwordx4: a wave instruction lands 64 x 16 B contiguously) in a 3-stage
-// ring, so two blocks are always in flight while one is multiplied; no operand passes through registers.
+// Workgroup tile: 128 weight rows x 128 tokens, 8 waves (two per SIMD, so one wave's fp32 epilogue overlaps the other's
+// matrix-core work) in a 2 x 4 grid of 64 rows x 32 tokens, each a 4 x 2 grid of 16 x 16 MFMA tiles.  K advances one
+// 128-column block at a time (two 64-deep MFMA steps per plane).  Operands reach LDS by direct global->LDS loads
+// (global_load_lds_dwordx4: a wave instruction lands 64 x 16 B contiguously) in a 3-stage ring, so two blocks are
+// always in flight while one is multiplied; no operand passes through registers.
 //   stage layout: weights, hi plane, lo plane, each [128 rows][128 B] with the 16-byte segments XOR-swizzled
-//   (physical segment = segment ^ (row & 7)) so 16-lane fragment reads hit distinct banks; then 128 block scales.
+//   (physical segment = segment ^ (row & 7)) so 16-lane fragment reads hit distinct banks; the tokens' block scales;
+//   the weight rows' block sums (precomputed once per matrix, k_rowsum_q8).
 //   fragments (v_mfma_i32_16x16x64_i8): lane l reads A = W[row l % 16][16 (l / 16) + 0..15] and B = plane[token l % 16]
 //   [16 (l / 16) + 0..15] - the same k set for A and B; C lane l holds rows 4 (l / 16) + 0..3 of token l % 16.
-//   sum(W) of each row over the block comes from one more MFMA against an all-ones B, landing in the C layout.
 // Rows or tokens past the end load a clamped (valid) address; their results are never stored.
-constexpr int kGM = 128, kGN = 128, kGStages = 3;
-constexpr int kGStage = 3 * 128 * 128 + 128 * 4;   // bytes per stage
+constexpr int kGM = 128, kGN = 128, kGStages = 3, kGWaves = 8;
+constexpr int kGStage = 3 * 128 * 128 + 128 * 4 + 128 * 4;   // bytes per stage
 size_t gemm_lds_bytes() { return (size_t)kGStages * kGStage; }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -84,8 +85,8 @@ __device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
   __builtin_amdgcn_global_load_lds((glb_void_t *)g, (lds_void_t *)lds_wave_base, 4, 0, 0);
 }
 // LDS reads of DMA-filled stages, kept out of the compiler's sight: it cannot tell which stage a DMA fills and would
-// otherwise wait for every load in flight before each read.  The results are only valid after lds_wait(), which takes
-// them as operands so no use can be scheduled before it.
+// otherwise wait for every load in flight before each read.  The results are only valid after the explicit lgkmcnt
+// wait that takes them as operands, so no use can be scheduled before it.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const lds_void_t *)p; }
 __device__ __forceinline__ v4i lds_read16(uint32_t addr) {
   v4i r;
@@ -98,129 +99,170 @@ __device__ __forceinline__ float lds_read4(uint32_t addr) {
   return r;
 }
 
-__global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
+// sum of each weight row over each 128-column block: out[row][block] (exact int32)
+__global__ __launch_bounds__(256) void k_rowsum_q8(const int8_t *w, int rows, int cols, int *out) {
+  const int nb = cols / kQB;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)rows * nb) return;
+  const v4i *p = (const v4i *)(w + (i / nb) * cols + (i % nb) * kQB);
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const v4i v = p[k];
+    s = __builtin_amdgcn_sdot4(v.x, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(v.y, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
+  }
+  out[i] = s;
+}
+hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipStream_t st) {
+  if (cols % kQB || rows <= 0) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)rows * (cols / kQB);
+  hipLaunchKernelGGL(k_rowsum_q8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, rows, cols, out);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave >> 1, wc = wave & 1, lr = lane & 15, lg = lane >> 4;
-  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin (linear id % 8), so XCD x is given the
-  // contiguous x-th eighth of the tiles in row-major order (token tile fastest): a weight tile is reused from that
-  // XCD's L2 by the token tiles that need it
+  const int wr = wave >> 2, wc = wave & 3, lr = lane & 15, lg = lane >> 4;
+  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin (linear id % 8).  When the token tiles split
+  // evenly over the XCDs, XCD x owns its eighth of them over all weight rows: its activation planes (a few MiB) stay in
+  // its L2 while the weights stream past from the last-level cache.  Otherwise XCD x owns the x-th eighth of the tiles
+  // in row-major order (token tile fastest), so a weight tile is reused from L2 by the token tiles that need it.
   int r0, t0;
   {
-    const int ntt = gridDim.x, n = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
-    const int xcd = lin & 7, k = lin >> 3, base = n >> 3, rem = n & 7;
-    const int tile = xcd * base + min(xcd, rem) + k;
-    r0 = (tile / ntt) * kGM; t0 = (tile % ntt) * kGN;
+    const int ntt = gridDim.x, nrt = gridDim.y, n = ntt * nrt, lin = blockIdx.y * gridDim.x + blockIdx.x;
+    const int xcd = lin & 7, k = lin >> 3;
+    if (ntt % 8 == 0) {
+      // each XCD: ntt / 8 token tiles x all nrt row tiles = n / 8 tiles, exactly its share of the round-robin
+      const int tn = ntt >> 3;
+      r0 = (k / tn) * kGM; t0 = (xcd * tn + k % tn) * kGN;
+    } else {
+      const int base = n >> 3, rem = n & 7;
+      const int tile = xcd * base + min(xcd, rem) + k;
+      r0 = (tile / ntt) * kGM; t0 = (tile % ntt) * kGN;
+    }
   }
   const int nb = a.cols / kQB;
 
-  // this lane's DMA sources: instruction j of the wave covers tile rows 8 (4 wave + j) + lane / 8; the lane fetches the
-  // segment that belongs at physical position lane % 8 of that row
+  // this lane's DMA sources.  Per stage the 48 1-KiB row groups (16 each of weights, hi plane, lo plane; 8 rows per
+  // group) go 6 to a wave; the lane fetches the 16-byte segment that belongs at physical position lane % 8 of its row.
   const int drow = lane >> 3, dseg = (lane & 7) ^ drow;
-  const int8_t *wsrc[4], *hsrc[4], *lsrc[4];
+  const int8_t *src[6];
+  int dst[6];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int row = 8 * (4 * wave + j) + drow;
-    const int r = min(r0 + row, a.rows - 1), t = min(t0 + row, a.ntok - 1);
-    wsrc[j] = a.w + (size_t)r * a.cols + dseg * 16;
-    hsrc[j] = a.xh + (size_t)t * a.ldq + dseg * 16;
-    lsrc[j] = a.xl + (size_t)t * a.ldq + dseg * 16;
+  for (int j = 0; j < 6; j++) {
+    const int q = wave * 6 + j, m = q >> 4, row = 8 * (q & 15) + drow;
+    dst[j] = m * 128 * 128 + 8 * (q & 15) * 128;
+    if (m == 0) src[j] = a.w + (size_t)min(r0 + row, a.rows - 1) * a.cols + dseg * 16;
+    else src[j] = (m == 1 ? a.xh : a.xl) + (size_t)min(t0 + row, a.ntok - 1) * a.ldq + dseg * 16;
   }
-  // block scales: waves w and w + 2 both fetch tokens 64 (w & 1) + lane (identical bytes to the same LDS slot), so
-  // every wave issues the same number of loads per stage
-  const float *bsrc = a.xb + (size_t)min(t0 + 64 * (wave & 1) + lane, a.ntok - 1) * a.ldb;
+  // one 4-byte load per wave and stage: waves 0 / 1 (and 4 / 5) the block scales of tokens 64 (w & 1) + lane, waves
+  // 2 / 3 (and 6 / 7) the block sums of rows 64 (w & 1) + lane - duplicates write identical bytes to the same slot,
+  // so every wave issues the same number of loads
+  const int half = wave & 1;
+  const bool sums = (wave & 2) != 0;
+  const char *esrc = sums ? (const char *)(a.wsum + (size_t)min(r0 + 64 * half + lane, a.rows - 1) * a.ldw)
+                          : (const char *)(a.xb + (size_t)min(t0 + 64 * half + lane, a.ntok - 1) * a.ldb);
+  const int edst = 3 * 128 * 128 + (sums ? 512 : 0) + 256 * half;
   auto issue = [&](int kb) {
     char *st = smem + (size_t)(kb % kGStages) * kGStage;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int rb = 8 * (4 * wave + j) * 128;
-      dma16(wsrc[j] + kb * kQB, st + rb);
-      dma16(hsrc[j] + kb * kQB, st + 128 * 128 + rb);
-      dma16(lsrc[j] + kb * kQB, st + 2 * 128 * 128 + rb);
-    }
-    dma4(bsrc + kb, st + 3 * 128 * 128 + 64 * 4 * (wave & 1));
+    for (int j = 0; j < 6; j++) dma16(src[j] + kb * kQB, st + dst[j]);
+    dma4(esrc + 4 * kb, st + edst);
   };
 
-  float acc[4][4][4];
+  float acc[4][2][4];
 #pragma unroll
   for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++)
+    for (int ni = 0; ni < 2; ni++)
 #pragma unroll
       for (int i = 0; i < 4; i++) acc[mi][ni][i] = 0.f;
-  const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
 
+  // software pipeline: block kb's MFMAs are issued while block kb - 1's epilogue (its exact int32 sums -> rows_q8's
+  // fma step) runs on the vector ALU - independent work the matrix cores and the VALU overlap
+  v4i pch[4][2], pcl[4][2];
+  float pbs[2];
+  auto epilogue_half = [&](int ni) {
+#pragma unroll
+    for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int isum = pch[mi][ni][i] * 256 + pcl[mi][ni][i];   // the lo accumulator started at 128 sum(W)
+        acc[mi][ni][i] = __builtin_fmaf(pbs[ni], (float)isum, acc[mi][ni][i]);
+      }
+  };
   issue(0);
   if (nb > 1) issue(1);
   for (int kb = 0; kb < nb; kb++) {
-    // this wave's loads of block kb have landed (block kb + 1's 13 may still be in flight), then everyone's
-    if (kb + 1 < nb) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");
+    // this wave's loads of block kb have landed (block kb + 1's 7 may still be in flight), then everyone's
+    if (kb + 1 < nb) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (kb + 2 < nb) issue(kb + 2);   // into the stage everyone finished reading in the previous iteration
     const uint32_t st = lds_addr(smem + (size_t)(kb % kGStages) * kGStage);
-    const uint32_t sw = st, sh = st + 128 * 128, sl = st + 2 * 128 * 128, sbs = st + 3 * 128 * 128;
-    v4i ch[4][4], cl[4][4], cw[4];
-#pragma unroll
-    for (int mi = 0; mi < 4; mi++) {
-      cw[mi] = (v4i){0, 0, 0, 0};
-#pragma unroll
-      for (int ni = 0; ni < 4; ni++) { ch[mi][ni] = (v4i){0, 0, 0, 0}; cl[mi][ni] = (v4i){0, 0, 0, 0}; }
-    }
-    float bsc[4];
+    const uint32_t sw = st, sh = st + 128 * 128, sl = st + 2 * 128 * 128, sbs = st + 3 * 128 * 128, sws = sbs + 512;
+    v4i ch[4][2], cl[4][2];
+    float bsc[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       const int seg = ks * 4 + lg;
-      v4i A[4], BH[4], BL[4];
+      v4i A[4], BH[2], BL[2];
 #pragma unroll
       for (int mi = 0; mi < 4; mi++) {
         const int row = wr * 64 + mi * 16 + lr;
         A[mi] = lds_read16(sw + row * 128 + ((seg ^ (row & 7)) << 4));
       }
 #pragma unroll
-      for (int ni = 0; ni < 4; ni++) {
-        const int tok = wc * 64 + ni * 16 + lr;
+      for (int ni = 0; ni < 2; ni++) {
+        const int tok = wc * 32 + ni * 16 + lr;
         const uint32_t o = tok * 128 + ((seg ^ (tok & 7)) << 4);
         BH[ni] = lds_read16(sh + o); BL[ni] = lds_read16(sl + o);
       }
-      if (ks == 1) {
+      if (ks == 0) {
+        // the block's row sums start the lo accumulators (isum = 256 hi + lo + 128 sum(W)); hi starts at zero
+        v4i wsv[4];
 #pragma unroll
-        for (int ni = 0; ni < 4; ni++) bsc[ni] = lds_read4(sbs + 4 * (wc * 64 + ni * 16 + lr));
+        for (int mi = 0; mi < 4; mi++) wsv[mi] = lds_read16(sws + 4 * (wr * 64 + mi * 16 + 4 * lg));
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) bsc[ni] = lds_read4(sbs + 4 * (wc * 32 + ni * 16 + lr));
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BH[2]), "+v"(BH[3]),
-                       "+v"(BL[0]), "+v"(BL[1]), "+v"(BL[2]), "+v"(BL[3]), "+v"(bsc[0]), "+v"(bsc[1]), "+v"(bsc[2]), "+v"(bsc[3]));
+                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BL[0]), "+v"(BL[1]),
+                       "+v"(bsc[0]), "+v"(bsc[1]), "+v"(wsv[0]), "+v"(wsv[1]), "+v"(wsv[2]), "+v"(wsv[3]));
+#pragma unroll
+        for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+          for (int ni = 0; ni < 2; ni++) { ch[mi][ni] = (v4i){0, 0, 0, 0}; cl[mi][ni] = wsv[mi] * 128; }
       } else {
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BH[2]), "+v"(BH[3]),
-                       "+v"(BL[0]), "+v"(BL[1]), "+v"(BL[2]), "+v"(BL[3]));
+                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BL[0]), "+v"(BL[1]));
       }
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++) cw[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], ones, cw[mi], 0, 0, 0);
-#pragma unroll
-      for (int ni = 0; ni < 4; ni++)
+      for (int ni = 0; ni < 2; ni++)
 #pragma unroll
         for (int mi = 0; mi < 4; mi++) {
           ch[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BH[ni], ch[mi][ni], 0, 0, 0);
           cl[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BL[ni], cl[mi][ni], 0, 0, 0);
         }
+      if (kb > 0) epilogue_half(ks);   // half of the previous block's epilogue under each step's MFMAs
     }
-    // the block's exact int32 sums, then rows_q8's fma step
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++)
+    for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int isum = ch[mi][ni][i] * 256 + cl[mi][ni][i] + 128 * cw[mi][i];
-          acc[mi][ni][i] = __builtin_fmaf(bsc[ni], (float)isum, acc[mi][ni][i]);
-        }
+      for (int ni = 0; ni < 2; ni++) { pch[mi][ni] = ch[mi][ni]; pcl[mi][ni] = cl[mi][ni]; }
+    pbs[0] = bsc[0]; pbs[1] = bsc[1];
   }
+  epilogue_half(0);
+  epilogue_half(1);
   // y = acc * scale (+ bias), or y += (residual stream)
 #pragma unroll
   for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++) {
-      const int t = t0 + wc * 64 + ni * 16 + lr;
+    for (int ni = 0; ni < 2; ni++) {
+      const int t = t0 + wc * 32 + ni * 16 + lr;
       if (t >= a.ntok) continue;
       float *yt = a.y + (size_t)t * a.ldy;
 #pragma unroll
@@ -236,9 +278,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st) {
   if (a.ntok <= 0) return hipSuccess;
-  if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
+  if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB || !a.wsum || a.ldw < a.cols / kQB)
+    return hipErrorInvalidValue;
   const dim3 grid((a.ntok + kGN - 1) / kGN, (a.rows + kGM - 1) / kGM);
-  hipLaunchKernelGGL(k_gemm_q8, grid, dim3(256), gemm_lds_bytes(), st, a);
+  hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
   return hipGetLastError();
 }
 

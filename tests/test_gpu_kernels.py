@@ -63,6 +63,7 @@ def test_matvec_q4_exact_sums(rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols,B", [(1000, 4096, 200), (256, 896, 129), (300, 14336, 17), (7, 128, 1), (4864, 896, 64),
+                                         (130, 512, 1024), (300, 896, 2048),
                                          (130, 512, 300)])
 def test_matmul_q8_rows_equal_decode_arithmetic(rows, cols, B):
     """batched prefill product (int8 MFMA, two activation planes): every token's row bit-identical to rows_q8 on that
