@@ -110,9 +110,10 @@ int qph_time_copy(int64_t bytes, int iters, float *ms);
  * and the per-block scales the kernel used. */
 int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int cols, const float *x, float *y,
                       int32_t *sums, int16_t *xq, float *bs);
-/* Runs the product's batched prefill kernels on one q8 matrix (host buffers): each row of X[B, cols] quantised as the
- * decode step quantises it, then Y[B, rows] = X W^T on the int8 matrix cores with rows_q8's float epilogue per token
- * (matmul / mm_q8, kernels.cpp:97-143, kernels_x86.cpp:287-340; so every Y row equals qph_kernel_matvec on that x). */
+/* Runs the product's batched prefill kernels on one matrix (host buffers; q and scale as in qph_kernel_matvec): each
+ * row of X[B, cols] quantised as the decode step quantises it, then Y[B, rows] = X W^T on the int8 matrix cores
+ * (matmul / mm_q8 / mm_q4, kernels.cpp:97-143, kernels_x86.cpp:287-371).  q8 rows use rows_q8's float epilogue per
+ * token, so every Y row equals qph_kernel_matvec on that x; q4 rows have exact int32 group sums and their own fp32 order. */
 int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y);
 
 /* ---- synthetic models (no reference counterpart: the reference's files come from convert_llama.py / qpack-quantize).

@@ -211,24 +211,35 @@ int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int 
   QPH_API_TRY({
     need(q, "q"); need(scale, "scale"); need(X, "X"); need(Y, "Y");
     if (rows <= 0 || B <= 0 || cols <= 0 || cols % 128) throw std::invalid_argument("matmul: rows, B > 0 and cols a positive multiple of 128 required");
-    if (kind != QPH_Q8) throw std::invalid_argument("matmul: the batched kernel takes q8 weights (QPH_Q8)");
-    const int nb = cols / 128;
+    if (kind != QPH_Q8 && kind != QPH_Q4) throw std::invalid_argument("matmul: kind must be QPH_Q8 or QPH_Q4");
+    const int nb = cols / 128, G = cols / 32, ldg = (G + 3) / 4 * 4;
+    const size_t qb = kind == QPH_Q8 ? (size_t)rows * cols : (size_t)rows * cols / 2;
+    const size_t sb = kind == QPH_Q8 ? 4ull * rows : 2ull * rows * G;
     std::vector<void *> bufs;
     auto alloc = [&](size_t n) { void *p = nullptr; hck(hipMalloc(&p, n), "hipMalloc"); bufs.push_back(p); return p; };
     try {
-      void *dq = alloc((size_t)rows * cols), *ds = alloc(4ull * rows);
+      void *dq = alloc(qb), *ds = alloc(sb);
       float *dx = (float *)alloc(4ull * B * cols), *dy = (float *)alloc(4ull * B * rows), *dxb = (float *)alloc(4ull * B * nb);
       int8_t *dxh = (int8_t *)alloc((size_t)B * cols), *dxl = (int8_t *)alloc((size_t)B * cols);
-      hck(hipMemcpy(dq, q, (size_t)rows * cols, hipMemcpyHostToDevice), "upload q");
-      hck(hipMemcpy(ds, scale, 4ull * rows, hipMemcpyHostToDevice), "upload scale");
+      int *dxg = (int *)alloc(4ull * B * ldg);
+      hck(hipMemcpy(dq, q, qb, hipMemcpyHostToDevice), "upload q");
+      hck(hipMemcpy(ds, scale, sb, hipMemcpyHostToDevice), "upload scale");
       hck(hipMemcpy(dx, X, 4ull * B * cols, hipMemcpyHostToDevice), "upload X");
       qph::PfQuantArgs qa{}; qa.x = dx; qa.ldx = cols; qa.cols = cols; qa.xh = dxh; qa.xl = dxl; qa.ldq = cols; qa.xb = dxb; qa.ldb = nb;
+      qa.xg = dxg; qa.ldg = ldg;
       hck(qph::launch_pf_quant(qph::PRO_QUANT, qa, B, nullptr), "launch quant");
-      int *dws = (int *)alloc(4ull * rows * nb);
-      hck(qph::launch_rowsum_q8((const int8_t *)dq, rows, cols, dws, nullptr), "launch rowsum");
-      qph::GemmArgs ga{}; ga.w = (const int8_t *)dq; ga.scale = (const float *)ds; ga.rows = rows; ga.cols = cols;
-      ga.wsum = dws; ga.ldw = nb;
-      ga.xh = dxh; ga.xl = dxl; ga.xb = dxb; ga.ntok = B; ga.ldq = cols; ga.ldb = nb; ga.y = dy; ga.ldy = rows;
+      qph::GemmArgs ga{}; ga.kind = kind == QPH_Q8 ? qph::MK_Q8 : qph::MK_Q4; ga.w = (const int8_t *)dq; ga.scale = (const float *)ds;
+      ga.rows = rows; ga.cols = cols; ga.xh = dxh; ga.xl = dxl; ga.xb = dxb; ga.ntok = B; ga.ldq = cols; ga.ldb = nb;
+      ga.xg = dxg; ga.ldg = ldg; ga.y = dy; ga.ldy = rows;
+      if (kind == QPH_Q8) {
+        int *dws = (int *)alloc(4ull * rows * nb);
+        hck(qph::launch_rowsum_q8((const int8_t *)dq, rows, cols, dws, nullptr), "launch rowsum");
+        ga.wsum = dws; ga.ldw = nb;
+      } else {
+        int *dns = (int *)alloc(4ull * rows * G); float *dsc = (float *)alloc(4ull * rows * G);
+        hck(qph::launch_q4_prep((const uint8_t *)dq, (const uint16_t *)ds, rows, cols, dns, dsc, nullptr), "launch q4 prep");
+        ga.q4ns = dns; ga.q4sc = dsc;
+      }
       hck(qph::launch_gemm(ga, nullptr), "launch gemm");
       hck(hipDeviceSynchronize(), "matmul");
       hck(hipMemcpy(Y, dy, 4ull * B * rows, hipMemcpyDeviceToHost), "download Y");

@@ -16,7 +16,11 @@ struct DMat {
   const void *q;       // q8: int8 [rows, cols]; q4: u8 [rows, cols / 2]; f32: float [rows, cols]
   const void *s;       // q8: f32 [rows]; q4: fp16 [rows, cols / 32]
   int rows, cols, kind;
-  const int *rs;       // q8 layer matrices on the batched prompt path: row sums per 128-column block [rows, cols / 128]
+  // layer matrices on the batched prompt path: q8 row sums per 128-column block [rows, cols / 128]; q4 nibble sums and
+  // f32 scales per (block, group, row), group-major within each block
+  const int *rs;
+  const int *q4ns;
+  const float *q4sc;
 };
 
 // device-resident decode control block: the token to embed, its position, and the greedy output cursor

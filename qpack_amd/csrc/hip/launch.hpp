@@ -97,13 +97,19 @@ struct PfQuantArgs {
   int cols;
   int8_t *xh, *xl; int ldq;
   float *xb; int ldb;
+  int *xg; int ldg;   // optional: sum of q per 32-column group [B][ldg] (the q4 product needs it)
 };
 hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st);
-// Y[t][r] = scale[r] * sum_b bs[t][b] * isum(r, t, b) (+ bias[r]), or Y[t][r] += that when resid; q8 weights with
-// their row block sums wsum [rows][ldw] (launch_rowsum_q8)
+// Y[t][r] = the row's dot product with token t's quantised activation (+ bias[r]), or Y[t][r] += that when resid.
+//   kind MK_Q8: w int8 [rows][cols], scale f32 [rows], wsum = row sums per 128-column block [rows][ldw] (launch_rowsum_q8)
+//   kind MK_Q4: w packed q4 [rows][cols / 2], q4ns / q4sc = per-group nibble sums and f32 scales, group-major per block
+//               (launch_q4_prep), and the activation's group sums xg [ntok][ldg] (launch_pf_quant)
 struct GemmArgs {
+  int kind;
   const int8_t *w; const float *scale; int rows, cols;
   const int *wsum; int ldw;
+  const int *q4ns; const float *q4sc;
+  const int *xg; int ldg;
   const int8_t *xh, *xl; const float *xb; int ntok, ldq, ldb;
   float *y; int ldy;
   const float *bias;
@@ -112,6 +118,8 @@ struct GemmArgs {
 size_t gemm_lds_bytes();
 // out[row][block] = sum of W[row] over each 128-column block
 hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipStream_t st);
+// q4 rows: per (block, group, row) the sum of the nibbles and the f32 scale, group-major within each 128-column block
+hipError_t launch_q4_prep(const uint8_t *w, const uint16_t *sc, int rows, int cols, int *out_ns, float *out_sc, hipStream_t st);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st);
 // token t of the batch at position p0 + t: RoPE on q [t][ldq] (in place) and k, fp16 k / v rows into the caches
 struct PfRopeArgs {

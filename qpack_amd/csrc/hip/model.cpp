@@ -110,16 +110,24 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   }
   ctl_ = (Ctl *)dalloc(sizeof(Ctl));
   out_tok_ = (int *)dalloc(4ull * (ctx_ + 1));
-  // batched prompt path: every layer matrix q8 (the int8 MFMA product); chunks of up to pf_cap_ tokens
+  // batched prompt path: every layer matrix q8 or q4 (the int8 MFMA products); chunks of up to pf_cap_ tokens
   pf_ok_ = true;
   for (const Layer &ly : layers_)
-    for (const DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd}) pf_ok_ = pf_ok_ && m->kind == MK_Q8;
+    for (const DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd})
+      pf_ok_ = pf_ok_ && (m->kind == MK_Q8 || m->kind == MK_Q4);
   if (pf_ok_) {
     for (Layer &ly : layers_)
       for (DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd}) {
-        int *rs = (int *)dalloc(4ull * m->rows * (m->cols / 128));
-        QPH_CK(launch_rowsum_q8((const int8_t *)m->q, m->rows, m->cols, rs, st_));
-        m->rs = rs;
+        if (m->kind == MK_Q8) {
+          int *rs = (int *)dalloc(4ull * m->rows * (m->cols / 128));
+          QPH_CK(launch_rowsum_q8((const int8_t *)m->q, m->rows, m->cols, rs, st_));
+          m->rs = rs;
+        } else {
+          int *ns = (int *)dalloc(4ull * m->rows * (m->cols / 32));
+          float *sc = (float *)dalloc(4ull * m->rows * (m->cols / 32));
+          QPH_CK(launch_q4_prep((const uint8_t *)m->q, (const uint16_t *)m->s, m->rows, m->cols, ns, sc, st_));
+          m->q4ns = ns; m->q4sc = sc;
+        }
       }
     QPH_CK(hipStreamSynchronize(st_));
     pf_cap_ = std::min(kPfChunk, ctx_);
@@ -131,6 +139,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     pf_g_ = (float *)dalloc(4 * B * ff); pf_u_ = (float *)dalloc(4 * B * ff);
     pf_xh_ = (int8_t *)dalloc(B * pf_ldq_); pf_xl_ = (int8_t *)dalloc(B * pf_ldq_);
     pf_xb_ = (float *)dalloc(4 * B * (pf_ldq_ / 128 + 1));
+    pf_ldg_ = (pf_ldq_ / 32 + 3) / 4 * 4;
+    pf_xg_ = (int *)dalloc(4 * B * pf_ldg_);
     pf_tok_ = (int *)dalloc(4 * B);
   }
   // RoPE tables in the reference's precision: inv_i = 1 / theta^(2i/hd) and angle pos * inv_i in double, cos / sin
@@ -303,12 +313,12 @@ void HipLlama::prefill_batched(const int *toks, int n) {
   const float eps = cfg_.rms_eps;
   auto quant = [&](int pro, const float *x, int ldx, const float *w, int cols, int B) {
     PfQuantArgs a{}; a.x = x; a.ldx = ldx; a.norm_w = w; a.eps = eps; a.cols = cols;
-    a.xh = pf_xh_; a.xl = pf_xl_; a.ldq = pf_ldq_; a.xb = pf_xb_; a.ldb = nb_ld;
+    a.xh = pf_xh_; a.xl = pf_xl_; a.ldq = pf_ldq_; a.xb = pf_xb_; a.ldb = nb_ld; a.xg = pf_xg_; a.ldg = pf_ldg_;
     QPH_CK(launch_pf_quant(pro, a, B, st_));
   };
   auto gemm = [&](const DMat &m, float *y, int ldy, const float *bias, bool resid, int B) {
-    GemmArgs a{}; a.w = (const int8_t *)m.q; a.scale = (const float *)m.s; a.rows = m.rows; a.cols = m.cols;
-    a.wsum = m.rs; a.ldw = m.cols / 128;
+    GemmArgs a{}; a.kind = m.kind; a.w = (const int8_t *)m.q; a.scale = (const float *)m.s; a.rows = m.rows; a.cols = m.cols;
+    a.wsum = m.rs; a.ldw = m.cols / 128; a.q4ns = m.q4ns; a.q4sc = m.q4sc; a.xg = pf_xg_; a.ldg = pf_ldg_;
     a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld;
     a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0;
     QPH_CK(launch_gemm(a, st_));

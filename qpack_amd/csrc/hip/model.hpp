@@ -67,14 +67,14 @@ class HipLlama {
   hipGraphExec_t g_state_ = nullptr, g_logits_ = nullptr, g_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
   void run_step(int parts);
-  // batched prompt path (all layer matrices q8)
+  // batched prompt path (layer matrices q8 / q4)
   static constexpr int kPfChunk = 2048;
   bool pf_ok_ = false;
-  int pf_cap_ = 0, pf_ldq_ = 0;
+  int pf_cap_ = 0, pf_ldq_ = 0, pf_ldg_ = 0;
   float *pf_x_ = nullptr, *pf_q_ = nullptr, *pf_k_ = nullptr, *pf_v_ = nullptr, *pf_att_ = nullptr, *pf_g_ = nullptr, *pf_u_ = nullptr;
   float *pf_xb_ = nullptr;
   int8_t *pf_xh_ = nullptr, *pf_xl_ = nullptr;
-  int *pf_tok_ = nullptr;
+  int *pf_tok_ = nullptr, *pf_xg_ = nullptr;
   void prefill_batched(const int *toks, int n);
 
   void *dalloc(size_t bytes);

@@ -50,6 +50,8 @@ __global__ __launch_bounds__(1024) void k_pf_quant(PfQuantArgs a) {
     *(uint4 *)(xl + c) = make_uint4(l.x ^ 0x80808080u, l.y ^ 0x80808080u, l.z ^ 0x80808080u, l.w ^ 0x80808080u);
   }
   for (int b = threadIdx.x; b < nb; b += blockDim.x) a.xb[(size_t)t * a.ldb + b] = av.bs[b];
+  if (a.xg)   // sum of q per 32-column group (the q4 product's nibble-offset correction)
+    for (int g = threadIdx.x; g < cols / 32; g += blockDim.x) a.xg[(size_t)t * a.ldg + g] = av.gsum[g];
 }
 hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st) {
   if (B <= 0) return hipSuccess;
@@ -276,12 +278,243 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ int8 MFMA matrix product (q4 weights)
+// The q8 product's tile, waves, stages and DMA ring, for q4 rows (byte j of a 32-column group holds column j in the low
+// nibble and column j + 16 in the high one; an fp16 scale per row and group).  Each group gets its exact int32 sum on
+// v_mfma_i32_16x16x32_i8 (one 32-deep step per plane): lane l's 8 A bytes are the low (l / 16 < 2) or high nibbles of
+// packed bytes 8 (l / 16 & 1) + 0..7 - unsigned 0..15 - against the planes' columns 8 (l / 16) + 0..7, and
+//     isum_g = 256 (nib . hi) + (nib . lo) + 128 sum(nib) - 8 sum(q)       (w = nib - 8, q = 256 hi + lo + 128)
+// with sum(nib) per (row, group) precomputed (k_q4_prep, together with the f32 scales, group-major) and sum(q) per
+// (token, group) from the quantiser.  Float step: blk = sum_g fma(scale_g, (float)isum_g), acc = fma(bs, blk, acc) per
+// block - another order than rows_q4's 8-lane partials, within the logit tolerance like the decode q4 path.
+//   stage: packed weights [128][64 B] (segments swizzled ^ (row & 3)), hi / lo planes as in the q8 product, block
+//   scales [128 tokens], sum(q) [128 tokens][4], sum(nib) [4][128 rows], weight scales [4][128 rows] f32.
+constexpr int kG4Stage = 128 * 64 + 2 * 128 * 128 + 512 + 2048 + 2048 + 2048;
+
+// per (block, group, row): sum of the row's nibbles over the group and its fp16 scale as f32, group-major within a
+// block: out_ns[(b * 4 + g) * rows + r], out_sc likewise
+__global__ __launch_bounds__(256) void k_q4_prep(const uint8_t *w, const uint16_t *sc, int rows, int cols, int *out_ns,
+                                                 float *out_sc) {
+  const int G = cols / 32;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)rows * G) return;
+  const int r = (int)(i / G), g = (int)(i % G);
+  const v4i v = *(const v4i *)(w + (size_t)r * (cols / 2) + 16 * g);
+  int s = 0;
+  const int words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    s = __builtin_amdgcn_sdot4(words[k] & 0x0f0f0f0f, 0x01010101, s, false);
+    s = __builtin_amdgcn_sdot4((words[k] >> 4) & 0x0f0f0f0f, 0x01010101, s, false);
+  }
+  const size_t o = ((size_t)(g >> 2) * 4 + (g & 3)) * rows + r;
+  out_ns[o] = s;
+  out_sc[o] = half_bits_to_float(sc[(size_t)r * G + g]);
+}
+hipError_t launch_q4_prep(const uint8_t *w, const uint16_t *sc, int rows, int cols, int *out_ns, float *out_sc,
+                          hipStream_t st) {
+  if (cols % kQB || rows <= 0) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)rows * (cols / 32);
+  hipLaunchKernelGGL(k_q4_prep, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, sc, rows, cols, out_ns, out_sc);
+  return hipGetLastError();
+}
+
+__device__ __forceinline__ uint2 lds_read8(uint32_t addr) {
+  uint2 r;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+__global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 2, wc = wave & 3, lr = lane & 15, lg = lane >> 4;
+  int r0, t0;
+  {
+    const int ntt = gridDim.x, n = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+    const int xcd = lin & 7, k = lin >> 3;
+    if (ntt % 8 == 0) {
+      const int tn = ntt >> 3;
+      r0 = (k / tn) * kGM; t0 = (xcd * tn + k % tn) * kGN;
+    } else {
+      const int base = n >> 3, rem = n & 7;
+      const int tile = xcd * base + min(xcd, rem) + k;
+      r0 = (tile / ntt) * kGM; t0 = (tile % ntt) * kGN;
+    }
+  }
+  const int nb = a.cols / kQB, rb = a.cols / 2;   // packed bytes per row
+  // DMA jobs per stage (64 wave instructions, 8 per wave; jobs 60..63 repeat 0..3 byte for byte):
+  //   0..7 packed weights (16 rows x 64 B each), 8..23 hi plane, 24..39 lo plane (8 rows x 128 B each),
+  //   40..47 sum(nib) and 48..55 scales (64 rows of one group each, 4 B per lane), 56..57 sum(q) (64 tokens x 16 B),
+  //   58..59 block scales (64 tokens x 4 B)
+  const char *src[8];
+  int dst[8], bytes[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    int q = wave * 8 + j;
+    if (q >= 60) q -= 60;
+    if (q < 8) {
+      const int row = 16 * q + (lane >> 2), seg = (lane & 3) ^ (row & 3);
+      src[j] = (const char *)a.w + (size_t)min(r0 + row, a.rows - 1) * rb + seg * 16;
+      dst[j] = 16 * q * 64; bytes[j] = 16;
+    } else if (q < 40) {
+      const int m = q < 24 ? 0 : 1, qq = (q - 8) & 15, row = 8 * qq + (lane >> 3), seg = (lane & 7) ^ (lane >> 3);
+      src[j] = (const char *)(m == 0 ? a.xh : a.xl) + (size_t)min(t0 + row, a.ntok - 1) * a.ldq + seg * 16;
+      dst[j] = 128 * 64 + m * 128 * 128 + 8 * qq * 128; bytes[j] = 16;
+    } else if (q < 56) {
+      const int which = q < 48 ? 0 : 1, qq = (q - 40) & 7, g = qq >> 1, row = 64 * (qq & 1) + lane;
+      // group-major per block: element (kb * 4 + g) * rows + row; the block offset is added at issue time
+      const char *base = which == 0 ? (const char *)a.q4ns : (const char *)a.q4sc;
+      src[j] = base + 4 * ((size_t)g * a.rows + min(r0 + row, a.rows - 1));
+      dst[j] = 128 * 64 + 2 * 128 * 128 + 512 + 2048 + which * 2048 + g * 512 + (qq & 1) * 256; bytes[j] = 4;
+    } else if (q < 58) {
+      const int tok = 64 * (q - 56) + lane;
+      src[j] = (const char *)(a.xg + (size_t)min(t0 + tok, a.ntok - 1) * a.ldg);
+      dst[j] = 128 * 64 + 2 * 128 * 128 + 512 + 64 * 16 * (q - 56); bytes[j] = 16;
+    } else {
+      const int tok = 64 * (q - 58) + lane;
+      src[j] = (const char *)(a.xb + (size_t)min(t0 + tok, a.ntok - 1) * a.ldb);
+      dst[j] = 128 * 64 + 2 * 128 * 128 + 256 * (q - 58); bytes[j] = 4;
+    }
+  }
+  auto issue = [&](int kb) {
+    char *st = smem + (size_t)(kb % kGStages) * kG4Stage;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int q = wave * 8 + j;
+      if (q >= 60) q -= 60;
+      size_t adv;
+      if (q < 8) adv = (size_t)kb * 64;                                     // packed row bytes of the block
+      else if (q < 40) adv = (size_t)kb * kQB;                              // plane bytes of the block
+      else if (q < 56) adv = (size_t)kb * 4 * a.rows * 4;                   // group-major block of 4 x rows
+      else if (q < 58) adv = (size_t)kb * 16;                               // 4 groups of sum(q)
+      else adv = (size_t)kb * 4;                                            // one block scale
+      if (bytes[j] == 16) dma16(src[j] + adv, st + dst[j]);
+      else dma4(src[j] + adv, st + dst[j]);
+    }
+  };
+
+  float acc[4][2][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[mi][ni][i] = 0.f;
+
+  issue(0);
+  if (nb > 1) issue(1);
+  for (int kb = 0; kb < nb; kb++) {
+    if (kb + 1 < nb) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (kb + 2 < nb) issue(kb + 2);
+    const uint32_t st = lds_addr(smem + (size_t)(kb % kGStages) * kG4Stage);
+    const uint32_t sw = st, sh = st + 128 * 64, sl = sh + 128 * 128, sbs = sl + 128 * 128, sgq = sbs + 512,
+                   sns = sgq + 2048, ssc = sns + 2048;
+    // per-lane block data: the tokens' block scales and sum(q) of the 4 groups
+    float bsc[2]; v4i gq[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+      const int tok = wc * 32 + ni * 16 + lr;
+      bsc[ni] = lds_read4(sbs + 4 * tok);
+      gq[ni] = lds_read16(sgq + 16 * tok);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bsc[0]), "+v"(bsc[1]), "+v"(gq[0]), "+v"(gq[1]));
+    float blk[4][2][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) blk[mi][ni][i] = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      long A[4], BH[2], BL[2];
+      v4i ns[4], scv[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++) {
+        const int row = wr * 64 + mi * 16 + lr;
+        const uint2 v = lds_read8(sw + row * 64 + ((g ^ (row & 3)) << 4) + 8 * (lg & 1));
+        A[mi] = (long)v.x | ((long)v.y << 32);   // raw bytes; nibbles extracted after the wait
+        const int r4 = wr * 64 + mi * 16 + 4 * lg;
+        ns[mi] = lds_read16(sns + 4 * (g * 128 + r4));
+        scv[mi] = lds_read16(ssc + 4 * (g * 128 + r4));
+      }
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++) {
+        const int tok = wc * 32 + ni * 16 + lr;
+        const uint32_t o = tok * 128 + (((2 * g + (lg >> 1)) ^ (tok & 7)) << 4) + 8 * (lg & 1);
+        const uint2 h = lds_read8(sh + o), l = lds_read8(sl + o);
+        BH[ni] = (long)h.x | ((long)h.y << 32);
+        BL[ni] = (long)l.x | ((long)l.y << 32);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BL[0]), "+v"(BL[1]),
+                     "+v"(ns[0]), "+v"(ns[1]), "+v"(ns[2]), "+v"(ns[3]), "+v"(scv[0]), "+v"(scv[1]), "+v"(scv[2]),
+                     "+v"(scv[3]));
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++) {   // low nibbles for k 0..15 of the group, high nibbles for 16..31
+        const uint32_t lo = (uint32_t)A[mi], hi = (uint32_t)((unsigned long)A[mi] >> 32);
+        const uint32_t x0 = lg < 2 ? lo & 0x0f0f0f0fu : (lo >> 4) & 0x0f0f0f0fu;
+        const uint32_t x1 = lg < 2 ? hi & 0x0f0f0f0fu : (hi >> 4) & 0x0f0f0f0fu;
+        A[mi] = (long)x0 | ((long)x1 << 32);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+          v4i ch = {0, 0, 0, 0};
+          v4i cl = ns[mi] * 128 - gq[ni][g] * 8;
+          ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[mi], BH[ni], ch, 0, 0, 0);
+          cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[mi], BL[ni], cl, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int isum = ch[i] * 256 + cl[i];
+            const int sbits = scv[mi][i];   // copied out first: this compiler lowers a bit_cast of a vector-element
+                                            // lvalue to a read of element 0
+            blk[mi][ni][i] = __builtin_fmaf(__builtin_bit_cast(float, sbits), (float)isum, blk[mi][ni][i]);
+          }
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[mi][ni][i] = __builtin_fmaf(bsc[ni], blk[mi][ni][i], acc[mi][ni][i]);
+  }
+#pragma unroll
+  for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+      const int t = t0 + wc * 32 + ni * 16 + lr;
+      if (t >= a.ntok) continue;
+      float *yt = a.y + (size_t)t * a.ldy;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = r0 + wr * 64 + mi * 16 + 4 * lg + i;
+        if (r >= a.rows) continue;
+        const float v = acc[mi][ni][i];
+        if (a.resid) yt[r] = yt[r] + v;
+        else yt[r] = a.bias ? v + a.bias[r] : v;
+      }
+    }
+}
+
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st) {
   if (a.ntok <= 0) return hipSuccess;
-  if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB || !a.wsum || a.ldw < a.cols / kQB)
-    return hipErrorInvalidValue;
+  if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
   const dim3 grid((a.ntok + kGN - 1) / kGN, (a.rows + kGM - 1) / kGM);
-  hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
+  if (a.kind == MK_Q8) {
+    if (!a.wsum || a.ldw < a.cols / kQB) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
+  } else if (a.kind == MK_Q4) {
+    if (!a.q4ns || !a.q4sc || !a.xg || a.ldg < a.cols / 32 || a.ldg % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gemm_q4, grid, dim3(64 * kGWaves), (size_t)kGStages * kG4Stage, st, a);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -155,16 +155,20 @@ def kernel_matvec(kind, q, scale, x):
     return y, sums, xq, bs
 
 
-def kernel_matmul(q, scale, X):
-    """the product's batched prefill kernels on one q8 matrix: Y[B, rows] = X[B, cols] W^T (qph_kernel_matmul)"""
-    from ._lib import QPH_Q8
-    q = np.ascontiguousarray(q, dtype=np.int8)
-    scale = np.ascontiguousarray(scale, dtype=np.float32)
+def kernel_matmul(q, scale, X, kind=None):
+    """the product's batched prefill kernels on one matrix: Y[B, rows] = X[B, cols] W^T (qph_kernel_matmul); q8 (int8
+    q, f32 scale) or q4 (packed u8 q, fp16-bits scale per 32 columns)"""
+    from ._lib import QPH_Q4, QPH_Q8
+    if kind is None:
+        kind = QPH_Q8 if q.dtype == np.int8 else QPH_Q4
+    q = np.ascontiguousarray(q)
+    scale = np.ascontiguousarray(scale)
     X = np.ascontiguousarray(X, dtype=np.float32)
-    rows, cols = q.shape
+    rows = q.shape[0]
+    cols = q.shape[1] if kind == QPH_Q8 else 2 * q.shape[1]
     B = X.shape[0]
     assert X.shape[1] == cols
     Y = np.empty((B, rows), np.float32)
-    check(lib().qph_kernel_matmul(QPH_Q8, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols,
+    check(lib().qph_kernel_matmul(kind, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols,
                                   _fptr(X), B, _fptr(Y)))
     return Y

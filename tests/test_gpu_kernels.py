@@ -77,3 +77,26 @@ def test_matmul_q8_rows_equal_decode_arithmetic(rows, cols, B):
     for b in range(B):
         xq, bs = O.quant_act(X[b])
         np.testing.assert_array_equal(Y[b], O.rows_q8(q, s, xq, bs), err_msg=f"token {b}")
+
+
+@pytest.mark.parametrize("rows,cols,B", [(1000, 4096, 200), (257, 896, 129), (300, 18944, 17), (9, 128, 1), (3584, 3584, 64),
+                                         (130, 512, 1024)])
+def test_matmul_q4(rows, cols, B):
+    """batched prefill product on q4 rows (int8 MFMA over unpacked nibbles, exact int32 group sums): every token's row
+    against rows_q4 on that token's quantised activation, within 2e-6 of the summed term magnitudes (its own fp32
+    order); ragged row / token counts exercise the tile edges"""
+    rng = np.random.default_rng(rows * 17 + cols + B)
+    q = rng.integers(0, 256, (rows, cols // 2)).astype(np.uint8)
+    q[0] = 0x00; q[min(1, rows - 1)] = 0xff                    # extreme nibbles (-8, 7)
+    s = (rng.random((rows, cols // 32)) * 0.01 + 1e-4).astype(np.float16).view(np.uint16)
+    X = np.stack([act_vector(rng, cols) * rng.uniform(0.1, 10) for _ in range(B)]).astype(np.float32)
+    X[B // 2] = 0
+    print(f"q4 matmul rows={rows} cols={cols} B={B}", flush=True)
+    Y = qa.kernel_matmul(q, s, X)
+    for b in range(0, B, max(1, B // 40)):
+        xq, bs = O.quant_act(X[b])
+        gs = O.group_sums_q4(q, xq)
+        comb = s.view(np.float16).astype(np.float32) * np.repeat(bs, 4)[None, :]
+        mag = np.abs(comb * gs).sum(1)
+        y_o = O.rows_q4(q, s, xq, bs)
+        assert np.all(np.abs(Y[b] - y_o) <= 2e-6 * mag + 1e-30), (b, float(np.max(np.abs(Y[b] - y_o) / (mag + 1e-30))))
