@@ -145,10 +145,9 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   for (int t0 = 0; t0 < total; t0 += D) {
 #pragma unroll
     for (int k = 0; k < D; k++) {
-      uint4 cur[NS]; uint16_t curs[NS];
-#pragma unroll
-      for (int s = 0; s < NS; s++) { cur[s] = wr[k][s]; curs[s] = sr[k][s]; }
-      issue(wr[k], sr[k]);
+      // consume slot k, then refill it: the load reuses the slot's registers (taking a copy first and loading
+      // before the use would need new registers and a copy per slot at the loop edge, which waits for the whole ring)
+      const uint4 (&cur)[NS] = wr[k]; const uint16_t (&curs)[NS] = sr[k];
       if (t0 + k < total) {
         if (dm & 1) {
 #pragma unroll
@@ -218,11 +217,13 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
           cc = 0; ci++;
         }
       }
+      issue(wr[k], sr[k]);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (dm & 4) return;   // timing: no epilogue
 
   // epilogue: lane j finishes (unit j / NS, row slot j % NS)
   float best_v = -INFINITY; int best_i = 0x7fffffff;
@@ -448,8 +449,10 @@ __device__ __forceinline__ void kv_load(const uint16_t *kc, const uint16_t *vc, 
 // waves per attention workgroup: 16 (four per SIMD, so the latency of one wave's LDS / DPP / exp chains is covered by
 // the others), 8 where 16 would not fit the registers (wide GQA groups)
 constexpr int attn_waves(int hd, int rep) { return (hd == 64 && rep >= 7) || (hd == 128 && rep >= 5) ? 8 : 16; }
+// Split s of S of kv group g (attn_waves(HD, REP) waves; ys = the partial buffer's split stride).  S == 1 writes the
+// normalised heads to a.att; otherwise the split's unnormalised output and (max, sum) go to a.part.
 template <int HD, int REP>
-__global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs a) {
+__device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
   using B = KvBlock<HD>;
   constexpr int NW = attn_waves(HD, REP), HALF = HD / 2, LPP = B::LPP, PPI = B::PPI, VD = B::VD;
   __shared__ __align__(16) float qs[REP][HD];
@@ -458,11 +461,7 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   __shared__ float ored[NW][REP][HD];
   __shared__ __align__(16) uint16_t knew[HD];
   __shared__ __align__(16) uint16_t vnew[HD];
-  __shared__ int last;
-  const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
-  // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
-  const int S = T <= 16 * NW ? 1 : min((int)gridDim.y, (T + 63) / 64);
-  if (s >= S) return;
+  const int pos = a.ctl->pos, T = pos + 1;
   const int kvd = a.nkv * HD;
   const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -593,19 +592,31 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
       const float f = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);
       L = __builtin_fmaf(wl[w][j], f, L); O = __builtin_fmaf(f, ored[w][j][i], O);
     }
-    if (S == 1) a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
-    else {
+    if (S == 1) {
+      a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
+    } else {
       // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback.
       // Layout: unnormalised outputs [nh][splits][HD], then (max, sum) pairs [nh][splits][2]
-      const size_t hs = (size_t)(g * REP + j) * gridDim.y + s;
+      const size_t hs = (size_t)(g * REP + j) * ys + s;
       if (i == 0) {
-        float *ml = a.part + (size_t)a.nh * gridDim.y * HD + 2 * hs;
+        float *ml = a.part + (size_t)a.nh * ys * HD + 2 * hs;
         __hip_atomic_store(ml, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(ml + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __hip_atomic_store(a.part + hs * HD + i, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+}
+
+template <int HD, int REP>
+__global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs a) {
+  constexpr int NW = attn_waves(HD, REP);
+  __shared__ int last;
+  const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
+  // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
+  const int S = T <= 16 * NW ? 1 : min((int)gridDim.y, (T + 63) / 64);
+  if (s >= S) return;
+  attn_split<HD, REP>(a, g, s, S, gridDim.y);
   if (S == 1) return;
   // this thread's coherent stores have completed before the workgroup's counter bump
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -617,6 +628,7 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   }
   __syncthreads();
   if (!last) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   // the last split merges the S partials (model_llama.cpp:160-165: M = max m_c, f_c = exp(m_c - M),
   // L = sum l_c f_c, O = sum f_c o_c / L).  One agent-scope acquire (an L2 invalidate: the partials were written
   // through by other workgroups); wave j reduces head j's (m, l) over the splits, one per lane; then P threads share

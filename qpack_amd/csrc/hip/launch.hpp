@@ -42,7 +42,7 @@ struct MvArgs {
   int32_t *dbg_sums;      // optional: exact int32 accumulators [rows, cols/128] (q8) or [rows, cols/32] (q4), segment 0
   int16_t *dbg_xq;        // optional: the quantised activation (workgroup 0 writes it)
   float *dbg_bs;          // optional: the activation block scales
-  int dbg_mode;           // measurement only: bit 0 skips the dot products, bit 1 skips the activation prologue
+  int dbg_mode;           // measurement only: bit 0 skips the dot products, bit 1 skips the activation prologue, bit 2 the epilogue
   int upw;                // set by the launcher: the most units one wave owns (sizes the per-wave LDS)
 };
 
