@@ -410,6 +410,7 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 constexpr int kAttnMaxSplits = 64;
 // positions per context split: one 16-position block per wave of the workgroup
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // sum / max over aligned rows of 16 lanes (every lane of the row gets the result)
 __device__ __forceinline__ float row16_sum(float v) {
@@ -614,7 +615,8 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   __shared__ int last;
   const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
   // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
-  const int S = T <= 16 * NW ? 1 : min((int)gridDim.y, (T + 63) / 64);
+  const int smax = a.single_max > 0 ? a.single_max : 16 * NW, sp = a.split_pos > 0 ? a.split_pos : 64;
+  const int S = T <= smax ? 1 : min((int)gridDim.y, (T + sp - 1) / sp);
   if (s >= S) return;
   attn_split<HD, REP>(a, g, s, S, gridDim.y);
   if (S == 1) return;
@@ -630,17 +632,19 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
   if (!last) return;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   // the last split merges the S partials (model_llama.cpp:160-165: M = max m_c, f_c = exp(m_c - M),
-  // L = sum l_c f_c, O = sum f_c o_c / L).  One agent-scope acquire (an L2 invalidate: the partials were written
-  // through by other workgroups); wave j reduces head j's (m, l) over the splits, one per lane; then P threads share
-  // each (head, 4 dims) column of partials, split c going to thread c mod P, and add their sums in LDS.
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // L = sum l_c f_c, O = sum f_c o_c / L).  The partials were written through to memory by other workgroups before
+  // their counter bumps; they are read with coherent loads (no acquire fence: that is an L2 invalidate, far slower).
+  // Wave j reduces head j's (m, l) over the splits, one per lane; then P threads share each (head, 4 dims) column of
+  // partials, split c going to thread c mod P, and add their sums in LDS.
+  auto cload = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   __shared__ float fw[REP][kAttnMaxSplits], linv[REP];
   __shared__ float4 opart[NW * 64];
   const float *ml = a.part + (size_t)a.nh * gridDim.y * HD + 2 * (size_t)g * REP * gridDim.y;
   if (wave < REP) {
     const int j = wave;
     const bool on = lane < S;
-    const float2 v = on ? *(const float2 *)(ml + 2 * ((size_t)j * gridDim.y + lane)) : make_float2(-INFINITY, 0.f);
+    const float *mp = ml + 2 * ((size_t)j * gridDim.y + lane);
+    const float2 v = on ? make_float2(cload(mp), cload(mp + 1)) : make_float2(-INFINITY, 0.f);
     const float M = wave_max(v.x);
     const float f = on && v.x != -INFINITY ? expf(v.x - M) : 0.f;
     const float L = wave_sum(v.y * f);
@@ -656,9 +660,13 @@ __global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs
     const int j = e / (HD / 4), i4 = e % (HD / 4);
     const float4 *ph = (const float4 *)(a.part + ((size_t)(g * REP + j) * gridDim.y) * HD) + i4;
     for (int c0 = part; c0 < S; c0 += 8 * P) {   // 8 independent loads in flight
-      float4 v[8];
+      f32x4 v[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = c0 + k * P < S ? ph[(size_t)(c0 + k * P) * (HD / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int k = 0; k < 8; k++) {   // coherent 16-byte loads (clamped in range; unused ones are not summed)
+        const int c = c0 + k * P < S ? c0 + k * P : 0;
+        asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[k]) : "v"(ph + (size_t)c * (HD / 4)));
+      }
+      asm volatile("s_waitcnt vmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
 #pragma unroll
       for (int k = 0; k < 8; k++)
         if (c0 + k * P < S) {

@@ -93,6 +93,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   // min(this, ceil(T / 64)) of them beyond one workgroup's reach)
   max_chunks_ = std::max(1, std::min(64, (ctx_ + 63) / 64));
   if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(64, atoi(e)));
+  if (const char *e = getenv("QPH_ATTN_SINGLE")) attn_single_ = std::max(0, atoi(e));
+  if (const char *e = getenv("QPH_ATTN_SPLIT_POS")) attn_split_pos_ = std::max(0, atoi(e));
   counters_ = (int *)dalloc(4ull * nkv);
   const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
   kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
@@ -186,6 +188,7 @@ void HipLlama::enqueue_layer(int l) {
     a.kc = kc_ + (size_t)l * ctx_ * kvd_; a.vc = vc_ + (size_t)l * ctx_ * kvd_;
     a.cos_t = cos_; a.sin_t = sin_; a.ctl = ctl_; a.part = part_; a.att = att_;
     a.nh = cfg_.heads; a.nkv = cfg_.kv_heads; a.hd = cfg_.head_dim; a.max_chunks = max_chunks_; a.counters = counters_;
+    a.single_max = attn_single_; a.split_pos = attn_split_pos_;
     QPH_CK(launch_attention(a, st_));
   }
   {  // wo + residual
@@ -453,7 +456,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
       case 5: {
         AttnArgs t{}; t.q = q_; t.k = k_; t.v = v_; t.kc = kc_; t.vc = vc_; t.cos_t = cos_; t.sin_t = sin_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
-        t.max_chunks = max_chunks_; t.counters = counters_;
+        t.max_chunks = max_chunks_; t.counters = counters_; t.single_max = attn_single_; t.split_pos = attn_split_pos_;
         QPH_CK(launch_attention(t, st_)); break;
       }
       default: throw std::runtime_error("time_kernel: unknown kernel id");

@@ -46,6 +46,7 @@ class HipLlama {
   qph_config cfg_;
   int ctx_ = 0, kvd_ = 0, qd_ = 0, max_chunks_ = 1, cus_ = 256, head_grid_ = 0;
   int *counters_ = nullptr;
+  int attn_single_ = 0, attn_split_pos_ = 0;   // attention split policy (0: the kernel's defaults)
   int pos_ = 0;
   unsigned slot_ = 0;
   hipStream_t st_ = nullptr;
