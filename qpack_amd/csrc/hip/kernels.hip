@@ -392,87 +392,130 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 }
 
 // ------------------------------------------------------------------ decode attention (split-K over the context)
-// grid (kv group g, split s), 16 waves (8 for wide GQA groups).  The number of active splits follows the context: while
-// every wave needs at most one 16-position block (T <= 16 x waves) one workgroup per kv group does everything and no
-// cross-workgroup merge is needed; beyond that S_eff = min(grid.y, ceil(T / 64)) splits, the waves of a split taking
-// contiguous runs of whole blocks - a mid-size context spreads over many CUs, a 16K context keeps all 16 waves busy.  Split s takes positions [s T / S_eff,
-// (s + 1) T / S_eff); each wave a contiguous sub-range, streamed straight from HBM 16 positions at a time with the next
-// block's K and V loads in flight (double-buffered registers).
+// grid (kv group g, split s), 8 waves.  The number of active splits follows the context: while every wave needs at
+// most one 32-position block (T <= 256) one workgroup per kv group does everything and no cross-workgroup merge is
+// needed; beyond that S_eff = min(grid.y, ceil(T / 64)) splits.  Split s takes positions [s T / S_eff, (s + 1) T /
+// S_eff); the waves take contiguous runs of whole blocks, streamed straight from HBM with the next block's loads in
+// flight.
 // The workgroup applies RoPE to its rep query heads (rotate-half with the reference's contraction
 // a' = fma(a, cos, -(b sin)), b' = fma(b, cos, a sin), model_llama.cpp:176); the workgroup owning the current position
-// writes the rotated k and the v row into the cache as fp16 (round to nearest even, to_f16).
-//   scores: LPP = HD / 8 lanes share a position, each holding 8 dims of K and of every query head; DPP sums the LPP
-//           partial dots; scale 1/sqrt(hd) as in attend() (model_llama.cpp:137-146).
-//   online softmax per wave and head (max and sum over rows of 16 lanes, one head per row); values: lane owns HD / 64 dims.
-// The wave partials merge in LDS; with several splits the last one to finish (release / acquire on a per-group
-// counter, which that workgroup resets) merges the split partials in split order - the merge of model_llama.cpp:160-165:
+// writes the rotated k and the v row into the cache as fp16 (round to nearest even, to_f16) and uses its LDS copy.
+// Per wave (MFMA, see attn_split): scores S^T = K q^T, an online softmax per head, values O^T += V^T P^T; the wave
+// partials merge in LDS; with several splits the last one to finish (a per-group counter, which that workgroup
+// resets) merges the split partials in split order - the merge of model_llama.cpp:160-165:
 // M = max m, L = sum l e^(m - M), out = sum o e^(m - M) * (1 / L).
 constexpr int kAttnMaxSplits = 64;
-// positions per context split: one 16-position block per wave of the workgroup
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// sum / max over aligned rows of 16 lanes (every lane of the row gets the result)
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_f<kDppQuadXor1>(v); v += dpp_f<kDppQuadXor2>(v); v += dpp_f<kDppHalfMirror>(v); v += dpp_f<0x140>(v);
-  return v;
-}
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f<kDppQuadXor1>(v)); v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
-  v = fmaxf(v, dpp_f<kDppHalfMirror>(v)); v = fmaxf(v, dpp_f<0x140>(v));
-  return v;
+// the waves of a split -> its [m, l, o]: S == 1 writes the normalised heads to a.att, otherwise the unnormalised
+// output and (max, sum) to a.part (waves 0 .. nact - 1 hold positions; ored rows HS floats apart)
+template <int HD, int REP, int NW, int HS>
+__device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s, int S, int ys, int nact,
+                                                const float (*wm)[REP], const float (*wl)[REP], const float (*ored)[REP][HS]) {
+  __shared__ float fwv[NW][REP], mlv[REP][2];
+  // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M) (in wave order)
+  if (threadIdx.x < REP) {
+    const int j = threadIdx.x;
+    float M = wm[0][j];
+    for (int w = 1; w < nact; w++) M = fmaxf(M, wm[w][j]);
+    float L = 0.f;
+    for (int w = 0; w < nact; w++) {
+      const float f = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);
+      fwv[w][j] = f; L = __builtin_fmaf(wl[w][j], f, L);
+    }
+    mlv[j][0] = M; mlv[j][1] = L;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
+    const int j = e / HD, i = e % HD;
+    float O = 0.f;
+    for (int w = 0; w < nact; w++) O = __builtin_fmaf(fwv[w][j], ored[w][j][i], O);
+    const float M = mlv[j][0], L = mlv[j][1];
+    if (S == 1) {
+      a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
+    } else {
+      // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback.
+      // Layout: unnormalised outputs [nh][splits][HD], then (max, sum) pairs [nh][splits][2]
+      const size_t hs = (size_t)(g * REP + j) * ys + s;
+      if (i == 0) {
+        float *ml = a.part + (size_t)a.nh * ys * HD + 2 * hs;
+        __hip_atomic_store(ml, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ml + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(a.part + hs * HD + i, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
-// one 16-position block of one wave: K pieces (lane = position-in-pass x 8-dim slice) and V dims (lane owns VD dims)
+// Split s of S of kv group g (ys = the partial buffer's split stride).  Each wave streams its positions in 32-position
+// blocks with the next block's K and V loads in flight (K in two register sets, alternating):
+//   scores  S^T[p][h] = K[p] . q[h] on v_mfma_f32_16x16x32_f16: A = K rows as stored (exact fp16, loaded straight
+//           from the cache in the A layout), B = q^T with the group's REP heads as columns; q (fp32, RoPE applied)
+//           enters as hi + lo halves (hi = f16(q), lo = f16(q - hi)) - two MFMAs, exact products, fp32 sums;
+//           scaled by 1/sqrt(hd) like attend() (model_llama.cpp:137-146);
+//   softmax online per head column: lane l holds head l % 16 at positions 4 (l / 16) + i of each 16-row tile;
+//   values  O^T[d][h] += V^T[d][p] P^T[p][h]; V goes through a per-wave LDS tile transposed (dims x positions) for
+//           the A operand; P (hi + lo halves) stays in registers: the C layout of the two score tiles is the B
+//           layout once the k index runs over positions {4 (l / 16) + i} and {16 + 4 (l / 16) + i}.
+constexpr int kAttnMfWaves = 8, kAttnMfBlk = 32;
 template <int HD>
-struct KvBlock {
-  static constexpr int LPP = HD / 8, PPI = kWave / LPP, KP = 16 / PPI, VD = HD / kWave;
-  u32x4 k[KP];
-  uint32_t v[16];
+struct MfK {   // K of one 32-position block in the A layout: [2 tiles][HD / 32] 16-byte pieces
+  static constexpr int KS = HD / 32;
+  u32x4 k[2][KS];
 };
 template <int HD>
-__device__ __forceinline__ void kv_load(const uint16_t *kc, const uint16_t *vc, int kvd, int g, int tb, int te, int lane, KvBlock<HD> &b) {
-  using B = KvBlock<HD>;
-  const int psub = lane / B::LPP, dsl = lane % B::LPP;
+struct MfV {   // V of one block: HD / 16 16-byte pieces, piece i = position (lane + 64 i) / (HD / 8)
+  static constexpr int NV = HD / 16;
+  u32x4 v[NV];
+};
+// rows past te read row tb instead (finite values, masked out of the softmax)
+template <int HD>
+__device__ __forceinline__ void mf_load_k(const uint16_t *kc, int kvd, int g, int tb, int te, int lane, MfK<HD> &b) {
+  const int lr = lane & 15, lg = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < B::KP; i++) {
-    const int t = tb + i * B::PPI + psub;
-    b.k[i] = *(const u32x4 *)(kc + (size_t)(t < te ? t : tb) * kvd + g * HD + dsl * 8);
+  for (int mt = 0; mt < 2; mt++) {
+    const int t = tb + 16 * mt + lr, tc = t < te ? t : tb;
+#pragma unroll
+    for (int s = 0; s < MfK<HD>::KS; s++) b.k[mt][s] = *(const u32x4 *)(kc + (size_t)tc * kvd + g * HD + 32 * s + 8 * lg);
   }
+}
+template <int HD>
+__device__ __forceinline__ void mf_load_v(const uint16_t *vc, int kvd, int g, int tb, int te, int lane, MfV<HD> &b) {
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int t = tb + i < te ? tb + i : tb;
-    if (B::VD == 2) b.v[i] = *(const uint32_t *)(vc + (size_t)t * kvd + g * HD + 2 * lane);
-    else b.v[i] = vc[(size_t)t * kvd + g * HD + lane];
+  for (int i = 0; i < MfV<HD>::NV; i++) {
+    const int c = lane + 64 * i, t = tb + c / (HD / 8), tc = t < te ? t : tb;
+    b.v[i] = *(const u32x4 *)(vc + (size_t)tc * kvd + g * HD + 8 * (c % (HD / 8)));
   }
 }
 
-// waves per attention workgroup: 16 (four per SIMD, so the latency of one wave's LDS / DPP / exp chains is covered by
-// the others), 8 where 16 would not fit the registers (wide GQA groups)
-constexpr int attn_waves(int hd, int rep) { return (hd == 64 && rep >= 7) || (hd == 128 && rep >= 5) ? 8 : 16; }
-// Split s of S of kv group g (attn_waves(HD, REP) waves; ys = the partial buffer's split stride).  S == 1 writes the
-// normalised heads to a.att; otherwise the split's unnormalised output and (max, sum) go to a.part.
 template <int HD, int REP>
 __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
-  using B = KvBlock<HD>;
-  constexpr int NW = attn_waves(HD, REP), HALF = HD / 2, LPP = B::LPP, PPI = B::PPI, VD = B::VD;
-  __shared__ __align__(16) float qs[REP][HD];
-  __shared__ float sc[NW][REP][16];
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  // LDS rows padded so the MFMA-layout accesses (16 heads / dims apart per lane) spread over the banks
+  constexpr int NW = kAttnMfWaves, HALF = HD / 2, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 4;   // VS: 8-byte aligned rows
+  constexpr int QS = HD + 4;
+  __shared__ __align__(16) float qs[REP][QS];
   __shared__ float wm[NW][REP], wl[NW][REP];
-  __shared__ float ored[NW][REP][HD];
+  __shared__ __align__(16) float ored[NW][REP][QS];
   __shared__ __align__(16) uint16_t knew[HD];
   __shared__ __align__(16) uint16_t vnew[HD];
+  __shared__ __align__(16) uint16_t vt[NW][HD * VS];
   const int pos = a.ctl->pos, T = pos + 1;
   const int kvd = a.nkv * HD;
   const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  // waves take contiguous runs of whole 16-position blocks (waves without a block idle)
-  const int nblk = (t1 - t0 + 15) / 16, bpw = (nblk + NW - 1) / NW;
-  const int wt0 = min(t1, t0 + 16 * wave * bpw), wt1 = min(t1, t0 + 16 * (wave + 1) * bpw);
-  const int nact = (nblk + bpw - 1) / bpw;   // waves holding positions (the wave merge reads only theirs)
-  // this wave's first block goes out before anything else
-  KvBlock<HD> cur, nxt;
-  if (wt0 < wt1) kv_load<HD>(a.kc, a.vc, kvd, g, wt0, wt1, lane, cur);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  // waves take contiguous runs of whole 32-position blocks (waves without a block idle)
+  const int nblk = (t1 - t0 + kAttnMfBlk - 1) / kAttnMfBlk, bpw = (nblk + NW - 1) / NW;
+  const int wt0 = min(t1, t0 + kAttnMfBlk * wave * bpw), wt1 = min(t1, t0 + kAttnMfBlk * (wave + 1) * bpw);
+  const int nact = (nblk + bpw - 1) / bpw;
+  MfK<HD> ka, kb;
+  MfV<HD> vb;
+  if (wt0 < wt1) {   // the first block goes out before anything else
+    mf_load_k<HD>(a.kc, kvd, g, wt0, wt1, lane, ka);
+    mf_load_v<HD>(a.vc, kvd, g, wt0, wt1, lane, vb);
+  }
   const float *cs = a.cos_t + (size_t)pos * HALF, *sn = a.sin_t + (size_t)pos * HALF;
   for (int e = threadIdx.x; e < REP * HALF; e += blockDim.x) {
     const int j = e / HALF, i = e % HALF; const float *qh = a.q + (size_t)(g * REP + j) * HD;
@@ -494,128 +537,133 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
     }
   }
   __syncthreads();
+  // q^T fragments: lane holds head lr (zero past REP), dims 32 s + 8 lg + 0..7, as hi / lo halves
+  h8 qh[KS], ql[KS];
+#pragma unroll
+  for (int k = 0; k < KS; k++) {
+    const float *qr = qs[lr < REP ? lr : 0] + 32 * k + 8 * lg;
+    const float4 x0 = *(const float4 *)qr, x1 = *(const float4 *)(qr + 4);
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float x = lr < REP ? xs[e] : 0.f;
+      const _Float16 h = (_Float16)x;
+      qh[k][e] = h; ql[k][e] = (_Float16)(x - (float)h);
+    }
+  }
   const float scl = 1.f / sqrtf((float)HD);
-  const int psub = lane / LPP, dsl = lane % LPP;
-  float o[REP][VD];
+  f4 o[DT];
 #pragma unroll
-  for (int j = 0; j < REP; j++)
+  for (int d = 0; d < DT; d++) o[d] = (f4){0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  uint16_t *vw = vt[wave];
+  // one block: V -> LDS, then the next block's loads (V into the same registers, K into the other set), then the
+  // scores from this block's K registers
+  auto block = [&](MfK<HD> &kcur, MfK<HD> &knxt, int tb) {
+    // V -> LDS transposed (this wave's tile; the current position's row from LDS).  Piece i of lane l holds position
+    // p, dims d0 .. d0 + 7; the lane HD / 8 away holds position p ^ 1, same dims.  The two swap halves so that the
+    // even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each writes
+    // four (p even, p odd) pairs of its dims as 32-bit words.
 #pragma unroll
-    for (int d = 0; d < VD; d++) o[j][d] = 0.f;
-  if (lane < REP) { wm[wave][lane] = -INFINITY; wl[wave][lane] = 0.f; }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  for (int tb = wt0; tb < wt1; tb += 16) {
-    const int np = wt1 - tb < 16 ? wt1 - tb : 16;
-    if (tb + 16 < wt1) kv_load<HD>(a.kc, a.vc, kvd, g, tb + 16, wt1, lane, nxt);   // next block in flight
-    // the current position's row comes from LDS (this workgroup wrote it)
-    const bool has_pos = tb <= pos && pos < tb + np;
-    // scores
+    for (int i = 0; i < NV; i++) {
+      const int c = lane + 64 * i, p = c / (HD / 8), d0 = 8 * (c % (HD / 8));
+      const u32x4 vv = tb + p == pos ? *(const u32x4 *)(vnew + d0) : vb.v[i];
+      const bool ev = (p & 1) == 0;
+      const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, kWave);
+      const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, kWave);
+      const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];   // own dims (low / high pair)
+      // word for dim pair member: (even position) | (odd position) << 16
+      const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
+      uint32_t *wr = (uint32_t *)(vw + (d0 + (ev ? 0 : 4)) * VS + (p & ~1));
+      wr[0] = (lo_x & 0xffffu) | (hi_x << 16);
+      wr[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
+      wr[VS] = (lo_y & 0xffffu) | (hi_y << 16);
+      wr[3 * VS / 2] = (lo_y >> 16) | (hi_y & 0xffff0000u);
+    }
+    if (tb + kAttnMfBlk < wt1) {
+      mf_load_v<HD>(a.vc, kvd, g, tb + kAttnMfBlk, wt1, lane, vb);
+      mf_load_k<HD>(a.kc, kvd, g, tb + kAttnMfBlk, wt1, lane, knxt);
+    }
+    // scores of the two 16-position tiles
+    f4 sc[2];
 #pragma unroll
-    for (int i = 0; i < B::KP; i++) {
-      const int p = i * PPI + psub, t = tb + p;
-      const u32x4 kw = (has_pos && t == pos) ? *(const u32x4 *)(knew + dsl * 8) : cur.k[i];
-      float kf[8];
+    for (int mt = 0; mt < 2; mt++) {
+      sc[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+      const bool cur = tb + 16 * mt + lr == pos;
 #pragma unroll
-      for (int q = 0; q < 4; q++) { kf[2 * q] = half_bits_to_float((uint16_t)(kw[q] & 0xffff)); kf[2 * q + 1] = half_bits_to_float((uint16_t)(kw[q] >> 16)); }
-#pragma unroll
-      for (int j = 0; j < REP; j++) {
-        const float4 qa = *(const float4 *)&qs[j][dsl * 8], qb = *(const float4 *)&qs[j][dsl * 8 + 4];
-        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        float d = 0.f;
-#pragma unroll
-        for (int q = 0; q < 8; q++) d = __builtin_fmaf(qv[q], kf[q], d);
-        d += dpp_f<kDppQuadXor1>(d);
-        d += dpp_f<kDppQuadXor2>(d);
-        d += dpp_f<kDppHalfMirror>(d);
-        if (LPP == 16) d += dpp_f<0x140>(d);   // row_mirror: lane i <-> 15 - i
-        if (dsl == 0 && p < np) sc[wave][j][p] = d * scl;
+      for (int k = 0; k < KS; k++) {
+        const u32x4 kw = cur ? *(const u32x4 *)(knew + 32 * k + 8 * lg) : kcur.k[mt][k];
+        const h8 kf = __builtin_bit_cast(h8, kw);
+        sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[k], sc[mt], 0, 0, 0);
+        sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[k], sc[mt], 0, 0, 0);
       }
     }
+    // online softmax of head lr over this block's positions
+    float sv[8], bm = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float x = tb + 16 * mt + 4 * lg + i < wt1 ? sc[mt][i] * scl : -INFINITY;
+        sv[4 * mt + i] = x; bm = fmaxf(bm, x);
+      }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+    const float mn = fmaxf(m, bm);
+    const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+    float rs = 0.f;
+    h8 ph, pl;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float pv = sv[j] == -INFINITY ? 0.f : expf(sv[j] - mn);
+      rs += pv;
+      const _Float16 h = (_Float16)pv;
+      ph[j] = h; pl[j] = (_Float16)(pv - (float)h);
+    }
+    rs += __shfl_xor(rs, 16, kWave);
+    rs += __shfl_xor(rs, 32, kWave);
+    l = l * corr + rs;
+    m = mn;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // online softmax: lane -> (head jp + lane / 16, position lane % 16)
-    float cfr[REP];
 #pragma unroll
-    for (int jp = 0; jp < REP; jp += 4) {
-      const int j = jp + (lane >> 4), p = lane & 15;
-      const bool hj = j < REP, ok = hj && p < np;
-      const float sv = ok ? sc[wave][hj ? j : 0][p] : -INFINITY;
-      const float mt = row16_max(sv);
-      const float mo = hj ? wm[wave][j] : 0.f, mn = fmaxf(mo, mt);
-      const float cf = mo == -INFINITY ? 0.f : expf(mo - mn);
-      const float pv = ok ? expf(sv - mn) : 0.f;
-      const float ls = row16_sum(pv);
-      if (ok) sc[wave][j][p] = pv;
-      if (hj && p == 0) { wl[wave][j] = wl[wave][j] * cf + ls; wm[wave][j] = mn; }
-#pragma unroll
-      for (int jj = jp; jj < jp + 4 && jj < REP; jj++) cfr[jj] = lane_bcast(cf, (jj - jp) * 16);
+    for (int d = 0; d < DT; d++) {
+      o[d] *= corr;
+      // V^T fragment: dim 16 d + lr, positions 4 lg + 0..3 and 16 + 4 lg + 0..3 (the k order of ph / pl)
+      const uint16_t *vr = vw + (16 * d + lr) * VS;
+      const uint2 v0 = *(const uint2 *)(vr + 4 * lg), v1 = *(const uint2 *)(vr + 16 + 4 * lg);
+      const h8 vf = __builtin_bit_cast(h8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
     }
+    // the tile is rewritten by the next block: its reads are done first
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int j = 0; j < REP; j++)
-#pragma unroll
-      for (int d = 0; d < VD; d++) o[j][d] *= cfr[j];
-    // values
-#pragma unroll
-    for (int t = 0; t < 16; t++) {
-      if (t < np) {
-        uint32_t vw = cur.v[t];
-        if (has_pos && tb + t == pos) vw = VD == 2 ? ((uint32_t)vnew[2 * lane] | ((uint32_t)vnew[2 * lane + 1] << 16)) : vnew[lane];
-        float vf[VD];
-        vf[0] = half_bits_to_float((uint16_t)(vw & 0xffff));
-        if (VD == 2) vf[VD - 1] = half_bits_to_float((uint16_t)(vw >> 16));
-#pragma unroll
-        for (int j = 0; j < REP; j++) {
-          const float p = sc[wave][j][t];
-#pragma unroll
-          for (int d = 0; d < VD; d++) o[j][d] = __builtin_fmaf(p, vf[d], o[j][d]);
-        }
-      }
-    }
-    cur = nxt;
+  };
+  for (int tb = wt0; tb < wt1; tb += 2 * kAttnMfBlk) {
+    block(ka, kb, tb);
+    if (tb + kAttnMfBlk >= wt1) break;
+    block(kb, ka, tb + kAttnMfBlk);
   }
-  // the waves -> this split's [m, l, o]
+  // this wave's (m, l, o) -> LDS: lane holds head lr, dims 16 d + 4 lg + i
+  if (lr < REP) {
+    if (lg == 0) { wm[wave][lr] = m; wl[wave][lr] = l; }
 #pragma unroll
-  for (int j = 0; j < REP; j++)
-#pragma unroll
-    for (int d = 0; d < VD; d++) ored[wave][j][lane * VD + d] = o[j][d];
+    for (int d = 0; d < DT; d++) *(float4 *)&ored[wave][lr][16 * d + 4 * lg] = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
+  }
   __syncthreads();
-  for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
-    const int j = e / HD, i = e % HD;
-    float M = wm[0][j];
-    for (int w = 1; w < nact; w++) M = fmaxf(M, wm[w][j]);
-    float L = 0.f, O = 0.f;
-    for (int w = 0; w < nact; w++) {
-      const float f = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);
-      L = __builtin_fmaf(wl[w][j], f, L); O = __builtin_fmaf(f, ored[w][j][i], O);
-    }
-    if (S == 1) {
-      a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
-    } else {
-      // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback.
-      // Layout: unnormalised outputs [nh][splits][HD], then (max, sum) pairs [nh][splits][2]
-      const size_t hs = (size_t)(g * REP + j) * ys + s;
-      if (i == 0) {
-        float *ml = a.part + (size_t)a.nh * ys * HD + 2 * hs;
-        __hip_atomic_store(ml, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(ml + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __hip_atomic_store(a.part + hs * HD + i, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored);
 }
 
 template <int HD, int REP>
-__global__ __launch_bounds__(attn_waves(HD, REP) * 64) void k_attention(AttnArgs a) {
-  constexpr int NW = attn_waves(HD, REP);
+__global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
+  constexpr int NW = kAttnMfWaves;
   __shared__ int last;
   const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
   // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
-  const int smax = a.single_max > 0 ? a.single_max : 16 * NW, sp = a.split_pos > 0 ? a.split_pos : 64;
+  const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * NW, sp = a.split_pos > 0 ? a.split_pos : 64;
   const int S = T <= smax ? 1 : min((int)gridDim.y, (T + sp - 1) / sp);
   if (s >= S) return;
   attn_split<HD, REP>(a, g, s, S, gridDim.y);
@@ -693,7 +741,11 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
   if (a.nh % a.nkv || a.nh / a.nkv > 8 || a.max_chunks < 1 || a.max_chunks > kAttnMaxSplits) return hipErrorInvalidValue;
   const dim3 grid(a.nkv, a.max_chunks);
   const int rep = a.nh / a.nkv;
-#define QPH_ATT(HD, R) if (a.hd == HD && rep == R) { const int nw = attn_waves(HD, R); hipLaunchKernelGGL((k_attention<HD, R>), grid, dim3(nw * 64), 0, st, a); return hipGetLastError(); }
+#define QPH_ATT(HD, R)                                                                                              \
+  if (a.hd == HD && rep == R) {                                                                                     \
+    hipLaunchKernelGGL((k_attention<HD, R>), grid, dim3(kAttnMfWaves * 64), 0, st, a);                              \
+    return hipGetLastError();                                                                                       \
+  }
   QPH_ATT(64, 1) QPH_ATT(64, 2) QPH_ATT(64, 3) QPH_ATT(64, 4) QPH_ATT(64, 5) QPH_ATT(64, 6) QPH_ATT(64, 7) QPH_ATT(64, 8)
   QPH_ATT(128, 1) QPH_ATT(128, 2) QPH_ATT(128, 3) QPH_ATT(128, 4) QPH_ATT(128, 5) QPH_ATT(128, 6) QPH_ATT(128, 7) QPH_ATT(128, 8)
 #undef QPH_ATT
