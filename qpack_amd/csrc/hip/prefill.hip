@@ -549,7 +549,7 @@ hipError_t launch_pf_rope(const PfRopeArgs &a, int B, hipStream_t st) {
 
 // ------------------------------------------------------------------ causal attention of a token batch (f16 MFMA)
 // Token t (position P = p0 + t) attends to cache positions [0, P] - the prompt path of model_llama.cpp:95-105.
-// A wave owns one unit = (16-token tile, query head); a workgroup's 4 waves share the kv group and stream its cache in
+// A wave owns one unit = (16-token tile, query head); a workgroup's 8 waves share the kv group and stream its cache in
 // 32-position blocks through LDS (K as stored, V transposed), with an online softmax per token:
 //   scores  S^T[p][t] = K[p] . q[t] on v_mfma_f32_16x16x32_f16: A = K rows (exact fp16), B = q^T; q is fp32, so it
 //           enters as hi + lo halves (hi = f16(q), lo = f16(q - hi)) - two MFMAs, products exact, fp32 accumulation;
@@ -558,18 +558,23 @@ hipError_t launch_pf_rope(const PfRopeArgs &a, int B, hipStream_t st) {
 //           (lane l: token l % 16, positions 4 (l / 16) + i of each 16-block) is the B layout the value MFMA needs once
 //           its k index runs over those 8 positions, so P never leaves the registers;
 //   softmax each lane keeps its token's running max and sum (reduced over the 4 lanes holding that token).
-constexpr int kPfKB = 32;   // cache positions per block
+constexpr int kPfKB = 32;      // cache positions per block
+constexpr int kPfAttnWaves = 8;   // units (16-token tile, query head) per workgroup, one per wave: they share the K / V
 template <int HD>
-__global__ __launch_bounds__(256) void k_pf_attn(PfAttnArgs a) {
+__global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
-  constexpr int KS = HD + 8, VS = kPfKB + 8, DT = HD / 16;
+  constexpr int KS = HD + 8, VS = kPfKB + 4, DT = HD / 16;   // VS: 8-byte aligned transposed rows
+  constexpr int NT = kPfAttnWaves * 64;
+  constexpr int NPC = kPfKB * (HD / 8);                        // 16-byte pieces of K (and of V) per block
+  constexpr int NP = (NPC + NT - 1) / NT;                      // ... per thread
+  static_assert(NPC % 64 == 0, "whole waves of pieces");
   __shared__ __align__(16) uint16_t ks[kPfKB * KS];
   __shared__ __align__(16) uint16_t vt[HD * VS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
   const int g = blockIdx.y, rep = a.nh / a.nkv, kvd = a.nkv * HD;
   const int ntiles = (a.ntok + 15) / 16, nunits = ntiles * rep;
-  const int u = blockIdx.x * 4 + wave;
+  const int u = blockIdx.x * kPfAttnWaves + wave;
   const bool live = u < nunits;
   const int tile = live ? u / rep : 0, head = g * rep + (live ? u % rep : 0);
   const int t = tile * 16 + lr;                        // this lane's token
@@ -577,7 +582,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(PfAttnArgs a) {
   const int ptok = a.p0 + t;                           // its position: attends to [0, ptok]
   const int wave_last = live ? a.p0 + min(tile * 16 + 15, a.ntok - 1) : -1;
   // the workgroup streams up to its last live unit's last token
-  const int ulast = min(blockIdx.x * 4 + 3, nunits - 1);
+  const int ulast = min(blockIdx.x * kPfAttnWaves + kPfAttnWaves - 1, nunits - 1);
   const int wg_last = a.p0 + min((ulast / rep) * 16 + 15, a.ntok - 1);
   const int nkb = wg_last / kPfKB + 1;
 
@@ -602,25 +607,45 @@ __global__ __launch_bounds__(256) void k_pf_attn(PfAttnArgs a) {
   const float scl = 1.f / sqrtf((float)HD);
   const uint16_t *kg = a.kc + g * HD, *vg = a.vc + g * HD;
 
+  // piece i of a block: position (tid + NT i) / (HD / 8), dims 8 ((tid + NT i) % (HD / 8)) + 0..7 (threads past the
+  // NPC pieces idle); the next block's pieces are loaded while the current one is computed
+  uint4 kr[NP], vr[NP];
+  auto load_block = [&](int pb) {
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+      const int c = tid + NT * i, pos = pb + c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+      if (c >= NPC) break;
+      const int pc = pos <= wg_last ? pos : wg_last;   // rows past the last one re-read it (masked out)
+      kr[i] = *(const uint4 *)(kg + (size_t)pc * kvd + d0);
+      vr[i] = *(const uint4 *)(vg + (size_t)pc * kvd + d0);
+    }
+  };
+  load_block(0);
   for (int kb = 0; kb < nkb; kb++) {
     const int pb = kb * kPfKB;
     __syncthreads();   // the previous block's LDS reads are done
-    for (int c = tid; c < kPfKB * (HD / 8); c += 256) {
-      const int p = c / (HD / 8), d0 = (c % (HD / 8)) * 8, pos = pb + p;
-      uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-      if (pos <= wg_last) {
-        kw = *(const uint4 *)(kg + (size_t)pos * kvd + d0);
-        vw = *(const uint4 *)(vg + (size_t)pos * kvd + d0);
-      }
-      *(uint4 *)(ks + p * KS + d0) = kw;
-      const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+    // K as stored; V transposed: the lane HD / 8 away holds position p ^ 1 with the same dims, the two swap halves so
+    // the even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each
+    // writes four (p even, p odd) pairs as 32-bit words
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        vt[(d0 + 2 * j) * VS + p] = (uint16_t)(vv[j] & 0xffff);
-        vt[(d0 + 2 * j + 1) * VS + p] = (uint16_t)(vv[j] >> 16);
-      }
+    for (int i = 0; i < NP; i++) {
+      const int c = tid + NT * i, p = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+      if (c >= NPC) break;   // wave-uniform (NPC is a multiple of 64): the shuffles below see whole waves
+      *(uint4 *)(ks + p * KS + d0) = kr[i];
+      const uint32_t vv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+      const bool ev = (p & 1) == 0;
+      const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, 64);
+      const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, 64);
+      const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
+      const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
+      uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS + (p & ~1));
+      w[0] = (lo_x & 0xffffu) | (hi_x << 16);
+      w[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
+      w[VS] = (lo_y & 0xffffu) | (hi_y << 16);
+      w[3 * VS / 2] = (lo_y >> 16) | (hi_y & 0xffff0000u);
     }
     __syncthreads();
+    if (kb + 1 < nkb) load_block(pb + kPfKB);
     if (!live || pb > wave_last) continue;
     // scores of the two 16-position halves
     f4 sc[2];
@@ -684,9 +709,9 @@ hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st) {
   if (a.ntok <= 0) return hipSuccess;
   if (a.nh % a.nkv || (a.hd != 64 && a.hd != 128) || a.lda % 4) return hipErrorInvalidValue;
   const int units = (a.ntok + 15) / 16 * (a.nh / a.nkv);
-  const dim3 grid((units + 3) / 4, a.nkv);
-  if (a.hd == 128) hipLaunchKernelGGL(k_pf_attn<128>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(k_pf_attn<64>, grid, dim3(256), 0, st, a);
+  const dim3 grid((units + kPfAttnWaves - 1) / kPfAttnWaves, a.nkv);
+  if (a.hd == 128) hipLaunchKernelGGL(k_pf_attn<128>, grid, dim3(kPfAttnWaves * 64), 0, st, a);
+  else hipLaunchKernelGGL(k_pf_attn<64>, grid, dim3(kPfAttnWaves * 64), 0, st, a);
   return hipGetLastError();
 }
 
