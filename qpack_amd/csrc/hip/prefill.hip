@@ -100,6 +100,19 @@ __device__ __forceinline__ float lds_read4(uint32_t addr) {
   asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
   return r;
 }
+// the same with a constant byte offset folded into the instruction
+template <int OFF>
+__device__ __forceinline__ v4i lds_read16o(uint32_t addr) {
+  v4i r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ float lds_read4o(uint32_t addr) {
+  float r;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
 
 // sum of each weight row over each 128-column block: out[row][block] (exact int32)
 __global__ __launch_bounds__(256) void k_rowsum_q8(const int8_t *w, int rows, int cols, int *out) {
@@ -184,11 +197,23 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) acc[mi][ni][i] = 0.f;
 
+  // per-lane LDS offsets within a stage.  Fragment rows (and tokens) 16 apart share the swizzle (row & 7), so the
+  // mi / ni / plane steps are constant offsets folded into the reads: per block only the stage base is added.
+  //   A[mi] of step ks: W row wr 64 + 16 mi + lr, segment 4 ks + lg; B[ni] likewise for token wc 32 + 16 ni + lr
+  uint32_t aoff[2], boff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    const int seg = ks * 4 + lg, row = wr * 64 + lr, tok = wc * 32 + lr;
+    aoff[ks] = row * 128 + ((seg ^ (row & 7)) << 4);
+    boff[ks] = 128 * 128 + tok * 128 + ((seg ^ (tok & 7)) << 4);
+  }
+  const uint32_t soff = 3 * 128 * 128 + 512 + 4 * (wr * 64 + 4 * lg);   // row block sums, + 64 mi
+  const uint32_t toff = 3 * 128 * 128 + 4 * (wc * 32 + lr);             // token block scales, + 64 ni
+  const uint32_t sbase = lds_addr(smem);
+
   // software pipeline: block kb's MFMAs are issued while block kb - 1's epilogue (its exact int32 sums -> rows_q8's
   // fma step) runs on the vector ALU - independent work the matrix cores and the VALU overlap
-  v4i pch[4][2], pcl[4][2];
-  float pbs[2];
-  auto epilogue_half = [&](int ni) {
+  auto epilogue_half = [&](const v4i (&pch)[4][2], const v4i (&pcl)[4][2], const float (&pbs)[2], int ni) {
 #pragma unroll
     for (int mi = 0; mi < 4; mi++)
 #pragma unroll
@@ -197,40 +222,28 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
         acc[mi][ni][i] = __builtin_fmaf(pbs[ni], (float)isum, acc[mi][ni][i]);
       }
   };
-  issue(0);
-  if (nb > 1) issue(1);
-  for (int kb = 0; kb < nb; kb++) {
+  // block kb into (ch, cl, bsc); the previous block's (pch, pcl, pbs) epilogue under its MFMAs when `prev`
+  auto block = [&](int kb, v4i (&ch)[4][2], v4i (&cl)[4][2], float (&bsc)[2], const v4i (&pch)[4][2],
+                   const v4i (&pcl)[4][2], const float (&pbs)[2], bool prev) {
     // this wave's loads of block kb have landed (block kb + 1's 7 may still be in flight), then everyone's
     if (kb + 1 < nb) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (kb + 2 < nb) issue(kb + 2);   // into the stage everyone finished reading in the previous iteration
-    const uint32_t st = lds_addr(smem + (size_t)(kb % kGStages) * kGStage);
-    const uint32_t sw = st, sh = st + 128 * 128, sl = st + 2 * 128 * 128, sbs = st + 3 * 128 * 128, sws = sbs + 512;
-    v4i ch[4][2], cl[4][2];
-    float bsc[2];
+    const uint32_t st = sbase + (uint32_t)((kb % kGStages) * kGStage);
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      const int seg = ks * 4 + lg;
+      const uint32_t pa = st + aoff[ks], pb = st + boff[ks];
       v4i A[4], BH[2], BL[2];
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++) {
-        const int row = wr * 64 + mi * 16 + lr;
-        A[mi] = lds_read16(sw + row * 128 + ((seg ^ (row & 7)) << 4));
-      }
-#pragma unroll
-      for (int ni = 0; ni < 2; ni++) {
-        const int tok = wc * 32 + ni * 16 + lr;
-        const uint32_t o = tok * 128 + ((seg ^ (tok & 7)) << 4);
-        BH[ni] = lds_read16(sh + o); BL[ni] = lds_read16(sl + o);
-      }
+      A[0] = lds_read16o<0>(pa); A[1] = lds_read16o<2048>(pa); A[2] = lds_read16o<4096>(pa); A[3] = lds_read16o<6144>(pa);
+      BH[0] = lds_read16o<0>(pb); BH[1] = lds_read16o<2048>(pb);
+      BL[0] = lds_read16o<16384>(pb); BL[1] = lds_read16o<16384 + 2048>(pb);
       if (ks == 0) {
         // the block's row sums start the lo accumulators (isum = 256 hi + lo + 128 sum(W)); hi starts at zero
+        const uint32_t ps = st + soff, pt = st + toff;
         v4i wsv[4];
-#pragma unroll
-        for (int mi = 0; mi < 4; mi++) wsv[mi] = lds_read16(sws + 4 * (wr * 64 + mi * 16 + 4 * lg));
-#pragma unroll
-        for (int ni = 0; ni < 2; ni++) bsc[ni] = lds_read4(sbs + 4 * (wc * 32 + ni * 16 + lr));
+        wsv[0] = lds_read16o<0>(ps); wsv[1] = lds_read16o<64>(ps); wsv[2] = lds_read16o<128>(ps); wsv[3] = lds_read16o<192>(ps);
+        bsc[0] = lds_read4o<0>(pt); bsc[1] = lds_read4o<64>(pt);
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BL[0]), "+v"(BL[1]),
                        "+v"(bsc[0]), "+v"(bsc[1]), "+v"(wsv[0]), "+v"(wsv[1]), "+v"(wsv[2]), "+v"(wsv[3]));
@@ -249,16 +262,23 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
           ch[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BH[ni], ch[mi][ni], 0, 0, 0);
           cl[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BL[ni], cl[mi][ni], 0, 0, 0);
         }
-      if (kb > 0) epilogue_half(ks);   // half of the previous block's epilogue under each step's MFMAs
+      if (prev) epilogue_half(pch, pcl, pbs, ks);   // half of the previous block's epilogue under each step's MFMAs
     }
+  };
+  v4i ch[4][2], cl[4][2], pch[4][2], pcl[4][2];
+  float bsc[2], pbs[2];
+  issue(0);
+  if (nb > 1) issue(1);
+  for (int kb = 0; kb < nb; kb++) {
+    block(kb, ch, cl, bsc, pch, pcl, pbs, kb > 0);
 #pragma unroll
     for (int mi = 0; mi < 4; mi++)
 #pragma unroll
       for (int ni = 0; ni < 2; ni++) { pch[mi][ni] = ch[mi][ni]; pcl[mi][ni] = cl[mi][ni]; }
     pbs[0] = bsc[0]; pbs[1] = bsc[1];
   }
-  epilogue_half(0);
-  epilogue_half(1);
+  epilogue_half(pch, pcl, pbs, 0);
+  epilogue_half(pch, pcl, pbs, 1);
   // y = acc * scale (+ bias), or y += (residual stream)
 #pragma unroll
   for (int mi = 0; mi < 4; mi++)
