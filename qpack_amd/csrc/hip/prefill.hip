@@ -138,6 +138,33 @@ hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipSt
   return hipGetLastError();
 }
 
+// rows rb .. rb + 3 of token row yt (the MFMA C layout gives a lane four consecutive rows of one token): y = v (* row
+// scale when `scaled`), then y += the residual or y = that + bias; one 16-byte access where the rows are in range and
+// the token rows 16-byte aligned
+__device__ __forceinline__ void gemm_store4(const GemmArgs &a, float *yt, int rb, float4 v, bool scaled) {
+  if (rb + 3 < a.rows && (a.ldy & 3) == 0) {
+    if (scaled) { const float4 s = *(const float4 *)(a.scale + rb); v.x = v.x * s.x; v.y = v.y * s.y; v.z = v.z * s.z; v.w = v.w * s.w; }
+    if (a.resid) {
+      const float4 o = *(const float4 *)(yt + rb);
+      v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+    } else if (a.bias) {
+      const float4 b = *(const float4 *)(a.bias + rb);
+      v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+    }
+    *(float4 *)(yt + rb) = v;
+    return;
+  }
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = rb + i;
+    if (r >= a.rows) continue;
+    float x = scaled ? vv[i] * a.scale[r] : vv[i];
+    if (a.resid) yt[r] = yt[r] + x;
+    else { if (a.bias) x = x + a.bias[r]; yt[r] = x; }
+  }
+}
+
 __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -231,36 +258,45 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
     __builtin_amdgcn_s_barrier();
     if (kb + 2 < nb) issue(kb + 2);   // into the stage everyone finished reading in the previous iteration
     const uint32_t st = sbase + (uint32_t)((kb % kGStages) * kGStage);
+    // both steps' fragments are read up front; step 1's land while step 0 multiplies
+    v4i A[2][4], BH[2][2], BL[2][2];
+    v4i wsv[4];
+    {
+      const uint32_t pa = st + aoff[0], pb = st + boff[0], ps = st + soff, pt = st + toff;
+      A[0][0] = lds_read16o<0>(pa); A[0][1] = lds_read16o<2048>(pa); A[0][2] = lds_read16o<4096>(pa); A[0][3] = lds_read16o<6144>(pa);
+      BH[0][0] = lds_read16o<0>(pb); BH[0][1] = lds_read16o<2048>(pb);
+      BL[0][0] = lds_read16o<16384>(pb); BL[0][1] = lds_read16o<16384 + 2048>(pb);
+      wsv[0] = lds_read16o<0>(ps); wsv[1] = lds_read16o<64>(ps); wsv[2] = lds_read16o<128>(ps); wsv[3] = lds_read16o<192>(ps);
+      bsc[0] = lds_read4o<0>(pt); bsc[1] = lds_read4o<64>(pt);
+    }
+    {
+      const uint32_t pa = st + aoff[1], pb = st + boff[1];
+      A[1][0] = lds_read16o<0>(pa); A[1][1] = lds_read16o<2048>(pa); A[1][2] = lds_read16o<4096>(pa); A[1][3] = lds_read16o<6144>(pa);
+      BH[1][0] = lds_read16o<0>(pb); BH[1][1] = lds_read16o<2048>(pb);
+      BL[1][0] = lds_read16o<16384>(pb); BL[1][1] = lds_read16o<16384 + 2048>(pb);
+    }
+    // LDS reads complete in order: 8 outstanding = step 1's
+    asm volatile("s_waitcnt lgkmcnt(8)"
+                 : "+v"(A[0][0]), "+v"(A[0][1]), "+v"(A[0][2]), "+v"(A[0][3]), "+v"(BH[0][0]), "+v"(BH[0][1]),
+                   "+v"(BL[0][0]), "+v"(BL[0][1]), "+v"(bsc[0]), "+v"(bsc[1]), "+v"(wsv[0]), "+v"(wsv[1]), "+v"(wsv[2]),
+                   "+v"(wsv[3]));
+    // the block's row sums start the lo accumulators (isum = 256 hi + lo + 128 sum(W)); hi starts at zero
+#pragma unroll
+    for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++) { ch[mi][ni] = (v4i){0, 0, 0, 0}; cl[mi][ni] = wsv[mi] * 128; }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      const uint32_t pa = st + aoff[ks], pb = st + boff[ks];
-      v4i A[4], BH[2], BL[2];
-      A[0] = lds_read16o<0>(pa); A[1] = lds_read16o<2048>(pa); A[2] = lds_read16o<4096>(pa); A[3] = lds_read16o<6144>(pa);
-      BH[0] = lds_read16o<0>(pb); BH[1] = lds_read16o<2048>(pb);
-      BL[0] = lds_read16o<16384>(pb); BL[1] = lds_read16o<16384 + 2048>(pb);
-      if (ks == 0) {
-        // the block's row sums start the lo accumulators (isum = 256 hi + lo + 128 sum(W)); hi starts at zero
-        const uint32_t ps = st + soff, pt = st + toff;
-        v4i wsv[4];
-        wsv[0] = lds_read16o<0>(ps); wsv[1] = lds_read16o<64>(ps); wsv[2] = lds_read16o<128>(ps); wsv[3] = lds_read16o<192>(ps);
-        bsc[0] = lds_read4o<0>(pt); bsc[1] = lds_read4o<64>(pt);
+      if (ks == 1)
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BL[0]), "+v"(BL[1]),
-                       "+v"(bsc[0]), "+v"(bsc[1]), "+v"(wsv[0]), "+v"(wsv[1]), "+v"(wsv[2]), "+v"(wsv[3]));
-#pragma unroll
-        for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-          for (int ni = 0; ni < 2; ni++) { ch[mi][ni] = (v4i){0, 0, 0, 0}; cl[mi][ni] = wsv[mi] * 128; }
-      } else {
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(BH[0]), "+v"(BH[1]), "+v"(BL[0]), "+v"(BL[1]));
-      }
+                     : "+v"(A[1][0]), "+v"(A[1][1]), "+v"(A[1][2]), "+v"(A[1][3]), "+v"(BH[1][0]), "+v"(BH[1][1]),
+                       "+v"(BL[1][0]), "+v"(BL[1][1]));
 #pragma unroll
       for (int ni = 0; ni < 2; ni++)
 #pragma unroll
         for (int mi = 0; mi < 4; mi++) {
-          ch[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BH[ni], ch[mi][ni], 0, 0, 0);
-          cl[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], BL[ni], cl[mi][ni], 0, 0, 0);
+          ch[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks][mi], BH[ks][ni], ch[mi][ni], 0, 0, 0);
+          cl[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks][mi], BL[ks][ni], cl[mi][ni], 0, 0, 0);
         }
       if (prev) epilogue_half(pch, pcl, pbs, ks);   // half of the previous block's epilogue under each step's MFMAs
     }
@@ -286,15 +322,8 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
     for (int ni = 0; ni < 2; ni++) {
       const int t = t0 + wc * 32 + ni * 16 + lr;
       if (t >= a.ntok) continue;
-      float *yt = a.y + (size_t)t * a.ldy;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = r0 + wr * 64 + mi * 16 + 4 * lg + i;
-        if (r >= a.rows) continue;
-        float v = acc[mi][ni][i] * a.scale[r];
-        if (a.resid) yt[r] = yt[r] + v;
-        else { if (a.bias) v = v + a.bias[r]; yt[r] = v; }
-      }
+      gemm_store4(a, a.y + (size_t)t * a.ldy, r0 + wr * 64 + mi * 16 + 4 * lg,
+                  make_float4(acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]), true);
     }
 }
 
@@ -510,15 +539,8 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
     for (int ni = 0; ni < 2; ni++) {
       const int t = t0 + wc * 32 + ni * 16 + lr;
       if (t >= a.ntok) continue;
-      float *yt = a.y + (size_t)t * a.ldy;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = r0 + wr * 64 + mi * 16 + 4 * lg + i;
-        if (r >= a.rows) continue;
-        const float v = acc[mi][ni][i];
-        if (a.resid) yt[r] = yt[r] + v;
-        else yt[r] = a.bias ? v + a.bias[r] : v;
-      }
+      gemm_store4(a, a.y + (size_t)t * a.ldy, r0 + wr * 64 + mi * 16 + 4 * lg,
+                  make_float4(acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]), false);
     }
 }
 
