@@ -76,6 +76,12 @@ int qph_prefill(qph_model *m, const int *tokens, int n, int want, float *out);
 int qph_greedy_run(qph_model *m, int token, int n, int *out, int *produced);
 /* Model::prefill_all (qpack.h:152): logits of every position, n x vocab floats */
 int qph_prefill_all(qph_model *m, const int *tokens, int n, float *logits);
+/* Model::step / prefill with the logits kept on the device: the M largest (index, value) pairs of the last token's
+ * logits, value descending and the lower index first among equal values - what the sampler's top_m and sort compute
+ * from a logits vector (/root/reference/src/sampler.cpp:12-27, :41-42), here without copying the vocab floats to the
+ * host.  1 <= M <= min(512, vocab); a caller wanting more candidates takes the logits (want = 1) instead. */
+int qph_step_topk(qph_model *m, int token, int M, int *idx, float *val);
+int qph_prefill_topk(qph_model *m, const int *tokens, int n, int M, int *idx, float *val);
 /* Model::reset (qpack.h:150) */
 int qph_reset(qph_model *m);
 /* Model::rewind (qpack.h:160): keep the first pos tokens (0 <= pos <= current); *ok = 0 when pos is out of range */
@@ -115,6 +121,9 @@ int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int 
  * (matmul / mm_q8 / mm_q4, kernels.cpp:97-143, kernels_x86.cpp:287-371).  q8 rows use rows_q8's float epilogue per
  * token, so every Y row equals qph_kernel_matvec on that x; q4 rows have exact int32 group sums and their own fp32 order. */
 int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y);
+
+/* The top-M selection of qph_step_topk on a host vector x[n] (parity hook; 1 <= M <= min(512, n)). */
+int qph_kernel_topk(const float *x, int n, int M, int *idx, float *val);
 
 /* ---- synthetic models (no reference counterpart: the reference's files come from convert_llama.py / qpack-quantize).
  * Writes a seeded random-init Llama-family QPACK2 file; see qpack_amd/csrc/host/synth.cpp for the exact rules. */

@@ -3,11 +3,12 @@
   HipLlama.load(path)   - a QPACK1/QPACK2 file on the GPU (the qp::Model surface: step / prefill / greedy_run / ...)
   write_synthetic(...)  - seeded random-init QPACK2 models of the BASELINE shapes
   kernel_matvec(...)    - the product's matvec kernel on one matrix, with its exact int32 accumulators (parity hook)
-  kernel_matmul(...)    - the product's batched prefill kernels on one q8 matrix (parity hook)
+  kernel_matmul(...)    - the product's batched prefill kernels on one q8 / q4 matrix (parity hook)
+  kernel_topk(...)      - the device top-M selection of step_topk on one vector (parity hook)
 """
 from ._lib import LIB_PATH, QPH_F32, QPH_Q4, QPH_Q8, QphError, device_count, lib
-from .model import HipLlama, kernel_matmul, kernel_matvec, time_copy
+from .model import HipLlama, kernel_matmul, kernel_matvec, kernel_topk, time_copy
 from .synth import CONFIGS, Shape, write_synthetic
 
-__all__ = ["HipLlama", "kernel_matmul", "kernel_matvec", "time_copy", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
+__all__ = ["HipLlama", "kernel_matmul", "kernel_matvec", "kernel_topk", "time_copy", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
            "QPH_F32", "QPH_Q8", "QPH_Q4"]

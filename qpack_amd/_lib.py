@@ -55,6 +55,8 @@ SIGNATURES = {
     "qph_prefill": (_I, [_P, _IP, _I, _I, _FP]),
     "qph_greedy_run": (_I, [_P, _I, _I, _IP, _IP]),
     "qph_prefill_all": (_I, [_P, _IP, _I, _FP]),
+    "qph_step_topk": (_I, [_P, _I, _I, _IP, _FP]),
+    "qph_prefill_topk": (_I, [_P, _IP, _I, _I, _IP, _FP]),
     "qph_reset": (_I, [_P]),
     "qph_rewind": (_I, [_P, _I, _IP]),
     "qph_set_pos": (_I, [_P, _I]),
@@ -66,6 +68,7 @@ SIGNATURES = {
     "qph_time_copy": (_I, [C.c_int64, _I, _FP]),
     "qph_kernel_matvec": (_I, [_I, _P, _P, _I, _I, _FP, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int16), _FP]),
     "qph_kernel_matmul": (_I, [_I, _P, _P, _I, _I, _FP, _I, _FP]),
+    "qph_kernel_topk": (_I, [_FP, _I, _I, _IP, _FP]),
     "qph_synth_write": (_I, [C.POINTER(SynthSpecC), C.c_char_p, _I]),
 }
 

@@ -126,6 +126,15 @@ int qph_greedy_run(qph_model *m, int token, int n, int *out, int *produced) {
 int qph_prefill_all(qph_model *m, const int *tokens, int n, float *logits) {
   QPH_API_TRY({ need(m, "model"); need(tokens, "tokens"); need(logits, "logits"); m->m->prefill_all(tokens, n, logits); });
 }
+int qph_step_topk(qph_model *m, int token, int M, int *idx, float *val) {
+  QPH_API_TRY({ need(m, "model"); need(idx, "idx"); need(val, "val"); m->m->step_topk(token, M, idx, val); });
+}
+int qph_prefill_topk(qph_model *m, const int *tokens, int n, int M, int *idx, float *val) {
+  QPH_API_TRY({
+    need(m, "model"); need(tokens, "tokens"); need(idx, "idx"); need(val, "val");
+    m->m->prefill_topk(tokens, n, M, idx, val);
+  });
+}
 int qph_reset(qph_model *m) { QPH_API_TRY({ need(m, "model"); m->m->reset(); }); }
 int qph_rewind(qph_model *m, int pos, int *ok) {
   QPH_API_TRY({ need(m, "model"); const bool r = m->m->rewind(pos); if (ok) *ok = r ? 1 : 0; });
@@ -207,6 +216,26 @@ int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int 
   });
 }
 
+int qph_kernel_topk(const float *x, int n, int M, int *idx, float *val) {
+  QPH_API_TRY({
+    need(x, "x"); need(idx, "idx"); need(val, "val");
+    if (n <= 0 || M < 1 || M > qph::kTopkMax || M > n) throw std::invalid_argument("topk: 1 <= M <= min(512, n) required");
+    std::vector<void *> bufs;
+    auto alloc = [&](size_t b) { void *p = nullptr; hck(hipMalloc(&p, b), "hipMalloc"); bufs.push_back(p); return p; };
+    try {
+      const size_t keys = qph::topk_scratch_keys(n, M);
+      float *dx = (float *)alloc(4ull * n), *dv = (float *)alloc(4ull * M);
+      int *di = (int *)alloc(4ull * M);
+      uint64_t *ka = (uint64_t *)alloc(8 * keys), *kb = (uint64_t *)alloc(8 * keys);
+      hck(hipMemcpy(dx, x, 4ull * n, hipMemcpyHostToDevice), "upload x");
+      hck(qph::launch_topk(dx, n, M, ka, kb, di, dv, nullptr), "launch topk");
+      hck(hipDeviceSynchronize(), "topk");
+      hck(hipMemcpy(idx, di, 4ull * M, hipMemcpyDeviceToHost), "download idx");
+      hck(hipMemcpy(val, dv, 4ull * M, hipMemcpyDeviceToHost), "download val");
+    } catch (...) { for (void *p : bufs) (void)hipFree(p); throw; }
+    for (void *p : bufs) (void)hipFree(p);
+  });
+}
 int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y) {
   QPH_API_TRY({
     need(q, "q"); need(scale, "scale"); need(X, "X"); need(Y, "Y");

@@ -4,6 +4,7 @@
 
 #include <stdexcept>
 #include <string>
+#include <utility>
 
 #include "common.hpp"
 
@@ -60,6 +61,13 @@ size_t mv_lds_bytes(int cols, int waves, int per_wave);
 void mv_plan(MvArgs &a, int epi);
 // grid_cap: the most workgroups (EPI_ARGMAX writes one (max, index) partial per workgroup launched)
 hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st);
+
+// the M largest (index, value) pairs of x[n] (device), value descending and the lower index first among equal values
+// (sampler.cpp:12-27), into idx[M] / val[M] (device); scratch buf_a / buf_b of topk_scratch_keys(n, M) keys each
+constexpr int kTopkMax = 512;
+size_t topk_scratch_keys(int n, int M);
+hipError_t launch_topk(const float *x, int n, int M, uint64_t *buf_a, uint64_t *buf_b, int *idx, float *val,
+                       hipStream_t st);
 
 // x[0..d) = row ctl->tok of the embedding (row_f32 semantics, /root/reference/src/kernels.cpp:146-162)
 hipError_t launch_embed(const DMat &embed, const Ctl *ctl, float *x, hipStream_t st);

@@ -159,6 +159,12 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   QPH_CK(hipHostMalloc((void **)&hctl_, kRing * sizeof(Ctl), hipHostMallocDefault));
   QPH_CK(hipHostMalloc((void **)&hout_, 4ull * std::max(V, d), hipHostMallocDefault));
   QPH_CK(hipHostMalloc((void **)&htok_, 4ull * (ctx_ + 1), hipHostMallocDefault));
+  QPH_CK(hipHostMalloc((void **)&htopk_, 8ull * kTopkMax, hipHostMallocDefault));
+  {
+    const size_t keys = topk_scratch_keys(V, std::min(kTopkMax, V));
+    topk_a_ = (uint64_t *)dalloc(8 * keys); topk_b_ = (uint64_t *)dalloc(8 * keys);
+    topk_val_ = (float *)dalloc(8ull * kTopkMax); topk_idx_ = (int *)(topk_val_ + kTopkMax);   // one copy back
+  }
   memset(hctl_, 0, kRing * sizeof(Ctl));
   QPH_CK(hipMemset(ctl_, 0, sizeof(Ctl)));
   build_graphs();
@@ -171,6 +177,7 @@ HipLlama::~HipLlama() {
   if (hctl_) (void)hipHostFree(hctl_);
   if (hout_) (void)hipHostFree(hout_);
   if (htok_) (void)hipHostFree(htok_);
+  if (htopk_) (void)hipHostFree(htopk_);
   if (st_) (void)hipStreamDestroy(st_);
 }
 
@@ -268,9 +275,9 @@ void HipLlama::step(int tok, int want, float *out) {
   if (pos_ >= ctx_) throw std::runtime_error("context window full (" + std::to_string(ctx_) + " tokens)");
   if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
   write_ctl(tok, pos_);
-  if (want == 1) {
+  if (want == 1 || want == 3) {   // 3 (internal): logits left on the device
     run_step(1);
-    QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
+    if (want == 1) QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
   } else {
     run_step(0);
     if (want == 2) {
@@ -279,7 +286,7 @@ void HipLlama::step(int tok, int want, float *out) {
     }
   }
   pos_++;
-  if (want) {
+  if (want == 1 || want == 2) {
     QPH_CK(hipStreamSynchronize(st_));
     if (out) memcpy(out, hout_, 4ull * (want == 1 ? cfg_.vocab : cfg_.hidden));
   }
@@ -296,13 +303,14 @@ void HipLlama::prefill(const int *toks, int n, int want, float *out) {
     return;
   }
   prefill_batched(toks, n);
-  if (want == 1) {
+  if (want == 1 || want == 3) {   // 3 (internal): logits left on the device
     enqueue_head();
-    QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
+    if (want == 1) QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
   } else if (want == 2) {
     QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
     QPH_CK(hipMemcpyAsync(hout_, xn_, 4ull * cfg_.hidden, hipMemcpyDeviceToHost, st_));
   }
+  if (want == 3) return;   // the caller works on the device logits next
   QPH_CK(hipStreamSynchronize(st_));
   if (want && out) memcpy(out, hout_, 4ull * (want == 1 ? cfg_.vocab : cfg_.hidden));
 }
@@ -357,6 +365,26 @@ void HipLlama::prefill_batched(const int *toks, int n) {
     pos_ += B;
   }
   QPH_CK(hipMemcpyAsync(x_, pf_x_ + (size_t)(B - 1) * d, 4ull * d, hipMemcpyDeviceToDevice, st_));
+}
+
+void HipLlama::topk_to_host(int M, int *idx, float *val) {
+  QPH_CK(launch_topk(logits_, cfg_.vocab, M, topk_a_, topk_b_, topk_idx_, topk_val_, st_));
+  // values at [0, M), indices at [kTopkMax, kTopkMax + M) of one device buffer: one copy of the used span
+  QPH_CK(hipMemcpyAsync(htopk_, topk_val_, 4ull * (kTopkMax + M), hipMemcpyDeviceToHost, st_));
+  QPH_CK(hipStreamSynchronize(st_));
+  memcpy(val, htopk_, 4ull * M);
+  memcpy(idx, htopk_ + kTopkMax, 4ull * M);
+}
+void HipLlama::step_topk(int tok, int M, int *idx, float *val) {
+  if (M < 1 || M > std::min(kTopkMax, cfg_.vocab)) throw std::runtime_error("top-M: M must be in [1, min(512, vocab)]");
+  step(tok, 3, nullptr);
+  topk_to_host(M, idx, val);
+}
+void HipLlama::prefill_topk(const int *toks, int n, int M, int *idx, float *val) {
+  if (M < 1 || M > std::min(kTopkMax, cfg_.vocab)) throw std::runtime_error("top-M: M must be in [1, min(512, vocab)]");
+  if (n <= 0) throw std::runtime_error("prefill: no tokens");
+  prefill(toks, n, 3, nullptr);
+  topk_to_host(M, idx, val);
 }
 
 int HipLlama::greedy_run(int tok, int n, int *out) {

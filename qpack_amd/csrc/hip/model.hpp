@@ -28,6 +28,10 @@ class HipLlama {
   void prefill(const int *toks, int n, int want, float *out);
   int greedy_run(int tok, int n, int *out);
   void prefill_all(const int *toks, int n, float *logits);
+  // step / prefill whose logits stay on the device and come back as their M largest (index, value) pairs, in the
+  // sampler's order (1 <= M <= min(kTopkMax, vocab))
+  void step_topk(int tok, int M, int *idx, float *val);
+  void prefill_topk(const int *toks, int n, int M, int *idx, float *val);
   void reset() { pos_ = 0; }
   bool rewind(int pos) { if (pos < 0 || pos > pos_) return false; pos_ = pos; return true; }
   void set_pos(int pos);
@@ -65,6 +69,12 @@ class HipLlama {
   Ctl *hctl_ = nullptr;
   float *hout_ = nullptr;
   int *htok_ = nullptr;
+  // top-M of the logits: device scratch keys, results (values, then indices at kTopkMax) and their pinned host copy
+  uint64_t *topk_a_ = nullptr, *topk_b_ = nullptr;
+  int *topk_idx_ = nullptr;
+  float *topk_val_ = nullptr;
+  uint32_t *htopk_ = nullptr;
+  void topk_to_host(int M, int *idx, float *val);
   hipGraphExec_t g_state_ = nullptr, g_logits_ = nullptr, g_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
   void run_step(int parts);

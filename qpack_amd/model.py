@@ -93,6 +93,20 @@ class HipLlama:
         check(lib().qph_prefill_all(self._h, _iptr(toks), len(toks), _fptr(out)))
         return out
 
+    def step_topk(self, token, M):
+        """step with the logits kept on the device: their M largest (index, value) pairs, value descending and the
+        lower index first among equal values (the sampler's top_m order, sampler.cpp:12-27)"""
+        idx = np.empty(M, np.int32); val = np.empty(M, np.float32)
+        check(lib().qph_step_topk(self._h, int(token), int(M), _iptr(idx), _fptr(val)))
+        return idx, val
+
+    def prefill_topk(self, tokens, M):
+        """prefill with the last token's logits kept on the device: their M largest (index, value) pairs"""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        idx = np.empty(M, np.int32); val = np.empty(M, np.float32)
+        check(lib().qph_prefill_topk(self._h, _iptr(toks), len(toks), int(M), _iptr(idx), _fptr(val)))
+        return idx, val
+
     def reset(self):
         check(lib().qph_reset(self._h))
 
@@ -172,3 +186,12 @@ def kernel_matmul(q, scale, X, kind=None):
     check(lib().qph_kernel_matmul(kind, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols,
                                   _fptr(X), B, _fptr(Y)))
     return Y
+
+
+def kernel_topk(x, M):
+    """the device top-M selection on a host vector (qph_kernel_topk): (idx, val) of the M largest, value descending,
+    lower index first among equal values"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    idx = np.empty(M, np.int32); val = np.empty(M, np.float32)
+    check(lib().qph_kernel_topk(_fptr(x), len(x), int(M), _iptr(idx), _fptr(val)))
+    return idx, val
