@@ -57,8 +57,11 @@ hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st)
   if (B <= 0) return hipSuccess;
   if (a.cols % kQB || a.cols > 32768 || a.ldq % 16) return hipErrorInvalidValue;
   const size_t lds = mv_lds_bytes(a.cols, 16, 0);
-  if (pro == PRO_NORM) hipLaunchKernelGGL(k_pf_quant<PRO_NORM>, dim3(B), dim3(1024), lds, st, a);
-  else hipLaunchKernelGGL(k_pf_quant<PRO_QUANT>, dim3(B), dim3(1024), lds, st, a);
+  // the fewest threads whose two act_load passes cover the row (8 per 128-column block and pass): small workgroups,
+  // so several tokens' load -> reduce -> store chains overlap on a CU
+  const int nb = a.cols / kQB, threads = std::min(1024, std::max(256, (4 * nb + 63) / 64 * 64));
+  if (pro == PRO_NORM) hipLaunchKernelGGL(k_pf_quant<PRO_NORM>, dim3(B), dim3(threads), lds, st, a);
+  else hipLaunchKernelGGL(k_pf_quant<PRO_QUANT>, dim3(B), dim3(threads), lds, st, a);
   return hipGetLastError();
 }
 
