@@ -124,6 +124,8 @@ struct GemmArgs {
   float *y; int ldy;
   const float *bias;
   int resid;
+  // optional, same layout as y: y = silu(gate) * product (SwiGLU on the up product; gate may be y itself)
+  const float *gate;
 };
 size_t gemm_lds_bytes();
 // out[row][block] = sum of W[row] over each 128-column block
@@ -148,7 +150,5 @@ struct PfAttnArgs {
   int ntok, p0, nh, nkv, hd;
 };
 hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st);
-// g = silu(g) * u over n floats
-hipError_t launch_pf_swiglu(float *g, const float *u, size_t n, hipStream_t st);
 
 }  // namespace qph

@@ -138,7 +138,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     pf_ldq_ = (int)(wide + 15) / 16 * 16;
     pf_x_ = (float *)dalloc(4 * B * d); pf_q_ = (float *)dalloc(4 * B * qd_); pf_att_ = (float *)dalloc(4 * B * qd_);
     pf_k_ = (float *)dalloc(4 * B * kvd_); pf_v_ = (float *)dalloc(4 * B * kvd_);
-    pf_g_ = (float *)dalloc(4 * B * ff); pf_u_ = (float *)dalloc(4 * B * ff);
+    pf_g_ = (float *)dalloc(4 * B * ff);
     pf_xh_ = (int8_t *)dalloc(B * pf_ldq_); pf_xl_ = (int8_t *)dalloc(B * pf_ldq_);
     pf_xb_ = (float *)dalloc(4 * B * (pf_ldq_ / 128 + 1));
     pf_ldg_ = (pf_ldq_ / 32 + 3) / 4 * 4;
@@ -317,8 +317,8 @@ void HipLlama::prefill(const int *toks, int n, int want, float *out) {
 
 // The prompt in chunks of up to pf_cap_ tokens, each layer as matrix products (model_llama.cpp:66-130): per chunk the
 // embeddings, then per layer RMSNorm + quantise -> q / k / v products (+ bias) -> RoPE and the fp16 cache rows ->
-// causal attention -> quantise -> wo product into the residual -> RMSNorm + quantise -> gate and up products ->
-// SwiGLU -> quantise -> down product into the residual.  Leaves the last token's hidden state in x_.
+// causal attention -> quantise -> wo product into the residual -> RMSNorm + quantise -> gate product, up product
+// with SwiGLU in its store -> quantise -> down product into the residual.  Leaves the last token's hidden state in x_.
 void HipLlama::prefill_batched(const int *toks, int n) {
   const int d = cfg_.hidden, ff = cfg_.ffn, nb_ld = pf_ldq_ / 128 + 1;
   const float eps = cfg_.rms_eps;
@@ -327,11 +327,11 @@ void HipLlama::prefill_batched(const int *toks, int n) {
     a.xh = pf_xh_; a.xl = pf_xl_; a.ldq = pf_ldq_; a.xb = pf_xb_; a.ldb = nb_ld; a.xg = pf_xg_; a.ldg = pf_ldg_;
     QPH_CK(launch_pf_quant(pro, a, B, st_));
   };
-  auto gemm = [&](const DMat &m, float *y, int ldy, const float *bias, bool resid, int B) {
+  auto gemm = [&](const DMat &m, float *y, int ldy, const float *bias, bool resid, int B, const float *gate = nullptr) {
     GemmArgs a{}; a.kind = m.kind; a.w = (const int8_t *)m.q; a.scale = (const float *)m.s; a.rows = m.rows; a.cols = m.cols;
     a.wsum = m.rs; a.ldw = m.cols / 128; a.q4ns = m.q4ns; a.q4sc = m.q4sc; a.xg = pf_xg_; a.ldg = pf_ldg_;
     a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld;
-    a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0;
+    a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0; a.gate = gate;
     QPH_CK(launch_gemm(a, st_));
   };
   int B = 0;
@@ -357,8 +357,7 @@ void HipLlama::prefill_batched(const int *toks, int n) {
       gemm(ly.wo, pf_x_, d, nullptr, true, B);
       quant(PRO_NORM, pf_x_, d, ly.fn, d, B);
       gemm(ly.wg, pf_g_, ff, nullptr, false, B);
-      gemm(ly.wu, pf_u_, ff, nullptr, false, B);
-      QPH_CK(launch_pf_swiglu(pf_g_, pf_u_, (size_t)B * ff, st_));
+      gemm(ly.wu, pf_g_, ff, nullptr, false, B, pf_g_);   // h = silu(gate) * up, in place over the gate product
       quant(PRO_QUANT, pf_g_, ff, nullptr, ff, B);
       gemm(ly.wd, pf_x_, d, nullptr, true, B);
     }

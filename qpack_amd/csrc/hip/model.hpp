@@ -82,7 +82,7 @@ class HipLlama {
   static constexpr int kPfChunk = 2048;
   bool pf_ok_ = false;
   int pf_cap_ = 0, pf_ldq_ = 0, pf_ldg_ = 0;
-  float *pf_x_ = nullptr, *pf_q_ = nullptr, *pf_k_ = nullptr, *pf_v_ = nullptr, *pf_att_ = nullptr, *pf_g_ = nullptr, *pf_u_ = nullptr;
+  float *pf_x_ = nullptr, *pf_q_ = nullptr, *pf_k_ = nullptr, *pf_v_ = nullptr, *pf_att_ = nullptr, *pf_g_ = nullptr;
   float *pf_xb_ = nullptr;
   int8_t *pf_xh_ = nullptr, *pf_xl_ = nullptr;
   int *pf_tok_ = nullptr, *pf_xg_ = nullptr;

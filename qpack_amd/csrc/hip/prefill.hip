@@ -141,13 +141,19 @@ hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipSt
   return hipGetLastError();
 }
 
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + exp_poly(0.f - g)) * u; }   // kernels_x86.cpp:427-431
+
 // rows rb .. rb + 3 of token row yt (the MFMA C layout gives a lane four consecutive rows of one token): y = v (* row
-// scale when `scaled`), then y += the residual or y = that + bias; one 16-byte access where the rows are in range and
-// the token rows 16-byte aligned
+// scale when `scaled`), then y += the residual, y = that + bias, or y = silu(gate) * that; one 16-byte access where the
+// rows are in range and the token rows 16-byte aligned
 __device__ __forceinline__ void gemm_store4(const GemmArgs &a, float *yt, int rb, float4 v, bool scaled) {
+  const float *gt = a.gate ? a.gate + (yt - a.y) : nullptr;   // the gate's token row
   if (rb + 3 < a.rows && (a.ldy & 3) == 0) {
     if (scaled) { const float4 s = *(const float4 *)(a.scale + rb); v.x = v.x * s.x; v.y = v.y * s.y; v.z = v.z * s.z; v.w = v.w * s.w; }
-    if (a.resid) {
+    if (gt) {
+      const float4 g = *(const float4 *)(gt + rb);
+      v = make_float4(silu_mul(g.x, v.x), silu_mul(g.y, v.y), silu_mul(g.z, v.z), silu_mul(g.w, v.w));
+    } else if (a.resid) {
       const float4 o = *(const float4 *)(yt + rb);
       v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
     } else if (a.bias) {
@@ -163,7 +169,8 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs &a, float *yt, int rb
     const int r = rb + i;
     if (r >= a.rows) continue;
     float x = scaled ? vv[i] * a.scale[r] : vv[i];
-    if (a.resid) yt[r] = yt[r] + x;
+    if (gt) yt[r] = silu_mul(gt[r], x);
+    else if (a.resid) yt[r] = yt[r] + x;
     else { if (a.bias) x = x + a.bias[r]; yt[r] = x; }
   }
 }
@@ -762,17 +769,4 @@ hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st) {
 
 // ------------------------------------------------------------------ SwiGLU of a token batch
 // g = silu(g) * u in place (silu_mul with exp256, kernels_x86.cpp:427-431, the decode epilogue's arithmetic)
-__global__ __launch_bounds__(256) void k_pf_swiglu(float *g, const float *u, size_t n) {
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-    const float v = g[i];
-    g[i] = v / (1.f + exp_poly(0.f - v)) * u[i];
-  }
-}
-hipError_t launch_pf_swiglu(float *g, const float *u, size_t n, hipStream_t st) {
-  if (!n) return hipSuccess;
-  const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
-  hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)blocks), dim3(256), 0, st, g, u, n);
-  return hipGetLastError();
-}
-
 }  // namespace qph
