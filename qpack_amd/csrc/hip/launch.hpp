@@ -126,6 +126,9 @@ struct GemmArgs {
   int resid;
   // optional, same layout as y: y = silu(gate) * product (SwiGLU on the up product; gate may be y itself)
   const float *gate;
+  // optional (q8): a second matrix of the same shape (the up matrix, with w / scale / wsum the gate's): one launch
+  // computes both products for each 64-row tile and stores only y = silu(gate product) * (up product)
+  const int8_t *w2; const float *scale2; const int *wsum2;
 };
 size_t gemm_lds_bytes();
 // out[row][block] = sum of W[row] over each 128-column block

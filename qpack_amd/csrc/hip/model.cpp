@@ -356,8 +356,16 @@ void HipLlama::prefill_batched(const int *toks, int n) {
       quant(PRO_QUANT, pf_att_, qd_, nullptr, qd_, B);
       gemm(ly.wo, pf_x_, d, nullptr, true, B);
       quant(PRO_NORM, pf_x_, d, ly.fn, d, B);
-      gemm(ly.wg, pf_g_, ff, nullptr, false, B);
-      gemm(ly.wu, pf_g_, ff, nullptr, false, B, pf_g_);   // h = silu(gate) * up, in place over the gate product
+      if (ly.wg.kind == MK_Q8 && ly.wu.kind == MK_Q8) {   // gate and up in one launch, only h = silu(gate) * up stored
+        GemmArgs a{}; a.kind = MK_Q8; a.w = (const int8_t *)ly.wg.q; a.scale = (const float *)ly.wg.s; a.wsum = ly.wg.rs;
+        a.w2 = (const int8_t *)ly.wu.q; a.scale2 = (const float *)ly.wu.s; a.wsum2 = ly.wu.rs;
+        a.rows = ff; a.cols = d; a.ldw = d / 128; a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B;
+        a.ldq = pf_ldq_; a.ldb = nb_ld; a.y = pf_g_; a.ldy = ff;
+        QPH_CK(launch_gemm(a, st_));
+      } else {
+        gemm(ly.wg, pf_g_, ff, nullptr, false, B);
+        gemm(ly.wu, pf_g_, ff, nullptr, false, B, pf_g_);   // h = silu(gate) * up, in place over the gate product
+      }
       quant(PRO_QUANT, pf_g_, ff, nullptr, ff, B);
       gemm(ly.wd, pf_x_, d, nullptr, true, B);
     }

@@ -183,6 +183,10 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   // evenly over the XCDs, XCD x owns its eighth of them over all weight rows: its activation planes (a few MiB) stay in
   // its L2 while the weights stream past from the last-level cache.  Otherwise XCD x owns the x-th eighth of the tiles
   // in row-major order (token tile fastest), so a weight tile is reused from L2 by the token tiles that need it.
+  // paired (a.w2): the tile's 128 weight rows are 64 rows of the gate matrix (waves 0-3) and the same 64 rows of the
+  // up matrix (waves 4-7)
+  const bool paired = a.w2 != nullptr;
+  const int RT = paired ? kGM / 2 : kGM;   // output rows per tile
   int r0, t0;
   {
     const int ntt = gridDim.x, nrt = gridDim.y, n = ntt * nrt, lin = blockIdx.y * gridDim.x + blockIdx.x;
@@ -190,11 +194,11 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
     if (ntt % 8 == 0) {
       // each XCD: ntt / 8 token tiles x all nrt row tiles = n / 8 tiles, exactly its share of the round-robin
       const int tn = ntt >> 3;
-      r0 = (k / tn) * kGM; t0 = (xcd * tn + k % tn) * kGN;
+      r0 = (k / tn) * RT; t0 = (xcd * tn + k % tn) * kGN;
     } else {
       const int base = n >> 3, rem = n & 7;
       const int tile = xcd * base + min(xcd, rem) + k;
-      r0 = (tile / ntt) * kGM; t0 = (tile % ntt) * kGN;
+      r0 = (tile / ntt) * RT; t0 = (tile % ntt) * kGN;
     }
   }
   const int nb = a.cols / kQB;
@@ -208,15 +212,20 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   for (int j = 0; j < 6; j++) {
     const int q = wave * 6 + j, m = q >> 4, row = 8 * (q & 15) + drow;
     dst[j] = m * 128 * 128 + 8 * (q & 15) * 128;
-    if (m == 0) src[j] = a.w + (size_t)min(r0 + row, a.rows - 1) * a.cols + dseg * 16;
-    else src[j] = (m == 1 ? a.xh : a.xl) + (size_t)min(t0 + row, a.ntok - 1) * a.ldq + dseg * 16;
+    if (m == 0) {
+      const int8_t *wm = paired && row >= 64 ? a.w2 : a.w;
+      src[j] = wm + (size_t)min(r0 + (paired ? (row & 63) : row), a.rows - 1) * a.cols + dseg * 16;
+    } else {
+      src[j] = (m == 1 ? a.xh : a.xl) + (size_t)min(t0 + row, a.ntok - 1) * a.ldq + dseg * 16;
+    }
   }
   // one 4-byte load per wave and stage: waves 0 / 1 (and 4 / 5) the block scales of tokens 64 (w & 1) + lane, waves
   // 2 / 3 (and 6 / 7) the block sums of rows 64 (w & 1) + lane - duplicates write identical bytes to the same slot,
   // so every wave issues the same number of loads
   const int half = wave & 1;
   const bool sums = (wave & 2) != 0;
-  const char *esrc = sums ? (const char *)(a.wsum + (size_t)min(r0 + 64 * half + lane, a.rows - 1) * a.ldw)
+  const int *wsm = paired && half ? a.wsum2 : a.wsum;
+  const char *esrc = sums ? (const char *)(wsm + (size_t)min(r0 + (paired ? 0 : 64 * half) + lane, a.rows - 1) * a.ldw)
                           : (const char *)(a.xb + (size_t)min(t0 + 64 * half + lane, a.ntok - 1) * a.ldb);
   const int edst = 3 * 128 * 128 + (sums ? 512 : 0) + 256 * half;
   auto issue = [&](int kb) {
@@ -325,6 +334,43 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   }
   epilogue_half(pch, pcl, pbs, 0);
   epilogue_half(pch, pcl, pbs, 1);
+  if (paired) {
+    // the gate waves hand gate = acc * scale to the up waves through LDS ([128 tokens][64 rows] floats over the
+    // stages, free once everyone is past the loop); they store y = silu(gate) * (acc * scale2)
+    __syncthreads();
+    float *gx = (float *)smem;
+    auto scaled = [&](const float *sc, int mi, int ni) {
+      float4 v = make_float4(acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]);
+      const int rb = r0 + mi * 16 + 4 * lg;
+      v.x = v.x * sc[min(rb, a.rows - 1)]; v.y = v.y * sc[min(rb + 1, a.rows - 1)];
+      v.z = v.z * sc[min(rb + 2, a.rows - 1)]; v.w = v.w * sc[min(rb + 3, a.rows - 1)];
+      return v;
+    };
+    if (wr == 0)
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) *(float4 *)(gx + (wc * 32 + ni * 16 + lr) * 64 + mi * 16 + 4 * lg) = scaled(a.scale, mi, ni);
+    __syncthreads();
+    if (wr == 1)
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+          const int t = t0 + wc * 32 + ni * 16 + lr;
+          if (t >= a.ntok) continue;
+          const float4 g = *(const float4 *)(gx + (wc * 32 + ni * 16 + lr) * 64 + mi * 16 + 4 * lg);
+          const float4 u = scaled(a.scale2, mi, ni);
+          const float h[4] = {silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w)};
+          float *yt = a.y + (size_t)t * a.ldy;
+          const int rb = r0 + mi * 16 + 4 * lg;
+          if (rb + 3 < a.rows && (a.ldy & 3) == 0) *(float4 *)(yt + rb) = make_float4(h[0], h[1], h[2], h[3]);
+          else
+#pragma unroll
+            for (int i = 0; i < 4; i++) if (rb + i < a.rows) yt[rb + i] = h[i];
+        }
+    return;
+  }
   // y = acc * scale (+ bias), or y += (residual stream)
 #pragma unroll
   for (int mi = 0; mi < 4; mi++)
@@ -557,7 +603,9 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st) {
   if (a.ntok <= 0) return hipSuccess;
   if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
-  const dim3 grid((a.ntok + kGN - 1) / kGN, (a.rows + kGM - 1) / kGM);
+  const int rt = a.w2 ? kGM / 2 : kGM;
+  const dim3 grid((a.ntok + kGN - 1) / kGN, (a.rows + rt - 1) / rt);
+  if (a.w2 && (a.kind != MK_Q8 || !a.scale2 || !a.wsum2 || a.resid || a.bias || a.gate)) return hipErrorInvalidValue;
   if (a.kind == MK_Q8) {
     if (!a.wsum || a.ldw < a.cols / kQB) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
