@@ -37,13 +37,17 @@ typedef struct {
 } qph_config;
 
 /* One tensor with the canonical name (/root/reference/python/qpack/convert_llama.py:5-11):
- * q8: data int8 [rows, cols], scale f32 [rows];  q4: data u8 [rows, cols/2], scale fp16 [rows, cols/32];  f32: data only. */
+ * q8: data int8 [rows, cols], scale f32 [rows];  q4: data u8 [rows, cols/2], scale fp16 [rows, cols/32];  f32: data only.
+ * data_coded / scale_coded: 0 for plain bytes; > 0 when the pointer holds a QPACK3 rANS blob of that many bytes
+ * (/root/reference/include/qpack/rans.h, QPACK2.md:30-51), which the model decodes in HBM (the reference Container
+ * decodes such blobs on the CPU at load, src/container.cpp:94-121). */
 typedef struct {
   const char *name;
   int kind;
   int64_t rows, cols;
   const void *data;
   const void *scale;
+  int64_t data_coded, scale_coded;
 } qph_tensor;
 
 const char *qph_last_error(void);
@@ -53,9 +57,17 @@ int qph_device_count(int *n);
 /* ---- construction (LlamaCuda::LlamaCuda, model_llama_cuda.cu:447-484; make_llama_cuda, qpack.h:175) */
 /* max_ctx <= 0 picks min(4096, max_pos) like the reference (model_llama.cpp:27). */
 int qph_create(const qph_config *cfg, const qph_tensor *tensors, int n_tensors, int max_ctx, qph_model **out);
-/* load_model(path, max_ctx) for arch "llama" (model_llama.cpp:221-235): mmap a QPACK1/QPACK2 file, read config.json and
- * the manifest, upload to HBM */
+/* load_model(path, max_ctx) for arch "llama" (model_llama.cpp:221-235): mmap a QPACK1/QPACK2/QPACK3 file, read
+ * config.json and the manifest, upload to HBM; QPACK3's coded blobs are uploaded coded and decoded on the GPU */
 int qph_load(const char *path, int max_ctx, qph_model **out);
+/* the QPACK3 decode of the model's load: coded planes, coded / raw bytes, upload and decode-kernel HIP-event times
+ * (zeros for a plain file) */
+typedef struct {
+  int planes;
+  int64_t coded_bytes, raw_bytes;
+  float upload_ms, decode_ms;
+} qph_load_stats;
+int qph_load_stats_of(const qph_model *m, qph_load_stats *out);
 void qph_destroy(qph_model *m);   /* ~LlamaCuda */
 
 /* ---- qp::Model queries (qpack.h:131-134, :164) */
@@ -124,6 +136,15 @@ int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int 
 
 /* The top-M selection of qph_step_topk on a host vector x[n] (parity hook; 1 <= M <= min(512, n)). */
 int qph_kernel_topk(const float *x, int n, int M, int *idx, float *val);
+/* rans::decode (/root/reference/include/qpack/rans.h:101-113) of one plain or chunked blob on the GPU: blob[len] (host)
+ * -> out[cap] (host, at least the blob's raw length, which *raw receives).  Errors carry the reference's messages
+ * (truncated / bad frequency table / unknown codec / stream overrun).  *ms (optional) = the decode kernel's HIP-event
+ * duration. */
+int qph_kernel_rans_decode(const uint8_t *blob, int64_t len, uint8_t *out, int64_t cap, int64_t *raw, float *ms);
+/* qpack-pack in out (/root/reference/tools/qpack-pack.cpp, all classes): a QPACK2 file -> QPACK3, each q4 / q8 / scale /
+ * f16 / f32 blob rANS-coded (16 MiB chunks above 32 MiB) where that makes it smaller; *coded = blobs coded.  Host only
+ * (the writer of the coded files the loader decodes on the GPU). */
+int qph_pack(const char *src, const char *dst, int threads, int *coded);
 
 /* ---- synthetic models (no reference counterpart: the reference's files come from convert_llama.py / qpack-quantize).
  * Writes a seeded random-init Llama-family QPACK2 file; see qpack_amd/csrc/host/synth.cpp for the exact rules. */

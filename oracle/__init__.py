@@ -26,8 +26,8 @@ class QpackFile:
     def __init__(self, path):
         self.f = open(path, "rb")
         self.mm = mmap.mmap(self.f.fileno(), 0, access=mmap.ACCESS_READ)
-        if self.mm[:8] not in (b"QPACK1\0\0", b"QPACK2\0\0"):
-            raise ValueError(f"not a QPACK1/QPACK2 file: {path}")
+        if self.mm[:8] not in (b"QPACK1\0\0", b"QPACK2\0\0", b"QPACK3\0\0"):
+            raise ValueError(f"not a QPACK1/QPACK2/QPACK3 file: {path}")
         n, _ = struct.unpack("<II", self.mm[8:16])
         self.toc = {}
         for i in range(n):
@@ -36,11 +36,17 @@ class QpackFile:
             off, ln = struct.unpack("<QQ", self.mm[b + 56:b + 72])
             self.toc[name] = (off, ln)
         self.buf = np.frombuffer(self.mm, np.uint8)
+        self.decoded = {}
         self.manifest = json.loads(bytes(self.blob("manifest.json")).decode())
+        # QPACK3: blobs named in "encoded" hold rANS streams, decoded once here (container.cpp:94-121)
+        for name in self.manifest.get("encoded", []):
+            self.decoded[name] = rans_decode(self.blob(name))
         self.config = json.loads(bytes(self.blob("config.json")).decode())
         self.tensors = {e["name"]: e for e in self.manifest["tensors"]}
 
     def blob(self, name):
+        if name in self.decoded:
+            return self.decoded[name]
         off, ln = self.toc[name]
         return self.buf[off:off + ln]
 
@@ -114,6 +120,10 @@ def olib():
             "or_greedy": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
             "or_kcache": (C.c_void_p, [C.c_void_p]), "or_vcache": (C.c_void_p, [C.c_void_p]),
             "or_set_threads": (None, [C.c_int]),
+            "or_rans_raw_size": (C.c_int64, [C.c_void_p, C.c_int64]),
+            "or_rans_decode": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64]),
+            "or_rans_encode": (C.c_int64, [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_int64]),
+            "or_rans_freqs": (C.c_int, [C.c_void_p, C.c_int64, C.c_int, C.c_void_p]),
         }
         for k, (r, a) in sig.items():
             getattr(L, k).restype = r
@@ -212,6 +222,134 @@ def silu_mul(g, u):
 
 def f32_to_f16(x):
     return np.array([olib().or_f32_to_f16(float(v)) for v in np.asarray(x, np.float32)], np.uint16)
+
+
+# ------------------------------------------------------------------ QPACK3 rANS (include/qpack/rans.h, QPACK2.md:30-51)
+# the reference's messages (rans.h:53-76, :107-113)
+_RANS_ERR = {-1: "rans: truncated", -2: "rans: bad frequency table", -3: "rans: stream overrun", -4: "rans: unknown codec",
+             -5: "rans: output capacity", -6: "rans: cannot normalise frequencies", -7: "rans: truncated plane",
+             -8: "rans: short blob", -9: "rans: short chunked blob", -10: "rans: truncated chunk table",
+             -11: "rans: truncated chunk"}
+
+
+def rans_raw_size(blob):
+    b = np.ascontiguousarray(blob, np.uint8)
+    n = olib().or_rans_raw_size(_p(b), len(b))
+    if n < 0:
+        raise ValueError(_RANS_ERR[n])
+    if len(b) and b[0] == 3 and len(b) >= 6:
+        n = int(b[2]) | int(b[3]) << 8 | int(b[4]) << 16 | int(b[5]) << 24
+    return n
+
+
+def rans_decode(blob):
+    """plain (codec 1 / 2) or chunked (codec 3) blob -> raw bytes (rans.h:101-113)"""
+    b = np.ascontiguousarray(blob, np.uint8)
+    n = rans_raw_size(b)
+    out = np.zeros(max(n, 1), np.uint8)
+    e = olib().or_rans_decode(_p(b), len(b), _p(out), n)
+    if e:
+        raise ValueError(_RANS_ERR[e])
+    return out[:n]
+
+
+def rans_encode(raw, codec, planes):
+    """raw bytes -> one plain codec 1 / 2 blob (rans.h:81-93)"""
+    r = np.ascontiguousarray(raw, np.uint8)
+    cap = 64 + 2 * 256 * 4 + 2 * 2 * len(r) + 64
+    out = np.empty(cap, np.uint8)
+    n = olib().or_rans_encode(_p(r), len(r), codec, planes, _p(out), cap)
+    if n < 0:
+        raise ValueError(_RANS_ERR[n])
+    return out[:n].copy()
+
+
+def rans_assemble_chunked(n, chunk_raw, chunks):
+    """u8 3 | u8 0 | u32 raw_len | u32 chunk_raw | u32 nchunks | u32 comp_len[nchunks] | chunks (rans.h:115-124)"""
+    head = struct.pack("<BBIII", 3, 0, n, chunk_raw, len(chunks)) + b"".join(struct.pack("<I", len(c)) for c in chunks)
+    return np.frombuffer(head + b"".join(bytes(c) for c in chunks), np.uint8)
+
+
+PACK_THRESH, PACK_CHUNK = 32 << 20, 16 << 20   # qpack-pack: blobs above 32 MiB are coded in 16 MiB chunks (:56)
+
+
+def pack_plan(manifest):
+    """blob name -> (codec, planes) of every blob qpack-pack codes, all classes (tools/qpack-pack.cpp:43-53)"""
+    plan = {}
+    for e in manifest["tensors"]:
+        k, b = e["kind"], e["blob"]
+        if k == "q4":
+            plan[b] = (2, 1); plan[e["scale"]] = (1, 2)
+        elif k == "q8":
+            plan[b] = (1, 1)
+        elif k in ("mxfp4",):
+            plan[b] = (1, 1); plan[e["scale"]] = (1, 1)
+        elif k in ("q1", "q8g"):
+            plan[b] = (1, 1); plan[e["scale"]] = (1, 2)
+        elif k == "f16":
+            plan[b] = (1, 2)
+        elif k == "f32":
+            plan[b] = (1, 4)
+    return plan
+
+
+def write_container(path, blobs, magic):
+    """blobs: list of (name, bytes) in file order; 64-byte aligned (container.cpp:136-153)"""
+    A = 64
+    off = (16 + 72 * len(blobs) + A - 1) // A * A
+    head = bytearray(magic + struct.pack("<II", len(blobs), 0))
+    offs = []
+    for name, data in blobs:
+        head += name.encode().ljust(56, b"\0") + struct.pack("<QQ", off, len(data))
+        offs.append(off)
+        off = (off + len(data) + A - 1) // A * A
+    with open(path, "wb") as f:
+        f.write(head)
+        pos = len(head)
+        for (name, data), o in zip(blobs, offs):
+            f.write(b"\0" * (o - pos))
+            f.write(bytes(data))
+            pos = o + len(data)
+
+
+def pack_qpack3(src, dst, threads=8):
+    """the qpack-pack transform (tools/qpack-pack.cpp:43-84): every blob of the plan is coded (chunked above 32 MiB) and
+    kept coded when that is smaller; the manifest gains "encoded" and "format": "QPACK3"; magic QPACK3"""
+    from concurrent.futures import ThreadPoolExecutor
+    f = QpackFile(src)
+    names = sorted(f.toc, key=lambda n: f.toc[n][0])
+    plan = pack_plan(f.manifest)
+    jobs = []
+    for n in names:
+        if n in plan and f.toc[n][1]:
+            d = f.blob(n)
+            if len(d) > PACK_THRESH:
+                jobs += [(n, o, d[o:o + PACK_CHUNK]) for o in range(0, len(d), PACK_CHUNK)]
+            else:
+                jobs.append((n, 0, d))
+    with ThreadPoolExecutor(threads) as ex:
+        outs = list(ex.map(lambda j: rans_encode(j[2], *plan[j[0]]), jobs))
+    coded = {}
+    for (n, o, _), c in zip(jobs, outs):
+        coded.setdefault(n, []).append(c)
+    man = dict(f.manifest)
+    encoded, blobs = [], []
+    for n in names:
+        d = f.blob(n)
+        if n in coded:
+            c = coded[n][0] if len(d) <= PACK_THRESH else rans_assemble_chunked(len(d), PACK_CHUNK, coded[n])
+            if len(c) < len(d):
+                encoded.append(n)
+                d = c
+        blobs.append([n, d])
+    man["encoded"] = encoded
+    man["format"] = "QPACK3"
+    for b in blobs:
+        if b[0] == "manifest.json":
+            b[1] = json.dumps(man).encode()
+    write_container(dst, blobs, b"QPACK3\0\0")
+    f.close()
+    return encoded
 
 
 # ------------------------------------------------------------------ the model
@@ -328,6 +466,8 @@ def rlib(threads=0):
             "qpref_rmsnorm": (None, [_FP, _FP, I, C.c_float, _FP]), "qpref_silu_mul": (None, [_FP, _FP, I]),
             "qpref_exp_v": (None, [_FP, _FP, I]), "qpref_to_f16": (None, [_FP, P, I]),
             "qpref_row_f32": (None, [I, P, P, I, I, I, _FP]),
+            "qpref_rans_encode": (I, [P, C.c_int64, I, I, P, C.c_int64, C.POINTER(C.c_int64)]),
+            "qpref_rans_decode": (I, [P, C.c_int64, P]), "qpref_rans_raw_size": (C.c_int64, [P, C.c_int64]),
         }
         for k, (r, a) in sig.items():
             getattr(L, k).restype = r

@@ -7,7 +7,9 @@
  *   - rows_q8 / rows_q4 / matvec / matmul / rmsnorm / exp / silu: bit-identical to the reference compiled from its own
  *     sources (oracle/_ref/libqpref.so) on seeded inputs, and to golden vectors in tests/golden/;
  *   - the full model (step / prefill / greedy): bit-identical logits and identical greedy streams against
- *     oracle/_ref/libqpref.so on seeded synthetic QPACK2 files, and against the golden fixtures.
+ *     oracle/_ref/libqpref.so on seeded synthetic QPACK2 files, and against the golden fixtures;
+ *   - the rANS codec: byte-identical blobs to the reference encoder and identical decodes of the reference's blobs
+ *     (oracle/_ref/libqpref.so), golden blobs in tests/golden/, and the round trip decode(encode(x)) == x.
  */
 #include "oracle.h"
 
@@ -482,4 +484,173 @@ int or_greedy(or_model *m, int tok, int n, int *out) {
   }
   free(l);
   return n;
+}
+
+/* ------------------------------------------------------------------ QPACK3 rANS (/root/reference/include/qpack/rans.h)
+ * Static per-plane model: 12-bit frequencies summing to 4096, four interleaved 32-bit states (symbol i uses state i & 3),
+ * byte-wise renormalisation into [2^23, 2^31).  The encoder walks the symbols backwards and the bytes are stored in
+ * decode order, after the four final states. */
+#define RANS_PBITS 12u
+#define RANS_PSCALE (1u << RANS_PBITS)
+#define RANS_L (1u << 23)
+
+static uint32_t rd32(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24); }
+static void wr32(uint8_t *p, uint32_t v) { for (int i = 0; i < 4; i++) p[i] = (uint8_t)(v >> (8 * i)); }
+
+/* rans.h:23-37: f = floor(h * 4096 / n), at least 1 for a present symbol; the most frequent symbol (first on ties) takes
+ * the rest; when the rest is < 1 the largest frequency (first on ties) is decremented until the sum is 4096 */
+int or_rans_freqs(const uint8_t *sym, int64_t n, int nsym, uint32_t *f) {
+  uint64_t h[256] = {0};
+  for (int64_t i = 0; i < n; i++) h[sym[i]]++;
+  for (int i = 0; i < nsym; i++) f[i] = 0;
+  if (n == 0) { f[0] = RANS_PSCALE; return 0; }
+  int64_t sum = 0; int big = 0;
+  for (int i = 0; i < nsym; i++) {
+    if (!h[i]) continue;
+    uint32_t v = (uint32_t)((h[i] * RANS_PSCALE) / (uint64_t)n);
+    f[i] = v ? v : 1;
+    sum += f[i];
+    if (h[i] > h[big]) big = i;
+  }
+  const int64_t rest = (int64_t)f[big] + RANS_PSCALE - sum;
+  if (rest >= 1) { f[big] = (uint32_t)rest; return 0; }
+  for (int64_t d = sum - RANS_PSCALE; d > 0; d--) {
+    int m = 0;
+    for (int i = 1; i < nsym; i++) if (f[i] > f[m]) m = i;
+    if (f[m] <= 1) return OR_RANS_NORMALISE;
+    f[m]--;
+  }
+  return 0;
+}
+
+/* one coded plane: u32 comp_len | u16 f[nsym] | u32 state[4] | bytes (rans.h:38-49) */
+static int64_t encode_plane(const uint8_t *sym, int64_t n, int nsym, uint8_t *out, int64_t cap) {
+  uint32_t f[256], c[257];
+  int e = or_rans_freqs(sym, n, nsym, f);
+  if (e) return e;
+  c[0] = 0;
+  for (int i = 0; i < nsym; i++) c[i + 1] = c[i] + f[i];
+  /* renormalisation bytes are produced last-first; at most 2 per symbol plus 16 for the final states */
+  uint8_t *rev = (uint8_t *)malloc((size_t)(2 * n + 16));
+  if (!rev) return OR_RANS_CAPACITY;
+  int64_t nr = 0;
+  uint32_t x[4] = {RANS_L, RANS_L, RANS_L, RANS_L};
+  for (int64_t i = n - 1; i >= 0; i--) {
+    uint32_t *st = &x[i & 3];
+    const uint32_t s = sym[i], fr = f[s], xmax = ((RANS_L >> RANS_PBITS) << 8) * fr;
+    while (*st >= xmax) { rev[nr++] = (uint8_t)*st; *st >>= 8; }
+    *st = ((*st / fr) << RANS_PBITS) + (*st % fr) + c[s];
+  }
+  const int64_t total = 4 + 2 * nsym + 16 + nr;
+  if (total > cap) { free(rev); return OR_RANS_CAPACITY; }
+  uint8_t *o = out + 4;
+  for (int i = 0; i < nsym; i++) { *o++ = (uint8_t)f[i]; *o++ = (uint8_t)(f[i] >> 8); }
+  for (int i = 0; i < 4; i++) { wr32(o, x[i]); o += 4; }
+  for (int64_t k = nr - 1; k >= 0; k--) *o++ = rev[k];
+  free(rev);
+  wr32(out, (uint32_t)(total - 4));
+  return total;
+}
+
+int64_t or_rans_encode(const uint8_t *raw, int64_t n, int codec, int planes, uint8_t *out, int64_t cap) {
+  if (cap < 6) return OR_RANS_CAPACITY;
+  if (!((codec == 2 && planes == 1) || (codec == 1 && planes >= 1 && planes <= 4))) return OR_RANS_BAD_CODEC;
+  out[0] = (uint8_t)codec; out[1] = (uint8_t)planes; wr32(out + 2, (uint32_t)n);
+  int64_t pos = 6;
+  if (codec == 2) {   /* each byte -> low nibble, then high nibble */
+    uint8_t *s = (uint8_t *)malloc((size_t)(2 * n + 1));
+    if (!s) return OR_RANS_CAPACITY;
+    for (int64_t i = 0; i < n; i++) { s[2 * i] = raw[i] & 15; s[2 * i + 1] = raw[i] >> 4; }
+    const int64_t r = encode_plane(s, 2 * n, 16, out + pos, cap - pos);
+    free(s);
+    if (r < 0) return r;
+    pos += r;
+  } else {            /* plane k = raw[k], raw[k + planes], ... */
+    uint8_t *s = (uint8_t *)malloc((size_t)(n / planes + 1));
+    if (!s) return OR_RANS_CAPACITY;
+    for (int k = 0; k < planes; k++) {
+      int64_t m = 0;
+      for (int64_t i = k; i < n; i += planes) s[m++] = raw[i];
+      const int64_t r = encode_plane(s, m, 256, out + pos, cap - pos);
+      if (r < 0) { free(s); return r; }
+      pos += r;
+    }
+    free(s);
+  }
+  return pos;
+}
+
+/* one plane (rans.h:53-71): symbol i -> out[(i * stride + phase)] (bytes) or its nibble i & 1 of out[i >> 1] (nibbles);
+ * returns the bytes consumed */
+static int64_t decode_plane(const uint8_t *p, int64_t avail, int nsym, int64_t n, uint8_t *out, int stride, int phase,
+                            int nibbles) {
+  if (avail < 4) return OR_RANS_TRUNCATED;
+  const uint32_t cl = rd32(p);
+  if ((int64_t)cl + 4 > avail || cl < 2u * (uint32_t)nsym + 16) return OR_RANS_TRUNCATED_PLANE;
+  const uint8_t *q = p + 4, *end = p + 4 + cl;
+  uint32_t f[256], c[257];
+  c[0] = 0;
+  for (int i = 0; i < nsym; i++) { f[i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 8); c[i + 1] = c[i] + f[i]; }
+  if (c[nsym] != RANS_PSCALE) return OR_RANS_BAD_TABLE;
+  q += 2 * nsym;
+  /* the symbol of a slot m is the s with c[s] <= m < c[s + 1] */
+  uint8_t slot[RANS_PSCALE];
+  for (int s = 0; s < nsym; s++) for (uint32_t k = c[s]; k < c[s + 1]; k++) slot[k] = (uint8_t)s;
+  uint32_t x[4];
+  for (int i = 0; i < 4; i++) { x[i] = rd32(q); q += 4; }
+  for (int64_t i = 0; i < n; i++) {
+    uint32_t *st = &x[i & 3];
+    const uint32_t m = *st & (RANS_PSCALE - 1), s = slot[m];
+    *st = f[s] * (*st >> RANS_PBITS) + m - c[s];
+    while (*st < RANS_L) {
+      if (q >= end) return OR_RANS_OVERRUN;
+      *st = (*st << 8) | *q++;
+    }
+    if (nibbles) out[i >> 1] |= (uint8_t)(s << (4 * (i & 1)));
+    else out[i * stride + phase] = (uint8_t)s;
+  }
+  return (int64_t)cl + 4;
+}
+
+int64_t or_rans_raw_size(const uint8_t *p, int64_t len) {
+  if (len < 6) return OR_RANS_SHORT;
+  return rd32(p + 2);
+}
+
+int or_rans_decode(const uint8_t *p, int64_t len, uint8_t *out, int64_t cap) {
+  if (len >= 1 && p[0] == 3) {   /* chunked: u8 3 | u8 0 | u32 raw_len | u32 chunk_raw | u32 nchunks | u32 comp_len[] | chunks */
+    if (len < 14) return OR_RANS_SHORT_CHUNKED;
+    const int64_t cr = rd32(p + 6), nc = rd32(p + 10);
+    int64_t pos = 14 + 4 * nc;
+    if (pos > len) return OR_RANS_TRUNCATED_TABLE;
+    for (int64_t i = 0; i < nc; i++) {
+      const int64_t cl = rd32(p + 14 + 4 * i);
+      if (pos + cl > len) return OR_RANS_TRUNCATED_CHUNK;
+      if (i * cr > cap) return OR_RANS_CAPACITY;
+      const int r = or_rans_decode(p + pos, cl, out + i * cr, cap - i * cr);
+      if (r) return r;
+      pos += cl;
+    }
+    return 0;
+  }
+  const int64_t n = or_rans_raw_size(p, len);
+  if (n < 0) return (int)n;
+  if (n > cap) return OR_RANS_CAPACITY;
+  const int codec = p[0], planes = p[1];
+  int64_t pos = 6;
+  if (codec == 2) {
+    memset(out, 0, (size_t)n);
+    const int64_t r = decode_plane(p + pos, len - pos, 16, 2 * n, out, 1, 0, 1);
+    return r < 0 ? (int)r : 0;
+  }
+  if (codec == 1 && planes >= 1 && planes <= 4) {
+    for (int k = 0; k < planes; k++) {
+      const int64_t cnt = (n + planes - 1 - k) / planes;
+      const int64_t r = decode_plane(p + pos, len - pos, 256, cnt, out, planes, k, 0);
+      if (r < 0) return (int)r;
+      pos += r;
+    }
+    return 0;
+  }
+  return OR_RANS_BAD_CODEC;
 }

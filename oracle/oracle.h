@@ -77,6 +77,20 @@ uint16_t *or_kcache(or_model *m);
 uint16_t *or_vcache(or_model *m);
 void or_set_threads(int n);
 
+/* QPACK3 static rANS codec (/root/reference/include/qpack/rans.h; format in /root/reference/QPACK2.md:30-51).
+ * Errors: OR_RANS_* (negative); the reference throws std::runtime_error at the same points. */
+enum { OR_RANS_TRUNCATED = -1, OR_RANS_BAD_TABLE = -2, OR_RANS_OVERRUN = -3, OR_RANS_BAD_CODEC = -4, OR_RANS_CAPACITY = -5,
+       OR_RANS_NORMALISE = -6, OR_RANS_TRUNCATED_PLANE = -7, OR_RANS_SHORT = -8, OR_RANS_SHORT_CHUNKED = -9,
+       OR_RANS_TRUNCATED_TABLE = -10, OR_RANS_TRUNCATED_CHUNK = -11 };
+/* raw (decoded) length of a blob, or an error (rans.h:75) */
+int64_t or_rans_raw_size(const uint8_t *p, int64_t len);
+/* a plain (codec 1 / 2) or chunked (codec 3) blob -> its raw bytes; out must hold or_rans_raw_size bytes (rans.h:101-113) */
+int or_rans_decode(const uint8_t *p, int64_t len, uint8_t *out, int64_t cap);
+/* raw bytes -> a plain codec 1 (planes 1..4) or codec 2 blob; returns the blob length or an error (rans.h:21-49, :81-93) */
+int64_t or_rans_encode(const uint8_t *raw, int64_t n, int codec, int planes, uint8_t *out, int64_t cap);
+/* the encoder's 12-bit frequency table for one plane of symbols (rans.h:23-37) */
+int or_rans_freqs(const uint8_t *sym, int64_t n, int nsym, uint32_t *f);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "qpack/qpack.h"
+#include "qpack/rans.h"
 
 namespace qp { namespace impl {
 // row kernels of /root/reference/src/kernels_impl.h:29-30 (declared there; repeated here so the shim needs only the
@@ -102,6 +103,20 @@ void qpref_exp_v(const float *x, float *y, int n) { qp::exp_v(x, y, n); }
 void qpref_to_f16(const float *x, uint16_t *y, int n) { qp::to_f16(x, y, n); }
 void qpref_row_f32(int kind, const void *q, const void *s, int rows, int cols, int r, float *out) {
   qp::Tensor t = mk(kind, q, s, rows, cols); qp::row_f32(t, r, out);
+}
+
+// QPACK3 rANS codec (include/qpack/rans.h): encode (:81-93) into out[cap]; *n_out = the blob length
+int qpref_rans_encode(const uint8_t *raw, int64_t n, int codec, int planes, uint8_t *out, int64_t cap, int64_t *n_out) {
+  QPREF_TRY({
+    const std::vector<uint8_t> b = qp::rans::encode(raw, (size_t)n, codec, planes);
+    if ((int64_t)b.size() > cap) throw std::runtime_error("qpref_rans_encode: output buffer too small");
+    memcpy(out, b.data(), b.size()); *n_out = (int64_t)b.size();
+  });
+}
+// decode (:101-113) of a plain or chunked blob; out must hold the raw size (:75)
+int qpref_rans_decode(const uint8_t *p, int64_t len, uint8_t *out) { QPREF_TRY(qp::rans::decode(p, (size_t)len, out)); }
+int64_t qpref_rans_raw_size(const uint8_t *p, int64_t len) {
+  try { return (int64_t)qp::rans::raw_size(p, (size_t)len); } catch (std::exception &e) { g_err = e.what(); return -1; }
 }
 
 }  // extern "C"

@@ -24,7 +24,12 @@ class Config(C.Structure):
 
 class Tensor(C.Structure):
     _fields_ = [("name", C.c_char_p), ("kind", C.c_int), ("rows", C.c_int64), ("cols", C.c_int64),
-                ("data", C.c_void_p), ("scale", C.c_void_p)]
+                ("data", C.c_void_p), ("scale", C.c_void_p), ("data_coded", C.c_int64), ("scale_coded", C.c_int64)]
+
+
+class LoadStatsC(C.Structure):
+    _fields_ = [("planes", C.c_int), ("coded_bytes", C.c_int64), ("raw_bytes", C.c_int64), ("upload_ms", C.c_float),
+                ("decode_ms", C.c_float)]
 
 
 class SynthSpecC(C.Structure):
@@ -70,6 +75,9 @@ SIGNATURES = {
     "qph_kernel_matmul": (_I, [_I, _P, _P, _I, _I, _FP, _I, _FP]),
     "qph_kernel_topk": (_I, [_FP, _I, _I, _IP, _FP]),
     "qph_synth_write": (_I, [C.POINTER(SynthSpecC), C.c_char_p, _I]),
+    "qph_load_stats_of": (_I, [C.c_void_p, C.POINTER(LoadStatsC)]),
+    "qph_kernel_rans_decode": (_I, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.POINTER(C.c_int64), _FP]),
+    "qph_pack": (_I, [C.c_char_p, C.c_char_p, _I, _IP]),
 }
 
 _lib = None

@@ -12,6 +12,7 @@
 #include "hip/launch.hpp"
 #include "hip/model.hpp"
 #include "host/container.hpp"
+#include "host/rans.hpp"
 #include "host/synth.hpp"
 
 struct qph_model {
@@ -83,6 +84,7 @@ int qph_load(const char *path, int max_ctx, qph_model **out) {
       qph_tensor q{}; q.name = t.name.c_str(); q.data = t.data; q.scale = t.scale;
       if (t.shape.size() == 1) { q.rows = t.shape[0]; q.cols = 1; } else { q.rows = t.rows(); q.cols = t.cols(); }
       q.kind = t.kind == qph::Kind::Q8 ? QPH_Q8 : t.kind == qph::Kind::Q4 ? QPH_Q4 : QPH_F32;
+      q.data_coded = (int64_t)t.data_coded; q.scale_coded = (int64_t)t.scale_coded;
       ts.push_back(q);
     }
     cfg.qkv_bias = c.get("layers.0.bq") ? 1 : 0;
@@ -93,6 +95,15 @@ int qph_load(const char *path, int max_ctx, qph_model **out) {
 }
 
 void qph_destroy(qph_model *m) { delete m; }
+
+int qph_load_stats_of(const qph_model *m, qph_load_stats *out) {
+  QPH_API_TRY({
+    need(m, "model"); need(out, "out");
+    const qph::RansTiming &t = m->m->load_timing();
+    out->planes = t.planes; out->coded_bytes = (int64_t)t.coded; out->raw_bytes = (int64_t)t.raw;
+    out->upload_ms = t.upload_ms; out->decode_ms = t.decode_ms;
+  });
+}
 
 int qph_vocab(const qph_model *m) { return m ? m->m->config().vocab : -1; }
 int qph_hidden(const qph_model *m) { return m ? m->m->config().hidden : -1; }
@@ -274,6 +285,35 @@ int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int 
       hck(hipMemcpy(Y, dy, 4ull * B * rows, hipMemcpyDeviceToHost), "download Y");
     } catch (...) { for (void *p : bufs) (void)hipFree(p); throw; }
     for (void *p : bufs) (void)hipFree(p);
+  });
+}
+
+int qph_kernel_rans_decode(const uint8_t *blob, int64_t len, uint8_t *out, int64_t cap, int64_t *raw, float *ms) {
+  QPH_API_TRY({
+    need(blob, "blob"); need(out, "out");
+    if (len < 0 || cap < 0) throw std::invalid_argument("rans: negative length");
+    const uint64_t n = qph::rans::raw_size(blob, (size_t)len);
+    if (raw) *raw = (int64_t)n;
+    if ((int64_t)n > cap) throw std::invalid_argument("rans: output buffer smaller than the raw length");
+    void *d = nullptr;
+    hck(hipMalloc(&d, n + 16), "hipMalloc");
+    try {
+      qph::RansBatch b;
+      qph::RansTiming tm;
+      b.add(blob, (size_t)len, d, n);
+      b.run(nullptr, &tm);
+      if (n) hck(hipMemcpy(out, d, n, hipMemcpyDeviceToHost), "download");
+      if (ms) *ms = tm.decode_ms;
+    } catch (...) { (void)hipFree(d); throw; }
+    hck(hipFree(d), "hipFree");
+  });
+}
+
+int qph_pack(const char *src, const char *dst, int threads, int *coded) {
+  QPH_API_TRY({
+    need(src, "src"); need(dst, "dst");
+    const int c = qph::rans::pack(src, dst, threads);
+    if (coded) *coded = c;
   });
 }
 

@@ -5,6 +5,7 @@
 #include <stdexcept>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "common.hpp"
 
@@ -153,5 +154,34 @@ struct PfAttnArgs {
   int ntok, p0, nh, nkv, hd;
 };
 hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st);
+
+// QPACK3 rANS decode (hip/rans_decode.hip): one task per coded plane, one wave per task
+struct RansTaskDev {
+  const uint8_t *plane;   // the plane's u32 comp_len field (device)
+  uint8_t *out;           // output byte of symbol 0 (device)
+  int64_t n;              // symbols
+  uint32_t comp_len;      // bytes after the comp_len field
+  int nsym, stride, nibbles;
+};
+hipError_t launch_rans(const RansTaskDev *tasks, int ntasks, int *status, hipStream_t st);
+struct RansTiming {
+  int planes = 0;
+  uint64_t coded = 0, raw = 0;
+  float upload_ms = 0, decode_ms = 0;
+};
+// Coded blobs (host memory) with their device destinations, decoded in one launch: run() uploads the blobs into one
+// staging buffer, plans the planes (throwing on malformed headers), decodes, waits, and throws on a stream overrun.
+class RansBatch {
+ public:
+  void add(const uint8_t *blob, size_t len, void *out, size_t out_cap);
+  void run(hipStream_t st, RansTiming *tm = nullptr);
+  bool empty() const { return items_.empty(); }
+
+ private:
+  struct Item { const uint8_t *blob; size_t len; uint8_t *out; size_t stage_off; };
+  std::vector<Item> items_;
+  size_t coded_ = 0;
+  uint64_t raw_ = 0;
+};
 
 }  // namespace qph

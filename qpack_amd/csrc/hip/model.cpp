@@ -7,6 +7,7 @@
 #include <map>
 #include <stdexcept>
 
+#include "../host/rans.hpp"
 #include "launch.hpp"
 
 namespace qph {
@@ -29,19 +30,32 @@ DMat HipLlama::upload(const qph_tensor &t) {
     m.kind = MK_Q4; qb = (size_t)t.rows * t.cols / 2; sb = 2ull * t.rows * (t.cols / 32);
   } else throw std::runtime_error(std::string("hip: matrix ") + t.name + " must be q8 or q4");
   if (!t.data || !t.scale) throw std::runtime_error(std::string("hip: tensor ") + t.name + " has no data");
-  void *q = dalloc(qb), *s = dalloc(sb);
-  QPH_CK(hipMemcpy(q, t.data, qb, hipMemcpyHostToDevice));
-  QPH_CK(hipMemcpy(s, t.scale, sb, hipMemcpyHostToDevice));
-  m.q = q; m.s = s;
+  m.q = place(t.data, t.data_coded, qb, t.name);
+  m.s = place(t.scale, t.scale_coded, sb, t.name);
   return m;
+}
+
+// a device copy of `bytes` raw bytes: copied now, or, from a rANS blob of `coded` bytes, decoded with the batch of
+// coded blobs that the constructor runs once every tensor is placed (the buffer is as large as the blob's raw length
+// when that is longer, as a longer plain blob would be)
+void *HipLlama::place(const void *src, int64_t coded, size_t bytes, const char *name) {
+  if (coded < 0) throw std::runtime_error(std::string("hip: tensor ") + name + " has a negative coded length");
+  if (!coded) {
+    void *p = dalloc(bytes);
+    QPH_CK(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice));
+    return p;
+  }
+  const uint64_t raw = rans::raw_size((const uint8_t *)src, (size_t)coded);
+  if (raw < bytes) throw std::runtime_error(std::string("hip: coded tensor ") + name + " decodes to fewer bytes than its shape needs");
+  void *p = dalloc(raw);
+  rans_.add((const uint8_t *)src, (size_t)coded, p, raw);
+  return p;
 }
 
 const float *HipLlama::upload_f32(const qph_tensor &t, int64_t n) {
   if (t.kind != QPH_F32) throw std::runtime_error(std::string("hip: tensor ") + t.name + " must be f32");
   if (t.rows * std::max<int64_t>(t.cols, 1) != n) throw std::runtime_error(std::string("hip: tensor ") + t.name + " has the wrong size");
-  void *p = dalloc(4ull * n);
-  QPH_CK(hipMemcpy(p, t.data, 4ull * n, hipMemcpyHostToDevice));
-  return (const float *)p;
+  return (const float *)place(t.data, t.data_coded, 4ull * n, t.name);
 }
 
 HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int max_ctx) : cfg_(cfg) {
@@ -89,6 +103,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     if (bq) { ly.bq = upload_f32(*bq, qd_); ly.bk = upload_f32(need(p + "bk"), kvd_); ly.bv = upload_f32(need(p + "bv"), kvd_); }
     layers_.push_back(ly);
   }
+  rans_.run(st_, &rans_tm_);   // QPACK3: every coded blob decodes in HBM in one launch
   // context splits per kv group: one per 64 positions of the full context, at most 64 (the kernel activates
   // min(this, ceil(T / 64)) of them beyond one workgroup's reach)
   max_chunks_ = std::max(1, std::min(64, (ctx_ + 63) / 64));

@@ -10,6 +10,7 @@
 
 #include "../../../include/qpack_hip.h"
 #include "common.hpp"
+#include "launch.hpp"
 
 namespace qph {
 
@@ -21,6 +22,7 @@ class HipLlama {
   HipLlama &operator=(const HipLlama &) = delete;
 
   const qph_config &config() const { return cfg_; }
+  const RansTiming &load_timing() const { return rans_tm_; }
   int max_ctx() const { return ctx_; }
   int pos() const { return pos_; }
 
@@ -55,6 +57,8 @@ class HipLlama {
   unsigned slot_ = 0;
   hipStream_t st_ = nullptr;
   std::vector<void *> allocs_;
+  RansBatch rans_;            // coded (QPACK3) tensors waiting for the load's one decode launch
+  RansTiming rans_tm_;
   DMat embed_{}, head_{};
   const float *fnorm_ = nullptr;
   std::vector<Layer> layers_;
@@ -91,6 +95,7 @@ class HipLlama {
   void *dalloc(size_t bytes);
   DMat upload(const qph_tensor &t);
   const float *upload_f32(const qph_tensor &t, int64_t n);
+  void *place(const void *src, int64_t coded, size_t bytes, const char *name);
   void enqueue_layers();
   void enqueue_layer(int l);
   void enqueue_head();

@@ -1,0 +1,217 @@
+// QPACK3 rANS decode in HBM (the format of /root/reference/include/qpack/rans.h; the reference decodes on the CPU at
+// load, /root/reference/src/container.cpp:94-121).
+//
+// A coded plane is one sequential stream: its four interleaved states share one byte stream, so symbol i + 1's bytes
+// start where symbol i's end and a plane decodes in order.  The parallelism is across planes (16 MiB chunks of large
+// blobs, the blobs themselves), so the kernel runs one wave per plane and spends that wave on the plane's latency chain:
+//   - the decode table sits in LDS, one packed word per 12-bit slot: symbol | (freq - 1) << 8 | cum << 20, so one LDS
+//     read gives a symbol's three values;
+//   - lanes 0..3 hold states 0..3 and decode the group of four symbols 4g .. 4g + 3 together: each lane needs 0, 1 or 2
+//     renormalisation bytes; a two-step DPP prefix sum gives each lane its byte offset in the stream, and the bytes come
+//     from an 8-byte window of the stream read (as three dwords) at the same time as the table;
+//   - the coded stream is staged in an 8 KiB LDS ring by 1 KiB coalesced loads issued one step (512 symbols) before use;
+//   - symbols collect in LDS and leave as 8-byte (bytes) or 4-byte (nibbles) stores of all 64 lanes per step.
+// The decoded bytes equal rans::decode's (bit-exact); a stream that needs a byte past its plane's end reports an
+// overrun, where the reference throws "rans: stream overrun".
+#include <algorithm>
+#include <stdexcept>
+#include <vector>
+
+#include "../host/rans.hpp"
+#include "launch.hpp"
+
+namespace qph {
+
+constexpr int kRansRing = 8192;    // LDS stream ring (bytes)
+constexpr int kRansBlk = 1024;     // one load: 64 lanes x 16 bytes
+constexpr int kRansStep = 512;     // symbols between ring refills / output flushes (at most 2 bytes each)
+constexpr int kRansAhead = 4096;   // a refill is issued while fewer bytes than this are loaded past the read position
+
+__device__ __forceinline__ uint32_t rd_u8(const uint8_t *p) { return *p; }
+__global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, int *status) {
+  __shared__ uint32_t tab[rans::kProbScale];
+  __shared__ uint32_t ring[kRansRing / 4];
+  __shared__ __align__(16) uint8_t symb[kRansStep];
+  __shared__ uint32_t cum[257];
+  const int lane = threadIdx.x;
+  const RansTaskDev t = tasks[blockIdx.x];
+  const int nsym = t.nsym;
+  const uint8_t *fq = t.plane + 4;
+
+  // cumulative frequencies: lane l sums symbols [l * per, (l + 1) * per), then an exclusive scan over the lanes
+  const int per = nsym / 64 ? nsym / 64 : 1;
+  uint32_t fl[4] = {0, 0, 0, 0}, own = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int s = lane * per + k;
+    if (k < per && s < nsym) { fl[k] = rd_u8(fq + 2 * s) | (rd_u8(fq + 2 * s + 1) << 8); own += fl[k]; }
+  }
+  uint32_t incl = own;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  uint32_t run = incl - own;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int s = lane * per + k;
+    if (k < per && s < nsym) { cum[s] = run; run += fl[k]; }
+  }
+  if (lane == 0) cum[nsym] = rans::kProbScale;
+  __syncthreads();
+  // table: lane l fills slots [64 l, 64 l + 64): the symbol of slot m is the s with cum[s] <= m < cum[s + 1]
+  {
+    const uint32_t m0 = lane * 64;
+    int lo = 0, hi = nsym - 1;   // largest s with cum[s] <= m0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cum[mid] <= m0) lo = mid; else hi = mid - 1;
+    }
+    int s = lo;
+    for (uint32_t m = m0; m < m0 + 64; m++) {
+      while (cum[s + 1] <= m) s++;
+      tab[m] = (uint32_t)s | ((cum[s + 1] - cum[s] - 1) << 8) | (cum[s] << 20);
+    }
+  }
+
+  // stream bytes: offsets are counted from `base`, the 16-byte aligned address at or below the first stream byte
+  const uint8_t *sp = t.plane + 4 + 2 * nsym + 16;
+  const uint8_t *base = (const uint8_t *)((uintptr_t)sp & ~(uintptr_t)15);
+  const uint64_t end_off = (uint64_t)(t.plane + 4 + t.comp_len - base);
+  uint64_t q = (uint64_t)(sp - base);
+  uint32_t st = 0;
+  if (lane < 4) {
+    const uint8_t *xs = t.plane + 4 + 2 * nsym + 4 * lane;
+    st = rd_u8(xs) | (rd_u8(xs + 1) << 8) | (rd_u8(xs + 2) << 16) | (rd_u8(xs + 3) << 24);
+  }
+  // loads stop at the plane's end (the bytes past it only feed a stream that has overrun, reported below)
+  const uint64_t load_max = (end_off + 15) & ~(uint64_t)15;
+  uint64_t issued = 0;
+  for (; issued < (uint64_t)kRansAhead; issued += kRansBlk) {
+    const uint4 v = *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane);
+    *(uint4 *)((uint8_t *)ring + ((issued + 16 * lane) & (kRansRing - 1))) = v;
+  }
+  uint4 pend = {0, 0, 0, 0};
+  uint64_t pend_at = 0;
+  bool pending = false;
+
+  const int64_t n = t.n;
+  for (int64_t s0 = 0; s0 < n; s0 += kRansStep) {
+    // refill: write the block loaded one step ago, issue the next while less than kRansAhead bytes are ahead
+    if (pending) *(uint4 *)((uint8_t *)ring + ((pend_at + 16 * lane) & (kRansRing - 1))) = pend;
+    pending = issued - q < (uint64_t)kRansAhead;
+    if (pending) { pend = *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane); pend_at = issued; issued += kRansBlk; }
+    __syncthreads();
+    const int ng = (int)std::min<int64_t>(kRansStep, n - s0);
+    for (int g = 0; g < ng; g += 4) {
+      const bool live = lane < 4 && g + lane < ng;
+      const uint32_t qa = (uint32_t)q & ~3u, sh = (uint32_t)q & 3u;   // window = stream bytes q .. q + 7
+      const uint32_t w0 = ring[(qa & (kRansRing - 1)) >> 2], w1 = ring[((qa + 4) & (kRansRing - 1)) >> 2],
+                     w2 = ring[((qa + 8) & (kRansRing - 1)) >> 2];
+      const uint64_t win = (uint64_t)__builtin_amdgcn_alignbyte(w2, w1, sh) << 32 | __builtin_amdgcn_alignbyte(w1, w0, sh);
+      const uint32_t m = st & (rans::kProbScale - 1), e = tab[m];
+      const uint32_t f = ((e >> 8) & 4095u) + 1, c = e >> 20;
+      uint32_t x = f * (st >> rans::kProbBits) + m - c;
+      const uint32_t cnt = live ? (uint32_t)(x < rans::kL) + (uint32_t)(x < (1u << 15)) : 0u;
+      // inclusive prefix of cnt over lanes 0..3 (row shifts fill with zeros)
+      uint32_t inc = cnt + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)cnt, 0x111, 0xf, 0xf, true);
+      inc = inc + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)inc, 0x112, 0xf, 0xf, true);
+      const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)inc, 3);
+      const uint32_t bb = (uint32_t)(win >> ((8 * (inc - cnt)) & 63));
+      const uint32_t b0 = bb & 255u, b1 = (bb >> 8) & 255u;
+      x = cnt == 2 ? (x << 16) | (b0 << 8) | b1 : cnt == 1 ? (x << 8) | b0 : x;
+      if (live) { st = x; symb[g + lane] = (uint8_t)(e & 255u); }
+      q += total;
+    }
+    __syncthreads();
+    // flush: lane l owns symbols [8 l, 8 l + 8) of the step
+    const int i0 = 8 * lane;
+    if (i0 < ng) {
+      const uint2 v = *(const uint2 *)(symb + i0);
+      const int64_t gi = s0 + i0;
+      if (t.nibbles) {
+        const uint32_t b = (v.x & 0x0f) | ((v.x >> 4) & 0xf0) | ((v.x >> 8) & 0x0f00) | ((v.x >> 12) & 0xf000) |
+                           ((v.y & 0x0f) << 16) | ((v.y << 12) & 0xf00000) | ((v.y & 0x0f0000) << 8) | ((v.y << 4) & 0xf0000000);
+        uint8_t *o = t.out + gi / 2;
+        if (i0 + 8 <= ng && !((uintptr_t)o & 3)) *(uint32_t *)o = b;
+        else for (int k = 0; k < 4 && 2 * k < ng - i0; k++) o[k] = (uint8_t)(b >> (8 * k));
+      } else if (t.stride == 1) {
+        uint8_t *o = t.out + gi;
+        if (i0 + 8 <= ng && !((uintptr_t)o & 7)) *(uint2 *)o = v;   // wide stores where aligned (always, for 16 MiB chunks)
+        else for (int k = 0; k < 8 && k < ng - i0; k++) o[k] = symb[i0 + k];
+      } else {
+        for (int k = 0; k < 8 && i0 + k < ng; k++) t.out[(gi + k) * t.stride] = symb[i0 + k];
+      }
+    }
+  }
+  if (lane == 0) status[blockIdx.x] = q > end_off ? 1 : 0;
+}
+
+hipError_t launch_rans(const RansTaskDev *tasks, int ntasks, int *status, hipStream_t st) {
+  if (ntasks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rans_decode, dim3(ntasks), dim3(64), 0, st, tasks, status);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ host side: many blobs, one launch
+void RansBatch::add(const uint8_t *blob, size_t len, void *out, size_t out_cap) {
+  const uint64_t raw = rans::raw_size(blob, len);
+  if (raw > out_cap) throw std::runtime_error("rans: decoded size exceeds the destination");
+  items_.push_back({blob, len, (uint8_t *)out, coded_});
+  coded_ += (len + 15) & ~(size_t)15;
+  raw_ += raw;
+}
+
+// a wave reads up to kRansAhead bytes from its stream's aligned start, and at most kRansBlk + 16 past its plane's end
+static constexpr size_t kRansSlack = kRansAhead + 2 * kRansBlk + 64;
+
+void RansBatch::run(hipStream_t st, RansTiming *tm) {
+  if (items_.empty()) return;
+  std::vector<RansTaskDev> tasks;
+  for (const Item &it : items_)
+    for (const rans::PlaneTask &p : rans::plan(it.blob, it.len)) {
+      RansTaskDev d{};
+      d.plane = (const uint8_t *)(uintptr_t)(it.stage_off + p.hdr);   // rebased onto the staging buffer below
+      d.out = it.out + p.out_off;
+      d.n = p.n; d.comp_len = p.comp_len; d.nsym = p.nsym; d.stride = p.stride; d.nibbles = p.nibbles ? 1 : 0;
+      tasks.push_back(d);
+    }
+  // longest planes first, so the last waves to start are short ones
+  std::stable_sort(tasks.begin(), tasks.end(), [](const RansTaskDev &a, const RansTaskDev &b) { return a.n > b.n; });
+  uint8_t *stage = nullptr; RansTaskDev *dt = nullptr; int *dst = nullptr;
+  hipEvent_t e[3] = {};
+  auto cleanup = [&] {
+    if (stage) (void)hipFree(stage);
+    if (dt) (void)hipFree(dt);
+    if (dst) (void)hipFree(dst);
+    for (hipEvent_t &x : e) if (x) (void)hipEventDestroy(x);
+  };
+  try {
+    auto ck = [](hipError_t r, const char *what) { if (r != hipSuccess) throw std::runtime_error(std::string("rans: ") + what + ": " + hipGetErrorString(r)); };
+    for (hipEvent_t &x : e) ck(hipEventCreate(&x), "event");
+    ck(hipMalloc(&stage, coded_ + kRansSlack), "staging allocation");
+    ck(hipMalloc(&dt, tasks.size() * sizeof(RansTaskDev) + 1), "task allocation");
+    ck(hipMalloc(&dst, tasks.size() * sizeof(int) + 4), "status allocation");
+    for (RansTaskDev &d : tasks) d.plane = stage + (uintptr_t)d.plane;
+    ck(hipEventRecord(e[0], st), "event");
+    for (const Item &it : items_) ck(hipMemcpyAsync(stage + it.stage_off, it.blob, it.len, hipMemcpyHostToDevice, st), "upload");
+    ck(hipMemsetAsync(stage + coded_, 0, kRansSlack, st), "staging clear");
+    ck(hipMemcpyAsync(dt, tasks.data(), tasks.size() * sizeof(RansTaskDev), hipMemcpyHostToDevice, st), "task upload");
+    ck(hipEventRecord(e[1], st), "event");
+    ck(launch_rans(dt, (int)tasks.size(), dst, st), "decode launch");
+    ck(hipEventRecord(e[2], st), "event");
+    std::vector<int> status(tasks.size());
+    ck(hipMemcpyAsync(status.data(), dst, status.size() * sizeof(int), hipMemcpyDeviceToHost, st), "status copy");
+    ck(hipStreamSynchronize(st), "decode");
+    for (int s : status) if (s) throw std::runtime_error("rans: stream overrun");
+    if (tm) {
+      tm->planes = (int)tasks.size(); tm->coded = coded_; tm->raw = raw_;
+      ck(hipEventElapsedTime(&tm->upload_ms, e[0], e[1]), "event");
+      ck(hipEventElapsedTime(&tm->decode_ms, e[1], e[2]), "event");
+    }
+  } catch (...) { cleanup(); items_.clear(); coded_ = raw_ = 0; throw; }
+  cleanup();
+  items_.clear(); coded_ = raw_ = 0;
+}
+
+}  // namespace qph

@@ -1,10 +1,13 @@
 #include "container.hpp"
 
+#include "rans.hpp"
+
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -24,9 +27,8 @@ Container::Container(const std::string &path) {
   if (map_ == MAP_FAILED) { map_ = nullptr; throw std::runtime_error("mmap failed: " + path); }
   if (!memcmp(map_, "QPACK1\0\0", 8)) version_ = 1;
   else if (!memcmp(map_, "QPACK2\0\0", 8)) version_ = 2;
-  else if (!memcmp(map_, "QPACK3\0\0", 8))
-    throw std::runtime_error(path + ": QPACK3 (rANS-coded blobs) is not read by the HIP loader; run `qpack-pack in out --unpack` first");
-  else throw std::runtime_error("not a QPACK1/QPACK2 file: " + path);
+  else if (!memcmp(map_, "QPACK3\0\0", 8)) version_ = 3;
+  else throw std::runtime_error("not a QPACK1/QPACK2/QPACK3 file: " + path);
   uint32_t n; memcpy(&n, map_ + 8, 4);
   if (16 + 72ull * n > size_) throw std::runtime_error("corrupt table of contents: " + path);
   for (uint32_t i = 0; i < n; i++) {
@@ -39,28 +41,40 @@ Container::Container(const std::string &path) {
   auto json_blob = [&](const char *b) { size_t l; const uint8_t *p = blob(b, &l); return Json::parse((const char *)p, l); };
   manifest_ = json_blob("manifest.json");
   config_ = json_blob("config.json");
+  for (const Json &e : manifest_["encoded"].arr) {
+    if (!toc_.count(e.string())) throw std::runtime_error("missing blob " + e.string());
+    coded_[e.string()] = true;
+  }
+  // a coded blob's length check uses its raw length (the u32 after codec and planes, the same for chunked blobs)
+  auto view = [&](const std::string &b, const void **p, uint64_t *coded) {
+    size_t l; *p = blob(b, &l);
+    if (!coded_.count(b)) return (uint64_t)l;
+    *coded = l;
+    return (uint64_t)rans::raw_size((const uint8_t *)*p, l);
+  };
   for (const Json &e : manifest_["tensors"].arr) {
     TensorView t; t.name = e["name"].string();
     for (const Json &s : e["shape"].arr) t.shape.push_back(s.integer(0));
-    const std::string &kind = e["kind"].string(); size_t len = 0;
-    t.data = blob(e["blob"].string(), &len);
-    const int64_t rows = t.rows(), cols = t.cols(); size_t sl = 0;
+    const std::string &kind = e["kind"].string();
+    const uint64_t len = view(e["blob"].string(), &t.data, &t.data_coded);
+    const int64_t rows = t.rows(), cols = t.cols(); uint64_t sl = 0;
     if (kind == "f32") {
       t.kind = Kind::F32;
       if (len < 4ull * t.numel()) throw std::runtime_error("tensor " + t.name + ": blob too short");
     } else if (kind == "f16") {
       t.kind = Kind::F16;
       if (len < 2ull * t.numel()) throw std::runtime_error("tensor " + t.name + ": blob too short");
+      if (t.shape.size() != 2 && t.data_coded) throw std::runtime_error("tensor " + t.name + ": a coded f16 vector is not read by the HIP loader");
       if (t.shape.size() != 2) {   // norms / biases: widened to f32 once
         std::vector<float> w((size_t)t.numel());
         for (size_t i = 0; i < w.size(); i++) { uint16_t h; memcpy(&h, (const uint8_t *)t.data + 2 * i, 2); w[i] = half_to_float(h); }
         widened_.push_back(std::move(w)); t.data = widened_.back().data(); t.kind = Kind::F32;
       }
     } else if (kind == "q8") {
-      t.kind = Kind::Q8; t.scale = blob(e["scale"].string(), &sl);
+      t.kind = Kind::Q8; sl = view(e["scale"].string(), &t.scale, &t.scale_coded);
       if (t.shape.size() != 2 || len < (size_t)(rows * cols) || sl < 4ull * rows) throw std::runtime_error("q8 tensor " + t.name + ": bad shape or blob size");
     } else if (kind == "q4") {
-      t.kind = Kind::Q4; t.scale = blob(e["scale"].string(), &sl);
+      t.kind = Kind::Q4; sl = view(e["scale"].string(), &t.scale, &t.scale_coded);
       if (e["group"].integer(32) != 32) throw std::runtime_error("q4 tensor " + t.name + ": only group 32 is supported");
       if (t.shape.size() != 2 || cols % 32) throw std::runtime_error("q4 tensor " + t.name + ": 2-D with cols % 32 == 0 required");
       if (len < (size_t)(rows * cols / 2) || sl < 2ull * rows * (cols / 32)) throw std::runtime_error("q4 tensor " + t.name + ": blob too short");
@@ -79,6 +93,14 @@ const uint8_t *Container::blob(const std::string &n, size_t *len) const {
   if (it == toc_.end()) throw std::runtime_error("missing blob " + n);
   if (len) *len = it->second.second;
   return map_ + it->second.first;
+}
+std::vector<std::string> Container::blob_names() const {
+  std::vector<std::pair<uint64_t, std::string>> v;
+  for (auto &kv : toc_) v.push_back({kv.second.first, kv.first});
+  std::sort(v.begin(), v.end());
+  std::vector<std::string> o;
+  for (auto &x : v) o.push_back(x.second);
+  return o;
 }
 const TensorView *Container::get(const std::string &n) const { auto it = tensors_.find(n); return it == tensors_.end() ? nullptr : &it->second; }
 const TensorView &Container::at(const std::string &n) const {

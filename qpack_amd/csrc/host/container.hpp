@@ -4,8 +4,10 @@
 //   magic "QPACK1\0\0" | "QPACK2\0\0" (8 bytes), count u32, pad u32,
 //   count x { name[56] NUL-padded, offset u64, length u64 }, blobs each aligned to 64 bytes.
 // manifest.json lists the tensors ({name, shape, kind, blob, scale, group}); config.json holds the model config.
-// Tensor kinds read here: f32, f16 (1-D f16 is widened to f32 at load, as the reference does), q8, q4.  QPACK3 (rANS-coded
-// blobs) is recognised and rejected with a message naming the unpack step.
+// Tensor kinds read here: f32, f16 (1-D f16 is widened to f32 at load, as the reference does), q8, q4.
+// QPACK3 (/root/reference/QPACK2.md:30-51): the blobs named in the manifest's "encoded" list hold rANS streams.  Unlike
+// the reference Container, which decodes them on the CPU at load (/root/reference/src/container.cpp:94-121), this view
+// leaves them coded: a tensor records the coded lengths, and the model decodes them in HBM (hip/rans_decode.hip).
 #pragma once
 #include <cstdint>
 #include <map>
@@ -24,6 +26,8 @@ struct TensorView {
   Kind kind = Kind::F32;
   const void *data = nullptr;    // q8: int8 [rows, cols]; q4: u8 [rows, cols / 2]; f32 / f16 dense
   const void *scale = nullptr;   // q8: f32 [rows]; q4: f16 [rows, cols / 32]
+  uint64_t data_coded = 0;       // QPACK3: > 0 when `data` is a rANS blob of this many bytes
+  uint64_t scale_coded = 0;      // QPACK3: > 0 when `scale` is a rANS blob of this many bytes
   int64_t rows() const { return shape.empty() ? 0 : shape[0]; }
   int64_t cols() const {
     if (shape.size() == 1) return shape[0];
@@ -43,6 +47,8 @@ class Container {
   const Json &config() const { return config_; }
   const Json &manifest() const { return manifest_; }
   bool has_blob(const std::string &n) const { return toc_.count(n) > 0; }
+  bool is_coded(const std::string &n) const { return coded_.count(n) > 0; }
+  std::vector<std::string> blob_names() const;                    // in file order
   const uint8_t *blob(const std::string &n, size_t *len) const;   // throws when absent
   const TensorView *get(const std::string &n) const;              // nullptr when absent
   const TensorView &at(const std::string &n) const;               // throws when absent
@@ -54,6 +60,7 @@ class Container {
   size_t size_ = 0;
   int version_ = 0;
   std::map<std::string, std::pair<uint64_t, uint64_t>> toc_;
+  std::map<std::string, bool> coded_;
   Json manifest_, config_;
   std::map<std::string, TensorView> tensors_;
   std::vector<std::vector<float>> widened_;   // storage of 1-D f16 tensors converted to f32

@@ -5,7 +5,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import Config, check, lib
+from ._lib import Config, LoadStatsC, check, lib
 
 
 def _fptr(a):
@@ -133,6 +133,13 @@ class HipLlama:
         check(lib().qph_restore(self._h, buf.ctypes.data_as(C.c_void_p), len(buf)))
 
     # ---- measurement
+    def load_stats(self):
+        """the QPACK3 decode of this model's load: planes, coded / raw bytes, upload and decode-kernel ms"""
+        st = LoadStatsC()
+        check(lib().qph_load_stats_of(self._h, C.byref(st)))
+        return {"planes": st.planes, "coded_bytes": st.coded_bytes, "raw_bytes": st.raw_bytes, "upload_ms": st.upload_ms,
+                "decode_ms": st.decode_ms}
+
     def time_greedy(self, token, n):
         ms = C.c_float(0)
         check(lib().qph_time_greedy(self._h, int(token), int(n), C.byref(ms)))
@@ -195,3 +202,22 @@ def kernel_topk(x, M):
     idx = np.empty(M, np.int32); val = np.empty(M, np.float32)
     check(lib().qph_kernel_topk(_fptr(x), len(x), int(M), _iptr(idx), _fptr(val)))
     return idx, val
+
+
+def kernel_rans_decode(blob):
+    """rans::decode of one QPACK3 blob on the GPU (qph_kernel_rans_decode): (raw bytes, decode-kernel ms)"""
+    b = np.ascontiguousarray(np.frombuffer(bytes(blob), np.uint8) if not isinstance(blob, np.ndarray) else blob, np.uint8)
+    raw = C.c_int64(0)
+    if len(b) >= 6:
+        raw.value = int(b[2]) | int(b[3]) << 8 | int(b[4]) << 16 | int(b[5]) << 24
+    out = np.empty(max(raw.value, 1), np.uint8)
+    ms = C.c_float(0)
+    check(lib().qph_kernel_rans_decode(b.ctypes.data, len(b), out.ctypes.data, len(out), C.byref(raw), C.byref(ms)))
+    return out[:raw.value], ms.value
+
+
+def pack(src, dst, threads=8):
+    """qpack-pack src dst (qph_pack): QPACK2 -> QPACK3; returns the number of coded blobs"""
+    n = C.c_int(0)
+    check(lib().qph_pack(str(src).encode(), str(dst).encode(), int(threads), C.byref(n)))
+    return n.value

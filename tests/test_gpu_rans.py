@@ -1,0 +1,108 @@
+"""QPACK3 rANS decode on the GPU (qph_kernel_rans_decode, and qph_load of a QPACK3 file) against the reference codec:
+the reference's own blobs and error messages (tests/golden/rans.npz), the oracle's decoder on seeded blobs of every
+codec / plane count / statistics, chunked blobs (including chunk sizes that are not multiples of 8, which take the
+byte-store path), and a model whose QPACK3 file must give exactly the logits of its QPACK2 file.  Bit-exact throughout."""
+import numpy as np
+import pytest
+
+import oracle as O
+import qpack_amd as qa
+
+from test_rans import golden
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_decode(blob):
+    out, ms = qa.kernel_rans_decode(np.ascontiguousarray(blob, np.uint8))
+    return out
+
+
+def test_reference_blobs():
+    cases, _, _ = golden()
+    for i, codec, planes, raw, blob in cases:
+        print(f"rans golden case {i} codec {codec} planes {planes} n {len(raw)}", flush=True)
+        np.testing.assert_array_equal(gpu_decode(blob), raw, err_msg=f"case {i}")
+
+
+def test_reference_error_messages():
+    _, bad, errors = golden()
+    for k, b in bad.items():
+        print(f"rans error case {k}", flush=True)
+        with pytest.raises(qa.QphError) as e:
+            gpu_decode(b)
+        assert errors[k] in str(e.value), (k, str(e.value), errors[k])
+
+
+def raw_of(rng, kind, n):
+    if kind == "uniform":
+        return rng.integers(0, 256, n, dtype=np.uint8)
+    if kind == "narrow":
+        return np.clip(rng.normal(128, 2.5, n), 0, 255).astype(np.uint8)
+    if kind == "zeros":
+        return np.zeros(n, np.uint8)
+    return np.where(rng.random(n) < 0.9995, 3, 250).astype(np.uint8)   # one symbol near probability 1
+
+
+@pytest.mark.parametrize("kind", ["uniform", "narrow", "zeros", "skewed"])
+@pytest.mark.parametrize("codec,planes", [(1, 1), (1, 2), (1, 3), (1, 4), (2, 1)])
+def test_random_blobs(kind, codec, planes):
+    rng = np.random.default_rng(hash((kind, codec, planes)) % 2 ** 32)
+    for n in [1, 4, 7, 8, 255, 256, 257, 511, 512, 513, 2048, 4099, 70001]:
+        raw = raw_of(rng, kind, n)
+        blob = O.rans_encode(raw, codec, planes)
+        print(f"rans random {kind} codec {codec} planes {planes} n {n}", flush=True)
+        np.testing.assert_array_equal(gpu_decode(blob), O.rans_decode(blob))
+        np.testing.assert_array_equal(gpu_decode(blob), raw)
+
+
+@pytest.mark.parametrize("chunk", [1000, 4096, 65536])
+@pytest.mark.parametrize("codec", [1, 2])
+def test_chunked_blobs(chunk, codec):
+    rng = np.random.default_rng(chunk + codec)
+    raw = np.clip(rng.normal(100, 4, 300000), 0, 255).astype(np.uint8)
+    chunks = [O.rans_encode(raw[o:o + chunk], codec, 1) for o in range(0, len(raw), chunk)]
+    blob = O.rans_assemble_chunked(len(raw), chunk, chunks)
+    print(f"rans chunked chunk {chunk} codec {codec}", flush=True)
+    np.testing.assert_array_equal(gpu_decode(blob), raw)
+
+
+def test_overrun_matches_oracle():
+    rng = np.random.default_rng(5)
+    blob = O.rans_encode(rng.integers(0, 256, 5000, dtype=np.uint8), 1, 1)
+    cl = int(np.frombuffer(blob[6:10].tobytes(), np.uint32)[0])
+    for cut in [1, 7, 100, 4000]:
+        b = blob.copy()
+        b[6:10] = np.frombuffer(np.uint32(cl - cut).tobytes(), np.uint8)
+        with pytest.raises(ValueError, match="stream overrun"):
+            O.rans_decode(b)
+        with pytest.raises(qa.QphError, match="stream overrun"):
+            gpu_decode(b)
+
+
+def test_large_chunked_q8_blob():
+    """a 40 MiB q8-like blob coded as qpack-pack codes it (16 MiB chunks): 3 planes of up to 16M symbols each"""
+    rng = np.random.default_rng(1)
+    w = rng.normal(0, 0.02, 40 << 20)
+    raw = np.clip(np.round(w / 0.0006), -127, 127).astype(np.int8).view(np.uint8)
+    C = O.PACK_CHUNK
+    blob = O.rans_assemble_chunked(len(raw), C, [O.rans_encode(raw[o:o + C], 1, 1) for o in range(0, len(raw), C)])
+    out, ms = qa.kernel_rans_decode(blob)
+    print(f"rans 40 MiB: {len(blob) / 2**20:.1f} MiB coded, decode {ms:.1f} ms ({len(raw) / ms / 1e6:.2f} GB/s)", flush=True)
+    np.testing.assert_array_equal(out, raw)
+
+
+@pytest.mark.parametrize("cfg", ["mini", "mini_q4m"])
+def test_qpack3_model_equals_qpack2(cfg, synth, tmp_path):
+    src = synth(cfg)
+    dst = str(tmp_path / "m3.qpack")
+    assert qa.pack(src, dst, 4) > 0
+    toks = list(range(3, 40))
+    a = qa.HipLlama.load(src, 128)
+    b = qa.HipLlama.load(dst, 128)
+    st = b.load_stats()
+    assert st["planes"] > 0 and st["raw_bytes"] > st["coded_bytes"] > 0
+    assert a.load_stats()["planes"] == 0
+    np.testing.assert_array_equal(a.prefill(toks, 1), b.prefill(toks, 1))
+    np.testing.assert_array_equal(a.greedy_run(7, 24), b.greedy_run(7, 24))
+    a.close(); b.close()
