@@ -4,16 +4,18 @@
 // A coded plane is one sequential stream: its four interleaved states share one byte stream, so symbol i + 1's bytes
 // start where symbol i's end and a plane decodes in order.  The parallelism is across planes (16 MiB chunks of large
 // blobs, the blobs themselves), so the kernel runs one wave per plane and spends that wave on the plane's latency chain:
-//   - the decode table sits in LDS, one packed word per 12-bit slot: symbol | (freq - 1) << 8 | cum << 20, so one LDS
-//     read gives a symbol's three values;
+//   - the decode table sits in LDS: per 12-bit slot m one word freq | (m - cum) << 16, so the state update
+//     freq * (x >> 12) + (m - cum) is one multiply-add, and the symbol in a byte table read alongside;
 //   - lanes 0..3 hold states 0..3 and decode the group of four symbols 4g .. 4g + 3 together: each lane needs 0, 1 or 2
 //     renormalisation bytes; a two-step DPP prefix sum gives each lane its byte offset in the stream, and the bytes come
-//     from an 8-byte window of the stream read (as three dwords) at the same time as the table;
+//     from an 8-byte window of the stream read (as three dwords) at the same time as the table, picked out with one
+//     byte permute;
 //   - the coded stream is staged in an 8 KiB LDS ring by 1 KiB coalesced loads issued one step (512 symbols) before use;
 //   - symbols collect in LDS and leave as 8-byte (bytes) or 4-byte (nibbles) stores of all 64 lanes per step.
 // The decoded bytes equal rans::decode's (bit-exact); a stream that needs a byte past its plane's end reports an
 // overrun, where the reference throws "rans: stream overrun".
 #include <algorithm>
+#include <type_traits>
 #include <stdexcept>
 #include <vector>
 
@@ -29,9 +31,10 @@ constexpr int kRansAhead = 4096;   // a refill is issued while fewer bytes than 
 
 __device__ __forceinline__ uint32_t rd_u8(const uint8_t *p) { return *p; }
 __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, int *status) {
-  __shared__ uint32_t tab[rans::kProbScale];
-  __shared__ uint32_t ring[kRansRing / 4];
-  __shared__ __align__(16) uint8_t symb[kRansStep];
+  __shared__ uint32_t tab[rans::kProbScale];             // slot m: freq | (m - cum) << 16
+  __shared__ uint8_t tsym[rans::kProbScale];             // slot m: symbol
+  __shared__ uint32_t ring[kRansRing / 4 + 4];           // + a copy of the first 16 bytes, so a window never wraps
+  __shared__ __align__(16) uint8_t symb[kRansStep + 64];
   __shared__ uint32_t cum[257];
   const int lane = threadIdx.x;
   const RansTaskDev t = tasks[blockIdx.x];
@@ -70,7 +73,8 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
     int s = lo;
     for (uint32_t m = m0; m < m0 + 64; m++) {
       while (cum[s + 1] <= m) s++;
-      tab[m] = (uint32_t)s | ((cum[s + 1] - cum[s] - 1) << 8) | (cum[s] << 20);
+      tab[m] = (cum[s + 1] - cum[s]) | ((m - cum[s]) << 16);
+      tsym[m] = (uint8_t)s;
     }
   }
 
@@ -87,42 +91,58 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
   // loads stop at the plane's end (the bytes past it only feed a stream that has overrun, reported below)
   const uint64_t load_max = (end_off + 15) & ~(uint64_t)15;
   uint64_t issued = 0;
-  for (; issued < (uint64_t)kRansAhead; issued += kRansBlk) {
-    const uint4 v = *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane);
-    *(uint4 *)((uint8_t *)ring + ((issued + 16 * lane) & (kRansRing - 1))) = v;
-  }
+  auto ring_put = [&](uint64_t at, const uint4 &v) {
+    const uint32_t o = (uint32_t)(at + 16 * lane) & (kRansRing - 1);
+    *(uint4 *)((uint8_t *)ring + o) = v;
+    if (o == 0) *(uint4 *)((uint8_t *)ring + kRansRing) = v;
+  };
+  for (; issued < (uint64_t)kRansAhead; issued += kRansBlk) ring_put(issued, *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane));
   uint4 pend = {0, 0, 0, 0};
   uint64_t pend_at = 0;
   bool pending = false;
 
   const int64_t n = t.n;
+  const int sbase = lane < 4 ? lane : kRansStep + lane;   // lanes 4..63 store their symbols in a spare area
   for (int64_t s0 = 0; s0 < n; s0 += kRansStep) {
     // refill: write the block loaded one step ago, issue the next while less than kRansAhead bytes are ahead
-    if (pending) *(uint4 *)((uint8_t *)ring + ((pend_at + 16 * lane) & (kRansRing - 1))) = pend;
+    if (pending) ring_put(pend_at, pend);
     pending = issued - q < (uint64_t)kRansAhead;
     if (pending) { pend = *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane); pend_at = issued; issued += kRansBlk; }
     __syncthreads();
     const int ng = (int)std::min<int64_t>(kRansStep, n - s0);
-    for (int g = 0; g < ng; g += 4) {
-      const bool live = lane < 4 && g + lane < ng;
-      const uint32_t qa = (uint32_t)q & ~3u, sh = (uint32_t)q & 3u;   // window = stream bytes q .. q + 7
-      const uint32_t w0 = ring[(qa & (kRansRing - 1)) >> 2], w1 = ring[((qa + 4) & (kRansRing - 1)) >> 2],
-                     w2 = ring[((qa + 8) & (kRansRing - 1)) >> 2];
-      const uint64_t win = (uint64_t)__builtin_amdgcn_alignbyte(w2, w1, sh) << 32 | __builtin_amdgcn_alignbyte(w1, w0, sh);
-      const uint32_t m = st & (rans::kProbScale - 1), e = tab[m];
-      const uint32_t f = ((e >> 8) & 4095u) + 1, c = e >> 20;
-      uint32_t x = f * (st >> rans::kProbBits) + m - c;
-      const uint32_t cnt = live ? (uint32_t)(x < rans::kL) + (uint32_t)(x < (1u << 15)) : 0u;
+    // one group of four symbols; MASKED: the step's last group may hold fewer (lanes 0..3 past ng keep their state).
+    // Lanes 4..63 compute on their own state without effect: the prefix reads lanes 0..3 only, their symbols go to a
+    // spare area, and every table index is in range.
+    auto group = [&](int g, auto masked) {
+      const uint32_t qa = (uint32_t)q & (kRansRing - 4), sh = (uint32_t)q & 3u;
+      const uint32_t m = st & (rans::kProbScale - 1), hi_st = st >> rans::kProbBits;
+      // table entry, symbol and stream window (bytes q .. q + 7 within three dwords) are read together
+      const uint32_t e = tab[m];
+      const uint32_t sy = tsym[m];
+      const uint32_t w0 = ring[qa >> 2], w1 = ring[(qa >> 2) + 1], w2 = ring[(qa >> 2) + 2];
+      __builtin_amdgcn_sched_barrier(0);   // keep the four reads ahead of the first use: one wait for all
+      uint32_t x = (e & 0xffffu) * hi_st + (e >> 16);
+      // renormalisation bytes: 2 below 2^15, 1 below 2^23 (x >= 2^11 and < 2^31 here, so clz(x) is 1 .. 20)
+      uint32_t cnt = (uint32_t)(__builtin_clz(x) - 1) >> 3;
+      bool live = true;
+      if (decltype(masked)::value) { live = lane < 4 && g + lane < ng; cnt = live ? cnt : 0u; }
       // inclusive prefix of cnt over lanes 0..3 (row shifts fill with zeros)
       uint32_t inc = cnt + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)cnt, 0x111, 0xf, 0xf, true);
       inc = inc + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)inc, 0x112, 0xf, 0xf, true);
       const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)inc, 3);
-      const uint32_t bb = (uint32_t)(win >> ((8 * (inc - cnt)) & 63));
-      const uint32_t b0 = bb & 255u, b1 = (bb >> 8) & 255u;
-      x = cnt == 2 ? (x << 16) | (b0 << 8) | b1 : cnt == 1 ? (x << 8) | b0 : x;
-      if (live) { st = x; symb[g + lane] = (uint8_t)(e & 255u); }
+      const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh), hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+      // the lane's bytes b0 = window[excl], b1 = window[excl + 1] as b0 << 8 | b1 (v_perm selectors; 0x0c gives 0)
+      const uint32_t sel = (inc - cnt) * 0x101u + 0x0c0c0001u;
+      const uint32_t be = __builtin_amdgcn_perm(hi, lo, sel);
+      const uint32_t sh8 = 8 * cnt;
+      x = (x << sh8) | (be >> (16 - sh8));
+      st = live ? x : st;
+      symb[sbase + g] = (uint8_t)sy;
       q += total;
-    }
+    };
+    const int nfull = ng & ~3;
+    for (int g = 0; g < nfull; g += 4) group(g, std::false_type{});
+    if (nfull < ng) group(nfull, std::true_type{});
     __syncthreads();
     // flush: lane l owns symbols [8 l, 8 l + 8) of the step
     const int i0 = 8 * lane;
