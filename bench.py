@@ -181,6 +181,48 @@ def cpu_baseline(path, threads, n_prompt=16, n_gen=16, reps=2):
                        f"(qpack-bench protocol, best of {reps}); its prefill rate {pp:.2f} tok/s")
 
 
+def qpack3_cpu_decode(path3, threads):
+    """the reference Container's QPACK3 decode (container.cpp:94-121: one task per coded blob or 16 MiB chunk, a pool of
+    threads) with the reference codec compiled from its sources (oracle/_ref): returns (seconds, raw bytes)"""
+    import ctypes as C
+    import struct
+    from concurrent.futures import ThreadPoolExecutor
+    import oracle
+    L = oracle.rlib()
+    buf = np.fromfile(path3, np.uint8)
+    n = struct.unpack("<I", buf[8:12].tobytes())[0]
+    toc = {}
+    for i in range(n):
+        b = 16 + 72 * i
+        name = buf[b:b + 56].tobytes().rstrip(b"\0").decode()
+        toc[name] = struct.unpack("<QQ", buf[b + 56:b + 72].tobytes())
+    off, ln = toc["manifest.json"]
+    enc = json.loads(buf[off:off + ln].tobytes())["encoded"]
+    tasks = []   # (offset, length, raw)
+    for name in enc:
+        off, ln = toc[name]
+        if buf[off] == 3:
+            cr, nc = struct.unpack("<II", buf[off + 6:off + 14].tobytes())
+            lens = np.frombuffer(buf[off + 14:off + 14 + 4 * nc].tobytes(), np.uint32)
+            pos = off + 14 + 4 * nc
+            for cl in lens:
+                tasks.append((pos, int(cl), struct.unpack("<I", buf[pos + 2:pos + 6].tobytes())[0]))
+                pos += int(cl)
+        else:
+            tasks.append((off, ln, struct.unpack("<I", buf[off + 2:off + 6].tobytes())[0]))
+    outs = [np.empty(r + 16, np.uint8) for _, _, r in tasks]
+    base = buf.ctypes.data
+
+    def one(i):
+        o, l, _ = tasks[i]
+        if L.qpref_rans_decode(C.c_void_p(base + o), l, outs[i].ctypes.data_as(C.c_void_p)):
+            raise RuntimeError(L.qpref_error().decode())
+    t = time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(one, range(len(tasks))))
+    return time.perf_counter() - t, sum(r for _, _, r in tasks)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -194,6 +236,7 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-qpack3", action="store_true", help="skip the QPACK3 (rANS-coded) load leg")
     ap.add_argument("--configs", default="c1,c2,c5",
                     help="other BASELINE configs whose decode rate is added to the line ('' for none)")
     ap.add_argument("--profile", action="store_true",
@@ -300,6 +343,42 @@ def main():
         log(f"{name}: {others_cfg[name]['tokens_per_s']} tok/s, {others_cfg[name]['hbm_pct_of_peak']}% of HBM peak "
             f"({time.time() - t:.1f}s)")
 
+    qpack3 = None
+    if not a.no_qpack3:
+        # the same weights rANS-coded (QPACK3, as qpack-pack writes them), loaded with the decode on the GPU
+        path3 = path + ".qpack3"
+        t = time.time()
+        ncoded = qa.pack(path, path3, min(16, os.cpu_count() or 8))
+        log(f"packed to QPACK3 ({ncoded} coded blobs, {os.path.getsize(path3) / 2**30:.2f} GiB) in {time.time() - t:.1f}s")
+        t = time.perf_counter()
+        m3 = qa.HipLlama.load(path3, max_ctx=64)
+        load3 = time.perf_counter() - t
+        st = m3.load_stats()
+        m3.close()
+        t = time.perf_counter()
+        m2 = qa.HipLlama.load(path, max_ctx=64)
+        load2 = time.perf_counter() - t
+        m2.close()
+        qpack3 = dict(planes=st["planes"], coded_bytes=st["coded_bytes"], raw_bytes=st["raw_bytes"],
+                      decode_ms=round(st["decode_ms"], 2), upload_ms=round(st["upload_ms"], 2),
+                      decode_gbs=round(st["raw_bytes"] / (st["decode_ms"] / 1e3) / 1e9, 2),
+                      load_s=round(load3, 3), qpack2_load_s=round(load2, 3),
+                      kernel="k_rans_decode: one wave per coded plane (16 MiB chunks); latency-bound per plane",
+                      cpu_baseline=None)
+        log(f"QPACK3 load: {load3:.2f}s (QPACK2 {load2:.2f}s); decode kernel {st['decode_ms']:.1f} ms for "
+            f"{st['raw_bytes'] / 1e9:.2f} GB raw over {st['planes']} planes -> {qpack3['decode_gbs']} GB/s")
+        if not a.no_cpu_baseline:
+            import oracle
+            if oracle.ref_available():
+                thr = min(16, os.cpu_count() or 1)
+                sec, raw = qpack3_cpu_decode(path3, thr)
+                qpack3["cpu_baseline"] = {"value": round(raw / sec / 1e9, 3), "unit": "GB/s raw", "cores": thr,
+                                          "kind": "reference",
+                                          "sample": f"every coded blob of this file ({raw / 1e9:.2f} GB raw), decoded as the "
+                                                    f"reference Container does (one task per blob / 16 MiB chunk, {thr} threads)"}
+                log(f"QPACK3 cpu baseline: {raw / sec / 1e9:.2f} GB/s on {thr} threads ({sec:.2f}s)")
+        os.remove(path3)
+
     cpu = None
     if not a.no_cpu_baseline:
         import oracle
@@ -332,6 +411,7 @@ def main():
         "kernels": others,
         "prefill": prefill,
         "other_configs": others_cfg,
+        "qpack3_load": qpack3,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
