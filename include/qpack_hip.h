@@ -23,8 +23,9 @@ extern "C" {
 
 typedef struct qph_model qph_model;
 
-/* tensor kinds (the QPACK2 kinds the Llama path reads, /root/reference/QPACK2.md table) */
-enum { QPH_F32 = 0, QPH_Q8 = 1, QPH_Q4 = 2 };
+/* tensor kinds (the QPACK2 kinds the Llama path reads, /root/reference/QPACK2.md table; the kinds LlamaCuda uploads,
+ * src/model_llama_cuda.cu:549-556) */
+enum { QPH_F32 = 0, QPH_Q8 = 1, QPH_Q4 = 2, QPH_Q1 = 3 };
 
 /* Model config: the config.json keys read by the reference (/root/reference/src/model_llama.cpp:21-27). */
 typedef struct {
@@ -37,7 +38,9 @@ typedef struct {
 } qph_config;
 
 /* One tensor with the canonical name (/root/reference/python/qpack/convert_llama.py:5-11):
- * q8: data int8 [rows, cols], scale f32 [rows];  q4: data u8 [rows, cols/2], scale fp16 [rows, cols/32];  f32: data only.
+ * q8: data int8 [rows, cols], scale f32 [rows];  q4: data u8 [rows, cols/2], scale fp16 [rows, cols/32];
+ * q1: data sign bits u8 [rows, cols/8] (bit c of a row's group g of 16 bytes = column 128g + c, 1 = +1), scale fp16
+ * [rows, cols/128], cols a multiple of 128 (as LlamaCuda requires);  f32: data only.
  * data_coded / scale_coded: 0 for plain bytes; > 0 when the pointer holds a QPACK3 rANS blob of that many bytes
  * (/root/reference/include/qpack/rans.h, QPACK2.md:30-51), which the model decodes in HBM (the reference Container
  * decodes such blobs on the CPU at load, src/container.cpp:94-121). */
@@ -124,7 +127,8 @@ int qph_time_copy(int64_t bytes, int iters, float *ms);
 /* ---- parity hooks (no reference counterpart; the int32 contract of rows_q8 / rows_q4, kernels_x86.cpp:55-106) */
 /* Runs the product's matvec kernel on one matrix (host buffers in, host buffers out): activation quantisation of x,
  * y[rows] = W x, and, when sums != NULL, the exact int32 accumulators: q8 one per (row, 128-column block)
- * [rows, cols/128], q4 one per (row, 32-column group) [rows, cols/32].  xq / bs (optional) receive the int16 activations
+ * [rows, cols/128], q4 one per (row, 32-column group) [rows, cols/32], q1 one per (row, 128-column group)
+ * [rows, cols/128] (rows_q1, kernels_x86.cpp:167-203).  xq / bs (optional) receive the int16 activations
  * and the per-block scales the kernel used. */
 int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int cols, const float *x, float *y,
                       int32_t *sums, int16_t *xq, float *bs);
@@ -158,6 +162,11 @@ typedef struct {
   float std;     /* weight standard deviation (0.02) */
   uint64_t seed;
   char model_type[32];
+  int more_bits; /* with q4 or mlp_q1: qpack-quantize's q4m / q1m policy (tools/qpack-quantize.cpp:67-74): wv and the
+                    w_down of the first and last eighth of the layers and of every third layer in between stay q8 */
+  int q4_head;   /* with q4: embed and lm_head q4 too (qpack-quantize --q4-head) */
+  int mlp_q1;    /* w_gate / w_up / w_down in q1 (sign bits, groups of 128, scale = fp16(mean |w|)), as qpack-quantize
+                    --type q1 writes them (:80-85); needs hidden and ffn multiples of 128 */
 } qph_synth_spec;
 int qph_synth_write(const qph_synth_spec *spec, const char *path, int threads);
 

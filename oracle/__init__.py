@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_LIB = os.path.join(HERE, "liboracle.so")
 REF_LIB = os.path.join(HERE, "_ref", "libqpref.so")
 
-OR_Q8, OR_Q4, OR_F32 = 0, 1, 2
+OR_Q8, OR_Q4, OR_F32, OR_Q1 = 0, 1, 2, 3
 
 
 class QpackFile:
@@ -60,6 +60,10 @@ class QpackFile:
             return OR_Q8, self.blob(e["blob"]).view(np.int8).reshape(rows, cols), self.blob(e["scale"]).view(np.float32), rows, cols
         if e["kind"] == "q4":
             return (OR_Q4, self.blob(e["blob"]).reshape(rows, cols // 2), self.blob(e["scale"]).view(np.uint16).reshape(rows, cols // 32),
+                    rows, cols)
+        if e["kind"] == "q1":
+            G = (cols + 127) // 128
+            return (OR_Q1, self.blob(e["blob"]).reshape(rows, G * 16), self.blob(e["scale"]).view(np.uint16).reshape(rows, G),
                     rows, cols)
         if e["kind"] == "f32":
             return OR_F32, self.blob(e["blob"]).view(np.float32).reshape(shape), None, rows, cols
@@ -106,6 +110,8 @@ def olib():
             "or_group_sums_q4": (None, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
             "or_rows_q8": (None, [C.c_void_p, C.c_void_p, C.c_void_p, _FP, _FP, C.c_int, C.c_int]),
             "or_rows_q4": (None, [C.c_void_p, C.c_void_p, C.c_void_p, _FP, _FP, C.c_int, C.c_int]),
+            "or_rows_q1": (None, [C.c_void_p, C.c_void_p, C.c_void_p, _FP, _FP, C.c_int, C.c_int]),
+            "or_group_sums_q1": (None, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
             "or_matvec": (None, [C.POINTER(OrMat), _FP, _FP]),
             "or_matmul": (None, [C.POINTER(OrMat), _FP, C.c_int, _FP]),
             "or_rmsnorm": (None, [_FP, _FP, C.c_int, C.c_float, _FP]),
@@ -167,6 +173,20 @@ def group_sums_q4(q, xq):
     return out
 
 
+def group_sums_q1(q, xq, cols):
+    rows, G = q.shape[0], (cols + 127) // 128
+    out = np.empty((rows, G), np.int32)
+    olib().or_group_sums_q1(_p(np.ascontiguousarray(q)), rows, cols, _p(xq), _p(out))
+    return out
+
+
+def rows_q1(q, s, xq, bs, cols):
+    rows = q.shape[0]
+    y = np.empty(rows, np.float32)
+    olib().or_rows_q1(_p(q), _p(s), _p(xq), _f(bs), _f(y), rows, cols)
+    return y
+
+
 def rows_q8(q, scale, xq, bs):
     rows, cols = q.shape
     y = np.empty(rows, np.float32)
@@ -181,18 +201,22 @@ def rows_q4(q, s, xq, bs):
     return y
 
 
-def matvec(kind, q, s, x):
+def _cols(kind, q):
+    return q.shape[1] * {OR_Q4: 2, OR_Q1: 8}.get(kind, 1)
+
+
+def matvec(kind, q, s, x, cols=None):
     rows = q.shape[0]
-    cols = q.shape[1] * (2 if kind == OR_Q4 else 1)
+    cols = cols or _cols(kind, q)
     m = ormat(kind, q, s, rows, cols)
     y = np.empty(rows, np.float32)
     olib().or_matvec(C.byref(m), _f(np.ascontiguousarray(x, np.float32)), _f(y))
     return y
 
 
-def matmul(kind, q, s, X):
+def matmul(kind, q, s, X, cols=None):
     rows = q.shape[0]
-    cols = q.shape[1] * (2 if kind == OR_Q4 else 1)
+    cols = cols or _cols(kind, q)
     X = np.ascontiguousarray(X, np.float32)
     m = ormat(kind, q, s, rows, cols)
     Y = np.empty((X.shape[0], rows), np.float32)
@@ -463,6 +487,7 @@ def rlib(threads=0):
             "qpref_snapshot": (C.c_int64, [P, P, C.c_int64]), "qpref_restore": (I, [P, P, C.c_int64]),
             "qpref_matvec": (I, [I, P, P, I, I, _FP, _FP]), "qpref_matmul": (I, [I, P, P, I, I, _FP, I, _FP, I]),
             "qpref_rows_q8": (None, [P, P, P, _FP, _FP, I, I]), "qpref_rows_q4": (None, [P, P, P, _FP, _FP, I, I]),
+            "qpref_rows_q1": (None, [P, P, P, _FP, _FP, I, I]),
             "qpref_rmsnorm": (None, [_FP, _FP, I, C.c_float, _FP]), "qpref_silu_mul": (None, [_FP, _FP, I]),
             "qpref_exp_v": (None, [_FP, _FP, I]), "qpref_to_f16": (None, [_FP, P, I]),
             "qpref_row_f32": (None, [I, P, P, I, I, I, _FP]),

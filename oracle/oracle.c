@@ -142,6 +142,42 @@ void or_rows_q4(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const fl
   #pragma omp parallel for schedule(static)
   for (int r = 0; r < rows; r++) y[r] = row_q4(Q + (int64_t)r * (cols / 2), S + (int64_t)r * G, xq, bs, cols);
 }
+/* q1 (kernels_x86.cpp:167-203): column 128g + c of a row is bit c (LSB first) of the group's 16 bytes, +1 when set,
+ * -1 when clear.  row_q1_nt: lane l (of 8) of group g sums columns 16i + 2l and 16i + 2l + 1 (i = 0..7) exactly;
+ * f_l = fma((float)lane, f16(scale_g) * bs[g], f_l); y = hsum(f).  A partial last group reads activations past cols
+ * as 0. */
+static int q1_sign(const uint8_t *g16, int c) { return (g16[c >> 3] >> (c & 7)) & 1 ? 1 : -1; }
+static float row_q1(const uint8_t *q, const uint16_t *s, const int16_t *xq, const float *bs, int cols) {
+  const int G = (cols + 127) / 128; float f[8] = {0};
+  for (int g = 0; g < G; g++) {
+    const float cb = or_f16_to_f32(s[g]) * bs[g];
+    for (int l = 0; l < 8; l++) {
+      int32_t a = 0;
+      for (int i = 0; i < 8; i++)
+        for (int t = 0; t < 2; t++) {
+          const int c = 16 * i + 2 * l + t, col = 128 * g + c;
+          a += q1_sign(q + 16 * g, c) * (col < cols ? (int32_t)xq[col] : 0);
+        }
+      f[l] = fmaf((float)a, cb, f[l]);
+    }
+  }
+  return hsum8(f);
+}
+void or_rows_q1(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float *bs, float *y, int rows, int cols) {
+  const int G = (cols + 127) / 128;
+  #pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; r++) y[r] = row_q1(Q + (int64_t)r * G * 16, S + (int64_t)r * G, xq, bs, cols);
+}
+void or_group_sums_q1(const uint8_t *Q, int rows, int cols, const int16_t *xq, int32_t *out) {
+  const int G = (cols + 127) / 128;
+  for (int r = 0; r < rows; r++)
+    for (int g = 0; g < G; g++) {
+      int32_t a = 0;
+      for (int c = 0; c < 128 && 128 * g + c < cols; c++) a += q1_sign(Q + ((int64_t)r * G + g) * 16, c) * xq[128 * g + c];
+      out[(int64_t)r * G + g] = a;
+    }
+}
+
 /* rows_f32 (kernels_x86.cpp:26-38): four 8-lane FMA accumulators over 32-column steps, hsum of their sum, scalar tail */
 static float row_f32(const float *w, const float *x, int cols) {
   float a[4][8] = {{0}}; int c = 0;
@@ -163,6 +199,7 @@ void or_matvec(const or_mat *W, const float *x, float *y) {
   int16_t *xq = (int16_t *)malloc(sizeof(int16_t) * (size_t)cols); float *bs = (float *)malloc(sizeof(float) * (size_t)nb);
   or_quant_act(x, cols, xq, bs);
   if (W->kind == OR_Q8) or_rows_q8((const int8_t *)W->q, (const float *)W->s, xq, bs, y, rows, cols);
+  else if (W->kind == OR_Q1) or_rows_q1((const uint8_t *)W->q, (const uint16_t *)W->s, xq, bs, y, rows, cols);
   else or_rows_q4((const uint8_t *)W->q, (const uint16_t *)W->s, xq, bs, y, rows, cols);
   free(xq); free(bs);
 }
@@ -210,6 +247,9 @@ void or_matmul(const or_mat *W, const float *X, int B, float *Y) {
       if (W->kind == OR_Q8) {
         const int8_t *q = (const int8_t *)W->q + (int64_t)r * cols; const float sc = ((const float *)W->s)[r];
         v = (b < B4 && cols % OR_QB == 0) ? mm_row_q8(q, sc, xb, sb, cols) : row_q8(q, sc, xb, sb, cols);
+      } else if (W->kind == OR_Q1) {   /* mm_q1 -> row_q1_multi: the row kernel's arithmetic for every vector */
+        const int G = (cols + 127) / 128;
+        v = row_q1((const uint8_t *)W->q + (int64_t)r * G * 16, (const uint16_t *)W->s + (int64_t)r * G, xb, sb, cols);
       } else {
         const uint8_t *q = (const uint8_t *)W->q + (int64_t)r * (cols / 2); const uint16_t *s = (const uint16_t *)W->s + (int64_t)r * (cols / 32);
         v = b < B4 ? mm_row_q4(q, s, xb, sb, cols) : row_q4(q, s, xb, sb, cols);

@@ -16,12 +16,12 @@
 extern "C" {
 #endif
 
-enum { OR_Q8 = 0, OR_Q4 = 1, OR_F32 = 2 };
+enum { OR_Q8 = 0, OR_Q4 = 1, OR_F32 = 2, OR_Q1 = 3 };
 #define OR_QB 128          /* activation block, /root/reference/src/kernels_impl.h:13 */
 #define OR_ACT_MAX 32767.f /* kActMax on x86, /root/reference/src/kernels_impl.h:19 */
 
 /* a weight matrix: q8 = int8 [rows, cols] + f32 scale [rows]; q4 = u8 [rows, cols/2] + f16 scale [rows, cols/32];
- * f32 = float [rows, cols] (s unused) */
+ * q1 = sign bits u8 [rows, G * 16] + f16 scale [rows, G], G = ceil(cols / 128); f32 = float [rows, cols] (s unused) */
 typedef struct { int kind, rows, cols; const void *q; const void *s; } or_mat;
 
 typedef struct {
@@ -50,6 +50,10 @@ void or_group_sums_q4(const uint8_t *Q, int rows, int cols, const int16_t *xq, i
 /* the row kernels on quantised activations: rows_q8 / rows_q4, /root/reference/src/kernels_x86.cpp:55-106 */
 void or_rows_q8(const int8_t *Q, const float *scale, const int16_t *xq, const float *bs, float *y, int rows, int cols);
 void or_rows_q4(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float *bs, float *y, int rows, int cols);
+/* q1 (sign bits, groups of 128 columns): rows_q1, /root/reference/src/kernels_x86.cpp:167-203; the exact int32 dot
+ * product of every (row, group) with the int16 activation (columns past cols read as 0) */
+void or_rows_q1(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float *bs, float *y, int rows, int cols);
+void or_group_sums_q1(const uint8_t *Q, int rows, int cols, const int16_t *xq, int32_t *out);
 /* matvec (kernels.cpp:72-96) and the tiled prompt product matmul (kernels.cpp:124-143 -> mm_q8 / mm_q4,
  * kernels_x86.cpp:287-371); Y is [B, rows] */
 void or_matvec(const or_mat *W, const float *x, float *y);

@@ -19,6 +19,7 @@ namespace qp { namespace impl {
 // public include directory)
 void rows_q8(const int8_t *Q, const float *scale, const int16_t *xq, const float *bs, float *y, int r0, int r1, int cols);
 void rows_q4(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float *bs, float *y, int r0, int r1, int cols);
+void rows_q1(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float *bs, float *y, int r0, int r1, int cols);
 }}
 
 static thread_local std::string g_err;
@@ -75,10 +76,11 @@ static qp::Tensor mk(int kind, const void *q, const void *s, int rows, int cols)
   if (kind == 0) { t.kind = qp::Kind::Q8; t.scale = (const float *)s; }
   else if (kind == 1) { t.kind = qp::Kind::Q4; t.scale16 = (const uint16_t *)s; t.group = 32; }
   else if (kind == 2) { t.kind = qp::Kind::F32; }
+  else if (kind == 3) { t.kind = qp::Kind::Q1; t.scale16 = (const uint16_t *)s; t.group = 128; }
   else throw std::runtime_error("shim: bad kind");
   return t;
 }
-// kind 0 = q8, 1 = q4, 2 = f32. matvec: quant_rows + rows_q8/rows_q4 (kernels.cpp:72-96)
+// kind 0 = q8, 1 = q4, 2 = f32, 3 = q1. matvec: quant_rows + rows_q8/rows_q4 (kernels.cpp:72-96)
 int qpref_matvec(int kind, const void *q, const void *s, int rows, int cols, const float *x, float *y) {
   QPREF_TRY({ qp::Tensor t = mk(kind, q, s, rows, cols); qp::matvec(t, x, y, rows, cols); });
 }
@@ -96,6 +98,9 @@ void qpref_rows_q8(const int8_t *Q, const float *scale, const int16_t *xq, const
 }
 void qpref_rows_q4(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float *bs, float *y, int rows, int cols) {
   qp::impl::rows_q4(Q, S, xq, bs, y, 0, rows, cols);
+}
+void qpref_rows_q1(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float *bs, float *y, int rows, int cols) {
+  qp::impl::rows_q1(Q, S, xq, bs, y, 0, rows, cols);
 }
 void qpref_rmsnorm(const float *x, const float *w, int n, float eps, float *out) { qp::rmsnorm(x, w, n, eps, out); }
 void qpref_silu_mul(float *g, const float *u, int n) { qp::silu_mul(g, u, n); }

@@ -6,9 +6,9 @@
   kernel_matmul(...)    - the product's batched prefill kernels on one q8 / q4 matrix (parity hook)
   kernel_topk(...)      - the device top-M selection of step_topk on one vector (parity hook)
 """
-from ._lib import LIB_PATH, QPH_F32, QPH_Q4, QPH_Q8, QphError, device_count, lib
+from ._lib import LIB_PATH, QPH_F32, QPH_Q1, QPH_Q4, QPH_Q8, QphError, device_count, lib
 from .model import HipLlama, kernel_matmul, kernel_matvec, kernel_rans_decode, kernel_topk, pack, time_copy
 from .synth import CONFIGS, Shape, write_synthetic
 
-__all__ = ["HipLlama", "kernel_matmul", "kernel_matvec", "kernel_topk", "time_copy", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
-           "QPH_F32", "QPH_Q8", "QPH_Q4"]
+__all__ = ["HipLlama", "kernel_matmul", "kernel_matvec", "kernel_rans_decode", "kernel_topk", "pack", "time_copy", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
+           "QPH_F32", "QPH_Q8", "QPH_Q4", "QPH_Q1"]

@@ -9,7 +9,7 @@ import os
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libqpack_hip.so")
 
-QPH_F32, QPH_Q8, QPH_Q4 = 0, 1, 2
+QPH_F32, QPH_Q8, QPH_Q4, QPH_Q1 = 0, 1, 2, 3
 
 
 class QphError(RuntimeError):
@@ -36,7 +36,8 @@ class SynthSpecC(C.Structure):
     _fields_ = [("hidden", C.c_int), ("layers", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int), ("head_dim", C.c_int),
                 ("ffn", C.c_int), ("vocab", C.c_int), ("tied", C.c_int), ("qkv_bias", C.c_int), ("max_pos", C.c_int),
                 ("q4", C.c_int), ("q4m_alt", C.c_int), ("rms_eps", C.c_float), ("rope_theta", C.c_double), ("std", C.c_float),
-                ("seed", C.c_uint64), ("model_type", C.c_char * 32)]
+                ("seed", C.c_uint64), ("model_type", C.c_char * 32), ("more_bits", C.c_int), ("q4_head", C.c_int),
+                ("mlp_q1", C.c_int)]
 
 
 _P = C.c_void_p

@@ -83,7 +83,7 @@ int qph_load(const char *path, int max_ctx, qph_model **out) {
       if (t.kind == qph::Kind::F16) continue;   // 2-D f16 matrices are not on the HIP path; a required one is reported missing
       qph_tensor q{}; q.name = t.name.c_str(); q.data = t.data; q.scale = t.scale;
       if (t.shape.size() == 1) { q.rows = t.shape[0]; q.cols = 1; } else { q.rows = t.rows(); q.cols = t.cols(); }
-      q.kind = t.kind == qph::Kind::Q8 ? QPH_Q8 : t.kind == qph::Kind::Q4 ? QPH_Q4 : QPH_F32;
+      q.kind = t.kind == qph::Kind::Q8 ? QPH_Q8 : t.kind == qph::Kind::Q4 ? QPH_Q4 : t.kind == qph::Kind::Q1 ? QPH_Q1 : QPH_F32;
       q.data_coded = (int64_t)t.data_coded; q.scale_coded = (int64_t)t.scale_coded;
       ts.push_back(q);
     }
@@ -199,10 +199,10 @@ int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int 
   QPH_API_TRY({
     need(q, "q"); need(scale, "scale"); need(x, "x"); need(y, "y");
     if (rows <= 0 || cols <= 0 || cols % 128) throw std::invalid_argument("matvec: rows > 0 and cols a positive multiple of 128 required");
-    if (kind != QPH_Q8 && kind != QPH_Q4) throw std::invalid_argument("matvec: kind must be QPH_Q8 or QPH_Q4");
-    const size_t qb = kind == QPH_Q8 ? (size_t)rows * cols : (size_t)rows * cols / 2;
-    const size_t sb = kind == QPH_Q8 ? 4ull * rows : 2ull * rows * (cols / 32);
-    const size_t nsum = kind == QPH_Q8 ? (size_t)rows * (cols / 128) : (size_t)rows * (cols / 32);
+    if (kind != QPH_Q8 && kind != QPH_Q4 && kind != QPH_Q1) throw std::invalid_argument("matvec: kind must be QPH_Q8, QPH_Q4 or QPH_Q1");
+    const size_t qb = kind == QPH_Q8 ? (size_t)rows * cols : kind == QPH_Q4 ? (size_t)rows * cols / 2 : (size_t)rows * cols / 8;
+    const size_t sb = kind == QPH_Q8 ? 4ull * rows : kind == QPH_Q4 ? 2ull * rows * (cols / 32) : 2ull * rows * (cols / 128);
+    const size_t nsum = kind == QPH_Q4 ? (size_t)rows * (cols / 32) : (size_t)rows * (cols / 128);
     std::vector<void *> bufs;
     auto alloc = [&](size_t n) { void *p = nullptr; hck(hipMalloc(&p, n), "hipMalloc"); bufs.push_back(p); return p; };
     try {
@@ -213,7 +213,7 @@ int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int 
       hck(hipMemcpy(dq, q, qb, hipMemcpyHostToDevice), "upload q");
       hck(hipMemcpy(ds, scale, sb, hipMemcpyHostToDevice), "upload scale");
       hck(hipMemcpy(dx, x, 4ull * cols, hipMemcpyHostToDevice), "upload x");
-      qph::MvArgs a{}; a.m[0].q = dq; a.m[0].s = ds; a.m[0].rows = rows; a.m[0].cols = cols; a.m[0].kind = kind == QPH_Q8 ? qph::MK_Q8 : qph::MK_Q4;
+      qph::MvArgs a{}; a.m[0].q = dq; a.m[0].s = ds; a.m[0].rows = rows; a.m[0].cols = cols; a.m[0].kind = kind == QPH_Q8 ? qph::MK_Q8 : kind == QPH_Q4 ? qph::MK_Q4 : qph::MK_Q1;
       a.nseg = 1; a.x = dx; a.out[0] = dy; a.dbg_sums = dsum; a.dbg_xq = dxq; a.dbg_bs = dbs;
       qph::mv_plan(a, qph::EPI_STORE);
       hck(qph::launch_matvec(qph::PRO_QUANT, qph::EPI_STORE, a, 256, nullptr), "launch matvec");

@@ -151,6 +151,9 @@ __device__ inline void embed_row(const DMat &e, int tok, float *x, int tid, int 
       const int g = i / 16, j = i % 16; const float sc = half_bits_to_float(s[g]); const uint8_t b = q[i];
       x[32 * g + j] = (float)((int)(b & 15) - 8) * sc; x[32 * g + j + 16] = (float)((int)(b >> 4) - 8) * sc;
     }
+  } else if (e.kind == MK_Q1) {   // row_f32 of a q1 row (kernels.cpp:162-166): (2 bit - 1) * scale
+    const uint8_t *q = (const uint8_t *)e.q + (size_t)tok * (n / 8); const uint16_t *s = (const uint16_t *)e.s + (size_t)tok * (n / 128);
+    for (int i = tid; i < n; i += nthreads) x[i] = ((q[i >> 3] >> (i & 7)) & 1 ? 1.f : -1.f) * half_bits_to_float(s[i >> 7]);
   } else {
     const float *q = (const float *)e.q + (size_t)tok * n;
     for (int i = tid; i < n; i += nthreads) x[i] = q[i];

@@ -9,12 +9,12 @@ constexpr int kQB = 128;            // activation block (/root/reference/src/ker
 constexpr float kActMax = 32767.f;  // x86 kActMax (/root/reference/src/kernels_impl.h:19)
 constexpr int kWave = 64;
 
-enum MatKind : int { MK_F32 = 0, MK_Q8 = 1, MK_Q4 = 2 };
+enum MatKind : int { MK_F32 = 0, MK_Q8 = 1, MK_Q4 = 2, MK_Q1 = 3 };
 
 // a weight matrix resident in HBM, row-major as in the QPACK2 file
 struct DMat {
-  const void *q;       // q8: int8 [rows, cols]; q4: u8 [rows, cols / 2]; f32: float [rows, cols]
-  const void *s;       // q8: f32 [rows]; q4: fp16 [rows, cols / 32]
+  const void *q;       // q8: int8 [rows, cols]; q4: u8 [rows, cols / 2]; q1: sign bits u8 [rows, cols / 8]; f32: float
+  const void *s;       // q8: f32 [rows]; q4: fp16 [rows, cols / 32]; q1: fp16 [rows, cols / 128]
   int rows, cols, kind;
   // layer matrices on the batched prompt path: q8 row sums per 128-column block [rows, cols / 128]; q4 nibble sums and
   // f32 scales per (block, group, row), group-major within each block

@@ -44,7 +44,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { retur
 template <int NS>
 struct UnitGeo {
   const uint8_t *p[NS];     // row bytes (clamped rows)
-  const uint16_t *sp[NS];   // q4 fp16 scale rows
+  const uint16_t *sp[NS];   // q4 / q1 fp16 scale rows
   const float *sc[NS];      // q8 row scale
   int row[NS];              // output rows (may be >= rows: computed, not stored)
   int rows, seg, kind, nch, rowbytes;
@@ -58,7 +58,8 @@ __device__ __forceinline__ UnitGeo<NS> unit_geo(const MvArgs &a, int u, int cols
   const DMat m0 = seg == 0 ? a.m[0] : (seg == 1 ? a.m[1] : a.m[2]);
   const int u0 = seg == 0 ? a.seg_tile0[0] : (seg == 1 ? a.seg_tile0[1] : a.seg_tile0[2]);
   g.seg = seg; g.kind = m0.kind; g.rows = m0.rows;
-  g.rowbytes = m0.kind == MK_Q8 ? cols : cols / 2;
+  g.rowbytes = m0.kind == MK_Q8 ? cols : m0.kind == MK_Q4 ? cols / 2 : cols / 8;
+  const int sgroups = m0.kind == MK_Q1 ? cols / 128 : cols / 32;   // fp16 scales per row (q4, q1)
   g.nch = (g.rowbytes + 1023) >> 10;
 #pragma unroll
   for (int s = 0; s < NS; s++) {
@@ -67,7 +68,7 @@ __device__ __forceinline__ UnitGeo<NS> unit_geo(const MvArgs &a, int u, int cols
     g.row[s] = r;
     const int rc = r < m.rows ? r : m.rows - 1;
     g.p[s] = (const uint8_t *)m.q + (size_t)rc * g.rowbytes;
-    g.sp[s] = (const uint16_t *)m.s + (size_t)rc * (cols / 32);
+    g.sp[s] = (const uint16_t *)m.s + (size_t)rc * sgroups;
     g.sc[s] = (const float *)m.s + rc;
   }
   return g;
@@ -97,7 +98,8 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   const int W = gridDim.x * WAVES, gw = wave * gridDim.x + blockIdx.x;
   const int U = a.seg_tile0[a.nseg];
   const int nmine = gw < U ? (U - gw + W - 1) / W : 0;
-  const int rowbytes = KIND == MK_Q8 ? cols : cols / 2;
+  const int rowbytes = KIND == MK_Q8 ? cols : KIND == MK_Q4 ? cols / 2 : cols / 8;
+  const int GS = KIND == MK_Q1 ? cols / 128 : G;   // the scale group a lane's 16 bytes belong to: 32 (q4) or 128 (q1) columns
   const int nch = (rowbytes + 1023) >> 10;
   const int total = nmine * nch;
   // per-wave LDS: q8 block sums [upw][NS][nbp] ints, q4 unit values [upw][NS] floats
@@ -118,11 +120,11 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
     const bool live = pi < nmine;
     const int off = pc * 1024 + lane * 16, grp = pc * 64 + lane;
     const int offc = !live ? 0 : (off < rowbytes ? off : rowbytes - 16);
-    const int grpc = !live ? 0 : (grp < G ? grp : G - 1);
+    const int grpc = !live ? 0 : (grp < GS ? grp : GS - 1);
 #pragma unroll
     for (int s = 0; s < NS; s++) {
       w[s] = ld16(pp[s] + offc);
-      if (KIND == MK_Q4) sv[s] = psp[s][grpc];
+      if (KIND != MK_Q8) sv[s] = psp[s][grpc];
     }
     if (live && ++pc == nch) { pc = 0; if (++pi < nmine) unit_rows<EPI, NS>(a, gw + pi * W, cols, pp, psp); }
   };
@@ -175,6 +177,43 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
               wsum[(ci * NS + s) * av.nbp + b] = p - 128 * av.lsum[b];
             }
           }
+        } else if (KIND == MK_Q1) {
+          // one lane = one 128-column group: sign bit c of its 16 bytes is column 128 g + c (+1 set, -1 clear).
+          // Each nibble becomes four byte masks (bit k -> byte k: nib * 0x204081 & 0x01010101), dotted with the high
+          // and low activation planes: S = sum of x over the set bits, exact; the group's dot product is 2 S - sum(x).
+          const int g = cc * 64 + lane;
+          const bool act = g < GS;
+          const int gc = act ? g : GS - 1;
+          const uint4 *hp = (const uint4 *)(av.xh + 128 * gc), *lp = (const uint4 *)(av.xl + 128 * gc);
+          const int4 gs4 = *(const int4 *)(av.gsum + 4 * gc);
+          const int xsum = gs4.x + gs4.y + gs4.z + gs4.w;
+          const float bsg = av.bs[gc];
+#pragma unroll
+          for (int s = 0; s < NS; s++) {
+            const uint32_t wd[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
+            int A = 0; uint32_t B = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {          // 32 columns per dword
+#pragma unroll
+              for (int hh = 0; hh < 2; hh++) {     // 16 columns per activation load
+                const uint4 h = hp[2 * j + hh], l = lp[2 * j + hh];
+                const uint32_t hx[4] = {h.x, h.y, h.z, h.w}, lx[4] = {l.x, l.y, l.z, l.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                  const uint32_t nib = (wd[j] >> (16 * hh + 4 * k)) & 15u;
+                  const uint32_t msk = (nib * 0x204081u) & 0x01010101u;
+                  A = __builtin_amdgcn_sdot4((int)msk, (int)hx[k], A, false);
+                  B = __builtin_amdgcn_udot4(msk, lx[k], B, false);
+                }
+              }
+            }
+            const int isum = 2 * (A * 256 + (int)B) - xsum;
+            if (DBG && act && a.dbg_sums) {
+              const UnitGeo<NS> og = unit_geo<EPI, NS>(a, gw + ci * W, cols);
+              if (og.seg == 0 && og.row[s] < og.rows) a.dbg_sums[(size_t)og.row[s] * GS + g] = isum;
+            }
+            if (act) acc[s] = __builtin_fmaf(half_bits_to_float(curs[s]) * bsg, (float)isum, acc[s]);
+          }
         } else {
           const int g = cc * 64 + lane;
           const bool act = g < G;
@@ -205,8 +244,8 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
             if (act) acc[s] = __builtin_fmaf(half_bits_to_float(curs[s]) * bsg, (float)isum, acc[s]);
           }
         }
-        if (++cc == nch) {   // unit complete: q4 values to LDS (LDS and cross-lane ops only inside the loop)
-          if (KIND == MK_Q4) {
+        if (++cc == nch) {   // unit complete: q4 / q1 values to LDS (LDS and cross-lane ops only inside the loop)
+          if (KIND != MK_Q8) {
 #pragma unroll
             for (int s = 0; s < NS; s++) {
               const float v = wave_sum(acc[s]);
@@ -355,7 +394,7 @@ hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStr
   const int cols = a.m[0].cols;
   if (cols % kQB || cols > 32768) return hipErrorInvalidValue;
   const int nseg = epi == EPI_SWIGLU ? 1 : a.nseg;
-  for (int k : {(int)MK_Q8, (int)MK_Q4}) {
+  for (int k : {(int)MK_Q8, (int)MK_Q4, (int)MK_Q1}) {
     MvArgs b = a; b.nseg = 0;
     for (int s = 0; s < nseg; s++)
       if (a.m[s].kind == k) { b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s]; b.nseg++; }
@@ -363,7 +402,9 @@ hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStr
     if (epi == EPI_SWIGLU) { b.m[1] = a.m[1]; b.nseg = 1; b.seg_tile0[0] = 0; b.seg_tile0[1] = a.m[0].rows; }
     if (b.nseg != nseg && (b.dbg_sums || epi == EPI_ARGMAX)) return hipErrorInvalidValue;
     const int ns = mv_ns(b, epi, g_mv_config.cus * 16);
-    const hipError_t e = k == MK_Q8 ? launch_mv_k<MK_Q8>(pro, epi, b, ns, grid_cap, st) : launch_mv_k<MK_Q4>(pro, epi, b, ns, grid_cap, st);
+    const hipError_t e = k == MK_Q8 ? launch_mv_k<MK_Q8>(pro, epi, b, ns, grid_cap, st)
+                         : k == MK_Q4 ? launch_mv_k<MK_Q4>(pro, epi, b, ns, grid_cap, st)
+                                      : launch_mv_k<MK_Q1>(pro, epi, b, ns, grid_cap, st);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -28,7 +28,10 @@ DMat HipLlama::upload(const qph_tensor &t) {
   else if (t.kind == QPH_Q4) {
     if (t.cols % 32) throw std::runtime_error(std::string("hip: q4 tensor ") + t.name + " needs cols % 32 == 0");
     m.kind = MK_Q4; qb = (size_t)t.rows * t.cols / 2; sb = 2ull * t.rows * (t.cols / 32);
-  } else throw std::runtime_error(std::string("hip: matrix ") + t.name + " must be q8 or q4");
+  } else if (t.kind == QPH_Q1) {   // LlamaCuda's condition (model_llama_cuda.cu:554)
+    if (t.cols % 128) throw std::runtime_error(std::string("hip: q1 tensor ") + t.name + " needs cols % 128 == 0");
+    m.kind = MK_Q1; qb = (size_t)t.rows * t.cols / 8; sb = 2ull * t.rows * (t.cols / 128);
+  } else throw std::runtime_error(std::string("hip: matrix ") + t.name + " must be q8, q4 or q1");
   if (!t.data || !t.scale) throw std::runtime_error(std::string("hip: tensor ") + t.name + " has no data");
   m.q = place(t.data, t.data_coded, qb, t.name);
   m.s = place(t.scale, t.scale_coded, sb, t.name);
@@ -127,7 +130,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   }
   ctl_ = (Ctl *)dalloc(sizeof(Ctl));
   out_tok_ = (int *)dalloc(4ull * (ctx_ + 1));
-  // batched prompt path: every layer matrix q8 or q4 (the int8 MFMA products); chunks of up to pf_cap_ tokens
+  // batched prompt path: every layer matrix q8 or q4 (the int8 MFMA products; a model with q1 layers takes its prompts
+  // through decode steps); chunks of up to pf_cap_ tokens
   pf_ok_ = true;
   for (const Layer &ly : layers_)
     for (const DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd})
@@ -470,7 +474,9 @@ float HipLlama::time_greedy(int tok, int n) {
 }
 
 static double mat_bytes(const DMat &m) {
-  return m.kind == MK_Q8 ? (double)m.rows * m.cols + 4.0 * m.rows : (double)m.rows * m.cols / 2 + 2.0 * m.rows * (m.cols / 32);
+  if (m.kind == MK_Q8) return (double)m.rows * m.cols + 4.0 * m.rows;
+  if (m.kind == MK_Q1) return (double)m.rows * m.cols / 8 + 2.0 * m.rows * (m.cols / 128);
+  return (double)m.rows * m.cols / 2 + 2.0 * m.rows * (m.cols / 32);
 }
 
 float HipLlama::time_kernel(int which, int iters, double *bytes) {

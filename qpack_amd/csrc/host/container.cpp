@@ -78,6 +78,11 @@ Container::Container(const std::string &path) {
       if (e["group"].integer(32) != 32) throw std::runtime_error("q4 tensor " + t.name + ": only group 32 is supported");
       if (t.shape.size() != 2 || cols % 32) throw std::runtime_error("q4 tensor " + t.name + ": 2-D with cols % 32 == 0 required");
       if (len < (size_t)(rows * cols / 2) || sl < 2ull * rows * (cols / 32)) throw std::runtime_error("q4 tensor " + t.name + ": blob too short");
+    } else if (kind == "q1") {   // /root/reference/QPACK2.md:18; the GPU path needs whole 128-column groups
+      t.kind = Kind::Q1; sl = view(e["scale"].string(), &t.scale, &t.scale_coded);
+      if (e["group"].integer(128) != 128) throw std::runtime_error("q1 tensor " + t.name + ": only group 128 is supported");
+      if (t.shape.size() != 2 || cols % 128) throw std::runtime_error("q1 tensor " + t.name + ": 2-D with cols % 128 == 0 required");
+      if (len < (size_t)(rows * cols / 8) || sl < 2ull * rows * (cols / 128)) throw std::runtime_error("q1 tensor " + t.name + ": blob too short");
     } else throw std::runtime_error("tensor " + t.name + ": kind '" + kind + "' is not supported by the HIP loader");
     tensors_[t.name] = std::move(t);
   }

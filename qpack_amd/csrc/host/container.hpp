@@ -4,7 +4,8 @@
 //   magic "QPACK1\0\0" | "QPACK2\0\0" (8 bytes), count u32, pad u32,
 //   count x { name[56] NUL-padded, offset u64, length u64 }, blobs each aligned to 64 bytes.
 // manifest.json lists the tensors ({name, shape, kind, blob, scale, group}); config.json holds the model config.
-// Tensor kinds read here: f32, f16 (1-D f16 is widened to f32 at load, as the reference does), q8, q4.
+// Tensor kinds read here: f32, f16 (1-D f16 is widened to f32 at load, as the reference does), q8, q4, q1 (2-D,
+// cols % 128 == 0).
 // QPACK3 (/root/reference/QPACK2.md:30-51): the blobs named in the manifest's "encoded" list hold rANS streams.  Unlike
 // the reference Container, which decodes them on the CPU at load (/root/reference/src/container.cpp:94-121), this view
 // leaves them coded: a tensor records the coded lengths, and the model decodes them in HBM (hip/rans_decode.hip).
@@ -18,14 +19,14 @@
 
 namespace qph {
 
-enum class Kind { F32, F16, Q8, Q4 };
+enum class Kind { F32, F16, Q8, Q4, Q1 };
 
 struct TensorView {
   std::string name;
   std::vector<int64_t> shape;
   Kind kind = Kind::F32;
-  const void *data = nullptr;    // q8: int8 [rows, cols]; q4: u8 [rows, cols / 2]; f32 / f16 dense
-  const void *scale = nullptr;   // q8: f32 [rows]; q4: f16 [rows, cols / 32]
+  const void *data = nullptr;    // q8: int8 [rows, cols]; q4: u8 [rows, cols / 2]; q1: sign bits [rows, cols / 8]; f32 / f16
+  const void *scale = nullptr;   // q8: f32 [rows]; q4: f16 [rows, cols / 32]; q1: f16 [rows, cols / 128]
   uint64_t data_coded = 0;       // QPACK3: > 0 when `data` is a rANS blob of this many bytes
   uint64_t scale_coded = 0;      // QPACK3: > 0 when `scale` is a rANS blob of this many bytes
   int64_t rows() const { return shape.empty() ? 0 : shape[0]; }

@@ -10,6 +10,11 @@
 //   q4 - per 32-column group s = fp16(max|w| / 7), q = clamp(lrintf(w / s), -8, 7) stored as q + 8 in the QPACK2 q4 layout
 //        (byte j = column j low nibble, column j + 16 high nibble).  This absmax scale is this build's choice; the
 //        reference's own writer searches the scale by squared error (qpack-quantize.cpp:34-58).  Kernels read both alike.
+//   q1 - per 128-column group: bit c (LSB first in 16 bytes) = (w >= 0), scale = fp16(mean |w|): q1_group without
+//        calibration (qpack-quantize.cpp:80-85).
+// Which matrices: q8 everything; q4 the layer matrices (q4m_alt: wv and even layers' w_down in q8; more_bits: the
+// quantiser's q4m policy, qpack-quantize.cpp:67-74; q4_head: embed / lm_head q4 too); mlp_q1: w_gate / w_up / w_down
+// in q1 (with more_bits the policy's downs stay q8, its q1m).
 // Norm weights are 1.0; biases are N(0, std) f32.  Tensor names follow /root/reference/python/qpack/convert_llama.py:5-11.
 #include <cmath>
 #include <cstdint>
@@ -56,7 +61,15 @@ static void parallel_rows(int64_t rows, int threads, const std::function<void(in
 static uint16_t to_half(float f) { const _Float16 h = (_Float16)f; uint16_t u; memcpy(&u, &h, 2); return u; }
 static float from_half(uint16_t u) { _Float16 h; memcpy(&h, &u, 2); return (float)h; }
 
-enum class Q { F32, Q8, Q4 };
+enum class Q { F32, Q8, Q4, Q1 };
+
+// tools/qpack-quantize.cpp:67-74 (without --q4m-last-half): wv, and the w_down of layers i < n/8, i >= 7n/8 or with
+// (i - n/8) % 3 == 2
+static bool more_bits(const std::string &tail, int i, int n) {
+  if (tail == "wv") return true;
+  if (tail != "w_down") return false;
+  return i < n / 8 || i >= 7 * n / 8 || (i - n / 8) % 3 == 2;
+}
 struct Plan { std::string name; std::vector<int64_t> shape; Q q; bool ones; uint64_t tid; };
 
 void synth_write(const SynthSpec &s, const std::string &path, int threads) {
@@ -68,20 +81,31 @@ void synth_write(const SynthSpec &s, const std::string &path, int threads) {
   std::vector<Plan> ts; uint64_t tid = 0;
   auto add = [&](const std::string &n, std::vector<int64_t> sh, Q q, bool ones = false) { ts.push_back({n, sh, q, ones, tid++}); };
   const Q lq = s.q4 ? Q::Q4 : Q::Q8;
-  add("embed", {V, d}, Q::Q8);
-  if (!s.tied) add("lm_head", {V, d}, Q::Q8);
+  const Q hq = s.q4 && s.q4_head ? Q::Q4 : Q::Q8;
+  add("embed", {V, d}, hq);
+  if (!s.tied) add("lm_head", {V, d}, hq);
+  // a layer matrix's kind: q1 for the MLP (mlp_q1), q8 where a policy keeps more bits, else the layers' kind
+  auto kind = [&](const std::string &tail, int l) {
+    if (s.mlp_q1 && (tail == "w_gate" || tail == "w_up" || tail == "w_down")) return s.more_bits && more_bits(tail, l, s.layers) ? Q::Q8 : Q::Q1;
+    if (!s.q4) return Q::Q8;
+    if (s.more_bits) return more_bits(tail, l, s.layers) ? Q::Q8 : Q::Q4;
+    if (s.q4m_alt && (tail == "wv" || (tail == "w_down" && l % 2 == 0))) return Q::Q8;
+    return Q::Q4;
+  };
   add("final_norm", {d}, Q::F32, true);
   for (int l = 0; l < s.layers; l++) {
     const std::string p = "layers." + std::to_string(l) + ".";
     add(p + "attn_norm", {d}, Q::F32, true); add(p + "ffn_norm", {d}, Q::F32, true);
-    add(p + "wq", {qd, d}, lq); add(p + "wk", {kvd, d}, lq);
-    add(p + "wv", {kvd, d}, s.q4 && s.q4m_alt ? Q::Q8 : lq);
-    add(p + "wo", {d, qd}, lq);
+    add(p + "wq", {qd, d}, kind("wq", l)); add(p + "wk", {kvd, d}, kind("wk", l));
+    add(p + "wv", {kvd, d}, kind("wv", l));
+    add(p + "wo", {d, qd}, kind("wo", l));
     if (s.qkv_bias) { add(p + "bq", {qd}, Q::F32); add(p + "bk", {kvd}, Q::F32); add(p + "bv", {kvd}, Q::F32); }
-    add(p + "w_gate", {ff, d}, lq); add(p + "w_up", {ff, d}, lq);
-    add(p + "w_down", {d, ff}, s.q4 && s.q4m_alt && l % 2 == 0 ? Q::Q8 : lq);
+    add(p + "w_gate", {ff, d}, kind("w_gate", l)); add(p + "w_up", {ff, d}, kind("w_up", l));
+    add(p + "w_down", {d, ff}, kind("w_down", l));
   }
+  (void)lq;
   for (auto &t : ts) if (t.q == Q::Q4 && t.shape[1] % 32) throw std::runtime_error("synth: q4 tensor " + t.name + " needs cols % 32 == 0");
+  for (auto &t : ts) if (t.q == Q::Q1 && t.shape[1] % 128) throw std::runtime_error("synth: q1 tensor " + t.name + " needs cols % 128 == 0");
 
   Json man = Json::object(), tl = Json::array();
   std::vector<std::pair<std::string, uint64_t>> plan;
@@ -94,13 +118,18 @@ void synth_write(const SynthSpec &s, const std::string &path, int threads) {
     else if (t.q == Q::Q8) {
       e.set("kind", "q8"); e.set("blob", std::string(bid) + ".q8"); e.set("scale", std::string(bid) + ".scale");
       plan.push_back({std::string(bid) + ".q8", (uint64_t)(rows * cols)}); plan.push_back({std::string(bid) + ".scale", 4ull * rows});
+    } else if (t.q == Q::Q1) {
+      e.set("kind", "q1"); e.set("blob", std::string(bid) + ".q1"); e.set("scale", std::string(bid) + ".scale"); e.set("group", 128);
+      plan.push_back({std::string(bid) + ".q1", (uint64_t)(rows * cols / 8)}); plan.push_back({std::string(bid) + ".scale", 2ull * rows * (cols / 128)});
     } else {
       e.set("kind", "q4"); e.set("blob", std::string(bid) + ".q4"); e.set("scale", std::string(bid) + ".scale"); e.set("group", 32);
       plan.push_back({std::string(bid) + ".q4", (uint64_t)(rows * cols / 2)}); plan.push_back({std::string(bid) + ".scale", 2ull * rows * (cols / 32)});
     }
     tl.push(e);
   }
-  man.set("format", "QPACK2"); man.set("quant", s.q4 ? (s.q4m_alt ? "q4m" : "q4") : "q8"); man.set("tensors", tl);
+  man.set("format", "QPACK2");
+  man.set("quant", s.mlp_q1 ? (s.more_bits ? "q1m" : "q1") : s.q4 ? (s.q4m_alt || s.more_bits ? "q4m" : "q4") : "q8");
+  man.set("tensors", tl);
   man.set("synthetic", Json::object()); man.obj.back().second.set("seed", Json((int64_t)s.seed)); man.obj.back().second.set("std", Json((double)s.std));
   Json cfg = Json::object();
   cfg.set("arch", "llama"); cfg.set("model_type", s.model_type[0] ? s.model_type : "llama");
@@ -132,6 +161,24 @@ void synth_write(const SynthSpec &s, const std::string &path, int threads) {
           float sr = mx / 127.f; if (sr == 0) sr = 1.f;
           for (int64_t c = 0; c < cols; c++) q[(size_t)(r * cols + c)] = (int8_t)std::max(-127, std::min(127, (int)std::nearbyint(row[(size_t)c] / sr)));
           sc[(size_t)r] = sr;
+        }
+      });
+      w.write(plan[pi].first, q.data(), plan[pi].second); pi++;
+      w.write(plan[pi].first, sc.data(), plan[pi].second); pi++;
+    } else if (t.q == Q::Q1) {
+      const int64_t G = cols / 128;
+      std::vector<uint8_t> q((size_t)(rows * cols / 8)); std::vector<uint16_t> sc((size_t)(rows * G));
+      parallel_rows(rows, threads, [&](int64_t a, int64_t b) {
+        std::vector<float> row((size_t)cols);
+        for (int64_t r = a; r < b; r++) {
+          normals(s.seed, t.tid, r * cols, (r + 1) * cols, s.std, row.data());
+          for (int64_t g = 0; g < G; g++) {
+            const float *wg = row.data() + 128 * g; double num = 0;
+            uint8_t *o = q.data() + (size_t)((r * G + g) * 16);
+            memset(o, 0, 16);
+            for (int i = 0; i < 128; i++) { num += std::fabs(wg[i]); if (wg[i] >= 0) o[i >> 3] |= (uint8_t)(1 << (i & 7)); }
+            sc[(size_t)(r * G + g)] = to_half((float)(num / 128.0));
+          }
         }
       });
       w.write(plan[pi].first, q.data(), plan[pi].second); pi++;

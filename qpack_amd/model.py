@@ -160,14 +160,14 @@ def time_copy(nbytes, iters=4):
 
 def kernel_matvec(kind, q, scale, x):
     """the product's matvec kernel on one matrix: returns (y, exact int32 sums, int16 activation, block scales)"""
-    from ._lib import QPH_Q8
+    from ._lib import QPH_Q1, QPH_Q4
     q = np.ascontiguousarray(q)
     scale = np.ascontiguousarray(scale)
     x = np.ascontiguousarray(x, dtype=np.float32)
     rows = q.shape[0]
-    cols = q.shape[1] if kind == QPH_Q8 else q.shape[1] * 2
+    cols = q.shape[1] * {QPH_Q4: 2, QPH_Q1: 8}.get(kind, 1)
     y = np.empty(rows, np.float32)
-    sums = np.empty((rows, cols // 128 if kind == QPH_Q8 else cols // 32), np.int32)
+    sums = np.empty((rows, cols // 32 if kind == QPH_Q4 else cols // 128), np.int32)
     xq = np.empty(cols, np.int16)
     bs = np.empty(cols // 128, np.float32)
     check(lib().qph_kernel_matvec(kind, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols, _fptr(x),

@@ -26,6 +26,9 @@ class Shape:
     max_pos: int = 32768
     q4: bool = False
     q4m_alt: bool = False
+    more_bits: bool = False
+    q4_head: bool = False
+    mlp_q1: bool = False
 
 
 QWEN05 = dict(hidden=896, layers=24, heads=14, kv_heads=2, head_dim=64, ffn=4864, vocab=151936, tied=True, qkv_bias=True,
@@ -50,6 +53,18 @@ CONFIGS = {
                      rope_theta=1e6, model_type="qwen2", q4=True),
     "mini_q4m": Shape(hidden=384, layers=3, heads=6, kv_heads=2, head_dim=64, ffn=640, vocab=1500, tied=False, qkv_bias=True,
                       rope_theta=1e6, model_type="qwen2", q4=True, q4m_alt=True),
+    # qpack-quantize's other outputs: q1 MLP matrices (q1m keeps the more_bits downs in q8), the real q4m layer policy,
+    # and q4 with a q4 embedding / head
+    "mini_q1": Shape(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000, tied=True, qkv_bias=True,
+                     rope_theta=1e6, model_type="qwen2", mlp_q1=True),
+    "mini_q1m": Shape(hidden=384, layers=9, heads=6, kv_heads=2, head_dim=64, ffn=640, vocab=1500, tied=False, qkv_bias=True,
+                      rope_theta=1e6, model_type="qwen2", mlp_q1=True, more_bits=True),
+    "mini_q4mb": Shape(hidden=384, layers=9, heads=6, kv_heads=2, head_dim=64, ffn=640, vocab=1500, tied=False, qkv_bias=True,
+                       rope_theta=1e6, model_type="qwen2", q4=True, more_bits=True),
+    "mini_q4h": Shape(hidden=512, layers=2, heads=4, kv_heads=1, head_dim=128, ffn=768, vocab=2048, tied=False, qkv_bias=False,
+                      rope_theta=5e5, model_type="llama", rms_eps=1e-5, q4=True, q4_head=True),
+    # the 8B shape with 1-bit MLP matrices (q1, attention q8): a decode workload for the q1 matvec
+    "c3_q1": Shape(**LLAMA8, mlp_q1=True),
 }
 
 
@@ -61,6 +76,7 @@ def write_synthetic(shape, path, seed=1234, std=0.02, threads=0):
     for f in ("hidden", "layers", "heads", "kv_heads", "head_dim", "ffn", "vocab", "max_pos"):
         setattr(s, f, int(getattr(shape, f)))
     s.tied, s.qkv_bias, s.q4, s.q4m_alt = int(shape.tied), int(shape.qkv_bias), int(shape.q4), int(shape.q4m_alt)
+    s.more_bits, s.q4_head, s.mlp_q1 = int(shape.more_bits), int(shape.q4_head), int(shape.mlp_q1)
     s.rms_eps, s.rope_theta, s.std, s.seed = shape.rms_eps, shape.rope_theta, std, seed
     s.model_type = shape.model_type.encode()[:31]
     check(lib().qph_synth_write(C.byref(s), str(path).encode(), int(threads)))

@@ -36,6 +36,10 @@ MODELS = {
     "mini_q4m": (100, 64, 256),
     "c1": (32, 128, 168),
     "c2": (512, 256, 776),
+    "mini_q1": (70, 64, 256),
+    "mini_q1m": (70, 64, 256),
+    "mini_q4mb": (70, 64, 256),
+    "mini_q4h": (70, 64, 256),
 }
 SEED = 1234
 PROMPT_SEED = 99
@@ -124,6 +128,20 @@ def kernel_fixture():
     ev = np.empty_like(e)
     L.qpref_exp_v(O._f(e), O._f(ev), 1005)
     out.update(dict(rms_x=x, rms_w=w, rms_out=o, silu_g=g, silu_u=u, silu_out=gs, exp_x=e, exp_out=ev))
+    # q1 (rows_q1 / mm_q1): sign bits and fp16 group scales; 1000 columns end in a partial group
+    r1 = np.random.default_rng(2025)
+    for rows, cols in [(48, 1024), (33, 896), (9, 1000)]:
+        G = (cols + 127) // 128
+        q1 = r1.integers(0, 256, (rows, G * 16)).astype(np.uint8)
+        s1 = (r1.random((rows, G)) * 0.01 + 1e-4).astype(np.float16).view(np.uint16)
+        x1 = act_vector(r1, cols)
+        y1 = np.empty(rows, np.float32)
+        assert L.qpref_matvec(3, q1.ctypes.data, s1.ctypes.data, rows, cols, O._f(x1), O._f(y1)) == 0
+        X1 = np.stack([act_vector(r1, cols) * (i + 1) for i in range(6)]).astype(np.float32)
+        Y1 = np.empty((6, rows), np.float32)
+        assert L.qpref_matmul(3, q1.ctypes.data, s1.ctypes.data, rows, cols, O._f(X1), 6, O._f(Y1), 0) == 0
+        k = f"q1_{rows}x{cols}"
+        out.update({k + "_q": q1, k + "_s": s1, k + "_x": x1, k + "_y": y1, k + "_X": X1, k + "_Y": Y1})
     np.savez_compressed(os.path.join(HERE, "kernels.npz"), **out)
     print("kernels.npz written", flush=True)
 

@@ -21,7 +21,8 @@ pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-@pytest.mark.parametrize("name", ["mini", "mini128", "mini_q4", "mini_q4m", "c1", "c2"])
+@pytest.mark.parametrize("name", ["mini", "mini128", "mini_q4", "mini_q4m", "c1", "c2", "mini_q1", "mini_q1m", "mini_q4mb",
+                                  "mini_q4h"])
 def test_matches_reference_fixture(name, synth):
     with open(os.path.join(GOLD, name + ".json")) as f:
         fx = json.load(f)

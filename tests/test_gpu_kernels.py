@@ -62,6 +62,30 @@ def test_matvec_q4_exact_sums(rows, cols):
     assert np.all(np.abs(y - y_o) <= 2e-6 * mag + 1e-30), float(np.max(np.abs(y - y_o) / (mag + 1e-30)))
 
 
+@pytest.mark.parametrize("rows,cols", [(1000, 4096), (257, 896), (300, 18944), (9, 128), (4096, 14336), (14336, 4096)])
+def test_matvec_q1_exact_sums(rows, cols):
+    """q1 (rows_q1, kernels_x86.cpp:167-203): the exact int32 dot product of every (row, 128-column group) equals a
+    brute-force numpy sum over the unpacked signs; y within 2e-6 of the summed magnitudes of the oracle's (fp32 order:
+    per-lane fma over the groups, then the wave sum, instead of the reference's 8 AVX lanes)"""
+    rng = np.random.default_rng(rows * 13 + cols)
+    G = cols // 128
+    q = rng.integers(0, 256, (rows, G * 16)).astype(np.uint8)
+    s = (rng.random((rows, G)) * 0.01 + 1e-4).astype(np.float16).view(np.uint16)
+    x = act_vector(rng, cols)
+    print(f"q1 matvec rows={rows} cols={cols}", flush=True)
+    y, sums, xq, bs = qa.kernel_matvec(qa.QPH_Q1, q, s, x)
+    xq_o, bs_o = O.quant_act(x)
+    np.testing.assert_array_equal(xq, xq_o)
+    sign = np.unpackbits(q, axis=1, bitorder="little").astype(np.int64) * 2 - 1      # [rows, cols]: +1 / -1
+    brute = (sign.reshape(rows, G, 128) * xq_o.astype(np.int64).reshape(1, G, 128)).sum(2)
+    np.testing.assert_array_equal(sums, brute)
+    np.testing.assert_array_equal(O.group_sums_q1(q, xq_o, cols), brute)
+    y_o = O.rows_q1(q, s, xq_o, bs_o, cols)
+    comb = s.view(np.float16).astype(np.float32) * bs_o[None, :]
+    mag = np.abs(comb * brute).sum(1)
+    assert np.all(np.abs(y - y_o) <= 2e-6 * mag + 1e-30), float(np.max(np.abs(y - y_o) / (mag + 1e-30)))
+
+
 @pytest.mark.parametrize("rows,cols,B", [(1000, 4096, 200), (256, 896, 129), (300, 14336, 17), (7, 128, 1), (4864, 896, 64),
                                          (130, 512, 1024), (300, 896, 2048),
                                          (130, 512, 300)])
@@ -77,6 +101,30 @@ def test_matmul_q8_rows_equal_decode_arithmetic(rows, cols, B):
     for b in range(B):
         xq, bs = O.quant_act(X[b])
         np.testing.assert_array_equal(Y[b], O.rows_q8(q, s, xq, bs), err_msg=f"token {b}")
+
+
+@pytest.mark.parametrize("rows,cols", [(1000, 4096), (257, 896), (300, 18944), (9, 128), (4096, 14336), (14336, 4096)])
+def test_matvec_q1_exact_sums(rows, cols):
+    """q1 (rows_q1, kernels_x86.cpp:167-203): the exact int32 dot product of every (row, 128-column group) equals a
+    brute-force numpy sum over the unpacked signs; y within 2e-6 of the summed magnitudes of the oracle's (fp32 order:
+    per-lane fma over the groups, then the wave sum, instead of the reference's 8 AVX lanes)"""
+    rng = np.random.default_rng(rows * 13 + cols)
+    G = cols // 128
+    q = rng.integers(0, 256, (rows, G * 16)).astype(np.uint8)
+    s = (rng.random((rows, G)) * 0.01 + 1e-4).astype(np.float16).view(np.uint16)
+    x = act_vector(rng, cols)
+    print(f"q1 matvec rows={rows} cols={cols}", flush=True)
+    y, sums, xq, bs = qa.kernel_matvec(qa.QPH_Q1, q, s, x)
+    xq_o, bs_o = O.quant_act(x)
+    np.testing.assert_array_equal(xq, xq_o)
+    sign = np.unpackbits(q, axis=1, bitorder="little").astype(np.int64) * 2 - 1      # [rows, cols]: +1 / -1
+    brute = (sign.reshape(rows, G, 128) * xq_o.astype(np.int64).reshape(1, G, 128)).sum(2)
+    np.testing.assert_array_equal(sums, brute)
+    np.testing.assert_array_equal(O.group_sums_q1(q, xq_o, cols), brute)
+    y_o = O.rows_q1(q, s, xq_o, bs_o, cols)
+    comb = s.view(np.float16).astype(np.float32) * bs_o[None, :]
+    mag = np.abs(comb * brute).sum(1)
+    assert np.all(np.abs(y - y_o) <= 2e-6 * mag + 1e-30), float(np.max(np.abs(y - y_o) / (mag + 1e-30)))
 
 
 @pytest.mark.parametrize("rows,cols,B", [(1000, 4096, 200), (257, 896, 129), (300, 18944, 17), (9, 128, 1), (3584, 3584, 64),

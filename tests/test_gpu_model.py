@@ -2,6 +2,8 @@
 
 Bar: logits within max-abs 1e-2 and relative 1e-3 of the reference, identical greedy streams.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -18,7 +20,7 @@ def close(a, b):
     return float(err.max()), bool(np.all(err <= np.maximum(ATOL, RTOL * np.abs(b))))
 
 
-@pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_q4", "mini_q4m"])
+@pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_q4", "mini_q4m", "mini_q1", "mini_q1m", "mini_q4mb", "mini_q4h"])
 def test_decode_and_greedy_match_oracle(cfg, synth):
     path = synth(cfg)
     gpu = qa.HipLlama.load(path, max_ctx=256)
@@ -179,4 +181,28 @@ def test_long_context_restore(cfg, T, synth):
         assert ok, f"step logits max|d| {err}"
     g, o = gpu.greedy_run(int(np.argmax(lg)), 16), orc.greedy_run(int(np.argmax(lo)), 16)
     np.testing.assert_array_equal(g, o)
+    gpu.close(); orc.close()
+
+
+REF_QUANT = os.path.join(os.path.dirname(O.REF_LIB), "qpack-quantize")
+
+
+@pytest.mark.skipif(not os.path.exists(REF_QUANT), reason="oracle/_ref/qpack-quantize not built")
+@pytest.mark.parametrize("src,args", [("mini128", ["--type", "q1"]), ("mini", ["--type", "q1", "--q1-attn", "q4"]),
+                                      ("mini128", ["--type", "q4", "--q4-head"]), ("mini_q4m", ["--type", "q4m"])])
+def test_files_of_the_reference_quantiser(src, args, synth, tmp_path):
+    """files written by the reference's own qpack-quantize (q1 MLP, q1 with q4 attention, q4 head, q4m policy) from a
+    synthetic q8 / q4m model: logits within the bar and identical greedy streams against the oracle"""
+    import subprocess
+    path = str(tmp_path / "rq.qpack")
+    subprocess.run([REF_QUANT, synth(src), path] + args, check=True, capture_output=True)
+    gpu = qa.HipLlama.load(path, max_ctx=160)
+    orc = O.Oracle(path, max_ctx=160)
+    rng = np.random.default_rng(5)
+    toks = rng.integers(0, gpu.vocab(), 40).astype(np.int32)
+    print(f"reference-quantised {src} {args}", flush=True)
+    lg, lo = gpu.prefill(toks, 1), orc.prefill(toks, 1)
+    err, ok = close(lg, lo)
+    assert ok, f"prefill logits max|d| {err}"
+    np.testing.assert_array_equal(gpu.greedy_run(int(np.argmax(lg)), 32), orc.greedy_run(int(np.argmax(lo)), 32))
     gpu.close(); orc.close()

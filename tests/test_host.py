@@ -105,3 +105,23 @@ def test_reference_reads_synthetic_files(tmp_path):
     r = O.Ref(p, 32)
     assert r.vocab() == qa.CONFIGS["mini_q4m"].vocab and r.hidden() == qa.CONFIGS["mini_q4m"].hidden
     r.close()
+
+
+REF_QUANT = os.path.join(os.path.dirname(O.REF_LIB), "qpack-quantize")
+
+
+@pytest.mark.skipif(not os.path.exists(REF_QUANT), reason="oracle/_ref/qpack-quantize not built")
+@pytest.mark.parametrize("name,args", [("mini_q1", ["--type", "q1"]), ("mini_q1m", ["--type", "q1m"]),
+                                       ("mini_q4mb", ["--type", "q4m"]), ("mini_q4h", ["--type", "q4", "--q4-head"])])
+def test_synthetic_policies_match_qpack_quantize(name, args, tmp_path):
+    """the synthetic writer puts every tensor in the kind the reference quantiser picks for it (q1 MLP matrices, the q4m
+    more_bits layer policy, the q4 head), given the same shape in q8"""
+    import dataclasses
+    import subprocess
+    q8 = dataclasses.replace(qa.CONFIGS[name], q4=False, mlp_q1=False, more_bits=False, q4_head=False)
+    src, out, mine = str(tmp_path / "q8.qpack"), str(tmp_path / "ref.qpack"), str(tmp_path / "mine.qpack")
+    qa.write_synthetic(q8, src, seed=3)
+    subprocess.run([REF_QUANT, src, out] + args, check=True, capture_output=True)
+    qa.write_synthetic(name, mine, seed=3)
+    kinds = lambda p: {e["name"]: (e["kind"], e.get("group")) for e in O.QpackFile(p).manifest["tensors"]}   # noqa: E731
+    assert kinds(mine) == kinds(out)

@@ -116,13 +116,34 @@ def test_matvec_matmul_golden(kern, shape):
     np.testing.assert_array_equal(O.matmul(O.OR_Q4, kern[k + "_q"], kern[k + "_s"], kern[k + "_X"]), kern[k + "_Y"])
 
 
+@pytest.mark.parametrize("shape", ["48x1024", "33x896", "9x1000"])
+def test_q1_matvec_matmul_golden(kern, shape):
+    k, cols = "q1_" + shape, int(shape.split("x")[1])
+    np.testing.assert_array_equal(O.matvec(O.OR_Q1, kern[k + "_q"], kern[k + "_s"], kern[k + "_x"], cols), kern[k + "_y"])
+    np.testing.assert_array_equal(O.matmul(O.OR_Q1, kern[k + "_q"], kern[k + "_s"], kern[k + "_X"], cols), kern[k + "_Y"])
+
+
+def test_q1_group_sums_brute_force():
+    """exact int32 per (row, 128-column group) against numpy on the unpacked sign bits, partial last group included"""
+    rng = np.random.default_rng(8)
+    for rows, cols in [(3, 128), (5, 1000), (4, 4096)]:
+        G = (cols + 127) // 128
+        q = rng.integers(0, 256, (rows, G * 16)).astype(np.uint8)
+        xq = rng.integers(-32767, 32768, cols).astype(np.int16)
+        sign = (np.unpackbits(q, axis=1, bitorder="little").astype(np.int64) * 2 - 1)[:, :cols]
+        xp = np.zeros(G * 128, np.int64); xp[:cols] = xq
+        brute = (np.pad(sign, ((0, 0), (0, G * 128 - cols))).reshape(rows, G, 128) * xp.reshape(1, G, 128)).sum(2)
+        np.testing.assert_array_equal(O.group_sums_q1(q, xq, cols), brute)
+
+
 def test_elementwise_golden(kern):
     np.testing.assert_array_equal(O.rmsnorm(kern["rms_x"], kern["rms_w"], 1e-6), kern["rms_out"])
     np.testing.assert_array_equal(O.silu_mul(kern["silu_g"], kern["silu_u"]), kern["silu_out"])
     np.testing.assert_array_equal(O.exp_v(kern["exp_x"]), kern["exp_out"])
 
 
-@pytest.mark.parametrize("name", ["mini", "mini128", "mini_q4", "mini_q4m", "c1"])
+@pytest.mark.parametrize("name", ["mini", "mini128", "mini_q4", "mini_q4m", "c1", "mini_q1", "mini_q1m", "mini_q4mb",
+                                  "mini_q4h"])
 def test_model_golden(name, tmp_path):
     """prefill logits sample and the whole greedy stream are bit-identical to the reference's"""
     fx = gold(name)
@@ -143,7 +164,7 @@ needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref/libqpr
 
 
 @needs_ref
-@pytest.mark.parametrize("name", ["mini_q4m", "mini128"])
+@pytest.mark.parametrize("name", ["mini_q4m", "mini128", "mini_q1m"])
 def test_model_matches_live_reference(name, tmp_path):
     path = str(tmp_path / f"{name}.qpack")
     qa.write_synthetic(name, path, seed=77)
