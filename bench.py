@@ -38,25 +38,44 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def step_bytes(shape, T):
-    """algorithmic HBM bytes of one decode step at context T: every weight byte + scale once, norms / biases, the embedding
-    row, and the fp16 K and V rows of positions [0, T) in every layer"""
-    d, ff, V, L = shape.hidden, shape.ffn, shape.vocab, shape.layers
-    qd, kvd = shape.heads * shape.head_dim, shape.kv_heads * shape.head_dim
+def quant_name(shape):
+    if shape.mlp_q1:
+        return "q1m" if shape.more_bits else "q1"
+    if shape.q4:
+        return "q4m" if (shape.q4m_alt or shape.more_bits) else "q4"
+    return "q8"
 
-    def mat(rows, cols, q4):
-        return rows * cols / 2 + 2 * rows * (cols // 32) if q4 else rows * cols + 4 * rows
-    q4 = shape.q4
-    layer = (mat(qd, d, q4) + mat(kvd, d, q4) + mat(kvd, d, q4 and not shape.q4m_alt) + mat(d, qd, q4)
-             + 2 * mat(ff, d, q4) + mat(d, ff, q4) + 2 * 4 * d + (4 * (qd + 2 * kvd) if shape.qkv_bias else 0))
-    if q4 and shape.q4m_alt:   # even layers keep w_down in q8
-        layer_down_q8 = mat(d, ff, False) - mat(d, ff, True)
-        weights = L * layer + (L + 1) // 2 * layer_down_q8
-    else:
-        weights = L * layer
-    head = mat(V, d, False) + 4 * d
-    kv = L * 2 * T * kvd * 2
-    return weights + head + d + kv
+
+def file_weight_bytes(path):
+    """HBM bytes one decode step reads from the weights of a QPACK2 file: every tensor's blobs (data + scale) once,
+    except the embedding, of which one row is read - unless it is tied, when it is also the output head"""
+    import struct
+    with open(path, "rb") as f:
+        head = f.read(16)
+        n = struct.unpack("<I", head[8:12])[0]
+        toc = {}
+        for _ in range(n):
+            e = f.read(72)
+            toc[e[:56].rstrip(b"\0").decode()] = struct.unpack("<QQ", e[56:72])
+        off, ln = toc["manifest.json"]
+        f.seek(off)
+        man = json.loads(f.read(ln))
+        f.seek(toc["config.json"][0])
+        cfg = json.loads(f.read(toc["config.json"][1]))
+    total = 0
+    for e in man["tensors"]:
+        b = toc[e["blob"]][1] + (toc[e["scale"]][1] if "scale" in e else 0)
+        if e["name"] == "embed":
+            b = b if cfg.get("tie_embeddings") else b // e["shape"][0]
+        total += b
+    return total
+
+
+def step_bytes(weight_bytes, shape, T):
+    """algorithmic HBM bytes of one decode step at context T: the weights (file_weight_bytes) and the fp16 K and V rows
+    of positions [0, T) in every layer"""
+    kvd = shape.kv_heads * shape.head_dim
+    return weight_bytes + shape.layers * 2 * T * kvd * 2
 
 
 def calibration_copy(reps=4):
@@ -120,6 +139,7 @@ def other_config(name, seed, steps_override=None):
     path = os.path.join(tmpdir, name + ".qpack")
     try:
         qa.write_synthetic(name, path, seed=seed, threads=min(16, os.cpu_count() or 8))
+        wbytes = file_weight_bytes(path)
         ctx = max(prompt, restore or 0) + steps + 16
         m = qa.HipLlama.load(path, max_ctx=ctx)
         rng = np.random.default_rng(seed)
@@ -145,9 +165,9 @@ def other_config(name, seed, steps_override=None):
             os.remove(path)
         os.rmdir(tmpdir)
     T2 = T1 + steps
-    sb = step_bytes(shape, (T1 + 1 + T2) / 2)
+    sb = step_bytes(wbytes, shape, (T1 + 1 + T2) / 2)
     gbs = sb / (ms / 1e3 / steps) / 1e9
-    kind = "q4m" if shape.q4m_alt else ("q4" if shape.q4 else "q8")
+    kind = quant_name(shape)
     ctx_desc = f"restored N(0,1) fp16 context of {restore}" if restore else f"{prompt}-token prompt"
     return dict(tokens_per_s=round(steps / (ms / 1e3), 1), ms_per_token=round(ms / steps, 4),
                 hbm_pct_of_peak=round(100 * gbs / HBM_PEAK_GBS, 2), bytes_per_token=round(sb),
@@ -296,7 +316,7 @@ def main():
     T1 = m.pos()
     tok_s = a.steps / (ms / 1e3)
     mean_T = (T0 + 1 + T1) / 2
-    sb = step_bytes(shape, mean_T)
+    sb = step_bytes(file_weight_bytes(path), shape, mean_T)
     step_gbs = sb / (ms / 1e3 / a.steps) / 1e9
     log(f"decode: {a.steps} tokens in {ms:.2f} ms (HIP events), wall {wall * 1e3:.2f} ms -> {tok_s:.1f} tok/s, "
         f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / HBM_PEAK_GBS:.1f}% of peak)")
@@ -396,8 +416,9 @@ def main():
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms / a.steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 weights x int16 activations -> int32 (fp32 epilogue, fp16 KV)",
-        "data": f"synthetic: seeded N(0,0.02) random-init weights quantised to q8 (seed {a.seed}), uniform random prompt ids",
-        "config": {"workload": f"{a.config}: Llama-3-8B-shape q8 batch-1 decode, {a.prompt}-token prompt + {a.warmup} warm-up + "
+        "data": f"synthetic: seeded N(0,0.02) random-init weights quantised to {quant_name(shape)} (seed {a.seed}), uniform "
+                "random prompt ids",
+        "config": {"workload": f"{a.config}: {shape.layers}-layer hidden-{shape.hidden} {quant_name(shape)} batch-1 decode, {a.prompt}-token prompt + {a.warmup} warm-up + "
                                f"{a.steps} timed greedy tokens, fp16 KV (context {T0}..{T1})",
                    "decode_tokens": a.steps, "prompt_tokens": a.prompt, "parallelism": "single GPU"},
         "hbm_pct_of_peak": round(100 * step_gbs / HBM_PEAK_GBS, 2),

@@ -66,7 +66,10 @@ __device__ __forceinline__ void act_load(const float *x, const float *w, int col
 }
 __device__ __forceinline__ float f4get(const float4 &v, int j) { return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w)); }
 
-template <int PRO>
+// CM (chunk-major, the q1 kernels): the 16-column piece k of 128-column block b is stored at byte (k * nb + b) * 16 of
+// each plane instead of b * 128 + 16 k, so lanes that own consecutive blocks read consecutive 16-byte pieces (the
+// row-major layout puts them 128 bytes apart: every lane in the same LDS banks).
+template <int PRO, bool CM = false>
 __device__ void act_build(const ActRegs &r, float eps, int cols, const ActView &a) {
   const int nb = cols / kQB, per = (int)blockDim.x / 8, sub = threadIdx.x & 7;
   float inv = 1.f;
@@ -126,8 +129,9 @@ __device__ void act_build(const ActRegs &r, float eps, int cols, const ActView &
         }
         hw[k] = hh; lw[k] = ll;
       }
-      *(uint4 *)(a.xh + c0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      *(uint4 *)(a.xl + c0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      const int at = CM ? (sub * nb + b) * 16 : c0;
+      *(uint4 *)(a.xh + at) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      *(uint4 *)(a.xl + at) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
       ls = sum8_i(ls);
       if (sub == 0) a.lsum[b] = ls;
       gs += dpp_i<kDppQuadXor1>(gs);

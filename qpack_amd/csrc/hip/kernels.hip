@@ -131,11 +131,13 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 #pragma unroll
   for (int k = 0; k < D; k++) issue(wr[k], sr[k]);
 
-  if (!(dm & 2)) act_build<PRO>(ar, a.eps, cols, av);
+  if (!(dm & 2)) act_build<PRO, KIND == MK_Q1>(ar, a.eps, cols, av);
   else __syncthreads();
   if (DBG && blockIdx.x == 0) {
-    for (int c = threadIdx.x; c < cols; c += blockDim.x)
-      if (a.dbg_xq) a.dbg_xq[c] = (int16_t)(((int)av.xh[c] << 8) | av.xl[c]);
+    for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+      const int at = KIND == MK_Q1 ? (((c & 127) >> 4) * nb + (c >> 7)) * 16 + (c & 15) : c;   // q1: chunk-major planes
+      if (a.dbg_xq) a.dbg_xq[c] = (int16_t)(((int)av.xh[at] << 8) | av.xl[at]);
+    }
     for (int b = threadIdx.x; b < nb; b += blockDim.x)
       if (a.dbg_bs) a.dbg_bs[b] = av.bs[b];
   }
@@ -184,7 +186,8 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
           const int g = cc * 64 + lane;
           const bool act = g < GS;
           const int gc = act ? g : GS - 1;
-          const uint4 *hp = (const uint4 *)(av.xh + 128 * gc), *lp = (const uint4 *)(av.xl + 128 * gc);
+          // chunk-major activation planes (act_build<PRO, true>): piece k of group gc at (k * nb + gc) * 16
+          const uint4 *hp = (const uint4 *)(av.xh + 16 * gc), *lp = (const uint4 *)(av.xl + 16 * gc);
           const int4 gs4 = *(const int4 *)(av.gsum + 4 * gc);
           const int xsum = gs4.x + gs4.y + gs4.z + gs4.w;
           const float bsg = av.bs[gc];
@@ -196,7 +199,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
             for (int j = 0; j < 4; j++) {          // 32 columns per dword
 #pragma unroll
               for (int hh = 0; hh < 2; hh++) {     // 16 columns per activation load
-                const uint4 h = hp[2 * j + hh], l = lp[2 * j + hh];
+                const uint4 h = hp[(2 * j + hh) * nb], l = lp[(2 * j + hh) * nb];
                 const uint32_t hx[4] = {h.x, h.y, h.z, h.w}, lx[4] = {l.x, l.y, l.z, l.w};
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
