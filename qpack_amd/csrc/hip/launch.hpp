@@ -118,7 +118,7 @@ hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st)
 struct GemmArgs {
   int kind;
   const int8_t *w; const float *scale; int rows, cols;
-  const int *wsum; int ldw;
+  const int *wsum; int ldw;   // q8: 128 x the row sums per 128-column block (k_rowsum_q8), [rows][ldw]
   const int *q4ns; const float *q4sc;
   const int *xg; int ldg;
   const int8_t *xh, *xl; const float *xb; int ntok, ldq, ldb;

@@ -117,7 +117,8 @@ __device__ __forceinline__ float lds_read4o(uint32_t addr) {
   return r;
 }
 
-// sum of each weight row over each 128-column block: out[row][block] (exact int32)
+// 128 x the sum of each weight row over each 128-column block: out[row][block] (exact int32; the product's lo
+// accumulators start at this value, isum = 256 hi + lo + 128 sum(W))
 __global__ __launch_bounds__(256) void k_rowsum_q8(const int8_t *w, int rows, int cols, int *out) {
   const int nb = cols / kQB;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256) void k_rowsum_q8(const int8_t *w, int rows, in
     s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
     s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
   }
-  out[i] = s;
+  out[i] = 128 * s;
 }
 hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipStream_t st) {
   if (cols % kQB || rows <= 0) return hipErrorInvalidValue;
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
 #pragma unroll
     for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-      for (int ni = 0; ni < 2; ni++) { ch[mi][ni] = (v4i){0, 0, 0, 0}; cl[mi][ni] = wsv[mi] * 128; }
+      for (int ni = 0; ni < 2; ni++) { ch[mi][ni] = (v4i){0, 0, 0, 0}; cl[mi][ni] = wsv[mi]; }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       if (ks == 1)
