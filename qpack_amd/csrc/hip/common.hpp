@@ -10,6 +10,7 @@ constexpr float kActMax = 32767.f;  // x86 kActMax (/root/reference/src/kernels_
 constexpr int kWave = 64;
 
 enum MatKind : int { MK_F32 = 0, MK_Q8 = 1, MK_Q4 = 2, MK_Q1 = 3 };
+constexpr int MK_MIX = 9;   // a matvec launch over q8 and q4 segments (each wave streams one kind)
 
 // a weight matrix resident in HBM, row-major as in the QPACK2 file
 struct DMat {

@@ -16,6 +16,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "act.hpp"
 #include "launch.hpp"
@@ -95,15 +96,22 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   const int cols = a.m[0].cols, G = cols / 32, nb = cols / kQB;
   const ActView av = act_view(smem, cols);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int W = gridDim.x * WAVES, gw = wave * gridDim.x + blockIdx.x;
-  const int U = a.seg_tile0[a.nseg];
-  const int nmine = gw < U ? (U - gw + W - 1) / W : 0;
-  const int rowbytes = KIND == MK_Q8 ? cols : KIND == MK_Q4 ? cols / 2 : cols / 8;
-  const int GS = KIND == MK_Q1 ? cols / 128 : G;   // the scale group a lane's 16 bytes belong to: 32 (q4) or 128 (q1) columns
+  const int Wg = gridDim.x * WAVES, gw = wave * gridDim.x + blockIdx.x;
+  // the wave's weight kind, its index among the waves of that kind (W of them) and its units [ub, ub + U): one kind per
+  // launch, or (MK_MIX) the first mix_w8 waves over the q8 segments' units and the rest over the q4 units
+  const bool mq8 = KIND == MK_MIX && gw < a.mix_w8;
+  const bool isq8 = KIND == MK_Q8 || mq8, isq1 = KIND == MK_Q1, isq4 = KIND == MK_Q4 || (KIND == MK_MIX && !mq8);
+  const int W = KIND != MK_MIX ? Wg : (mq8 ? a.mix_w8 : Wg - a.mix_w8);
+  const int gk = KIND != MK_MIX || mq8 ? gw : gw - a.mix_w8;
+  const int ub = KIND != MK_MIX || mq8 ? 0 : a.mix_u8;
+  const int U = (KIND != MK_MIX ? a.seg_tile0[a.nseg] : (mq8 ? a.mix_u8 : a.seg_tile0[a.nseg])) - ub;
+  const int nmine = gk < U ? (U - gk + W - 1) / W : 0;
+  const int rowbytes = isq8 ? cols : isq4 ? cols / 2 : cols / 8;
+  const int GS = isq1 ? cols / 128 : G;   // the scale group a lane's 16 bytes belong to: 32 (q4) or 128 (q1) columns
   const int nch = (rowbytes + 1023) >> 10;
   const int total = nmine * nch;
-  // per-wave LDS: q8 block sums [upw][NS][nbp] ints, q4 unit values [upw][NS] floats
-  int *wsum = av.sums + wave * (a.upw * NS * (KIND == MK_Q8 ? av.nbp : 1));
+  // per-wave LDS: q8 block sums [upw][NS][nbp] ints, q4 / q1 unit values [upw][NS] floats (MK_MIX: the q8 size for all)
+  int *wsum = av.sums + wave * (a.upw * NS * (KIND == MK_Q8 || KIND == MK_MIX ? av.nbp : 1));
   float *wval = (float *)wsum;
 
   ActRegs ar;
@@ -114,7 +122,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   uint16_t sr[D][NS];
   int pi = 0, pc = 0;
   const uint8_t *pp[NS]; const uint16_t *psp[NS];
-  unit_rows<EPI, NS>(a, nmine ? gw : 0, cols, pp, psp);
+  unit_rows<EPI, NS>(a, ub + (nmine ? gk : 0), cols, pp, psp);
   auto issue = [&](uint4 (&w)[NS], uint16_t (&sv)[NS]) {
     // past the wave's last unit every lane re-reads the same 16 bytes (one cache line, no HBM traffic)
     const bool live = pi < nmine;
@@ -124,9 +132,9 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 #pragma unroll
     for (int s = 0; s < NS; s++) {
       w[s] = ld16(pp[s] + offc);
-      if (KIND != MK_Q8) sv[s] = psp[s][grpc];
+      if (!isq8) sv[s] = psp[s][grpc];
     }
-    if (live && ++pc == nch) { pc = 0; if (++pi < nmine) unit_rows<EPI, NS>(a, gw + pi * W, cols, pp, psp); }
+    if (live && ++pc == nch) { pc = 0; if (++pi < nmine) unit_rows<EPI, NS>(a, ub + gk + pi * W, cols, pp, psp); }
   };
 #pragma unroll
   for (int k = 0; k < D; k++) issue(wr[k], sr[k]);
@@ -156,7 +164,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
         if (dm & 1) {
 #pragma unroll
           for (int s = 0; s < NS; s++) acc[s] += (float)(cur[s].x ^ cur[s].y ^ cur[s].z ^ cur[s].w);
-        } else if (KIND == MK_Q8) {
+        } else if (isq8) {
           const int col = cc * 1024 + lane * 16;
           const bool act = col < cols;
           const int colc = act ? col : cols - 16;
@@ -179,7 +187,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
               wsum[(ci * NS + s) * av.nbp + b] = p - 128 * av.lsum[b];
             }
           }
-        } else if (KIND == MK_Q1) {
+        } else if (isq1) {
           // one lane = one 128-column group: sign bit c of its 16 bytes is column 128 g + c (+1 set, -1 clear).
           // Each nibble becomes four byte masks (bit k -> byte k: nib * 0x204081 & 0x01010101), dotted with the high
           // and low activation planes: S = sum of x over the set bits, exact; the group's dot product is 2 S - sum(x).
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
             }
             const int isum = 2 * (A * 256 + (int)B) - xsum;
             if (DBG && act && a.dbg_sums) {
-              const UnitGeo<NS> og = unit_geo<EPI, NS>(a, gw + ci * W, cols);
+              const UnitGeo<NS> og = unit_geo<EPI, NS>(a, ub + gk + ci * W, cols);
               if (og.seg == 0 && og.row[s] < og.rows) a.dbg_sums[(size_t)og.row[s] * GS + g] = isum;
             }
             if (act) acc[s] = __builtin_fmaf(half_bits_to_float(curs[s]) * bsg, (float)isum, acc[s]);
@@ -241,14 +249,14 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
             }
             const int isum = A * 256 + (int)B - corr;
             if (DBG && act && a.dbg_sums) {
-              const UnitGeo<NS> og = unit_geo<EPI, NS>(a, gw + ci * W, cols);
+              const UnitGeo<NS> og = unit_geo<EPI, NS>(a, ub + gk + ci * W, cols);
               if (og.seg == 0 && og.row[s] < og.rows) a.dbg_sums[(size_t)og.row[s] * G + g] = isum;
             }
             if (act) acc[s] = __builtin_fmaf(half_bits_to_float(curs[s]) * bsg, (float)isum, acc[s]);
           }
         }
         if (++cc == nch) {   // unit complete: q4 / q1 values to LDS (LDS and cross-lane ops only inside the loop)
-          if (KIND != MK_Q8) {
+          if (!isq8) {
 #pragma unroll
             for (int s = 0; s < NS; s++) {
               const float v = wave_sum(acc[s]);
@@ -272,13 +280,13 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   for (int j0 = 0; j0 < nmine * NS; j0 += kWave) {
     const int j = j0 + lane, u = j / NS, s = j % NS;
     const bool live = j < nmine * NS;
-    const UnitGeo<NS> og = unit_geo<EPI, NS>(a, gw + (live ? u : 0) * W, cols);
+    const UnitGeo<NS> og = unit_geo<EPI, NS>(a, ub + gk + (live ? u : 0) * W, cols);
     int row = og.row[0]; const float *scl = og.sc[0];
 #pragma unroll
     for (int t = 1; t < NS; t++) if (s == t) { row = og.row[t]; scl = og.sc[t]; }
     float v = 0.f;
     if (live) {
-      if (KIND == MK_Q8) {
+      if (isq8) {
         const int *ss = wsum + (u * NS + s) * av.nbp;
         float ch = 0.f;   // rows_q8's block order; LDS read 16 blocks at a time so the chain is not latency-bound
         int b = 0;
@@ -368,12 +376,26 @@ static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
   // a wave may own one unit more than u when the grid rounds: size the per-wave LDS for ceil(units / waves)
   const int waves = grid * w;
   a.upw = (units + waves - 1) / waves;
+  if (KIND == MK_MIX) {
+    // q8 segments first: their units [0, u8) go to the first w8 waves, w8 in proportion to their bytes
+    int n8 = 0;
+    while (n8 < a.nseg && a.m[n8].kind == MK_Q8) n8++;
+    const int u8 = a.seg_tile0[n8];
+    double b8 = 0, b4 = 0;
+    for (int s = 0; s < a.nseg; s++) (s < n8 ? b8 : b4) += (double)a.m[s].rows * (s < n8 ? cols : cols / 2);
+    if (n8 == 0 || n8 == a.nseg || waves < 2) return hipErrorInvalidValue;
+    int w8 = (int)(waves * b8 / (b8 + b4) + 0.5);
+    w8 = w8 < 1 ? 1 : (w8 > waves - 1 ? waves - 1 : w8);
+    a.mix_w8 = w8; a.mix_u8 = u8;
+    const int up8 = (u8 + w8 - 1) / w8, up4 = (units - u8 + (waves - w8) - 1) / (waves - w8);
+    a.upw = up8 > up4 ? up8 : up4;
+  }
   const int nbp = ((cols / kQB) + 3) / 4 * 4;
-  const size_t lds = mv_lds_bytes(cols, w, a.upw * NS * (KIND == MK_Q8 ? nbp : 1));
+  const size_t lds = mv_lds_bytes(cols, w, a.upw * NS * (KIND == MK_Q8 || KIND == MK_MIX ? nbp : 1));
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   const bool dbg = a.dbg_sums || a.dbg_xq || a.dbg_bs;
   if (dbg) {
-    if (PRO != PRO_QUANT || EPI != EPI_STORE) return hipErrorInvalidValue;
+    if (PRO != PRO_QUANT || EPI != EPI_STORE || KIND == MK_MIX) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_matvec<PRO_QUANT, EPI_STORE, NS, KIND, true>), dim3(grid), dim3(w * 64), lds, st, a);
   } else {
     hipLaunchKernelGGL((k_matvec<PRO, EPI, NS, KIND, false>), dim3(grid), dim3(w * 64), lds, st, a);
@@ -392,11 +414,26 @@ static hipError_t launch_mv_k(int pro, int epi, const MvArgs &a, int ns, int gri
 }
 MvConfig g_mv_config;
 // grid_cap: the most workgroups one launch may use (EPI_ARGMAX writes one (max, index) partial per workgroup).
-// Segments of different kinds (q4m: q4 wq / wk with a q8 wv) go out as one launch per kind.
+// Segments of q8 and q4 (q4m: q4 wq / wk with a q8 wv) go out as one MK_MIX launch of the stored-output kernels, where
+// each wave streams one kind; other mixes (q1) as one launch per kind.
 hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st) {
   const int cols = a.m[0].cols;
   if (cols % kQB || cols > 32768) return hipErrorInvalidValue;
   const int nseg = epi == EPI_SWIGLU ? 1 : a.nseg;
+  bool has8 = false, has4 = false, has1 = false;
+  for (int s = 0; s < nseg; s++) { has8 |= a.m[s].kind == MK_Q8; has4 |= a.m[s].kind == MK_Q4; has1 |= a.m[s].kind == MK_Q1; }
+  const bool dbg = a.dbg_sums || a.dbg_xq || a.dbg_bs;
+  if (has8 && has4 && !has1 && epi == EPI_STORE && !dbg && !getenv("QPH_MV_NOMIX")) {
+    MvArgs b = a; b.nseg = 0;
+    for (int k : {(int)MK_Q8, (int)MK_Q4})
+      for (int s = 0; s < nseg; s++)
+        if (a.m[s].kind == k) { b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s]; b.nseg++; }
+    const int ns = mv_ns(b, epi, g_mv_config.cus * 16);
+    if (pro == PRO_NORM) return ns == 2 ? launch_mv_t<PRO_NORM, EPI_STORE, 2, MK_MIX>(b, grid_cap, st)
+                                        : launch_mv_t<PRO_NORM, EPI_STORE, 1, MK_MIX>(b, grid_cap, st);
+    return ns == 2 ? launch_mv_t<PRO_QUANT, EPI_STORE, 2, MK_MIX>(b, grid_cap, st)
+                   : launch_mv_t<PRO_QUANT, EPI_STORE, 1, MK_MIX>(b, grid_cap, st);
+  }
   for (int k : {(int)MK_Q8, (int)MK_Q4, (int)MK_Q1}) {
     MvArgs b = a; b.nseg = 0;
     for (int s = 0; s < nseg; s++)

@@ -46,6 +46,9 @@ struct MvArgs {
   float *dbg_bs;          // optional: the activation block scales
   int dbg_mode;           // measurement only: bit 0 skips the dot products, bit 1 skips the activation prologue, bit 2 the epilogue
   int upw;                // set by the launcher: the most units one wave owns (sizes the per-wave LDS)
+  // set by the launcher for one launch over q8 and q4 segments (MK_MIX): the q8 segments come first, their units are
+  // [0, mix_u8), and waves gw < mix_w8 take them; the other waves take the q4 units
+  int mix_w8, mix_u8;
 };
 
 // The matvec kernel runs one workgroup of up to 16 waves per CU; every wave streams its own units of 1 or 2 rows
