@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """bench.py - batch-1 decode tokens/s (+ % of HBM peak) and prefill tokens/s of the 8B-shape q8 Llama on one MI355X.
 
-Workload (BASELINE.json configs[2] / [3]): Llama-3-8B shape (32 layers, hidden 4096, 32 / 8 heads, head_dim 128,
+Workload (the C3 / C4 benchmark configurations): Llama-3-8B shape (32 layers, hidden 4096, 32 / 8 heads, head_dim 128,
 SwiGLU 14336, vocab 128256, untied head), seeded N(0, 0.02) random-init weights in q8, fp16 KV cache.
   decode  - 128-token prompt, `--warmup` untimed greedy tokens, then exactly `--steps` greedy tokens timed (device
             argmax feeds the next step; HIP events on the model's stream, host clock around it)
@@ -115,7 +115,7 @@ def read_traffic():
 
 
 def kv_fill_snapshot(shape, T, seed):
-    """a snapshot in the reference layout (model_llama.cpp:55-63) whose fp16 K / V rows are N(0, 1), as BASELINE's C5
+    """a snapshot in the reference layout (model_llama.cpp:55-63) whose fp16 K / V rows are N(0, 1), as the C5 workload specifies
     fills its 16K context"""
     kvd = shape.kv_heads * shape.head_dim
     rng = np.random.default_rng(seed)
@@ -127,7 +127,7 @@ def kv_fill_snapshot(shape, T, seed):
 
 
 def other_config(name, seed, steps_override=None):
-    """decode tokens/s of another BASELINE config on its own workload: C1 / C2 prompt + greedy tokens (prompt through
+    """decode tokens/s of another benchmark configuration on its own workload: C1 / C2 prompt + greedy tokens (prompt through
     the product's prefill), C5 greedy tokens after restoring a 16384-position N(0, 1) context"""
     import qpack_amd as qa
     shape = qa.CONFIGS[name]
@@ -258,7 +258,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-qpack3", action="store_true", help="skip the QPACK3 (rANS-coded) load leg")
     ap.add_argument("--configs", default="c1,c2,c5",
-                    help="other BASELINE configs whose decode rate is added to the line ('' for none)")
+                    help="other benchmark configurations whose decode rate is added to the line ('' for none)")
     ap.add_argument("--profile", action="store_true",
                     help="launch kernels one by one (no HIP graphs) so a profiler sees every dispatch, and run a "
                          "calibration copy of known size for the byte counters")

@@ -3,7 +3,7 @@
  * This is the drop-in boundary for qpack's GPU model (`LlamaCuda`, /root/reference/src/model_llama_cuda.cu:445-632),
  * selected by QPACK_DEVICE in load_model (/root/reference/src/model_llama.cpp:221-235).  Each model entry point replaces
  * one method of the C++ interface qp::Model (/root/reference/include/qpack/qpack.h:128-171); the reference-side adapter
- * a maintainer adds (a qp::Model subclass forwarding to these functions) is shown in INTEGRATION.md.
+ * a maintainer adds is a qp::Model subclass forwarding each method to these functions.
  *
  * Conventions
  *   - Every function returns int status: 0 = ok, -1 = error; qph_last_error() gives the calling thread's message.  The C++

@@ -1,7 +1,7 @@
 """qpack_amd: the MI355X (gfx950) Llama-family token loop of qpack behind a C ABI.
 
   HipLlama.load(path)   - a QPACK1/QPACK2 file on the GPU (the qp::Model surface: step / prefill / greedy_run / ...)
-  write_synthetic(...)  - seeded random-init QPACK2 models of the BASELINE shapes
+  write_synthetic(...)  - seeded random-init QPACK2 models of the benchmark shapes (C1-C5)
   kernel_matvec(...)    - the product's matvec kernel on one matrix, with its exact int32 accumulators (parity hook)
   kernel_matmul(...)    - the product's batched prefill kernels on one q8 / q4 matrix (parity hook)
   kernel_topk(...)      - the device top-M selection of step_topk on one vector (parity hook)

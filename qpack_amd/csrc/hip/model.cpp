@@ -316,7 +316,7 @@ void HipLlama::prefill(const int *toks, int n, int want, float *out) {
   if (pos_ + n > ctx_) throw std::runtime_error("context window full (" + std::to_string(ctx_) + " tokens)");
   for (int i = 0; i < n; i++) if (toks[i] < 0 || toks[i] >= cfg_.vocab) throw std::runtime_error("token id out of range");
   const bool force_steps = getenv("QPH_PREFILL_STEPS") != nullptr;   // test hook: the decode-step path
-  if (n == 1 || !pf_ok_ || force_steps) {   // one token (the reference's n == 1 case) or q4 layers: decode steps
+  if (n == 1 || !pf_ok_ || force_steps) {   // one token (the reference's n == 1 case) or q1 layers: decode steps
     for (int i = 0; i < n; i++) step(toks[i], i + 1 == n ? want : 0, i + 1 == n ? out : nullptr);
     if (!want) QPH_CK(hipStreamSynchronize(st_));
     return;

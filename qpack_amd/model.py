@@ -1,6 +1,6 @@
 """HipLlama: the Python face of the C ABI, method for method the reference's qp::Model
 (/root/reference/include/qpack/qpack.h:128-171).  Used by the tests and bench.py; C++ callers use include/qpack_hip.h
-directly (see INTEGRATION.md)."""
+directly."""
 import ctypes as C
 
 import numpy as np

@@ -1,6 +1,6 @@
-"""Seeded synthetic Llama-family QPACK2 files (random init; rules in csrc/host/synth.cpp) and the BASELINE configs.
+"""Seeded synthetic Llama-family QPACK2 files (random init; rules in csrc/host/synth.cpp) and the benchmark configurations.
 
-The five configs are the shapes of BASELINE.json: C1 Qwen2.5-0.5B q8, C2 the same in q4 (embed / head q8), C3
+The five benchmark configurations: C1 Qwen2.5-0.5B q8, C2 the same in q4 (embed / head q8), C3
 Llama-3-8B q8, C4 the same model for prefill, C5 Qwen2.5-7B q4m.  MINI is a small shape for CPU-side oracle checks.
 """
 import ctypes as C

@@ -1,5 +1,5 @@
 """The HIP token loop against the reference's own outputs (tests/golden/*.json, written by the reference engine compiled
-from its sources) at the BASELINE shapes C1 (Qwen2.5-0.5B q8: 32-token prompt + 128 greedy tokens) and C2 (the same
+from its sources) at the benchmark shapes C1 (Qwen2.5-0.5B q8: 32-token prompt + 128 greedy tokens) and C2 (the same
 model in q4: 512 + 256), plus the small shapes.
 
 Bar: prefill logits within max-abs 1e-2 / relative 1e-3 on a fixed sample; the greedy stream identical token for token

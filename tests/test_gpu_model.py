@@ -1,6 +1,6 @@
 """GPU parity of the whole token loop (qp::Model surface over the C ABI) against the oracle on small seeded models.
 
-Bar: logits within max-abs 1e-2 and relative 1e-3 of the reference, identical greedy streams.
+Bar (the parity contract of this path): logits within max-abs 1e-2 and relative 1e-3 of the reference, identical greedy streams.
 """
 import os
 
@@ -159,7 +159,7 @@ def kv_snapshot(k, v):
 
 @pytest.mark.parametrize("cfg,T", [("mini_q4m", 3000), ("mini128", 2500)])
 def test_long_context_restore(cfg, T, synth):
-    """decode at a long restored context (N(0,1) fp16 keys / values, as BASELINE's C5 fills its 16K cache): many
+    """decode at a long restored context (N(0,1) fp16 keys / values, as the C5 workload fills its 16K cache): many
     context splits per kv group and their merge; logits against the oracle holding the same cache, then greedy"""
     path = synth(cfg)
     shape = qa.CONFIGS[cfg]
