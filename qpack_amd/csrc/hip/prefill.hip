@@ -673,9 +673,14 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   __shared__ __align__(16) uint16_t ks[kPfKB * KS];
   __shared__ __align__(16) uint16_t vt[HD * VS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
-  const int g = blockIdx.y, rep = a.nh / a.nkv, kvd = a.nkv * HD;
+  // longest first over all kv groups: workgroup L (in dispatch order) takes the (L / ngroups)-th last token tiles of
+  // group L % ngroups, so the first workgroups on the CUs are the ones that stream the most of the cache and the short
+  // ones fill in behind them (causal work grows with the tile index)
+  const int L = blockIdx.y * gridDim.x + blockIdx.x;
+  const int bx = gridDim.x - 1 - L / gridDim.y, g = L % gridDim.y;
+  const int rep = a.nh / a.nkv, kvd = a.nkv * HD;
   const int ntiles = (a.ntok + 15) / 16, nunits = ntiles * rep;
-  const int u = blockIdx.x * kPfAttnWaves + wave;
+  const int u = bx * kPfAttnWaves + wave;
   const bool live = u < nunits;
   const int tile = live ? u / rep : 0, head = g * rep + (live ? u % rep : 0);
   const int t = tile * 16 + lr;                        // this lane's token
@@ -683,7 +688,7 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   const int ptok = a.p0 + t;                           // its position: attends to [0, ptok]
   const int wave_last = live ? a.p0 + min(tile * 16 + 15, a.ntok - 1) : -1;
   // the workgroup streams up to its last live unit's last token
-  const int ulast = min(blockIdx.x * kPfAttnWaves + kPfAttnWaves - 1, nunits - 1);
+  const int ulast = min(bx * kPfAttnWaves + kPfAttnWaves - 1, nunits - 1);
   const int wg_last = a.p0 + min((ulast / rep) * 16 + 15, a.ntok - 1);
   const int nkb = wg_last / kPfKB + 1;
 
