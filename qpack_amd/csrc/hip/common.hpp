@@ -61,6 +61,7 @@ __device__ __forceinline__ float dpp_f(float v) { return __builtin_bit_cast(floa
 constexpr int kDppQuadXor1 = 0xb1;       // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4e;       // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;    // row_half_mirror: lane i <-> 7 - i within 8 lanes
+constexpr int kDppMirror = 0x140;        // row_mirror: lane i <-> 15 - i within 16 lanes
 
 // sum over aligned groups of 8 lanes, result in every lane of the group (exact for integers)
 __device__ __forceinline__ int sum8_i(int v) {
@@ -74,6 +75,19 @@ __device__ __forceinline__ float max8_f(float v) {
   v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
   v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
   return v;
+}
+
+// full-wave sum without LDS traffic (for loops that stream memory): DPP sums over each 16-lane row, then the four row
+// sums in order ((r0 + r1) + (r2 + r3)); the value in every lane (the row sums are read as scalars)
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<kDppQuadXor1>(v);
+  v += dpp_f<kDppQuadXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppMirror>(v);
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // full-wave reductions (shuffles; not on the hot inner loops)

@@ -259,7 +259,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
           if (!isq8) {
 #pragma unroll
             for (int s = 0; s < NS; s++) {
-              const float v = wave_sum(acc[s]);
+              const float v = wave_sum_dpp(acc[s]);
               if (lane == 0) wval[ci * NS + s] = v;
               acc[s] = 0.f;
             }
