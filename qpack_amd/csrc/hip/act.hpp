@@ -146,9 +146,16 @@ __device__ void act_build(const ActRegs &r, float eps, int cols, const ActView &
 __device__ inline void embed_row(const DMat &e, int tok, float *x, int tid, int nthreads) {
   tok = tok < 0 ? 0 : (tok >= e.rows ? e.rows - 1 : tok);
   const int n = e.cols;
-  if (e.kind == MK_Q8) {
+  if (e.kind == MK_Q8) {   // 16 columns per thread and step (n is a multiple of 128): one 16-byte load, four float4 stores
     const int8_t *q = (const int8_t *)e.q + (size_t)tok * n; const float s = ((const float *)e.s)[tok];
-    for (int i = tid; i < n; i += nthreads) x[i] = (float)q[i] * s;
+    for (int c = 16 * tid; c < n; c += 16 * nthreads) {
+      const int4 v = *(const int4 *)(q + c);
+      const int w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        *(float4 *)(x + c + 4 * k) = make_float4((float)(int8_t)(w[k] & 255) * s, (float)(int8_t)((w[k] >> 8) & 255) * s,
+                                                 (float)(int8_t)((w[k] >> 16) & 255) * s, (float)(int8_t)(w[k] >> 24) * s);
+    }
   } else if (e.kind == MK_Q4) {
     const uint8_t *q = (const uint8_t *)e.q + (size_t)tok * (n / 2); const uint16_t *s = (const uint16_t *)e.s + (size_t)tok * (n / 32);
     for (int i = tid; i < n / 2; i += nthreads) {

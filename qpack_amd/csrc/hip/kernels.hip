@@ -835,21 +835,22 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 
 // ------------------------------------------------------------------ greedy pick
 __global__ __launch_bounds__(kThreads) void k_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens) {
-  __shared__ float bv_s[kThreads]; __shared__ int bi_s[kThreads];
+  constexpr int NW = kThreads / kWave;
+  __shared__ float bv_s[NW]; __shared__ int bi_s[NW];
   float bv = -INFINITY; int bi = 0x7fffffff;
   for (int i = threadIdx.x; i < n; i += kThreads) {
     const float v = amax[i].x; const int idx = __builtin_bit_cast(int, amax[i].y);
     if (better(v, idx, bv, bi)) { bv = v; bi = idx; }
   }
-  bv_s[threadIdx.x] = bv; bi_s[threadIdx.x] = bi;
-  __syncthreads();
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s && better(bv_s[threadIdx.x + s], bi_s[threadIdx.x + s], bv_s[threadIdx.x], bi_s[threadIdx.x])) {
-      bv_s[threadIdx.x] = bv_s[threadIdx.x + s]; bi_s[threadIdx.x] = bi_s[threadIdx.x + s];
-    }
-    __syncthreads();
+  // strict > with the lower index winning ties is associative: wave shuffles, then the wave results in order
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave); const int oi = __shfl_xor(bi, o, kWave);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
+  if ((threadIdx.x & (kWave - 1)) == 0) { bv_s[threadIdx.x / kWave] = bv; bi_s[threadIdx.x / kWave] = bi; }
+  __syncthreads();
   if (threadIdx.x == 0) {
+    for (int w = 1; w < NW; w++) if (better(bv_s[w], bi_s[w], bv_s[0], bi_s[0])) { bv_s[0] = bv_s[w]; bi_s[0] = bi_s[w]; }
     int t = bi_s[0]; if (t == 0x7fffffff) t = 0;
     out_tokens[ctl->n_out] = t;
     ctl->tok = t; ctl->pos = ctl->pos + 1; ctl->n_out = ctl->n_out + 1;
