@@ -106,3 +106,53 @@ def test_qpack3_model_equals_qpack2(cfg, synth, tmp_path):
     np.testing.assert_array_equal(a.prefill(toks, 1), b.prefill(toks, 1))
     np.testing.assert_array_equal(a.greedy_run(7, 24), b.greedy_run(7, 24))
     a.close(); b.close()
+
+
+def test_create_with_coded_tensors(synth, tmp_path):
+    """qph_create with the tensors of a QPACK3 file passed still coded (qph_tensor data_coded / scale_coded), the path a
+    caller with its own container reader takes: the same logits and greedy stream as qph_load of the QPACK2 file"""
+    import ctypes as C
+    import json
+    import struct
+    from qpack_amd._lib import Config, Tensor, check, lib
+    src = synth("mini_q4m")
+    dst = str(tmp_path / "m3.qpack")
+    qa.pack(src, dst, 2)
+    raw = open(dst, "rb").read()
+    n = struct.unpack("<I", raw[8:12])[0]
+    toc = {}
+    for i in range(n):
+        e = raw[16 + 72 * i:16 + 72 * (i + 1)]
+        toc[e[:56].rstrip(b"\0").decode()] = struct.unpack("<QQ", e[56:72])
+    blob = lambda name: raw[toc[name][0]:toc[name][0] + toc[name][1]]   # noqa: E731
+    man, cfgj = json.loads(blob("manifest.json")), json.loads(blob("config.json"))
+    coded = set(man["encoded"])
+    keep, ts = [], []
+    for e in man["tensors"]:
+        shape = e["shape"]
+        rows, cols = (shape[0], shape[1]) if len(shape) == 2 else (shape[0], 1)
+        kind = {"q8": qa.QPH_Q8, "q4": qa.QPH_Q4, "f32": qa.QPH_F32}[e["kind"]]
+        d = C.create_string_buffer(blob(e["blob"]), toc[e["blob"]][1])
+        s = C.create_string_buffer(blob(e["scale"]), toc[e["scale"]][1]) if "scale" in e else None
+        keep += [d, s, e["name"].encode()]
+        t = Tensor(name=keep[-1], kind=kind, rows=rows, cols=cols, data=C.cast(d, C.c_void_p),
+                   scale=C.cast(s, C.c_void_p) if s else None,
+                   data_coded=toc[e["blob"]][1] if e["blob"] in coded else 0,
+                   scale_coded=toc[e["scale"]][1] if "scale" in e and e["scale"] in coded else 0)
+        ts.append(t)
+    assert any(t.data_coded for t in ts) and any(t.scale_coded for t in ts)
+    cfg = Config(hidden=cfgj["hidden_size"], layers=cfgj["num_hidden_layers"], heads=cfgj["num_attention_heads"],
+                 kv_heads=cfgj["num_key_value_heads"], head_dim=cfgj["head_dim"], ffn=cfgj["intermediate_size"],
+                 vocab=cfgj["vocab_size"], tied=int(cfgj["tie_embeddings"]), qkv_bias=int(cfgj["qkv_bias"]), max_pos=cfgj["max_position_embeddings"],
+                 rms_eps=cfgj["rms_norm_eps"], rope_theta=cfgj["rope_theta"])
+    arr = (Tensor * len(ts))(*ts)
+    h = C.c_void_p()
+    check(lib().qph_create(C.byref(cfg), arr, len(ts), 128, C.byref(h)))
+    m = qa.HipLlama(h.value)
+    del keep, arr   # the library holds its own copies in HBM
+    ref = qa.HipLlama.load(src, 128)
+    toks = list(range(11, 50))
+    np.testing.assert_array_equal(m.prefill(toks, 1), ref.prefill(toks, 1))
+    np.testing.assert_array_equal(m.greedy_run(3, 20), ref.greedy_run(3, 20))
+    assert m.load_stats()["planes"] > 0
+    m.close(); ref.close()
