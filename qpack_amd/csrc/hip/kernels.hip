@@ -485,7 +485,7 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 // partials merge in LDS; with several splits the last one to finish (a per-group counter, which that workgroup
 // resets) merges the split partials in split order - the merge of model_llama.cpp:160-165:
 // M = max m, L = sum l e^(m - M), out = sum o e^(m - M) * (1 / L).
-constexpr int kAttnMaxSplits = 64;
+constexpr int kAttnMaxSplits = 64, kAttnParMerge = 16;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -738,33 +738,12 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
   attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored);
 }
 
-template <int HD, int REP>
-__global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
-  constexpr int NW = kAttnMfWaves;
-  __shared__ int last;
-  const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
-  // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
-  const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * NW, sp = a.split_pos > 0 ? a.split_pos : 64;
-  const int S = T <= smax ? 1 : min((int)gridDim.y, (T + sp - 1) / sp);
-  if (s >= S) return;
-  attn_split<HD, REP>(a, g, s, S, gridDim.y);
-  if (S == 1) return;
-  // this thread's coherent stores have completed before the workgroup's counter bump
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(a.counters + g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = prev == S - 1;
-    if (last) __hip_atomic_store(a.counters + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last) return;
+// One workgroup merges every head of group g over the S splits: wave j reduces head j's (m, l) over the splits, one
+// per lane; then P threads share each (head, 4 dims) column of partials, split c going to thread c mod P, with 8
+// coherent 16-byte loads in flight per thread, and add their sums in LDS.
+template <int HD, int REP, int NW>
+__device__ void attn_merge_all(const AttnArgs &a, int g, int S) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  // the last split merges the S partials (model_llama.cpp:160-165: M = max m_c, f_c = exp(m_c - M),
-  // L = sum l_c f_c, O = sum f_c o_c / L).  The partials were written through to memory by other workgroups before
-  // their counter bumps; they are read with coherent loads (no acquire fence: that is an L2 invalidate, far slower).
-  // Wave j reduces head j's (m, l) over the splits, one per lane; then P threads share each (head, 4 dims) column of
-  // partials, split c going to thread c mod P, and add their sums in LDS.
   auto cload = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   __shared__ float fw[REP][kAttnMaxSplits], linv[REP];
   __shared__ float4 opart[NW * 64];
@@ -788,10 +767,10 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   if (part < P) {
     const int j = e / (HD / 4), i4 = e % (HD / 4);
     const float4 *ph = (const float4 *)(a.part + ((size_t)(g * REP + j) * gridDim.y) * HD) + i4;
-    for (int c0 = part; c0 < S; c0 += 8 * P) {   // 8 independent loads in flight
+    for (int c0 = part; c0 < S; c0 += 8 * P) {
       f32x4 v[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) {   // coherent 16-byte loads (clamped in range; unused ones are not summed)
+      for (int k = 0; k < 8; k++) {   // clamped in range; unused ones are not summed
         const int c = c0 + k * P < S ? c0 + k * P : 0;
         asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[k]) : "v"(ph + (size_t)c * (HD / 4)));
       }
@@ -815,6 +794,113 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
     }
     const float li = linv[j];
     *(float4 *)(a.att + (size_t)(g * REP + j) * HD + 4 * i4) = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
+  }
+}
+
+// Merger r of MG merges heads r, r + MG, ... of group g over the S splits.  Per head: thread t takes column t % (HD / 4)
+// of 4 dims and the splits t / (HD / 4) + (NW * 256 / HD) k, all its loads issued at once; wave 0 also reduces M and L
+// over the splits (one split per lane).  late: the wait for the other splits ran out (the outputs are then NaN).
+template <int HD, int REP, int NW>
+__device__ void attn_merge_heads(const AttnArgs &a, int g, int S, int r, int MG, bool late) {
+  constexpr int NCOL = HD / 4, NGRP = NW * 64 / NCOL, PER = (kAttnMaxSplits + NGRP - 1) / NGRP;
+  __shared__ float Ms, Linv;
+  __shared__ float4 opart[NGRP][NCOL];
+  const int col = threadIdx.x % NCOL, grp = threadIdx.x / NCOL;
+  const float *mlb = a.part + (size_t)a.nh * gridDim.y * HD;
+  for (int j = r; j < REP; j += MG) {
+    const size_t hs0 = (size_t)(g * REP + j) * gridDim.y;
+    f32x4 v[PER];
+    float2 mlk[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {   // coherent loads (clamped in range; unused ones are not summed)
+      const int c = grp + NGRP * k < S ? grp + NGRP * k : 0;
+      const float4 *ph = (const float4 *)(a.part + (hs0 + c) * HD) + col;
+      asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[k]) : "v"(ph));
+      mlk[k] = make_float2(__hip_atomic_load(mlb + 2 * (hs0 + c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                           __hip_atomic_load(mlb + 2 * (hs0 + c) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    if (threadIdx.x < 64) {
+      const bool on = threadIdx.x < S;
+      const float m = on ? __hip_atomic_load(mlb + 2 * (hs0 + threadIdx.x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+      const float l = on ? __hip_atomic_load(mlb + 2 * (hs0 + threadIdx.x) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      const float M = wave_max(m);
+      const float L = wave_sum(on && m != -INFINITY ? l * expf(m - M) : 0.f);
+      if (threadIdx.x == 0) { Ms = M; Linv = 1.f / L; }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < PER; k++) asm volatile("" : "+v"(v[k]));   // the values are used only after the wait
+    __syncthreads();
+    const float M = Ms;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+      if (grp + NGRP * k < S) {
+        const float f = mlk[k].x == -INFINITY ? 0.f : expf(mlk[k].x - M);
+        O.x = __builtin_fmaf(f, v[k][0], O.x); O.y = __builtin_fmaf(f, v[k][1], O.y);
+        O.z = __builtin_fmaf(f, v[k][2], O.z); O.w = __builtin_fmaf(f, v[k][3], O.w);
+      }
+    opart[grp][col] = O;
+    __syncthreads();
+    if (threadIdx.x < NCOL) {
+      for (int q = 1; q < NGRP; q++) {
+        const float4 t = opart[q][threadIdx.x];
+        O.x += t.x; O.y += t.y; O.z += t.z; O.w += t.w;
+      }
+      const float li = late ? __builtin_nanf("") : Linv;   // a wait that ran out leaves NaN, never stale values
+      *(float4 *)(a.att + (size_t)(g * REP + j) * HD + 4 * threadIdx.x) = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
+    }
+    __syncthreads();
+  }
+}
+
+template <int HD, int REP>
+__global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
+  constexpr int NW = kAttnMfWaves;
+  const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
+  // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
+  const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * NW, sp = a.split_pos > 0 ? a.split_pos : 64;
+  const int S = T <= smax ? 1 : min((int)gridDim.y, (T + sp - 1) / sp);
+  if (s >= S) return;
+  attn_split<HD, REP>(a, g, s, S, gridDim.y);
+  if (S == 1) return;
+  // this thread's coherent stores have completed before the workgroup's counter bump
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // The last MG splits to arrive merge the S partials of the group's heads (model_llama.cpp:160-165: M = max m_c,
+  // f_c = exp(m_c - M), L = sum l_c f_c, O = sum f_c o_c / L): from kAttnParMerge splits up MG = min(REP, S), head j
+  // by merger j % MG; below, the merge is short and the last arrival does it alone (MG = 1, all heads).  Counter
+  // a.counters[g] counts arrivals, a.counters[nkv + g] mergers done waiting; the last of those resets both for the next
+  // launch (a lone merger resets the arrivals at once).  A merger waits for the arrivals behind it: those splits are already resident or wait only for workgroups
+  // that finish without waiting (at most nh mergers wait at any time), and the wait is bounded.
+  __shared__ int rank, late;
+  int *arrive = a.counters + g, *done = a.counters + a.nkv + g;
+  const int MG = S >= kAttnParMerge ? min(REP, S) : 1;
+  if (threadIdx.x == 0) {
+    const int r = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - (S - MG);
+    if (MG == 1 && r == 0) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int spins = 0;
+    if (r >= 0 && r < MG - 1)
+      while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < S && ++spins < (1 << 22))
+        __builtin_amdgcn_s_sleep(1);
+    rank = r < 0 ? -1 : r;
+    late = spins >= (1 << 22);
+  }
+  __syncthreads();
+  const int r = rank;
+  if (r < 0) return;
+  // The partials were written through to memory by other workgroups before their counter bumps; they are read with
+  // coherent loads (no acquire fence: that is an L2 invalidate, far slower).
+  if (MG == 1) {
+    attn_merge_all<HD, REP, NW>(a, g, S);
+    return;
+  }
+  // this merger no longer reads the arrivals; the round trip overlaps the merge
+  const int d = threadIdx.x == 0 ? __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+  attn_merge_heads<HD, REP, NW>(a, g, S, r, MG, late);
+  if (threadIdx.x == 0 && d == MG - 1) {
+    __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

@@ -84,7 +84,7 @@ struct AttnArgs {
   const float *cos_t, *sin_t;  // RoPE tables [ctx][hd / 2]
   const Ctl *ctl;
   float *part;                 // unnormalised outputs [nh][splits][hd], then (max, sum) [nh][splits][2]
-  int *counters;               // [nkv] zero; each group's last split resets its counter
+  int *counters;               // [2 nkv] zero: arrivals and finished mergers per group; the last merger resets both
   float *att;                  // output [nh * hd]
   int nh, nkv, hd;
   int max_chunks;              // splits S of the context per kv group (grid.y)

@@ -113,7 +113,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(64, atoi(e)));
   if (const char *e = getenv("QPH_ATTN_SINGLE")) attn_single_ = std::max(0, atoi(e));
   if (const char *e = getenv("QPH_ATTN_SPLIT_POS")) attn_split_pos_ = std::max(0, atoi(e));
-  counters_ = (int *)dalloc(4ull * nkv);
+  counters_ = (int *)dalloc(8ull * nkv);
   const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
   kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
   QPH_CK(hipMemset(kc_, 0, kvn * 2)); QPH_CK(hipMemset(vc_, 0, kvn * 2));
@@ -121,7 +121,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   k_ = (float *)dalloc(4ull * kvd_); v_ = (float *)dalloc(4ull * kvd_); att_ = (float *)dalloc(4ull * qd_);
   h_ = (float *)dalloc(4ull * ff); logits_ = (float *)dalloc(4ull * V);
   part_ = (float *)dalloc(4ull * nh * max_chunks_ * (hd + 2));
-  QPH_CK(hipMemset(counters_, 0, 4ull * nkv));
+  QPH_CK(hipMemset(counters_, 0, 8ull * nkv));
   head_grid_ = cus_ * 4;
   amax_ = (float2 *)dalloc(sizeof(float2) * head_grid_);
   {  // partials of workgroups a smaller launch does not use must never win the pick
