@@ -118,6 +118,12 @@ hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st)
 //   kind MK_Q8: w int8 [rows][cols], scale f32 [rows], wsum = row sums per 128-column block [rows][ldw] (launch_rowsum_q8)
 //   kind MK_Q4: w packed q4 [rows][cols / 2], q4ns / q4sc = per-group nibble sums and f32 scales, group-major per block
 //               (launch_q4_prep), and the activation's group sums xg [ntok][ldg] (launch_pf_quant)
+// one matrix of a multi-matrix product launch (GemmArgs::nseg > 1): its own weights, scales, bias and output
+struct GemmSeg {
+  const int8_t *w; const float *scale; const int *wsum; const int *q4ns; const float *q4sc;
+  const float *bias; float *y; int rows, ldy;
+};
+constexpr int kGemmMaxSeg = 3;
 struct GemmArgs {
   int kind;
   const int8_t *w; const float *scale; int rows, cols;
@@ -133,6 +139,10 @@ struct GemmArgs {
   // optional (q8): a second matrix of the same shape (the up matrix, with w / scale / wsum the gate's): one launch
   // computes both products for each 64-row tile and stores only y = silu(gate product) * (up product)
   const int8_t *w2; const float *scale2; const int *wsum2;
+  // optional: nseg (2 .. kGemmMaxSeg) matrices of this kind and column count over the same activations (q / k / v), the
+  // segment fields replacing w / scale / wsum / q4ns / q4sc / bias / y / ldy / rows; each starts on a fresh row tile
+  int nseg;
+  GemmSeg seg[kGemmMaxSeg];
 };
 size_t gemm_lds_bytes();
 // out[row][block] = sum of W[row] over each 128-column block

@@ -353,6 +353,25 @@ void HipLlama::prefill_batched(const int *toks, int n) {
     a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0; a.gate = gate;
     QPH_CK(launch_gemm(a, st_));
   };
+  // q / k / v: runs of consecutive matrices of one kind share a launch (q8 files: one launch; q4m: q + k, then v)
+  auto gemm_qkv = [&](const Layer &ly, int B) {
+    const DMat *m[3] = {&ly.wq, &ly.wk, &ly.wv};
+    float *y[3] = {pf_q_, pf_k_, pf_v_};
+    const int ld[3] = {qd_, kvd_, kvd_};
+    const float *bias[3] = {ly.bq, ly.bk, ly.bv};
+    for (int i = 0; i < 3;) {
+      int j = i + 1;
+      while (j < 3 && m[j]->kind == m[i]->kind && m[j]->cols == m[i]->cols) j++;
+      if (j - i == 1 || (m[i]->kind != MK_Q8 && m[i]->kind != MK_Q4)) { gemm(*m[i], y[i], ld[i], bias[i], false, B); i++; continue; }
+      GemmArgs a{}; a.kind = m[i]->kind; a.cols = m[i]->cols; a.ldw = a.cols / 128; a.xg = pf_xg_; a.ldg = pf_ldg_;
+      a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld;
+      a.nseg = j - i;
+      for (int s = i; s < j; s++)
+        a.seg[s - i] = GemmSeg{(const int8_t *)m[s]->q, (const float *)m[s]->s, m[s]->rs, m[s]->q4ns, m[s]->q4sc, bias[s], y[s], m[s]->rows, ld[s]};
+      QPH_CK(launch_gemm(a, st_));
+      i = j;
+    }
+  };
   int B = 0;
   for (int s0 = 0; s0 < n; s0 += B) {
     B = std::min(pf_cap_, n - s0);
@@ -363,9 +382,7 @@ void HipLlama::prefill_batched(const int *toks, int n) {
       const Layer &ly = layers_[l];
       uint16_t *kc = kc_ + (size_t)l * ctx_ * kvd_, *vc = vc_ + (size_t)l * ctx_ * kvd_;
       quant(PRO_NORM, pf_x_, d, ly.an, d, B);
-      gemm(ly.wq, pf_q_, qd_, ly.bq, false, B);
-      gemm(ly.wk, pf_k_, kvd_, ly.bk, false, B);
-      gemm(ly.wv, pf_v_, kvd_, ly.bv, false, B);
+      gemm_qkv(ly, B);
       PfRopeArgs r{}; r.q = pf_q_; r.ldq = qd_; r.k = pf_k_; r.v = pf_v_; r.ldk = kvd_; r.cos_t = cos_; r.sin_t = sin_;
       r.kc = kc; r.vc = vc; r.p0 = p0; r.nh = cfg_.heads; r.nkv = cfg_.kv_heads; r.hd = cfg_.head_dim;
       QPH_CK(launch_pf_rope(r, B, st_));

@@ -176,6 +176,29 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs &a, float *yt, int rb
   }
 }
 
+// multi-matrix launches: row tile r0 / rt of the grid -> the matrix it belongs to (wave-uniform), whose fields replace
+// the launch's; returns the tile's first row within that matrix
+__device__ __forceinline__ int gemm_segment(GemmArgs &a, int r0, int rt) {
+  if (a.nseg < 2) return r0;
+  const int tile = r0 / rt;
+  int base = 0, first = 0;
+  bool found = false;
+#pragma unroll
+  for (int s = 0; s < kGemmMaxSeg; s++) {   // constant indices: the segment table stays in kernel-argument memory
+    if (!found && s < a.nseg) {
+      const GemmSeg &g = a.seg[s];
+      const int nt = (g.rows + rt - 1) / rt;
+      if (tile < base + nt || s == a.nseg - 1) {
+        a.w = g.w; a.scale = g.scale; a.wsum = g.wsum; a.q4ns = g.q4ns; a.q4sc = g.q4sc;
+        a.bias = g.bias; a.y = g.y; a.rows = g.rows; a.ldy = g.ldy;
+        first = base; found = true;
+      }
+      base += nt;
+    }
+  }
+  return (tile - first) * rt;
+}
+
 __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -202,6 +225,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
       r0 = (tile / ntt) * RT; t0 = (tile % ntt) * kGN;
     }
   }
+  r0 = gemm_segment(a, r0, RT);
   const int nb = a.cols / kQB;
 
   // this lane's DMA sources.  Per stage the 48 1-KiB row groups (16 each of weights, hi plane, lo plane; 8 rows per
@@ -448,6 +472,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
       r0 = (tile / ntt) * kGM; t0 = (tile % ntt) * kGN;
     }
   }
+  r0 = gemm_segment(a, r0, kGM);
   const int nb = a.cols / kQB, rb = a.cols / 2;   // packed bytes per row
   // DMA jobs per stage (64 wave instructions, 8 per wave; jobs 60..63 repeat 0..3 byte for byte):
   //   0..7 packed weights (16 rows x 64 B each), 8..23 hi plane, 24..39 lo plane (8 rows x 128 B each),
@@ -601,11 +626,29 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
     }
 }
 
-hipError_t launch_gemm(const GemmArgs &a, hipStream_t st) {
-  if (a.ntok <= 0) return hipSuccess;
-  if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
+hipError_t launch_gemm(const GemmArgs &a0, hipStream_t st) {
+  if (a0.ntok <= 0) return hipSuccess;
+  GemmArgs a = a0;
+  int tiles;
   const int rt = a.w2 ? kGM / 2 : kGM;
-  const dim3 grid((a.ntok + kGN - 1) / kGN, (a.rows + rt - 1) / rt);
+  if (a.nseg > 1) {
+    // the first matrix also stands in the launch's own fields, so the checks below cover every segment's pointers
+    if (a.nseg > kGemmMaxSeg || a.w2 || a.resid || a.gate) return hipErrorInvalidValue;
+    tiles = 0;
+    for (int s = 0; s < a.nseg; s++) {
+      const GemmSeg &g = a.seg[s];
+      if (g.rows <= 0 || !g.w || !g.scale || !g.y || (a.kind == MK_Q8 ? !g.wsum : (!g.q4ns || !g.q4sc))) return hipErrorInvalidValue;
+      tiles += (g.rows + rt - 1) / rt;
+    }
+    const GemmSeg &g = a.seg[0];
+    a.w = g.w; a.scale = g.scale; a.wsum = g.wsum; a.q4ns = g.q4ns; a.q4sc = g.q4sc; a.bias = g.bias; a.y = g.y;
+    a.rows = g.rows; a.ldy = g.ldy;
+  } else {
+    a.nseg = 0;
+    tiles = (a.rows + rt - 1) / rt;
+  }
+  if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
+  const dim3 grid((a.ntok + kGN - 1) / kGN, tiles);
   if (a.w2 && (a.kind != MK_Q8 || !a.scale2 || !a.wsum2 || a.resid || a.bias || a.gate)) return hipErrorInvalidValue;
   if (a.kind == MK_Q8) {
     if (!a.wsum || a.ldw < a.cols / kQB) return hipErrorInvalidValue;
