@@ -53,6 +53,11 @@ CONFIGS = {
                      rope_theta=1e6, model_type="qwen2", q4=True),
     "mini_q4m": Shape(hidden=384, layers=3, heads=6, kv_heads=2, head_dim=64, ffn=640, vocab=1500, tied=False, qkv_bias=True,
                       rope_theta=1e6, model_type="qwen2", q4=True, q4m_alt=True),
+    # k / v row counts that end inside a 128-row product tile (192 and 64 rows): the prompt's segmented q / k / v launch
+    "mini_odd": Shape(hidden=256, layers=2, heads=6, kv_heads=3, head_dim=64, ffn=384, vocab=900, tied=False, qkv_bias=True,
+                      rope_theta=1e6, model_type="qwen2"),
+    "mini_odd_q4": Shape(hidden=256, layers=2, heads=2, kv_heads=1, head_dim=64, ffn=384, vocab=900, tied=True,
+                         qkv_bias=True, rope_theta=1e6, model_type="qwen2", q4=True),
     # qpack-quantize's other outputs: q1 MLP matrices (q1m keeps the more_bits downs in q8), the real q4m layer policy,
     # and q4 with a q4 embedding / head
     "mini_q1": Shape(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000, tied=True, qkv_bias=True,

@@ -20,7 +20,8 @@ def close(a, b):
     return float(err.max()), bool(np.all(err <= np.maximum(ATOL, RTOL * np.abs(b))))
 
 
-@pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_q4", "mini_q4m", "mini_q1", "mini_q1m", "mini_q4mb", "mini_q4h"])
+@pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_q4", "mini_q4m", "mini_q1", "mini_q1m", "mini_q4mb", "mini_q4h",
+                                 "mini_odd", "mini_odd_q4"])
 def test_decode_and_greedy_match_oracle(cfg, synth):
     path = synth(cfg)
     gpu = qa.HipLlama.load(path, max_ctx=256)
@@ -92,12 +93,13 @@ def split_snapshot(snap, layers, kvd):
     return pos, body[:, 0], body[:, 1]
 
 
-@pytest.mark.parametrize("cfg,chunk", [("mini", 48), ("mini128", 0), ("mini128", 37)])
+@pytest.mark.parametrize("cfg,chunk", [("mini", 48), ("mini128", 0), ("mini128", 37), ("mini_odd", 0), ("mini_odd_q4", 29)])
 def test_batched_prefill(cfg, chunk, synth, monkeypatch):
     """the int8-MFMA prompt path: chunked (ragged last chunk), a second prompt continuing at p0 > 0; logits and every
     cache row against the oracle (within the tolerance / fp16 rounding), the greedy continuation identical, and the
-    layer-0 cache rows bit-identical to the GPU's own decode-step path (exact products, same quantised activations,
-    same RoPE and fp16 rounding; the decode path differs from the reference only by its RMSNorm summation order)"""
+    layer-0 cache rows bit-identical to the GPU's own decode-step path for q8 (exact products, same quantised
+    activations, same RoPE and fp16 rounding; the decode path differs from the reference only by its RMSNorm summation
+    order); for q4 within one fp16 rounding step (the prompt product's group sums run in another float order)"""
     if chunk:
         monkeypatch.setenv("QPH_PF_CHUNK", str(chunk))
     path = synth(cfg)
@@ -128,8 +130,12 @@ def test_batched_prefill(cfg, chunk, synth, monkeypatch):
     for a, b in prompts:
         gpu.prefill(toks[a:b], 0)
     _, ks, vs = split_snapshot(gpu.snapshot(), shape.layers, kvd)
-    np.testing.assert_array_equal(kb[0].view(np.uint16), ks[0].view(np.uint16))
-    np.testing.assert_array_equal(vb[0].view(np.uint16), vs[0].view(np.uint16))
+    for a, b in ((kb[0], ks[0]), (vb[0], vs[0])):
+        if not shape.q4:
+            np.testing.assert_array_equal(a.view(np.uint16), b.view(np.uint16))
+        else:   # q4 products sum their groups in another float order than rows_q4: within one fp16 rounding step
+            a32, b32 = a.astype(np.float32), b.astype(np.float32)
+            assert np.all(np.abs(a32 - b32) <= np.abs(b32) * 2.0 ** -10 + 2.0 ** -24), float(np.abs(a32 - b32).max())
     gpu.close(); orc.close()
 
 
