@@ -58,6 +58,11 @@ CONFIGS = {
                       rope_theta=1e6, model_type="qwen2"),
     "mini_odd_q4": Shape(hidden=256, layers=2, heads=2, kv_heads=1, head_dim=64, ffn=384, vocab=900, tied=True,
                          qkv_bias=True, rope_theta=1e6, model_type="qwen2", q4=True),
+    # seven query heads per kv group, as C1 (head dim 64) and C5 (head dim 128) have them
+    "mini_r7": Shape(hidden=256, layers=2, heads=14, kv_heads=2, head_dim=64, ffn=512, vocab=1000, tied=True,
+                     qkv_bias=True, rope_theta=1e6, model_type="qwen2"),
+    "mini_r7h": Shape(hidden=256, layers=2, heads=7, kv_heads=1, head_dim=128, ffn=512, vocab=1000, tied=False,
+                      qkv_bias=True, rope_theta=1e6, model_type="qwen2", q4=True, q4m_alt=True),
     # qpack-quantize's other outputs: q1 MLP matrices (q1m keeps the more_bits downs in q8), the real q4m layer policy,
     # and q4 with a q4 embedding / head
     "mini_q1": Shape(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000, tied=True, qkv_bias=True,

@@ -21,7 +21,7 @@ def close(a, b):
 
 
 @pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_q4", "mini_q4m", "mini_q1", "mini_q1m", "mini_q4mb", "mini_q4h",
-                                 "mini_odd", "mini_odd_q4"])
+                                 "mini_odd", "mini_odd_q4", "mini_r7", "mini_r7h"])
 def test_decode_and_greedy_match_oracle(cfg, synth):
     path = synth(cfg)
     gpu = qa.HipLlama.load(path, max_ctx=256)
@@ -163,7 +163,7 @@ def kv_snapshot(k, v):
     return b"".join(parts)
 
 
-@pytest.mark.parametrize("cfg,T", [("mini_q4m", 3000), ("mini128", 2500)])
+@pytest.mark.parametrize("cfg,T", [("mini_q4m", 3000), ("mini128", 2500), ("mini_r7", 1500), ("mini_r7h", 1200)])
 def test_long_context_restore(cfg, T, synth):
     """decode at a long restored context (N(0,1) fp16 keys / values, as the C5 workload fills its 16K cache): many
     context splits per kv group and their merge; logits against the oracle holding the same cache, then greedy"""
