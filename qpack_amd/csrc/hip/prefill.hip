@@ -361,7 +361,9 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   epilogue_half(pch, pcl, pbs, 1);
   if (paired) {
     // the gate waves hand gate = acc * scale to the up waves through LDS ([128 tokens][64 rows] floats over the
-    // stages, free once everyone is past the loop); they store y = silu(gate) * (acc * scale2)
+    // stages, free once everyone is past the loop; rows padded to 68 floats so a lane group's 16-byte accesses 68
+    // floats apart spread over the banks); they store y = silu(gate) * (acc * scale2)
+    constexpr int GXS = 68;
     __syncthreads();
     float *gx = (float *)smem;
     auto scaled = [&](const float *sc, int mi, int ni) {
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
 #pragma unroll
       for (int mi = 0; mi < 4; mi++)
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) *(float4 *)(gx + (wc * 32 + ni * 16 + lr) * 64 + mi * 16 + 4 * lg) = scaled(a.scale, mi, ni);
+        for (int ni = 0; ni < 2; ni++) *(float4 *)(gx + (wc * 32 + ni * 16 + lr) * GXS + mi * 16 + 4 * lg) = scaled(a.scale, mi, ni);
     __syncthreads();
     if (wr == 1)
 #pragma unroll
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
         for (int ni = 0; ni < 2; ni++) {
           const int t = t0 + wc * 32 + ni * 16 + lr;
           if (t >= a.ntok) continue;
-          const float4 g = *(const float4 *)(gx + (wc * 32 + ni * 16 + lr) * 64 + mi * 16 + 4 * lg);
+          const float4 g = *(const float4 *)(gx + (wc * 32 + ni * 16 + lr) * GXS + mi * 16 + 4 * lg);
           const float4 u = scaled(a.scale2, mi, ni);
           const float h[4] = {silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w)};
           float *yt = a.y + (size_t)t * a.ldy;
@@ -787,7 +789,10 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
       const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, 64);
       const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
       const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-      uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS + (p & ~1));
+      // dword (p / 2) of the row, XOR 2 (d0 / 8 mod 8): rows 8 apart (the lanes' d0) land 144 dwords apart, on a few
+      // banks only; the swizzle spreads them (even, so the (4 lg, 4 lg + 1) pairs the reads take stay adjacent)
+      const int sw = 2 * ((d0 >> 3) & 7);
+      uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ sw);
       w[0] = (lo_x & 0xffffu) | (hi_x << 16);
       w[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
       w[VS] = (lo_y & 0xffffu) | (hi_y << 16);
@@ -839,8 +844,9 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
     for (int d = 0; d < DT; d++) {
       o[d] *= corr;
       // V^T fragment: dim 16 d + lr, positions 4 lg + 0..3 and 16 + 4 lg + 0..3 (the k order of ph / pl)
-      const uint16_t *vr = vt + (16 * d + lr) * VS;
-      const uint2 v0 = *(const uint2 *)(vr + 4 * lg), v1 = *(const uint2 *)(vr + 16 + 4 * lg);
+      const int row = 16 * d + lr, sw = 2 * ((row >> 3) & 7);   // the writes' swizzle
+      const uint32_t *vr = (const uint32_t *)(vt + row * VS);
+      const uint2 v0 = *(const uint2 *)(vr + ((2 * lg) ^ sw)), v1 = *(const uint2 *)(vr + ((8 + 2 * lg) ^ sw));
       const uint4 vv = make_uint4(v0.x, v0.y, v1.x, v1.y);
       const h8 vf = __builtin_bit_cast(h8, vv);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
