@@ -575,7 +575,7 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   // LDS rows padded so the MFMA-layout accesses (16 heads / dims apart per lane) spread over the banks
-  constexpr int NW = kAttnMfWaves, HALF = HD / 2, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 4;   // VS: 8-byte aligned rows
+  constexpr int NW = kAttnMfWaves, HALF = HD / 2, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 8;   // VS: rows of 20 dwords
   constexpr int QS = HD + 4;
   __shared__ __align__(16) float qs[REP][QS];
   __shared__ float wm[NW][REP], wl[NW][REP];
@@ -655,7 +655,9 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
       const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];   // own dims (low / high pair)
       // word for dim pair member: (even position) | (odd position) << 16
       const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-      uint32_t *wr = (uint32_t *)(vw + (d0 + (ev ? 0 : 4)) * VS + (p & ~1));
+      // dword (p / 2) XOR 2 (d0 / 8 mod 8): with 20-dword rows the stores of rows 8 apart and the fragment reads
+      // below spread over the LDS banks (the XOR is even: the position pairs stay adjacent)
+      uint32_t *wr = (uint32_t *)(vw + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ (2 * ((d0 >> 3) & 7)));
       wr[0] = (lo_x & 0xffffu) | (hi_x << 16);
       wr[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
       wr[VS] = (lo_y & 0xffffu) | (hi_y << 16);
@@ -712,8 +714,9 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
     for (int d = 0; d < DT; d++) {
       o[d] *= corr;
       // V^T fragment: dim 16 d + lr, positions 4 lg + 0..3 and 16 + 4 lg + 0..3 (the k order of ph / pl)
-      const uint16_t *vr = vw + (16 * d + lr) * VS;
-      const uint2 v0 = *(const uint2 *)(vr + 4 * lg), v1 = *(const uint2 *)(vr + 16 + 4 * lg);
+      const int row = 16 * d + lr, sw = 2 * ((row >> 3) & 7);   // the stores' swizzle
+      const uint32_t *vr = (const uint32_t *)(vw + row * VS);
+      const uint2 v0 = *(const uint2 *)(vr + ((2 * lg) ^ sw)), v1 = *(const uint2 *)(vr + ((8 + 2 * lg) ^ sw));
       const h8 vf = __builtin_bit_cast(h8, make_uint4(v0.x, v0.y, v1.x, v1.y));
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
       o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);

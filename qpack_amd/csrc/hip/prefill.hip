@@ -710,7 +710,7 @@ template <int HD>
 __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
-  constexpr int KS = HD + 8, VS = kPfKB + 4, DT = HD / 16;   // VS: 8-byte aligned transposed rows
+  constexpr int KS = HD + 8, VS = kPfKB + 8, DT = HD / 16;   // VS: transposed rows of 20 dwords (see the V stores)
   constexpr int NT = kPfAttnWaves * 64;
   constexpr int NPC = kPfKB * (HD / 8);                        // 16-byte pieces of K (and of V) per block
   constexpr int NP = (NPC + NT - 1) / NT;                      // ... per thread
@@ -789,8 +789,9 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
       const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, 64);
       const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
       const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-      // dword (p / 2) of the row, XOR 2 (d0 / 8 mod 8): rows 8 apart (the lanes' d0) land 144 dwords apart, on a few
-      // banks only; the swizzle spreads them (even, so the (4 lg, 4 lg + 1) pairs the reads take stay adjacent)
+      // dword (p / 2) of the row, XOR 2 (d0 / 8 mod 8): without it the lanes' rows, 8 apart, land on a few banks only;
+      // with 20-dword rows and the swizzle (even, so the pairs the reads take stay adjacent) both the stores and the
+      // V^T fragment reads below spread over the banks
       const int sw = 2 * ((d0 >> 3) & 7);
       uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ sw);
       w[0] = (lo_x & 0xffffu) | (hi_x << 16);
