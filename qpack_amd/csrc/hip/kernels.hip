@@ -741,56 +741,58 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
   attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored);
 }
 
-// One workgroup merges every head of group g over the S splits: wave j reduces head j's (m, l) over the splits, one
-// per lane; then P threads share each (head, 4 dims) column of partials, split c going to thread c mod P, with 8
-// coherent 16-byte loads in flight per thread, and add their sums in LDS.
+// One workgroup merges every head of group g over S < kAttnParMerge splits, in one round of loads: P threads share
+// each (head, 4 dims) column of partials, split c going to thread c mod P, and issue all their coherent 16-byte loads
+// at once, together with wave j's loads of head j's (m, l) pairs (one split per lane); wave j then forms head j's
+// factors e^(m_c - M) and 1 / L, and the column sums go through LDS.
 template <int HD, int REP, int NW>
 __device__ void attn_merge_all(const AttnArgs &a, int g, int S) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   auto cload = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-  __shared__ float fw[REP][kAttnMaxSplits], linv[REP];
-  __shared__ float4 opart[NW * 64];
-  const float *ml = a.part + (size_t)a.nh * gridDim.y * HD + 2 * (size_t)g * REP * gridDim.y;
-  if (wave < REP) {
-    const int j = wave;
-    const bool on = lane < S;
-    const float *mp = ml + 2 * ((size_t)j * gridDim.y + lane);
-    const float2 v = on ? make_float2(cload(mp), cload(mp + 1)) : make_float2(-INFINITY, 0.f);
-    const float M = wave_max(v.x);
-    const float f = on && v.x != -INFINITY ? expf(v.x - M) : 0.f;
-    const float L = wave_sum(v.y * f);
-    if (on) fw[j][lane] = f;
-    if (lane == 0) linv[j] = 1.f / L;
-  }
-  __syncthreads();
   constexpr int NC = REP * HD / 4;                            // output columns of 4 dims
   constexpr int P = NW * 64 / NC >= 4 ? 4 : (NW * 64 / NC >= 2 ? 2 : 1);
+  constexpr int K = (kAttnParMerge - 1 + P - 1) / P;          // loads per thread
+  __shared__ float fw[REP][kAttnParMerge], linv[REP];
+  __shared__ float4 opart[NW * 64];
+  const float *ml = a.part + (size_t)a.nh * gridDim.y * HD + 2 * (size_t)g * REP * gridDim.y;
   const int e = threadIdx.x % NC, part = threadIdx.x / NC;
+  const int j = e / (HD / 4), i4 = e % (HD / 4);
+  f32x4 v[K];
+  if (part < P) {
+    const float4 *ph = (const float4 *)(a.part + ((size_t)(g * REP + j) * gridDim.y) * HD) + i4;
+#pragma unroll
+    for (int k = 0; k < K; k++) {   // clamped in range; unused ones are not summed
+      const int c = part + k * P < S ? part + k * P : 0;
+      asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[k]) : "v"(ph + (size_t)c * (HD / 4)));
+    }
+  }
+  if (wave < REP) {
+    const bool on = lane < S;
+    const float *mp = ml + 2 * ((size_t)wave * gridDim.y + lane);
+    const float2 mv = on ? make_float2(cload(mp), cload(mp + 1)) : make_float2(-INFINITY, 0.f);
+    const float M = wave_max(mv.x);
+    const float f = on && mv.x != -INFINITY ? expf(mv.x - M) : 0.f;
+    const float L = wave_sum(mv.y * f);
+    if (on) fw[wave][lane] = f;
+    if (lane == 0) linv[wave] = 1.f / L;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int k = 0; k < K; k++) asm volatile("" : "+v"(v[k]));   // the values are used only after the wait
+  __syncthreads();
   float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
   if (part < P) {
-    const int j = e / (HD / 4), i4 = e % (HD / 4);
-    const float4 *ph = (const float4 *)(a.part + ((size_t)(g * REP + j) * gridDim.y) * HD) + i4;
-    for (int c0 = part; c0 < S; c0 += 8 * P) {
-      f32x4 v[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) {   // clamped in range; unused ones are not summed
-        const int c = c0 + k * P < S ? c0 + k * P : 0;
-        asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[k]) : "v"(ph + (size_t)c * (HD / 4)));
+    for (int k = 0; k < K; k++)
+      if (part + k * P < S) {
+        const float f = fw[j][part + k * P];
+        O.x = __builtin_fmaf(f, v[k][0], O.x); O.y = __builtin_fmaf(f, v[k][1], O.y);
+        O.z = __builtin_fmaf(f, v[k][2], O.z); O.w = __builtin_fmaf(f, v[k][3], O.w);
       }
-      asm volatile("s_waitcnt vmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
-#pragma unroll
-      for (int k = 0; k < 8; k++)
-        if (c0 + k * P < S) {
-          const float f = fw[j][c0 + k * P];
-          O.x = __builtin_fmaf(f, v[k].x, O.x); O.y = __builtin_fmaf(f, v[k].y, O.y);
-          O.z = __builtin_fmaf(f, v[k].z, O.z); O.w = __builtin_fmaf(f, v[k].w, O.w);
-        }
-    }
     opart[threadIdx.x] = O;
   }
   __syncthreads();
   if (threadIdx.x < NC) {
-    const int j = e / (HD / 4), i4 = e % (HD / 4);
     for (int q = 1; q < P; q++) {
       const float4 t = opart[q * NC + threadIdx.x];
       O.x += t.x; O.y += t.y; O.z += t.z; O.w += t.w;
@@ -872,7 +874,8 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   __syncthreads();
   // The last MG splits to arrive merge the S partials of the group's heads (model_llama.cpp:160-165: M = max m_c,
   // f_c = exp(m_c - M), L = sum l_c f_c, O = sum f_c o_c / L): from kAttnParMerge splits up MG = min(REP, S), head j
-  // by merger j % MG; below, the merge is short and the last arrival does it alone (MG = 1, all heads).  Counter
+  // by merger j % MG, each head's loads in one round; below, the merge is short and the last arrival does it alone
+  // (MG = 1, all heads in one round of loads).  Counter
   // a.counters[g] counts arrivals, a.counters[nkv + g] mergers done waiting; the last of those resets both for the next
   // launch (a lone merger resets the arrivals at once).  A merger waits for the arrivals behind it: those splits are already resident or wait only for workgroups
   // that finish without waiting (at most nh mergers wait at any time), and the wait is bounded.
@@ -894,7 +897,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   if (r < 0) return;
   // The partials were written through to memory by other workgroups before their counter bumps; they are read with
   // coherent loads (no acquire fence: that is an L2 invalidate, far slower).
-  if (MG == 1) {
+  if (S < kAttnParMerge) {
     attn_merge_all<HD, REP, NW>(a, g, S);
     return;
   }
