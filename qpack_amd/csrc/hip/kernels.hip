@@ -863,8 +863,9 @@ template <int HD, int REP>
 __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   constexpr int NW = kAttnMfWaves;
   const int pos = a.ctl->pos, T = pos + 1, g = blockIdx.x, s = blockIdx.y;
-  // one workgroup per kv group while every wave needs at most one block; beyond that up to 64 splits of >= 64 positions
-  const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * NW, sp = a.split_pos > 0 ? a.split_pos : 64;
+  // one workgroup per kv group while the group's K and V are at most 64 KiB (a CU streams ~55 GB/s: 128 positions at
+  // head dim 128, 256 at 64); beyond that up to 64 splits of >= 64 positions
+  const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * NW * 64 / HD, sp = a.split_pos > 0 ? a.split_pos : 64;
   const int S = T <= smax ? 1 : min((int)gridDim.y, (T + sp - 1) / sp);
   if (s >= S) return;
   attn_split<HD, REP>(a, g, s, S, gridDim.y);

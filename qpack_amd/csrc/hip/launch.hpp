@@ -88,7 +88,7 @@ struct AttnArgs {
   float *att;                  // output [nh * hd]
   int nh, nkv, hd;
   int max_chunks;              // splits S of the context per kv group (grid.y)
-  int single_max;              // contexts up to this many positions run one split per group (0: 16 x waves)
+  int single_max;              // contexts up to this many positions run one split per group (0: 64 KiB of K and V)
   int split_pos;               // beyond: S = min(max_chunks, ceil(T / split_pos)) (0: 64)
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
