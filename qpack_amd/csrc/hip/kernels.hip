@@ -202,7 +202,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 #pragma unroll
           for (int s = 0; s < NS; s++) {
             const uint32_t wd[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
-            int A = 0; uint32_t B = 0;
+            int A[4] = {0, 0, 0, 0}; uint32_t B[4] = {0, 0, 0, 0};   // per dword: 4 chains of 8, integer sums
 #pragma unroll
             for (int j = 0; j < 4; j++) {          // 32 columns per dword
 #pragma unroll
@@ -213,12 +213,12 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
                 for (int k = 0; k < 4; k++) {
                   const uint32_t nib = (wd[j] >> (16 * hh + 4 * k)) & 15u;
                   const uint32_t msk = (nib * 0x204081u) & 0x01010101u;
-                  A = __builtin_amdgcn_sdot4((int)msk, (int)hx[k], A, false);
-                  B = __builtin_amdgcn_udot4(msk, lx[k], B, false);
+                  A[j] = __builtin_amdgcn_sdot4((int)msk, (int)hx[k], A[j], false);
+                  B[j] = __builtin_amdgcn_udot4(msk, lx[k], B[j], false);
                 }
               }
             }
-            const int isum = 2 * (A * 256 + (int)B) - xsum;
+            const int isum = 2 * ((A[0] + A[1] + A[2] + A[3]) * 256 + (int)(B[0] + B[1] + B[2] + B[3])) - xsum;
             if (DBG && act && a.dbg_sums) {
               const UnitGeo<NS> og = unit_geo<EPI, NS>(a, ub + gk + ci * W, cols);
               if (og.seg == 0 && og.row[s] < og.rows) a.dbg_sums[(size_t)og.row[s] * GS + g] = isum;
@@ -238,16 +238,18 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 #pragma unroll
           for (int s = 0; s < NS; s++) {
             const uint32_t wd[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
-            int A = 0; uint32_t B = 0;
+            // low and high nibbles in separate accumulators: four dependent chains of 4 instead of two of 8 (integer
+            // sums, so the result is the same)
+            int A0 = 0, A1 = 0; uint32_t B0 = 0, B1 = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
               const uint32_t lo = wd[j] & 0x0f0f0f0fu, hi = (wd[j] >> 4) & 0x0f0f0f0fu;
-              A = __builtin_amdgcn_sdot4((int)lo, hx[j], A, false);
-              A = __builtin_amdgcn_sdot4((int)hi, hx[4 + j], A, false);
-              B = __builtin_amdgcn_udot4(lo, lx[j], B, false);
-              B = __builtin_amdgcn_udot4(hi, lx[4 + j], B, false);
+              A0 = __builtin_amdgcn_sdot4((int)lo, hx[j], A0, false);
+              A1 = __builtin_amdgcn_sdot4((int)hi, hx[4 + j], A1, false);
+              B0 = __builtin_amdgcn_udot4(lo, lx[j], B0, false);
+              B1 = __builtin_amdgcn_udot4(hi, lx[4 + j], B1, false);
             }
-            const int isum = A * 256 + (int)B - corr;
+            const int isum = (A0 + A1) * 256 + (int)(B0 + B1) - corr;
             if (DBG && act && a.dbg_sums) {
               const UnitGeo<NS> og = unit_geo<EPI, NS>(a, ub + gk + ci * W, cols);
               if (og.seg == 0 && og.row[s] < og.rows) a.dbg_sums[(size_t)og.row[s] * G + g] = isum;
