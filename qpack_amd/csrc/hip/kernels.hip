@@ -373,7 +373,10 @@ static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
   int u = (upc + w - 1) / w;                                        // units per wave
   const int cols = a.m[0].cols;
   if (cols / kQB > 2 * w * 8) { w = 16; u = (upc + 15) / 16; }     // the prologue covers 2 x (threads / 8) blocks
-  const int grid = (units + w * u - 1) / (w * u);
+  int grid = (units + w * u - 1) / (w * u);
+  // units are dealt round-robin over all the launch's waves, so a grid short of the CU count (units per CU with no
+  // divisor in 4..16) only leaves CUs idle: one workgroup per CU then
+  if (grid < cus && units >= cus) grid = cus;
   if (grid > grid_cap) return hipErrorInvalidValue;
   // a wave may own one unit more than u when the grid rounds: size the per-wave LDS for ceil(units / waves)
   const int waves = grid * w;
