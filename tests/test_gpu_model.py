@@ -163,7 +163,8 @@ def kv_snapshot(k, v):
     return b"".join(parts)
 
 
-@pytest.mark.parametrize("cfg,T", [("mini_q4m", 3000), ("mini128", 2500), ("mini_r7", 1500), ("mini_r7h", 1200)])
+@pytest.mark.parametrize("cfg,T", [("mini_q4m", 3000), ("mini128", 2500), ("mini_r7", 1500), ("mini_r7h", 1200),
+                                   ("mini", 700), ("mini128", 400)])
 def test_long_context_restore(cfg, T, synth):
     """decode at a long restored context (N(0,1) fp16 keys / values, as the C5 workload fills its 16K cache): many
     context splits per kv group and their merge; logits against the oracle holding the same cache, then greedy"""
