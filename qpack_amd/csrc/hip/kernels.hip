@@ -500,17 +500,20 @@ template <int HD, int REP, int NW, int HS>
 __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s, int S, int ys, int nact,
                                                 const float (*wm)[REP], const float (*wl)[REP], const float (*ored)[REP][HS]) {
   __shared__ float fwv[NW][REP], mlv[REP][2];
-  // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M) (in wave order)
-  if (threadIdx.x < REP) {
-    const int j = threadIdx.x;
-    float M = wm[0][j];
-    for (int w = 1; w < nact; w++) M = fmaxf(M, wm[w][j]);
-    float L = 0.f;
-    for (int w = 0; w < nact; w++) {
-      const float f = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);
-      fwv[w][j] = f; L = __builtin_fmaf(wl[w][j], f, L);
-    }
-    mlv[j][0] = M; mlv[j][1] = L;
+  // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M).  Wave 0 holds every
+  // (wave w, head j) pair, lane 8 w + j (NW, REP <= 8), and reduces over w with xor shuffles of 8, 16 and 32
+  static_assert(NW <= 8, "one lane per (wave, head)");
+  if (threadIdx.x < 64) {
+    const int w = threadIdx.x >> 3, j = threadIdx.x & 7;
+    const bool on = w < nact && j < REP;
+    const float mw = on ? wm[w][j] : -INFINITY, lw = on ? wl[w][j] : 0.f;
+    float M = mw;
+    M = fmaxf(M, __shfl_xor(M, 8, 64)); M = fmaxf(M, __shfl_xor(M, 16, 64)); M = fmaxf(M, __shfl_xor(M, 32, 64));
+    const float f = mw == -INFINITY ? 0.f : expf(mw - M);
+    float L = lw * f;
+    L += __shfl_xor(L, 8, 64); L += __shfl_xor(L, 16, 64); L += __shfl_xor(L, 32, 64);
+    if (on) fwv[w][j] = f;
+    if (w == 0 && j < REP) { mlv[j][0] = M; mlv[j][1] = L; }
   }
   __syncthreads();
   for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
