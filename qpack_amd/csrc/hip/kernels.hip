@@ -516,15 +516,24 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
     if (w == 0 && j < REP) { mlv[j][0] = M; mlv[j][1] = L; }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < REP * HD; e += blockDim.x) {
-    const int j = e / HD, i = e % HD;
-    float O = 0.f;
-    for (int w = 0; w < nact; w++) O = __builtin_fmaf(fwv[w][j], ored[w][j][i], O);
+  // 4 dims per thread (one pass over every head at REP * HD <= 4 x 512): float4 reads of the padded rows, one 16-byte
+  // store
+  for (int e = threadIdx.x; e < REP * HD / 4; e += blockDim.x) {
+    const int j = e / (HD / 4), i = 4 * (e % (HD / 4));
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int w = 0; w < nact; w++) {
+      const float f = fwv[w][j];
+      const float4 x = *(const float4 *)&ored[w][j][i];
+      O.x = __builtin_fmaf(f, x.x, O.x); O.y = __builtin_fmaf(f, x.y, O.y);
+      O.z = __builtin_fmaf(f, x.z, O.z); O.w = __builtin_fmaf(f, x.w, O.w);
+    }
     const float M = mlv[j][0], L = mlv[j][1];
     if (S == 1) {
-      a.att[(size_t)(g * REP + j) * HD + i] = O * (1.f / L);
+      const float li = 1.f / L;
+      *(float4 *)(a.att + (size_t)(g * REP + j) * HD + i) = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
     } else {
-      // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback.
+      // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback; the
+      // caller's s_waitcnt vmcnt(0) before the arrival counter covers them.
       // Layout: unnormalised outputs [nh][splits][HD], then (max, sum) pairs [nh][splits][2]
       const size_t hs = (size_t)(g * REP + j) * ys + s;
       if (i == 0) {
@@ -532,7 +541,8 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
         __hip_atomic_store(ml, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(ml + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __hip_atomic_store(a.part + hs * HD + i, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const f32x4 v = {O.x, O.y, O.z, O.w};
+      asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(a.part + hs * HD + i), "v"(v) : "memory");
     }
   }
 }
