@@ -114,18 +114,6 @@ def read_traffic():
     return None
 
 
-def kv_fill_snapshot(shape, T, seed):
-    """a snapshot in the reference layout (model_llama.cpp:55-63) whose fp16 K / V rows are N(0, 1), as the C5 workload specifies
-    fills its 16K context"""
-    kvd = shape.kv_heads * shape.head_dim
-    rng = np.random.default_rng(seed)
-    parts = [np.int32(T).tobytes()]
-    for _ in range(shape.layers):
-        for _ in range(2):
-            parts.append(rng.standard_normal((T, kvd), dtype=np.float32).astype(np.float16).tobytes())
-    return b"".join(parts)
-
-
 def other_config(name, seed, steps_override=None):
     """decode tokens/s of another benchmark configuration on its own workload: C1 / C2 prompt + greedy tokens (prompt through
     the product's prefill), C5 greedy tokens after restoring a 16384-position N(0, 1) context"""
@@ -144,7 +132,7 @@ def other_config(name, seed, steps_override=None):
         m = qa.HipLlama.load(path, max_ctx=ctx)
         rng = np.random.default_rng(seed)
         if restore:
-            m.restore(kv_fill_snapshot(shape, restore, seed))
+            m.restore(qa.kv_fill_snapshot(shape, restore, seed))
             tok = 1
         else:
             ptoks = rng.integers(0, shape.vocab, prompt).astype(np.int32)

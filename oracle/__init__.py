@@ -126,6 +126,7 @@ def olib():
             "or_greedy": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
             "or_kcache": (C.c_void_p, [C.c_void_p]), "or_vcache": (C.c_void_p, [C.c_void_p]),
             "or_set_threads": (None, [C.c_int]),
+            "or_set_order": (None, [C.c_int]),
             "or_rans_raw_size": (C.c_int64, [C.c_void_p, C.c_int64]),
             "or_rans_decode": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64]),
             "or_rans_encode": (C.c_int64, [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_int64]),

@@ -20,6 +20,12 @@
 
 void or_set_threads(int n) { if (n > 0) omp_set_num_threads(n); }
 
+/* Evaluation-order variants (OR_ORD_* bits, 0 = the reference's orders).  They exist to measure which float-order
+ * difference between the HIP path and the reference decides a greedy token: each bit swaps one reference order for the
+ * HIP path's (or, for attention, for float64 arithmetic standing in for "another order"). */
+static int g_order = 0;
+void or_set_order(int flags) { g_order = flags; }
+
 /* ------------------------------------------------------------------ fp16 */
 uint16_t or_f32_to_f16(float f) {
   uint32_t x; memcpy(&x, &f, 4);
@@ -246,13 +252,13 @@ void or_matmul(const or_mat *W, const float *X, int B, float *Y) {
       const int16_t *xb = xq + (size_t)b * cols; const float *sb = bs + (size_t)b * nb; float v;
       if (W->kind == OR_Q8) {
         const int8_t *q = (const int8_t *)W->q + (int64_t)r * cols; const float sc = ((const float *)W->s)[r];
-        v = (b < B4 && cols % OR_QB == 0) ? mm_row_q8(q, sc, xb, sb, cols) : row_q8(q, sc, xb, sb, cols);
+        v = (b < B4 && cols % OR_QB == 0 && !(g_order & OR_ORD_ROWS_PREFILL)) ? mm_row_q8(q, sc, xb, sb, cols) : row_q8(q, sc, xb, sb, cols);
       } else if (W->kind == OR_Q1) {   /* mm_q1 -> row_q1_multi: the row kernel's arithmetic for every vector */
         const int G = (cols + 127) / 128;
         v = row_q1((const uint8_t *)W->q + (int64_t)r * G * 16, (const uint16_t *)W->s + (int64_t)r * G, xb, sb, cols);
       } else {
         const uint8_t *q = (const uint8_t *)W->q + (int64_t)r * (cols / 2); const uint16_t *s = (const uint16_t *)W->s + (int64_t)r * (cols / 32);
-        v = b < B4 ? mm_row_q4(q, s, xb, sb, cols) : row_q4(q, s, xb, sb, cols);
+        v = (b < B4 && !(g_order & OR_ORD_ROWS_PREFILL)) ? mm_row_q4(q, s, xb, sb, cols) : row_q4(q, s, xb, sb, cols);
       }
       Y[(size_t)b * rows + r] = v;
     }
@@ -262,7 +268,28 @@ void or_matmul(const or_mat *W, const float *X, int B, float *Y) {
 /* ------------------------------------------------------------------ elementwise */
 /* rmsnorm (kernels.cpp:184-189) as g++ vectorises it: the squares of the first n - n % 4 elements are rounded products
  * summed in order, the last n % 4 are fused (ss = fma(x, x, ss)); inv = 1 / sqrt(ss / n + eps); out = x * inv * w */
+/* the HIP prologue's order (act.hpp): per 128-column block, 8 lanes fma-sum 16 columns each in order, then
+ * ((l0+l1)+(l2+l3)) + ((l7+l6)+(l5+l4)) by DPP; the block sums b[0..255] (zero past nb) enter a 64-lane wave as
+ * (b[l]+b[l+64]) + (b[l+128]+b[l+192]) and a butterfly over xor 32, 16, .., 1 gives lane 0's total */
+static float tree_ss(const float *x, int n) {
+  const int nb = n / OR_QB; float bsum[256] = {0}, v[64];
+  for (int b = 0; b < nb; b++) {
+    float l[8];
+    for (int j = 0; j < 8; j++) { float t = 0; for (int k = 0; k < 16; k++) { const float a = x[b * OR_QB + 16 * j + k]; t = fmaf(a, a, t); } l[j] = t; }
+    float p[8]; for (int j = 0; j < 8; j++) p[j] = l[j] + l[j ^ 1];
+    float q[8]; for (int j = 0; j < 8; j++) q[j] = p[j] + p[j ^ 2];
+    bsum[b] = q[0] + q[7];
+  }
+  for (int i = 0; i < 64; i++) v[i] = (bsum[i] + bsum[i + 64]) + (bsum[i + 128] + bsum[i + 192]);
+  for (int o = 32; o > 0; o >>= 1) { float w[64]; for (int i = 0; i < 64; i++) w[i] = v[i] + v[i ^ o]; memcpy(v, w, sizeof v); }
+  return v[0];
+}
 void or_rmsnorm(const float *x, const float *w, int n, float eps, float *out) {
+  if ((g_order & OR_ORD_TREE_NORM) && n % OR_QB == 0 && n <= 256 * OR_QB) {
+    const float inv = 1.f / sqrtf(tree_ss(x, n) / (float)n + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+    return;
+  }
   float ss = 0; const int nv = n - n % 4;
   for (int i = 0; i < nv; i++) { const float p = x[i] * x[i]; ss = ss + p; }
   for (int i = nv; i < n; i++) ss = fmaf(x[i], x[i], ss);
@@ -283,9 +310,10 @@ static float exp_lane(float x) {
   return p * s;
 }
 /* exp_v (kernels_x86.cpp:418-421): exp256 on every full group of 8 from the start, libm expf on the tail */
+static float or_expf(float x) { return (g_order & OR_ORD_EXP_F64) ? (float)exp((double)x) : expf(x); }
 void or_exp_v(const float *x, float *y, int n) {
   int i = 0; for (; i + 8 <= n; i += 8) for (int l = 0; l < 8; l++) y[i + l] = exp_lane(x[i + l]);
-  for (; i < n; i++) y[i] = expf(x[i]);
+  for (; i < n; i++) y[i] = or_expf(x[i]);
 }
 /* silu_mul (kernels_x86.cpp:427-434): g = g / (1 + exp(0 - g)) * u, exp256 on full groups of 8, expf on the tail */
 void or_silu_mul(float *g, const float *u, int n) {
@@ -369,7 +397,25 @@ static void rope_tables(const or_model *m, int pos, float *cs, float *sn) {
 
 /* decode attention (model_llama.cpp:134-166): items (kv group g, 64-position chunk c); scores_tpl (kernels_x86.cpp:474-486),
  * chunk max / exp_v / sum, values_tpl (:487-496), then the chunks merged in order per head */
+/* one query head over cache positions [0, T) of kv group g in float64, rounded to float at the end */
+static void attn_head_f64(const float *qh, const uint16_t *kl, const uint16_t *vl, int T, int g, int hd, int kvd, float *out) {
+  double *sc = (double *)malloc(8 * (size_t)T), mx = -1e300, sum = 0, o[256] = {0};
+  for (int t = 0; t < T; t++) {
+    double s = 0; for (int i = 0; i < hd; i++) s += (double)qh[i] * or_f16_to_f32(kl[(size_t)t * kvd + g * hd + i]);
+    sc[t] = s / sqrt((double)hd); if (sc[t] > mx) mx = sc[t];
+  }
+  for (int t = 0; t < T; t++) { sc[t] = exp(sc[t] - mx); sum += sc[t]; }
+  for (int t = 0; t < T; t++) for (int i = 0; i < hd; i++) o[i] += sc[t] * or_f16_to_f32(vl[(size_t)t * kvd + g * hd + i]);
+  for (int i = 0; i < hd; i++) out[i] = (float)(o[i] / sum);
+  free(sc);
+}
+static void attend_f64(or_model *m, const uint16_t *kl, const uint16_t *vl, const float *q, int T, float *out) {
+  const int nh = m->c.nh, rep = nh / m->c.nkv, hd = m->c.hd;
+  #pragma omp parallel for schedule(dynamic, 1)
+  for (int h = 0; h < nh; h++) attn_head_f64(q + h * hd, kl, vl, T, h / rep, hd, m->kvd, out + h * hd);
+}
 static void attend(or_model *m, const uint16_t *kl, const uint16_t *vl, const float *q, int T, float *out) {
+  if (g_order & OR_ORD_ATTN_F64) { attend_f64(m, kl, vl, q, T, out); return; }
   const int C = 64, nc = (T + C - 1) / C, nh = m->c.nh, rep = nh / m->c.nkv, hd = m->c.hd, kvd = m->kvd;
   const float scl = 1.f / sqrtf((float)hd);
   const size_t need = (size_t)nh * nc * (hd + 2);
@@ -413,7 +459,7 @@ static void attend(or_model *m, const uint16_t *kl, const uint16_t *vl, const fl
     for (int c = 0; c < nc; c++) if (M < ph[(size_t)c * (hd + 2)]) M = ph[(size_t)c * (hd + 2)];
     float *o = out + h * hd, L = 0; memset(o, 0, 4 * (size_t)hd);
     for (int c = 0; c < nc; c++) {
-      const float *pc = ph + (size_t)c * (hd + 2); const float f = expf(pc[0] - M);
+      const float *pc = ph + (size_t)c * (hd + 2); const float f = or_expf(pc[0] - M);
       L = fmaf(pc[1], f, L);
       for (int i = 0; i < hd; i++) o[i] = fmaf(f, pc[2 + i], o[i]);
     }
@@ -490,6 +536,7 @@ int or_prefill(or_model *m, const int *toks, int n, int want, float *out) {
       for (int w = 0; w < B * c->nh; w++) {
         const int i = w / c->nh, h = w % c->nh, T = p0 + i + 1, g = h / rep;
         const float *qh = Q + (size_t)i * qd + h * hd; float mx = -1e30f;
+        if (g_order & OR_ORD_ATTN_F64) { attn_head_f64(qh, kl, vl, T, g, hd, kvd, A + (size_t)i * qd + h * hd); continue; }
         float *sc = (float *)malloc(4 * (size_t)T);
         for (int t = 0; t < T; t++) { float s = dot_f16(qh, kl + (size_t)t * kvd + g * hd, hd); s *= scl; sc[t] = s; if (mx < s) mx = s; }
         float sum = 0; for (int t = 0; t < T; t++) sc[t] -= mx;

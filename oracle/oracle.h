@@ -80,6 +80,9 @@ int or_greedy(or_model *m, int tok, int n, int *out);
 uint16_t *or_kcache(or_model *m);
 uint16_t *or_vcache(or_model *m);
 void or_set_threads(int n);
+/* evaluation-order variants for experiments (0 = the reference's orders everywhere) */
+enum { OR_ORD_TREE_NORM = 1, OR_ORD_ROWS_PREFILL = 2, OR_ORD_ATTN_F64 = 4, OR_ORD_EXP_F64 = 8 };
+void or_set_order(int flags);
 
 /* QPACK3 static rANS codec (/root/reference/include/qpack/rans.h; format in /root/reference/QPACK2.md:30-51).
  * Errors: OR_RANS_* (negative); the reference throws std::runtime_error at the same points. */

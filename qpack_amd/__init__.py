@@ -8,7 +8,7 @@
 """
 from ._lib import LIB_PATH, QPH_F32, QPH_Q1, QPH_Q4, QPH_Q8, QphError, device_count, lib
 from .model import HipLlama, kernel_matmul, kernel_matvec, kernel_rans_decode, kernel_topk, pack, time_copy
-from .synth import CONFIGS, Shape, write_synthetic
+from .synth import CONFIGS, Shape, kv_fill_snapshot, write_synthetic
 
-__all__ = ["HipLlama", "kernel_matmul", "kernel_matvec", "kernel_rans_decode", "kernel_topk", "pack", "time_copy", "write_synthetic", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
+__all__ = ["HipLlama", "kernel_matmul", "kernel_matvec", "kernel_rans_decode", "kernel_topk", "pack", "time_copy", "write_synthetic", "kv_fill_snapshot", "CONFIGS", "Shape", "QphError", "device_count", "lib", "LIB_PATH",
            "QPH_F32", "QPH_Q8", "QPH_Q4", "QPH_Q1"]

@@ -1,6 +1,6 @@
 """ctypes binding of libqpack_hip.so (the C ABI declared in include/qpack_hip.h).
 
-The library is built in-tree by qpack_amd/build.py.  Loading fails loudly when it is missing: there is no CPU fallback
+The library is built in-tree by qpack_amd/csrc/Makefile (driven by __graft_entry__.build()).  Loading fails loudly when it is missing: there is no CPU fallback
 on the product path.
 """
 import ctypes as C
@@ -69,11 +69,13 @@ SIGNATURES = {
     "qph_snapshot_size": (_I, [_P, C.POINTER(C.c_int64)]),
     "qph_snapshot": (_I, [_P, C.c_void_p, C.c_int64]),
     "qph_restore": (_I, [_P, C.c_void_p, C.c_int64]),
+    "qph_set_order": (_I, [_P, _I]),
     "qph_time_greedy": (_I, [_P, _I, _I, _FP]),
     "qph_time_kernel": (_I, [_P, _I, _I, _FP, C.POINTER(C.c_double)]),
     "qph_time_copy": (_I, [C.c_int64, _I, _FP]),
     "qph_kernel_matvec": (_I, [_I, _P, _P, _I, _I, _FP, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int16), _FP]),
     "qph_kernel_matmul": (_I, [_I, _P, _P, _I, _I, _FP, _I, _FP]),
+    "qph_kernel_matmul_ref": (_I, [_I, _P, _P, _I, _I, _FP, _I, _FP]),
     "qph_kernel_topk": (_I, [_FP, _I, _I, _IP, _FP]),
     "qph_synth_write": (_I, [C.POINTER(SynthSpecC), C.c_char_p, _I]),
     "qph_load_stats_of": (_I, [C.c_void_p, C.POINTER(LoadStatsC)]),

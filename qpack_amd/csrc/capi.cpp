@@ -155,6 +155,8 @@ int qph_snapshot_size(const qph_model *m, int64_t *bytes) { QPH_API_TRY({ need(m
 int qph_snapshot(qph_model *m, uint8_t *buf, int64_t cap) { QPH_API_TRY({ need(m, "model"); need(buf, "buf"); m->m->snapshot(buf, cap); }); }
 int qph_restore(qph_model *m, const uint8_t *buf, int64_t n) { QPH_API_TRY({ need(m, "model"); need(buf, "buf"); m->m->restore(buf, n); }); }
 
+int qph_set_order(qph_model *m, int mode) { QPH_API_TRY({ need(m, "model"); m->m->set_order(mode); }); }
+
 int qph_time_greedy(qph_model *m, int token, int n, float *ms) {
   QPH_API_TRY({ need(m, "model"); need(ms, "ms"); *ms = m->m->time_greedy(token, n); });
 }
@@ -281,6 +283,36 @@ int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int 
         ga.q4ns = dns; ga.q4sc = dsc;
       }
       hck(qph::launch_gemm(ga, nullptr), "launch gemm");
+      hck(hipDeviceSynchronize(), "matmul");
+      hck(hipMemcpy(Y, dy, 4ull * B * rows, hipMemcpyDeviceToHost), "download Y");
+    } catch (...) { for (void *p : bufs) (void)hipFree(p); throw; }
+    for (void *p : bufs) (void)hipFree(p);
+  });
+}
+
+int qph_kernel_matmul_ref(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y) {
+  QPH_API_TRY({
+    need(q, "q"); need(scale, "scale"); need(X, "X"); need(Y, "Y");
+    if (rows <= 0 || B <= 0 || cols <= 0 || cols % 128) throw std::invalid_argument("matmul: rows, B > 0 and cols a positive multiple of 128 required");
+    if (kind != QPH_Q8 && kind != QPH_Q4) throw std::invalid_argument("matmul: kind must be QPH_Q8 or QPH_Q4");
+    const int nb = cols / 128, G = cols / 32;
+    const size_t qb = kind == QPH_Q8 ? (size_t)rows * cols : (size_t)rows * cols / 2;
+    const size_t sb = kind == QPH_Q8 ? 4ull * rows : 2ull * rows * G;
+    std::vector<void *> bufs;
+    auto alloc = [&](size_t n) { void *p = nullptr; hck(hipMalloc(&p, n), "hipMalloc"); bufs.push_back(p); return p; };
+    try {
+      void *dq = alloc(qb), *ds = alloc(sb);
+      float *dx = (float *)alloc(4ull * B * cols), *dy = (float *)alloc(4ull * B * rows), *dxb = (float *)alloc(4ull * B * nb);
+      int8_t *dxh = (int8_t *)alloc((size_t)B * cols), *dxl = (int8_t *)alloc((size_t)B * cols);
+      hck(hipMemcpy(dq, q, qb, hipMemcpyHostToDevice), "upload q");
+      hck(hipMemcpy(ds, scale, sb, hipMemcpyHostToDevice), "upload scale");
+      hck(hipMemcpy(dx, X, 4ull * B * cols, hipMemcpyHostToDevice), "upload X");
+      qph::PfQuantArgs qa{}; qa.x = dx; qa.ldx = cols; qa.cols = cols; qa.xh = dxh; qa.xl = dxl; qa.ldq = cols; qa.xb = dxb; qa.ldb = nb;
+      hck(qph::launch_pf_quant(qph::PRO_QUANT, qa, B, nullptr), "launch quant");
+      qph::ExGemmArgs ga{}; ga.kind = kind == QPH_Q8 ? qph::MK_Q8 : qph::MK_Q4; ga.w = dq; ga.scale = (const float *)ds;
+      ga.s16 = (const uint16_t *)ds; ga.rows = rows; ga.cols = cols; ga.xh = dxh; ga.xl = dxl; ga.ldq = cols; ga.xb = dxb;
+      ga.ldb = nb; ga.ntok = B; ga.mm_below = B - B % 4; ga.tt = B == 1 ? 1 : 16; ga.y = dy; ga.ldy = rows;
+      hck(qph::launch_ex_gemm(ga, nullptr), "launch gemm");
       hck(hipDeviceSynchronize(), "matmul");
       hck(hipMemcpy(Y, dy, 4ull * B * rows, hipMemcpyDeviceToHost), "download Y");
     } catch (...) { for (void *p : bufs) (void)hipFree(p); throw; }

@@ -34,6 +34,13 @@ struct Ctl {
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// an fp32 result rounded to fp32 first and then to fp16, like the reference's to_f16 of a stored float vector
+// (kernels_x86.cpp:449-452): without the barrier the compiler fuses an fma feeding the conversion into v_fma_mix, which
+// rounds once, straight to fp16 (a different fp16 value when the fp32 result sits next to an fp16 midpoint)
+__device__ __forceinline__ uint16_t f32_to_half_bits(float f) {
+  asm volatile("" : "+v"(f));
+  return float_to_half_bits(f);
+}
 
 // exp256 of /root/reference/src/kernels_x86.cpp:406-417 for one lane: clamp to [-87, 88], k = rint(x log2 e),
 // two-constant reduction, degree-6 polynomial, scale by 2^k.  Written with explicit fmaf so it is bit-identical.

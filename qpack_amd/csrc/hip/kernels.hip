@@ -625,8 +625,8 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
   if (t0 <= pos && pos < t1) {
     for (int i = threadIdx.x; i < HALF; i += blockDim.x) {
       const float *kh = a.k + (size_t)g * HD; const float x0 = kh[i], x1 = kh[i + HALF];
-      const uint16_t k0 = float_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
-      const uint16_t k1 = float_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
+      const uint16_t k0 = f32_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
+      const uint16_t k1 = f32_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
       knew[i] = k0; knew[i + HALF] = k1;
       a.kc[(size_t)pos * kvd + g * HD + i] = k0; a.kc[(size_t)pos * kvd + g * HD + i + HALF] = k1;
     }
@@ -905,11 +905,13 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
     const int r = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - (S - MG);
     if (MG == 1 && r == 0) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int spins = 0;
+    const int lim = a.spin_limit > 0 ? a.spin_limit : (1 << 22);
     if (r >= 0 && r < MG - 1)
-      while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < S && ++spins < (1 << 22))
+      while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < S && ++spins < lim)
         __builtin_amdgcn_s_sleep(1);
     rank = r < 0 ? -1 : r;
-    late = spins >= (1 << 22);
+    late = spins >= lim;
+    if (late && a.status) *(volatile int *)a.status = 1;   // the step's outputs are invalid: the host raises an error
   }
   __syncthreads();
   const int r = rank;

@@ -90,6 +90,8 @@ struct AttnArgs {
   int max_chunks;              // splits S of the context per kv group (grid.y)
   int single_max;              // contexts up to this many positions run one split per group (0: 64 KiB of K and V)
   int split_pos;               // beyond: S = min(max_chunks, ceil(T / split_pos)) (0: 64)
+  int *status;                 // optional (host-visible): set to 1 when a merger's bounded wait for the partials ran out
+  int spin_limit;              // the bound of that wait in polls (0: 1 << 22)
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 
@@ -167,6 +169,55 @@ struct PfAttnArgs {
   int ntok, p0, nh, nkv, hd;
 };
 hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st);
+
+// ---- reference-order mode (exact.hip): the reference CPU path's float orders, bit-identical results
+// RMSNorm of `rows` vectors [ldx] with the sequential sum of squares, out [ldo]
+hipError_t launch_ex_rmsnorm(const float *x, int ldx, const float *w, int n, float eps, float *out, int ldo, int rows,
+                             hipStream_t st);
+// decode RoPE: q -> qr rotated; k rotated and v, as fp16, into the cache row ctl->pos
+struct ExRopeArgs {
+  const float *q, *k, *v;
+  float *qr;
+  const float *cos_t, *sin_t;
+  const Ctl *ctl;
+  uint16_t *kc, *vc;
+  int nh, nkv, hd;
+};
+hipError_t launch_ex_rope(const ExRopeArgs &a, hipStream_t st);
+// decode attention over 64-position chunks (partials [nh][ncmax][hd + 2]) and their ordered merge into att [nh * hd]
+struct ExAttnArgs {
+  const float *qr;
+  const uint16_t *kc, *vc;
+  const Ctl *ctl;
+  float *part;
+  float *att;
+  int nh, nkv, hd, ncmax;
+};
+hipError_t launch_ex_attention(const ExAttnArgs &a, hipStream_t st);
+// prompt attention: the batch's rotated queries q [B][ldq] at positions p0 .. p0 + B - 1 -> att [B][lda]
+struct ExPfAttnArgs {
+  const float *q; int ldq;
+  const uint16_t *kc, *vc;
+  float *att; int lda;
+  int p0, nh, nkv, hd;
+};
+hipError_t launch_ex_pf_attn(const ExPfAttnArgs &a, int B, hipStream_t st);
+// y [ntok][ldy] = W x_t (+ bias; or += when resid) over the quantiser's planes; vectors t < mm_below in mm_q8 / mm_q4
+// order, the rest in rows_q8 / rows_q4 order; tt = vectors per workgroup tile (1 or 16)
+struct ExGemmArgs {
+  int kind;
+  const void *w; const float *scale; const uint16_t *s16;
+  int rows, cols;
+  const int8_t *xh, *xl; int ldq;
+  const float *xb; int ldb;
+  int ntok, mm_below, tt;
+  float *y; int ldy;
+  const float *bias;
+  int resid;
+};
+hipError_t launch_ex_gemm(const ExGemmArgs &a, hipStream_t st);
+// g = silu(g) * u on rows of n values
+hipError_t launch_ex_silu(float *g, const float *u, int n, int ld, int rows, hipStream_t st);
 
 // QPACK3 rANS decode (hip/rans_decode.hip): one task per coded plane, one wave per task
 struct RansTaskDev {

@@ -113,6 +113,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(64, atoi(e)));
   if (const char *e = getenv("QPH_ATTN_SINGLE")) attn_single_ = std::max(0, atoi(e));
   if (const char *e = getenv("QPH_ATTN_SPLIT_POS")) attn_split_pos_ = std::max(0, atoi(e));
+  // test hook: the bound of a merger's wait for the other splits (the failure path forced from the host)
+  if (const char *e = getenv("QPH_ATTN_SPIN")) attn_spin_ = std::max(0, atoi(e));
   counters_ = (int *)dalloc(8ull * nkv);
   const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
   kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
@@ -184,6 +186,9 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     topk_a_ = (uint64_t *)dalloc(8 * keys); topk_b_ = (uint64_t *)dalloc(8 * keys);
     topk_val_ = (float *)dalloc(8ull * kTopkMax); topk_idx_ = (int *)(topk_val_ + kTopkMax);   // one copy back
   }
+  QPH_CK(hipHostMalloc((void **)&hstatus_, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent));
+  *hstatus_ = 0;
+  QPH_CK(hipHostGetDevicePointer((void **)&dstatus_, hstatus_, 0));
   memset(hctl_, 0, kRing * sizeof(Ctl));
   QPH_CK(hipMemset(ctl_, 0, sizeof(Ctl)));
   build_graphs();
@@ -191,12 +196,14 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
 
 HipLlama::~HipLlama() {
   if (st_) (void)hipStreamSynchronize(st_);
-  for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_}) if (g) (void)hipGraphExecDestroy(g);
+  for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_, g_ex_state_, g_ex_logits_, g_ex_greedy_})
+    if (g) (void)hipGraphExecDestroy(g);
   for (void *p : allocs_) (void)hipFree(p);
   if (hctl_) (void)hipHostFree(hctl_);
   if (hout_) (void)hipHostFree(hout_);
   if (htok_) (void)hipHostFree(htok_);
   if (htopk_) (void)hipHostFree(htopk_);
+  if (hstatus_) (void)hipHostFree(hstatus_);
   if (st_) (void)hipStreamDestroy(st_);
 }
 
@@ -214,7 +221,7 @@ void HipLlama::enqueue_layer(int l) {
     a.kc = kc_ + (size_t)l * ctx_ * kvd_; a.vc = vc_ + (size_t)l * ctx_ * kvd_;
     a.cos_t = cos_; a.sin_t = sin_; a.ctl = ctl_; a.part = part_; a.att = att_;
     a.nh = cfg_.heads; a.nkv = cfg_.kv_heads; a.hd = cfg_.head_dim; a.max_chunks = max_chunks_; a.counters = counters_;
-    a.single_max = attn_single_; a.split_pos = attn_split_pos_;
+    a.single_max = attn_single_; a.split_pos = attn_split_pos_; a.status = dstatus_; a.spin_limit = attn_spin_;
     QPH_CK(launch_attention(a, st_));
   }
   {  // wo + residual
@@ -242,13 +249,26 @@ void HipLlama::enqueue_head() {
   QPH_CK(launch_matvec(PRO_NORM, EPI_ARGMAX, a, head_grid_, st_));
 }
 
+// one decode step in the current arithmetic order: parts 0 = layers, 1 = + output head (logits), 2 = + greedy pick
+// (ctl advances on the device)
+void HipLlama::enqueue_step(int parts) {
+  QPH_CK(launch_embed(embed_, ctl_, x_, st_));
+  for (int l = 0; l < cfg_.layers; l++) {
+    if (order_) ex_enqueue_layer(l);
+    else enqueue_layer(l);
+  }
+  if (parts >= 1) {
+    if (order_) ex_enqueue_head();
+    else enqueue_head();
+  }
+  if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
+}
+
 hipGraphExec_t HipLlama::capture(int parts) {
   hipGraph_t g = nullptr; hipGraphExec_t ge = nullptr;
   QPH_CK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
   try {
-    enqueue_layers();
-    if (parts >= 1) enqueue_head();
-    if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
+    enqueue_step(parts);
   } catch (...) {
     (void)hipStreamEndCapture(st_, &g);
     if (g) (void)hipGraphDestroy(g);
@@ -262,21 +282,35 @@ hipGraphExec_t HipLlama::capture(int parts) {
 
 void HipLlama::build_graphs() {
   const char *ng = getenv("QPH_NO_GRAPH");
-  if (ng && atoi(ng) > 0) { use_graphs_ = false; return; }
+  // Under rocprofv3 (its tool library is announced in ROCP_TOOL_LIBRARIES) the kernels are enqueued directly: the
+  // profiler's interception of graph launches crashed the host process (SIGSEGV in the tool, below hipGraphLaunch, at
+  // the first replay) while direct launches of the same kernels profile normally.
+  const char *prof = getenv("ROCP_TOOL_LIBRARIES");
+  if ((ng && atoi(ng) > 0) || (prof && *prof)) { use_graphs_ = false; return; }
   g_state_ = capture(0);
   g_logits_ = capture(1);
   g_greedy_ = capture(2);
 }
 
-// one decode step: parts 0 = layers, 1 = + output head (logits), 2 = + greedy pick (ctl advances on the device)
 void HipLlama::run_step(int parts) {
   if (use_graphs_) {
-    QPH_CK(hipGraphLaunch(parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_, st_));
+    hipGraphExec_t g = order_ ? (parts == 0 ? g_ex_state_ : parts == 1 ? g_ex_logits_ : g_ex_greedy_)
+                              : (parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_);
+    QPH_CK(hipGraphLaunch(g, st_));
     return;
   }
-  enqueue_layers();
-  if (parts >= 1) enqueue_head();
-  if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
+  enqueue_step(parts);
+}
+
+// Called after every wait for the stream: a decode attention merger whose bounded wait for the other splits' partials
+// ran out wrote NaN outputs and set the status word.  The split counters may then be stale, so they are cleared before
+// the error is raised; the position is left as it was (the caller may rewind and retry).
+void HipLlama::check_status() {
+  if (!*(volatile int *)hstatus_) return;
+  *(volatile int *)hstatus_ = 0;
+  QPH_CK(hipMemsetAsync(counters_, 0, 8ull * cfg_.kv_heads, st_));
+  QPH_CK(hipStreamSynchronize(st_));
+  throw std::runtime_error("decode attention: a split merge timed out waiting for its partials; this call's outputs are invalid");
 }
 
 void HipLlama::write_ctl(int tok, int pos) {
@@ -287,7 +321,7 @@ void HipLlama::write_ctl(int tok, int pos) {
   c.tok = tok; c.pos = pos; c.n_out = 0; c.pad = 0;
   QPH_CK(hipMemcpyAsync(ctl_, &c, sizeof(Ctl), hipMemcpyHostToDevice, st_));
   slot_++;
-  if (slot_ % (kRing / 2) == 0) QPH_CK(hipStreamSynchronize(st_));
+  if (slot_ % (kRing / 2) == 0) { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
 }
 
 void HipLlama::step(int tok, int want, float *out) {
@@ -300,13 +334,14 @@ void HipLlama::step(int tok, int want, float *out) {
   } else {
     run_step(0);
     if (want == 2) {
-      QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
+      if (order_) ex_norm(x_, fnorm_, xn_, 1, cfg_.hidden);
+      else QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
       QPH_CK(hipMemcpyAsync(hout_, xn_, 4ull * cfg_.hidden, hipMemcpyDeviceToHost, st_));
     }
   }
   pos_++;
   if (want == 1 || want == 2) {
-    QPH_CK(hipStreamSynchronize(st_));
+    { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
     if (out) memcpy(out, hout_, 4ull * (want == 1 ? cfg_.vocab : cfg_.hidden));
   }
 }
@@ -318,19 +353,22 @@ void HipLlama::prefill(const int *toks, int n, int want, float *out) {
   const bool force_steps = getenv("QPH_PREFILL_STEPS") != nullptr;   // test hook: the decode-step path
   if (n == 1 || !pf_ok_ || force_steps) {   // one token (the reference's n == 1 case) or q1 layers: decode steps
     for (int i = 0; i < n; i++) step(toks[i], i + 1 == n ? want : 0, i + 1 == n ? out : nullptr);
-    if (!want) QPH_CK(hipStreamSynchronize(st_));
+    if (!want) { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
     return;
   }
-  prefill_batched(toks, n);
+  if (order_) ex_prefill(toks, n);
+  else prefill_batched(toks, n);
   if (want == 1 || want == 3) {   // 3 (internal): logits left on the device
-    enqueue_head();
+    if (order_) ex_enqueue_head();
+    else enqueue_head();
     if (want == 1) QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
   } else if (want == 2) {
-    QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
+    if (order_) ex_norm(x_, fnorm_, xn_, 1, cfg_.hidden);
+    else QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
     QPH_CK(hipMemcpyAsync(hout_, xn_, 4ull * cfg_.hidden, hipMemcpyDeviceToHost, st_));
   }
   if (want == 3) return;   // the caller works on the device logits next
-  QPH_CK(hipStreamSynchronize(st_));
+  { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
   if (want && out) memcpy(out, hout_, 4ull * (want == 1 ? cfg_.vocab : cfg_.hidden));
 }
 
@@ -414,7 +452,7 @@ void HipLlama::topk_to_host(int M, int *idx, float *val) {
   QPH_CK(launch_topk(logits_, cfg_.vocab, M, topk_a_, topk_b_, topk_idx_, topk_val_, st_));
   // values at [0, M), indices at [kTopkMax, kTopkMax + M) of one device buffer: one copy of the used span
   QPH_CK(hipMemcpyAsync(htopk_, topk_val_, 4ull * (kTopkMax + M), hipMemcpyDeviceToHost, st_));
-  QPH_CK(hipStreamSynchronize(st_));
+  { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
   memcpy(val, htopk_, 4ull * M);
   memcpy(idx, htopk_ + kTopkMax, 4ull * M);
 }
@@ -437,7 +475,7 @@ int HipLlama::greedy_run(int tok, int n, int *out) {
   write_ctl(tok, pos_);
   for (int i = 0; i < n; i++) run_step(2);
   QPH_CK(hipMemcpyAsync(htok_, out_tok_, 4ull * n, hipMemcpyDeviceToHost, st_));
-  QPH_CK(hipStreamSynchronize(st_));
+  { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
   memcpy(out, htok_, 4ull * n);
   pos_ += n;
   return n;
@@ -455,7 +493,7 @@ void HipLlama::set_pos(int pos) {
 
 void HipLlama::snapshot(uint8_t *buf, int64_t cap) {
   if (cap < snapshot_size()) throw std::runtime_error("snapshot buffer too small");
-  QPH_CK(hipStreamSynchronize(st_));
+  { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
   memcpy(buf, &pos_, 4); uint8_t *p = buf + 4; const size_t nb = (size_t)pos_ * kvd_ * 2;
   for (int l = 0; l < cfg_.layers; l++)
     for (uint16_t *c : {kc_, vc_}) { QPH_CK(hipMemcpy(p, c + (size_t)l * ctx_ * kvd_, nb, hipMemcpyDeviceToHost)); p += nb; }
@@ -467,11 +505,147 @@ void HipLlama::restore(const uint8_t *buf, int64_t n) {
   if (pos < 0 || pos > ctx_) throw std::runtime_error("snapshot position out of range");
   const size_t nb = (size_t)pos * kvd_ * 2;
   if (n < (int64_t)(4 + 2 * nb * cfg_.layers)) throw std::runtime_error("snapshot too short");
-  QPH_CK(hipStreamSynchronize(st_));
+  { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
   const uint8_t *p = buf + 4;
   for (int l = 0; l < cfg_.layers; l++)
     for (uint16_t *c : {kc_, vc_}) { QPH_CK(hipMemcpy(c + (size_t)l * ctx_ * kvd_, p, nb, hipMemcpyHostToDevice)); p += nb; }
   pos_ = pos;
+}
+
+// ------------------------------------------------------------------ reference-order mode
+// The reference CPU path's arithmetic order everywhere (exact.hip holds what the default kernels do differently):
+// RMSNorm's sequential sum, attention over 64-position chunks with an ordered merge (decode) or full rows (prompt),
+// rows_q4 for the q4 products, the prompt's products in mm_q8 / mm_q4 order for the first B - B % 4 vectors of each
+// 64-token batch, and the C library's expf on softmax tails.  q8 decode products, quantisation, RoPE, the fp16 cache
+// rows and every epilogue are the default kernels, which already follow the reference's order.
+void HipLlama::set_order(int mode) {
+  if (mode != 0 && mode != 1) throw std::runtime_error("order: mode must be 0 (default) or 1 (reference order)");
+  if (mode == 1) {
+    if (!pf_ok_) throw std::runtime_error("order: reference order needs q8 / q4 layer matrices");
+    if (head_.kind != MK_Q8) throw std::runtime_error("order: reference order needs a q8 output head");
+    if (!ex_part_) {
+      ex_ncmax_ = (ctx_ + 63) / 64;
+      ex_part_ = (float *)dalloc(4ull * cfg_.heads * ex_ncmax_ * (cfg_.head_dim + 2));
+      ex_qr_ = (float *)dalloc(4ull * qd_);
+      const int B = std::min(64, pf_cap_);
+      ex_u_ = (float *)dalloc(4ull * B * cfg_.ffn);
+      ex_xn_ = (float *)dalloc(4ull * B * cfg_.hidden);
+    }
+  }
+  QPH_CK(hipStreamSynchronize(st_));
+  order_ = mode;
+  if (mode == 1 && use_graphs_ && !g_ex_state_) {
+    g_ex_state_ = capture(0);
+    g_ex_logits_ = capture(1);
+    g_ex_greedy_ = capture(2);
+  }
+}
+
+void HipLlama::ex_norm(const float *x, const float *w, float *out, int rows, int ldx) {
+  QPH_CK(launch_ex_rmsnorm(x, ldx, w, cfg_.hidden, cfg_.rms_eps, out, cfg_.hidden, rows, st_));
+}
+
+// y [ntok][ldy] = m x_t (+ bias, or += when resid) in the reference's order; x [ntok][ldx] is quantised into the prompt
+// planes first unless `quantised` says they already hold it
+void HipLlama::ex_product(const DMat &m, const float *x, int ldx, int ntok, int mm_below, float *y, int ldy,
+                          const float *bias, bool resid, bool quantised) {
+  const int nb_ld = pf_ldq_ / 128 + 1;
+  if (!quantised) {
+    PfQuantArgs q{}; q.x = x; q.ldx = ldx; q.cols = m.cols; q.xh = pf_xh_; q.xl = pf_xl_; q.ldq = pf_ldq_;
+    q.xb = pf_xb_; q.ldb = nb_ld;
+    QPH_CK(launch_pf_quant(PRO_QUANT, q, ntok, st_));
+  }
+  ExGemmArgs a{}; a.kind = m.kind; a.w = m.q; a.scale = (const float *)m.s; a.s16 = (const uint16_t *)m.s;
+  a.rows = m.rows; a.cols = m.cols; a.xh = pf_xh_; a.xl = pf_xl_; a.ldq = pf_ldq_; a.xb = pf_xb_; a.ldb = nb_ld;
+  a.ntok = ntok; a.mm_below = mm_below; a.tt = ntok == 1 ? 1 : 16; a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0;
+  QPH_CK(launch_ex_gemm(a, st_));
+}
+
+void HipLlama::ex_enqueue_layer(int l) {
+  const Layer &ly = layers_[l];
+  const int d = cfg_.hidden, ff = cfg_.ffn, cap = 1 << 20;
+  uint16_t *kc = kc_ + (size_t)l * ctx_ * kvd_, *vc = vc_ + (size_t)l * ctx_ * kvd_;
+  // the q8 matrices of a group share one launch of the default matvec (PRO_QUANT: x is already normalised); q4 ones
+  // take the rows_q4-order product
+  auto group = [&](const DMat *const *m, float *const *y, const float *const *bias, int n, const float *x, int ldx) {
+    MvArgs a{}; a.x = x;
+    bool quantised = false;
+    for (int s = 0; s < n; s++)
+      if (m[s]->kind == MK_Q8) { a.m[a.nseg] = *m[s]; a.out[a.nseg] = y[s]; a.bias[a.nseg] = bias[s]; a.nseg++; }
+    if (a.nseg) { mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); }
+    for (int s = 0; s < n; s++)
+      if (m[s]->kind != MK_Q8) { ex_product(*m[s], x, ldx, 1, 0, y[s], 0, bias[s], false, quantised); quantised = true; }
+  };
+  auto resid = [&](const DMat &m, const float *x, int cols) {
+    if (m.kind == MK_Q8) {
+      MvArgs a{}; a.m[0] = m; a.nseg = 1; a.x = x; a.out[0] = x_;
+      mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_));
+    } else ex_product(m, x, cols, 1, 0, x_, 0, nullptr, true, false);
+  };
+  ex_norm(x_, ly.an, xn_, 1, d);
+  {
+    const DMat *m[3] = {&ly.wq, &ly.wk, &ly.wv};
+    float *y[3] = {q_, k_, v_};
+    const float *b[3] = {ly.bq, ly.bk, ly.bv};
+    group(m, y, b, 3, xn_, d);
+  }
+  ExRopeArgs r{}; r.q = q_; r.k = k_; r.v = v_; r.qr = ex_qr_; r.cos_t = cos_; r.sin_t = sin_; r.ctl = ctl_;
+  r.kc = kc; r.vc = vc; r.nh = cfg_.heads; r.nkv = cfg_.kv_heads; r.hd = cfg_.head_dim;
+  QPH_CK(launch_ex_rope(r, st_));
+  ExAttnArgs t{}; t.qr = ex_qr_; t.kc = kc; t.vc = vc; t.ctl = ctl_; t.part = ex_part_; t.att = att_;
+  t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim; t.ncmax = ex_ncmax_;
+  QPH_CK(launch_ex_attention(t, st_));
+  resid(ly.wo, att_, qd_);
+  ex_norm(x_, ly.fn, xn_, 1, d);
+  {
+    const DMat *m[2] = {&ly.wg, &ly.wu};
+    float *y[2] = {h_, ex_u_};
+    const float *b[2] = {nullptr, nullptr};
+    group(m, y, b, 2, xn_, d);
+  }
+  QPH_CK(launch_ex_silu(h_, ex_u_, ff, ff, 1, st_));
+  resid(ly.wd, h_, ff);
+}
+
+void HipLlama::ex_enqueue_head() {
+  ex_norm(x_, fnorm_, xn_, 1, cfg_.hidden);
+  MvArgs a{}; a.m[0] = head_; a.nseg = 1; a.x = xn_; a.out[0] = logits_; a.amax = amax_;
+  mv_plan(a, EPI_ARGMAX);
+  QPH_CK(launch_matvec(PRO_QUANT, EPI_ARGMAX, a, head_grid_, st_));
+}
+
+// the prompt in the reference's batches of 64 tokens (model_llama.cpp:66-130)
+void HipLlama::ex_prefill(const int *toks, int n) {
+  const int d = cfg_.hidden, ff = cfg_.ffn, PB = std::min(64, pf_cap_);
+  int B = 0;
+  for (int s0 = 0; s0 < n; s0 += B) {
+    B = std::min(PB, n - s0);
+    const int p0 = pos_, b4 = B - B % 4;
+    QPH_CK(hipMemcpyAsync(pf_tok_, toks + s0, 4ull * B, hipMemcpyHostToDevice, st_));
+    QPH_CK(launch_pf_embed(embed_, pf_tok_, B, pf_x_, d, st_));
+    for (int l = 0; l < cfg_.layers; l++) {
+      const Layer &ly = layers_[l];
+      uint16_t *kc = kc_ + (size_t)l * ctx_ * kvd_, *vc = vc_ + (size_t)l * ctx_ * kvd_;
+      ex_norm(pf_x_, ly.an, ex_xn_, B, d);
+      ex_product(ly.wq, ex_xn_, d, B, b4, pf_q_, qd_, ly.bq, false, false);
+      ex_product(ly.wk, ex_xn_, d, B, b4, pf_k_, kvd_, ly.bk, false, true);
+      ex_product(ly.wv, ex_xn_, d, B, b4, pf_v_, kvd_, ly.bv, false, true);
+      PfRopeArgs r{}; r.q = pf_q_; r.ldq = qd_; r.k = pf_k_; r.v = pf_v_; r.ldk = kvd_; r.cos_t = cos_; r.sin_t = sin_;
+      r.kc = kc; r.vc = vc; r.p0 = p0; r.nh = cfg_.heads; r.nkv = cfg_.kv_heads; r.hd = cfg_.head_dim;
+      QPH_CK(launch_pf_rope(r, B, st_));
+      ExPfAttnArgs t{}; t.q = pf_q_; t.ldq = qd_; t.kc = kc; t.vc = vc; t.att = pf_att_; t.lda = qd_;
+      t.p0 = p0; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
+      QPH_CK(launch_ex_pf_attn(t, B, st_));
+      ex_product(ly.wo, pf_att_, qd_, B, b4, pf_x_, d, nullptr, true, false);
+      ex_norm(pf_x_, ly.fn, ex_xn_, B, d);
+      ex_product(ly.wg, ex_xn_, d, B, b4, pf_g_, ff, nullptr, false, false);
+      ex_product(ly.wu, ex_xn_, d, B, b4, ex_u_, ff, nullptr, false, true);
+      QPH_CK(launch_ex_silu(pf_g_, ex_u_, ff, ff, B, st_));
+      ex_product(ly.wd, pf_g_, ff, B, b4, pf_x_, d, nullptr, true, false);
+    }
+    pos_ += B;
+  }
+  QPH_CK(hipMemcpyAsync(x_, pf_x_ + (size_t)(B - 1) * d, 4ull * d, hipMemcpyDeviceToDevice, st_));
 }
 
 float HipLlama::time_greedy(int tok, int n) {
@@ -483,7 +657,7 @@ float HipLlama::time_greedy(int tok, int n) {
   QPH_CK(hipEventRecord(e0, st_));
   for (int i = 0; i < n; i++) run_step(2);
   QPH_CK(hipEventRecord(e1, st_));
-  QPH_CK(hipEventSynchronize(e1));
+  QPH_CK(hipEventSynchronize(e1)); check_status();
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
   pos_ += n;
@@ -530,6 +704,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         AttnArgs t{}; t.q = q_; t.k = k_; t.v = v_; t.kc = kc_; t.vc = vc_; t.cos_t = cos_; t.sin_t = sin_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         t.max_chunks = max_chunks_; t.counters = counters_; t.single_max = attn_single_; t.split_pos = attn_split_pos_;
+        t.status = dstatus_; t.spin_limit = attn_spin_;
         QPH_CK(launch_attention(t, st_)); break;
       }
       default: throw std::runtime_error("time_kernel: unknown kernel id");
@@ -555,7 +730,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   QPH_CK(hipEventRecord(e0, st_));
   for (int i = 0; i < iters; i++) launch();
   QPH_CK(hipEventRecord(e1, st_));
-  QPH_CK(hipEventSynchronize(e1));
+  QPH_CK(hipEventSynchronize(e1)); check_status();
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
   return ms / iters;

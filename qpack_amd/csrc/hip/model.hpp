@@ -41,6 +41,11 @@ class HipLlama {
   void snapshot(uint8_t *buf, int64_t cap);
   void restore(const uint8_t *buf, int64_t n);
 
+  // arithmetic order: 0 = this library's kernels (default), 1 = the reference CPU path's order everywhere, so logits,
+  // caches and greedy streams are bit-identical to qp::Llama's (slower: a test and verification mode)
+  void set_order(int mode);
+  int order() const { return order_; }
+
   float time_greedy(int tok, int n);
   float time_kernel(int which, int iters, double *bytes);
 
@@ -52,7 +57,7 @@ class HipLlama {
   qph_config cfg_;
   int ctx_ = 0, kvd_ = 0, qd_ = 0, max_chunks_ = 1, cus_ = 256, head_grid_ = 0;
   int *counters_ = nullptr;
-  int attn_single_ = 0, attn_split_pos_ = 0;   // attention split policy (0: the kernel's defaults)
+  int attn_single_ = 0, attn_split_pos_ = 0, attn_spin_ = 0;   // attention split policy (0: the kernel's defaults)
   int pos_ = 0;
   unsigned slot_ = 0;
   hipStream_t st_ = nullptr;
@@ -78,10 +83,22 @@ class HipLlama {
   int *topk_idx_ = nullptr;
   float *topk_val_ = nullptr;
   uint32_t *htopk_ = nullptr;
+  int *hstatus_ = nullptr, *dstatus_ = nullptr;   // attention status word: mapped pinned host memory, its device alias
   void topk_to_host(int M, int *idx, float *val);
   hipGraphExec_t g_state_ = nullptr, g_logits_ = nullptr, g_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
   void run_step(int parts);
+  // reference-order mode (exact.hip)
+  int order_ = 0, ex_ncmax_ = 0;
+  float *ex_qr_ = nullptr, *ex_part_ = nullptr, *ex_u_ = nullptr, *ex_xn_ = nullptr;
+  hipGraphExec_t g_ex_state_ = nullptr, g_ex_logits_ = nullptr, g_ex_greedy_ = nullptr;
+  void ex_norm(const float *x, const float *w, float *out, int rows, int ldx);
+  void ex_product(const DMat &m, const float *x, int ldx, int ntok, int mm_below, float *y, int ldy, const float *bias,
+                  bool resid, bool quantised);
+  void ex_enqueue_layer(int l);
+  void ex_enqueue_head();
+  void ex_prefill(const int *toks, int n);
+  void enqueue_step(int parts);
   // batched prompt path (layer matrices q8 / q4)
   static constexpr int kPfChunk = 2048;
   bool pf_ok_ = false;
@@ -101,6 +118,7 @@ class HipLlama {
   void enqueue_head();
   void build_graphs();
   hipGraphExec_t capture(int parts);
+  void check_status();
   void write_ctl(int tok, int pos);
 };
 

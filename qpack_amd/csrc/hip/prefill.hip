@@ -682,8 +682,8 @@ __global__ __launch_bounds__(256) void k_pf_rope(PfRopeArgs a) {
   for (int e = threadIdx.x; e < a.nkv * half; e += blockDim.x) {
     const int g = e / half, i = e % half;
     const float x0 = k[g * a.hd + i], x1 = k[g * a.hd + i + half];
-    kr[g * a.hd + i] = float_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
-    kr[g * a.hd + i + half] = float_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
+    kr[g * a.hd + i] = f32_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
+    kr[g * a.hd + i + half] = f32_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
   }
   for (int e = threadIdx.x; e < kvd; e += blockDim.x) vr[e] = float_to_half_bits(v[e]);
 }

@@ -110,6 +110,11 @@ class HipLlama:
     def reset(self):
         check(lib().qph_reset(self._h))
 
+    def set_order(self, mode):
+        """0: this library's kernels (default); 1: the reference CPU path's arithmetic order everywhere (bit-identical
+        logits and greedy streams; slower)"""
+        check(lib().qph_set_order(self._h, int(mode)))
+
     def rewind(self, pos):
         ok = C.c_int(0)
         check(lib().qph_rewind(self._h, int(pos), C.byref(ok)))
@@ -176,9 +181,10 @@ def kernel_matvec(kind, q, scale, x):
     return y, sums, xq, bs
 
 
-def kernel_matmul(q, scale, X, kind=None):
+def kernel_matmul(q, scale, X, kind=None, order=0):
     """the product's batched prefill kernels on one matrix: Y[B, rows] = X[B, cols] W^T (qph_kernel_matmul); q8 (int8
-    q, f32 scale) or q4 (packed u8 q, fp16-bits scale per 32 columns)"""
+    q, f32 scale) or q4 (packed u8 q, fp16-bits scale per 32 columns); order=1: the reference-order products
+    (qph_kernel_matmul_ref)"""
     from ._lib import QPH_Q4, QPH_Q8
     if kind is None:
         kind = QPH_Q8 if q.dtype == np.int8 else QPH_Q4
@@ -190,8 +196,8 @@ def kernel_matmul(q, scale, X, kind=None):
     B = X.shape[0]
     assert X.shape[1] == cols
     Y = np.empty((B, rows), np.float32)
-    check(lib().qph_kernel_matmul(kind, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols,
-                                  _fptr(X), B, _fptr(Y)))
+    f = lib().qph_kernel_matmul_ref if order else lib().qph_kernel_matmul
+    check(f(kind, q.ctypes.data_as(C.c_void_p), scale.ctypes.data_as(C.c_void_p), rows, cols, _fptr(X), B, _fptr(Y)))
     return Y
 
 

@@ -91,3 +91,19 @@ def write_synthetic(shape, path, seed=1234, std=0.02, threads=0):
     s.model_type = shape.model_type.encode()[:31]
     check(lib().qph_synth_write(C.byref(s), str(path).encode(), int(threads)))
     return str(path)
+
+
+def kv_fill_snapshot(shape, T, seed):
+    """a snapshot in the reference's layout (/root/reference/src/model_llama.cpp:55-63: int32 position, then per layer the
+    K rows and the V rows of positions [0, T)) whose fp16 values are N(0, 1) from `seed`: how the C5 workload fills its
+    16K context"""
+    import numpy as np
+    if isinstance(shape, str):
+        shape = CONFIGS[shape]
+    kvd = shape.kv_heads * shape.head_dim
+    rng = np.random.default_rng(seed)
+    parts = [np.int32(T).tobytes()]
+    for _ in range(shape.layers):
+        for _ in range(2):
+            parts.append(rng.standard_normal((T, kvd), dtype=np.float32).astype(np.float16).tobytes())
+    return b"".join(parts)

@@ -8,12 +8,19 @@ the seed by the tests), a seeded prompt, and what the reference computes on it w
 (/root/reference/tools/qpack-bench.cpp:40-45): prefill(prompt) -> logits, then greedy decoding by step(tok, 1) + argmax
 (the default Model::greedy_run, /root/reference/include/qpack/qpack.h:143-149).  Stored: the greedy stream, the top-2 gap
 of every step, top-5 ids / logits of the prefill and of the first decode steps, and a fixed sample of the prefill logits
-with their float64 sum.
+with their float64 sum, and for every decode step a 64-bit hash of the float32 logits (blake2b of their bytes), so a
+path that claims the reference's arithmetic can be checked bit for bit at every step.
+
+Benchmark-shape fixtures: c3 (8B q8: 128-token prompt, 256 greedy tokens), c4 (8B q8: one 2048-token prompt; prefill
+logits plus fp16 K / V rows of three layers at five positions, c4_kv.npz, and a hash of every layer's cache) and c5
+(7B q4m: a restored 16384-position N(0, 1) fp16 context, qpack_amd.kv_fill_snapshot with KV_SEED, then 128 greedy
+tokens from token 1).  Slow on a CPU (minutes at 8 threads); run one by name, e.g. `make_golden.py c4`.
 
 Kernel fixtures (kernels.npz): seeded q8 / q4 matrices and activations with edge cases (zero block, outliers), the
 reference's matvec output for each (qp::matvec: quant_rows + rows_q8 / rows_q4), its tiled matmul output (mm_q8 /
 mm_q4, 6 vectors), rmsnorm and silu_mul outputs.
 """
+import hashlib
 import json
 import os
 import sys
@@ -28,21 +35,27 @@ import qpack_amd as qa  # noqa: E402
 HERE = os.path.dirname(os.path.abspath(__file__))
 TMP = os.environ.get("TMPDIR", "/tmp")
 
-# name: (prompt tokens, greedy tokens, max_ctx)
+# name: (prompt tokens, greedy tokens, max_ctx, restored context)
 MODELS = {
-    "mini": (70, 64, 256),
-    "mini128": (131, 64, 256),
-    "mini_q4": (70, 64, 256),
-    "mini_q4m": (100, 64, 256),
-    "c1": (32, 128, 168),
-    "c2": (512, 256, 776),
-    "mini_q1": (70, 64, 256),
-    "mini_q1m": (70, 64, 256),
-    "mini_q4mb": (70, 64, 256),
-    "mini_q4h": (70, 64, 256),
+    "mini": (70, 64, 256, 0),
+    "mini128": (131, 64, 256, 0),
+    "mini_q4": (70, 64, 256, 0),
+    "mini_q4m": (100, 64, 256, 0),
+    "c1": (32, 128, 168, 0),
+    "c2": (512, 256, 776, 0),
+    "mini_q1": (70, 64, 256, 0),
+    "mini_q1m": (70, 64, 256, 0),
+    "mini_q4mb": (70, 64, 256, 0),
+    "mini_q4h": (70, 64, 256, 0),
+    "c3": (128, 256, 400, 0),
+    "c4": (2048, 0, 2048, 0),
+    "c5": (0, 128, 16384 + 144, 16384),
 }
 SEED = 1234
 PROMPT_SEED = 99
+KV_SEED = 5
+C4_LAYERS = [0, 15, 31]
+C4_POS = [0, 1, 511, 1024, 2047]
 
 
 def prompt_for(name, vocab):
@@ -54,35 +67,72 @@ def top(l, k):
     return i.tolist(), l[i].astype(float).tolist()
 
 
+def logits_hash(l):
+    """64-bit hash of a float32 logits vector's bytes (the bit-exactness check)"""
+    return hashlib.blake2b(np.ascontiguousarray(l, np.float32).tobytes(), digest_size=8).hexdigest()
+
+
+def cache_hashes(snap, layers, T, kvd):
+    """per layer (K, V) hashes of a snapshot in the reference layout"""
+    body = np.frombuffer(snap, np.uint8, offset=4)
+    n = T * kvd * 2
+    out = []
+    for l in range(layers):
+        k = body[(2 * l) * n:(2 * l + 1) * n]
+        v = body[(2 * l + 1) * n:(2 * l + 2) * n]
+        out.append([hashlib.blake2b(k.tobytes(), digest_size=8).hexdigest(), hashlib.blake2b(v.tobytes(), digest_size=8).hexdigest()])
+    return out
+
+
 def model_fixture(name):
-    n_prompt, n_gen, ctx = MODELS[name]
+    n_prompt, n_gen, ctx, restore = MODELS[name]
     path = os.path.join(TMP, f"golden_{name}.qpack")
-    qa.write_synthetic(name, path, seed=SEED)
+    qa.write_synthetic(name, path, seed=SEED, threads=8)
+    shape = qa.CONFIGS[name]
     ref = O.Ref(path, ctx)
     V = ref.vocab()
-    toks = prompt_for(name, V)
-    lg = ref.prefill(toks, 1)
-    pi, pv = top(lg, 10)
-    sample_idx = np.arange(0, V, max(1, V // 512))
-    tok = int(np.argmax(lg))
-    stream, gaps, tops = [], [], []
+    fx = dict(config=name, seed=SEED, max_ctx=ctx)
+    if restore:
+        ref.restore(qa.kv_fill_snapshot(shape, restore, KV_SEED))
+        fx.update(kv_seed=KV_SEED, restore=restore, first_token=1, prompt=[])
+        tok = 1
+    else:
+        toks = prompt_for(name, V)
+        lg = ref.prefill(toks, 1)
+        pi, pv = top(lg, 10)
+        sample_idx = np.arange(0, V, max(1, V // 512))
+        tok = int(np.argmax(lg))
+        fx.update(prompt_seed=PROMPT_SEED, prompt=toks.tolist(), prefill_top10=[pi, pv], prefill_sample_idx=sample_idx.tolist(),
+                  prefill_sample=lg[sample_idx].astype(float).tolist(), prefill_sum=float(lg.astype(np.float64).sum()),
+                  prefill_hash=logits_hash(lg), first_token=tok)
+    if name == "c4":
+        kvd = shape.kv_heads * shape.head_dim
+        snap = ref.snapshot()
+        fx["cache_hash"] = cache_hashes(snap, shape.layers, n_prompt, kvd)
+        body = np.frombuffer(snap, np.float16, offset=4).reshape(shape.layers, 2, n_prompt, kvd)
+        np.savez_compressed(os.path.join(HERE, "c4_kv.npz"), layers=np.array(C4_LAYERS), pos=np.array(C4_POS),
+                            k=body[C4_LAYERS][:, 0][:, C4_POS], v=body[C4_LAYERS][:, 1][:, C4_POS])
+    stream, gaps, tops, hashes, samples = [], [], [], [], {}
     for i in range(n_gen):
         l = ref.step(tok, 1)
         s = np.sort(l)
         gaps.append(float(s[-1] - s[-2]))
-        if i < 16:
-            tops.append(top(l, 5))
+        tops.append(top(l, 5))
+        hashes.append(logits_hash(l))
+        if restore and i in (0, n_gen // 2, n_gen - 1):
+            idx = np.arange(0, V, max(1, V // 512))
+            samples[str(i)] = l[idx].astype(float).tolist()
+            fx["step_sample_idx"] = idx.tolist()
         tok = int(np.argmax(l))
         stream.append(tok)
-    fx = dict(config=name, seed=SEED, prompt_seed=PROMPT_SEED, max_ctx=ctx, prompt=toks.tolist(), prefill_top10=[pi, pv],
-              prefill_sample_idx=sample_idx.tolist(), prefill_sample=lg[sample_idx].astype(float).tolist(),
-              prefill_sum=float(lg.astype(np.float64).sum()), first_token=int(np.argmax(lg)), greedy=stream,
-              greedy_top2_gap=gaps, decode_top5=tops, pos_after=int(ref.pos()))
+    fx.update(greedy=stream, greedy_top2_gap=gaps, decode_top5=tops, step_hash=hashes, pos_after=int(ref.pos()))
+    if samples:
+        fx["step_sample"] = samples
     ref.close()
     os.remove(path)
     with open(os.path.join(HERE, f"{name}.json"), "w") as f:
         json.dump(fx, f)
-    print(f"{name}: stream {stream[:12]}..., min top-2 gap {min(gaps):.3g}", flush=True)
+    print(f"{name}: stream {stream[:12]}..., min top-2 gap {min(gaps) if gaps else 0:.3g}", flush=True)
 
 
 def act_vector(rng, cols):
@@ -148,6 +198,8 @@ def kernel_fixture():
 
 if __name__ == "__main__":
     O.rlib(int(os.environ.get("QPREF_THREADS", "8")))
-    kernel_fixture()
-    for name in (sys.argv[1:] or MODELS):
+    names = sys.argv[1:] or [n for n in MODELS if n not in ("c3", "c4", "c5")]
+    if not sys.argv[1:]:
+        kernel_fixture()
+    for name in names:
         model_fixture(name)

@@ -1,14 +1,18 @@
 """The HIP token loop against the reference's own outputs (tests/golden/*.json, written by the reference engine compiled
-from its sources) at the benchmark shapes C1 (Qwen2.5-0.5B q8: 32-token prompt + 128 greedy tokens) and C2 (the same
-model in q4: 512 + 256), plus the small shapes.
+from its sources by tests/golden/make_golden.py) at every benchmark shape (C1-C5) and the small shapes.
 
-Bar: prefill logits within max-abs 1e-2 / relative 1e-3 on a fixed sample; the greedy stream identical token for token
-up to the first step whose reference top-2 logit gap is below TIE = 20 x the measured prefill logit error (at least
-1e-5).  The HIP RMSNorm sums x^2 in a parallel tree while the reference sums sequentially (kernels.cpp:185), so logits
-agree to ~1e-6 relative, not bit for bit; at a step where the reference's two best logits are closer than that, its
-own pick is a rounding accident.  A divergence before such a step fails the test; the number of agreeing tokens and
-the step where a near-tie stopped the comparison are printed.
+Two arithmetic orders are checked:
+  - reference order (HipLlama.set_order(1)): every logits vector must be bit-identical to the reference's (a 64-bit hash
+    of its float32 bytes per prompt and per decode step), every fp16 cache row too (C4, per-layer hashes), so the greedy
+    stream is identical token for token: C1 128/128, C2 256/256, C3 256/256, C5 128/128;
+  - the default order (the fast kernels): prefill logits within max-abs 1e-2 / relative 1e-3 on a fixed sample, the
+    top-5 logits of every decode step within the same bound while the streams agree, and the greedy stream identical up
+    to the first step whose reference top-2 gap is below TIE = 20 x the measured logit error.  Reordering a float sum
+    moves C1's logits by ~5e-4 (measured with the oracle's order variants, oracle.c OR_ORD_*), so near-ties narrower than
+    that are decided by rounding order; the default order is held to the tolerance there and the reference order to bit
+    equality.
 """
+import hashlib
 import json
 import os
 
@@ -20,31 +24,146 @@ import qpack_amd as qa
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
+SMALL = ["mini", "mini128", "mini_q4", "mini_q4m", "mini_q1", "mini_q1m", "mini_q4mb", "mini_q4h"]
+# q1 layers and q4 heads have no reference-order kernels (their reference orders are not on the benchmark path)
+NO_EXACT = {"mini_q1", "mini_q1m", "mini_q4h"}
 
-@pytest.mark.parametrize("name", ["mini", "mini128", "mini_q4", "mini_q4m", "c1", "c2", "mini_q1", "mini_q1m", "mini_q4mb",
-                                  "mini_q4h"])
-def test_matches_reference_fixture(name, synth):
+
+def fixture(name):
     with open(os.path.join(GOLD, name + ".json")) as f:
-        fx = json.load(f)
-    path = synth(name, fx["seed"])
-    print(f"{name}: prompt {len(fx['prompt'])}, greedy {len(fx['greedy'])}", flush=True)
+        return json.load(f)
+
+
+def lhash(l):
+    return hashlib.blake2b(np.ascontiguousarray(l, np.float32).tobytes(), digest_size=8).hexdigest()
+
+
+def synth_name(name):
+    return "c3" if name == "c4" else name   # C4 is the C3 model (same shape, same seed, same bytes)
+
+
+def start(name, fx, synth, exact):
+    """the model loaded, in the requested order, with the fixture's prompt or restored context; returns (model, prompt
+    logits or None)"""
+    path = synth(synth_name(name), fx["seed"])
     m = qa.HipLlama.load(path, max_ctx=fx["max_ctx"])
-    lg = m.prefill(np.array(fx["prompt"], np.int32), 1)
+    if exact:
+        m.set_order(1)
+    if fx.get("restore"):
+        print(f"{name}: restoring an N(0,1) context of {fx['restore']}", flush=True)
+        m.restore(qa.kv_fill_snapshot(name, fx["restore"], fx["kv_seed"]))
+        return m, None
+    print(f"{name}: prompt of {len(fx['prompt'])} tokens ({'reference' if exact else 'default'} order)", flush=True)
+    return m, m.prefill(np.array(fx["prompt"], np.int32), 1)
+
+
+@pytest.mark.parametrize("name", SMALL + ["c1", "c2", "c3", "c5"])
+def test_reference_order_bit_identical(name, synth):
+    if name in NO_EXACT:
+        pytest.skip("no reference-order kernels for q1 layers / a q4 head")
+    fx = fixture(name)
+    m, lg = start(name, fx, synth, True)
+    if lg is not None:
+        assert lhash(lg) == fx["prefill_hash"], "prompt logits differ from the reference's bits"
+    p0 = m.pos()
+    tok = fx["first_token"]
+    for i, want in enumerate(fx["greedy"]):
+        l = m.step(tok, 1)
+        if lhash(l) != fx["step_hash"][i]:
+            pytest.fail(f"{name}: decode step {i}: logits differ from the reference's bits")
+        tok = int(np.argmax(l))
+        assert tok == want
+    n = len(fx["greedy"])
+    assert m.pos() == fx["pos_after"]
+    # the device-side greedy chain (graph replays) in the same order
+    assert m.rewind(p0)
+    g = m.greedy_run(fx["first_token"], n)
+    m.close()
+    np.testing.assert_array_equal(g, fx["greedy"])
+    print(f"{name}: reference order, {n}/{n} steps bit-identical, greedy {n}/{n}", flush=True)
+
+
+@pytest.mark.parametrize("name", SMALL + ["c1", "c2", "c3", "c5"])
+def test_default_order_within_tolerance(name, synth):
+    fx = fixture(name)
+    m, lg = start(name, fx, synth, False)
+    e = 0.0
+    if lg is not None:
+        ref = np.float32(fx["prefill_sample"])
+        got = lg[fx["prefill_sample_idx"]]
+        err = np.abs(got - ref)
+        assert np.all(err <= np.maximum(1e-2, 1e-3 * np.abs(ref))), f"prefill logits max|d| {err.max()}"
+        assert int(np.argmax(lg)) == fx["first_token"]
+        e = float(err.max())
+    tok = fx["first_token"]
+    stream, top_err = [], 0.0
+    for i in range(len(fx["greedy"])):
+        l = m.step(tok, 1)
+        if fx.get("step_sample") and str(i) in fx["step_sample"]:
+            ref = np.float32(fx["step_sample"][str(i)])
+            err = np.abs(l[fx["step_sample_idx"]] - ref)
+            assert np.all(err <= np.maximum(1e-2, 1e-3 * np.abs(ref))), f"step {i} logits max|d| {err.max()}"
+            e = max(e, float(err.max()))
+        tok = int(np.argmax(l))
+        stream.append(tok)
+        if stream != fx["greedy"][:i + 1]:
+            break   # past a divergence the inputs differ; the tolerance applies while the streams agree
+        ids, vals = fx["decode_top5"][i]
+        d = np.abs(l[ids] - np.float32(vals))
+        assert np.all(d <= np.maximum(1e-2, 1e-3 * np.abs(np.float32(vals)))), f"step {i}: top-5 logits max|d| {d.max()}"
+        top_err = max(top_err, float(d.max()))
+    m.close()
+    tie = max(20 * max(e, top_err), 1e-5)
+    gaps = np.array(fx["greedy_top2_gap"])
+    ref_stream = np.array(fx["greedy"])
+    got = np.array(stream)
+    mism = np.nonzero(got != ref_stream[:len(got)])[0]
+    agree = int(mism[0]) if len(mism) else len(got)
+    first_tie = int(np.argmax(gaps < tie)) if np.any(gaps < tie) else len(gaps)
+    print(f"{name}: default order: logit max|d| {max(e, top_err):.3g}, greedy agrees for {agree}/{len(ref_stream)} tokens, "
+          f"first reference near-tie (gap < {tie:.3g}) at step {first_tie}", flush=True)
+    if agree < len(ref_stream) and agree < first_tie:
+        pytest.fail(f"greedy stream differs at step {agree} (reference top-2 gap there {gaps[agree]:.3g} > {tie:.3g})")
+
+
+def c4_cache_rows(m, fx, layers, pos):
+    snap = np.frombuffer(m.snapshot(), np.uint8)
+    shape = qa.CONFIGS["c4"]
+    kvd = shape.kv_heads * shape.head_dim
+    T = len(fx["prompt"])
+    body = np.frombuffer(snap.tobytes(), np.float16, offset=4).reshape(shape.layers, 2, T, kvd)
+    return snap, body[layers][:, 0][:, pos], body[layers][:, 1][:, pos]
+
+
+@pytest.mark.parametrize("exact", [False, True], ids=["default", "reference_order"])
+def test_c4_prefill(exact, synth):
+    """C4: one 2048-token prompt on the 8B q8 model.  Default order: logits within the tolerance and the sampled fp16
+    cache rows within the logits' absolute bound (1e-2) plus 2 fp16 ulps of the reference's (the rows of layers 15 and
+    31 carry the residual stream's reordering drift, not only their own rounding); reference order: logits and every
+    layer's K / V cache bit-identical (per-layer hashes)."""
+    fx = fixture("c4")
+    kv = np.load(os.path.join(GOLD, "c4_kv.npz"))
+    m, lg = start("c4", fx, synth, exact)
+    snap, k, v = c4_cache_rows(m, fx, kv["layers"], kv["pos"])
+    m.close()
+    if exact:
+        assert lhash(lg) == fx["prefill_hash"]
+        shape = qa.CONFIGS["c4"]
+        n = len(fx["prompt"]) * shape.kv_heads * shape.head_dim * 2
+        body = snap[4:]
+        for l in range(shape.layers):
+            hk = hashlib.blake2b(body[(2 * l) * n:(2 * l + 1) * n].tobytes(), digest_size=8).hexdigest()
+            hv = hashlib.blake2b(body[(2 * l + 1) * n:(2 * l + 2) * n].tobytes(), digest_size=8).hexdigest()
+            assert [hk, hv] == fx["cache_hash"][l], f"layer {l}: cache differs from the reference's bits"
+        return
     ref = np.float32(fx["prefill_sample"])
-    got = lg[fx["prefill_sample_idx"]]
-    err = np.abs(got - ref)
+    err = np.abs(lg[fx["prefill_sample_idx"]] - ref)
     assert np.all(err <= np.maximum(1e-2, 1e-3 * np.abs(ref))), f"prefill logits max|d| {err.max()}"
     assert int(np.argmax(lg)) == fx["first_token"]
-    e = float(err.max())
-    tie = max(20 * e, 1e-5)
-    g = m.greedy_run(fx["first_token"], len(fx["greedy"]))
-    assert m.pos() == fx["pos_after"]
-    m.close()
-    gaps = np.array(fx["greedy_top2_gap"])
-    mism = np.nonzero(g != np.array(fx["greedy"]))[0]
-    first_tie = int(np.argmax(gaps < tie)) if np.any(gaps < tie) else len(gaps)
-    agree = int(mism[0]) if len(mism) else len(g)
-    print(f"{name}: prefill logit max|d| {e:.3g}, tie threshold {tie:.3g}, greedy agrees for {agree}/{len(g)} tokens, "
-          f"first reference near-tie at step {first_tie}", flush=True)
-    if agree < len(g) and agree < first_tie:
-        pytest.fail(f"greedy stream differs at step {agree} (reference top-2 gap there {gaps[agree]:.3g} > tie threshold {tie:.3g})")
+    for got, want in ((k, kv["k"]), (v, kv["v"])):
+        g32, w32 = got.astype(np.float32), want.astype(np.float32)
+        ulp = np.spacing(np.abs(want)).astype(np.float32)
+        d = np.abs(g32 - w32)
+        assert np.all(d <= 2 * ulp + 1e-2), f"cache rows max|d| {d.max()}"
+    print(f"c4: prefill logit max|d| {err.max():.3g}; cache rows max|d| K {np.abs(k.astype(np.float32) - kv['k']).max():.3g}, "
+          f"V {np.abs(v.astype(np.float32) - kv['v']).max():.3g}", flush=True)

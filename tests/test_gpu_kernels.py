@@ -103,30 +103,6 @@ def test_matmul_q8_rows_equal_decode_arithmetic(rows, cols, B):
         np.testing.assert_array_equal(Y[b], O.rows_q8(q, s, xq, bs), err_msg=f"token {b}")
 
 
-@pytest.mark.parametrize("rows,cols", [(1000, 4096), (257, 896), (300, 18944), (9, 128), (4096, 14336), (14336, 4096)])
-def test_matvec_q1_exact_sums(rows, cols):
-    """q1 (rows_q1, kernels_x86.cpp:167-203): the exact int32 dot product of every (row, 128-column group) equals a
-    brute-force numpy sum over the unpacked signs; y within 2e-6 of the summed magnitudes of the oracle's (fp32 order:
-    per-lane fma over the groups, then the wave sum, instead of the reference's 8 AVX lanes)"""
-    rng = np.random.default_rng(rows * 13 + cols)
-    G = cols // 128
-    q = rng.integers(0, 256, (rows, G * 16)).astype(np.uint8)
-    s = (rng.random((rows, G)) * 0.01 + 1e-4).astype(np.float16).view(np.uint16)
-    x = act_vector(rng, cols)
-    print(f"q1 matvec rows={rows} cols={cols}", flush=True)
-    y, sums, xq, bs = qa.kernel_matvec(qa.QPH_Q1, q, s, x)
-    xq_o, bs_o = O.quant_act(x)
-    np.testing.assert_array_equal(xq, xq_o)
-    sign = np.unpackbits(q, axis=1, bitorder="little").astype(np.int64) * 2 - 1      # [rows, cols]: +1 / -1
-    brute = (sign.reshape(rows, G, 128) * xq_o.astype(np.int64).reshape(1, G, 128)).sum(2)
-    np.testing.assert_array_equal(sums, brute)
-    np.testing.assert_array_equal(O.group_sums_q1(q, xq_o, cols), brute)
-    y_o = O.rows_q1(q, s, xq_o, bs_o, cols)
-    comb = s.view(np.float16).astype(np.float32) * bs_o[None, :]
-    mag = np.abs(comb * brute).sum(1)
-    assert np.all(np.abs(y - y_o) <= 2e-6 * mag + 1e-30), float(np.max(np.abs(y - y_o) / (mag + 1e-30)))
-
-
 @pytest.mark.parametrize("rows,cols,B", [(1000, 4096, 200), (257, 896, 129), (300, 18944, 17), (9, 128, 1), (3584, 3584, 64),
                                          (130, 512, 1024)])
 def test_matmul_q4(rows, cols, B):
@@ -148,3 +124,32 @@ def test_matmul_q4(rows, cols, B):
         mag = np.abs(comb * gs).sum(1)
         y_o = O.rows_q4(q, s, xq, bs)
         assert np.all(np.abs(Y[b] - y_o) <= 2e-6 * mag + 1e-30), (b, float(np.max(np.abs(Y[b] - y_o) / (mag + 1e-30))))
+
+
+@pytest.mark.parametrize("kind", ["q8", "q4"])
+@pytest.mark.parametrize("rows,cols,B", [(48, 1024, 6), (257, 896, 64), (300, 4096, 1), (130, 512, 27), (64, 14336, 5),
+                                         (1000, 4096, 40)])
+def test_matmul_reference_order_bit_exact(kind, rows, cols, B):
+    """the reference-order products (qph_kernel_matmul_ref, the prompt products of set_order(1)): bit-identical to the
+    oracle's matmul - mm_q8 / mm_q4 lane order for the first B - B % 4 vectors, rows_q8 / rows_q4 for the rest - which
+    is pinned bit-exact to the reference's matmul (tests/test_oracle.py, tests/golden/kernels.npz)"""
+    rng = np.random.default_rng(rows * 19 + cols + B)
+    if kind == "q8":
+        q, s = q8_matrix(rng, rows, cols)
+        k = O.OR_Q8
+    else:
+        q = rng.integers(0, 256, (rows, cols // 2)).astype(np.uint8)
+        s = (rng.random((rows, cols // 32)) * 0.01 + 1e-4).astype(np.float16).view(np.uint16)
+        k = O.OR_Q4
+    X = np.stack([act_vector(rng, cols) * rng.uniform(0.1, 10) for _ in range(B)]).astype(np.float32)
+    print(f"reference-order {kind} matmul rows={rows} cols={cols} B={B}", flush=True)
+    Y = qa.kernel_matmul(q, s, X, order=1)
+    np.testing.assert_array_equal(Y, O.matmul(k, q, s, X))
+
+
+def test_matmul_reference_order_golden():
+    """the same products on the reference's own outputs (tests/golden/kernels.npz: its matmul of 6 vectors)"""
+    g = np.load(__file__.replace("test_gpu_kernels.py", "golden/kernels.npz"))
+    for key in ("q8_48x1024", "q8_33x896", "q4_48x1024", "q4_33x896"):
+        Y = qa.kernel_matmul(g[key + "_q"], g[key + "_s"], g[key + "_X"], order=1)
+        np.testing.assert_array_equal(Y, g[key + "_Y"], err_msg=key)

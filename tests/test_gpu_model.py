@@ -213,3 +213,57 @@ def test_files_of_the_reference_quantiser(src, args, synth, tmp_path):
     assert ok, f"prefill logits max|d| {err}"
     np.testing.assert_array_equal(gpu.greedy_run(int(np.argmax(lg)), 32), orc.greedy_run(int(np.argmax(lo)), 32))
     gpu.close(); orc.close()
+
+
+def test_attention_merge_timeout_is_an_error(synth, monkeypatch):
+    """the decode attention's failure path, forced from the host: with the mergers' bounded wait cut to one poll
+    (QPH_ATTN_SPIN=1, read at load) a merger gives up, writes NaN and sets the status word; the call raises instead of
+    returning those outputs, the split counters are cleared, and every kernel still runs to completion (a fresh model
+    at the same context decodes normally afterwards)"""
+    cfg, T = "mini_r7", 1500   # 24 splits per kv group, 7 heads per group: the parallel merge with waiting mergers
+    path = synth(cfg)
+    shape = qa.CONFIGS[cfg]
+    kvd = shape.kv_heads * shape.head_dim
+    rng = np.random.default_rng(11)
+    k = rng.standard_normal((shape.layers, T, kvd)).astype(np.float16)
+    v = rng.standard_normal((shape.layers, T, kvd)).astype(np.float16)
+    snap = kv_snapshot(k, v)
+    monkeypatch.setenv("QPH_ATTN_SPIN", "1")
+    bad = qa.HipLlama.load(path, max_ctx=T + 64)
+    monkeypatch.delenv("QPH_ATTN_SPIN")
+    bad.restore(snap)
+    with pytest.raises(qa.QphError, match="timed out"):
+        bad.step(5, 1)
+    with pytest.raises(qa.QphError, match="timed out"):
+        bad.greedy_run(5, 4)
+    bad.close()
+    good = qa.HipLlama.load(path, max_ctx=T + 64)
+    good.restore(snap)
+    orc = O.Oracle(path, max_ctx=T + 64)
+    ko, vo = orc.kv_cache()
+    ko[:, :T] = k.view(np.uint16); vo[:, :T] = v.view(np.uint16)
+    orc.set_pos(T)
+    err, ok = close(good.step(5, 1), orc.step(5, 1))
+    assert ok, err
+    good.close(); orc.close()
+
+
+def test_graph_replays_with_device_logits(synth):
+    """many back-to-back graph replays whose logits stay on the device (step_topk: want = 3, no host wait inside the
+    step), past two turns of the 256-slot control ring, each checked against step(tok, 1) on a twin model"""
+    path = synth("c1") if os.environ.get("QPH_TEST_C1") else synth("mini")
+    a = qa.HipLlama.load(path, max_ctx=700)
+    b = qa.HipLlama.load(path, max_ctx=700)
+    toks = np.arange(3, 35, dtype=np.int32) % a.vocab()
+    a.prefill(toks, 0); b.prefill(toks, 0)
+    print("step_topk x 600", flush=True)
+    for i in range(600):
+        t = (100 + 7 * i) % a.vocab()
+        M = 40 if i % 2 else 512
+        idx, val = a.step_topk(t, M)
+        lg = b.step(t, 1)
+        order = np.lexsort((np.arange(len(lg)), -lg.astype(np.float64)))[:M]
+        np.testing.assert_array_equal(idx, order)
+        np.testing.assert_array_equal(val, lg[order])
+    assert a.pos() == b.pos() == 32 + 600
+    a.close(); b.close()
