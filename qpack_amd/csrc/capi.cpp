@@ -67,19 +67,19 @@ int qph_load(const char *path, int max_ctx, qph_model **out) {
     need(path, "path"); need(out, "out");
     *out = nullptr;
     qph::Container c(path);
-    const qph::Json &j = c.config();
-    if (j["arch"].string() != "llama") throw std::runtime_error(std::string(path) + ": arch '" + j["arch"].string() + "' is not a Llama-family model");
+    const qph::JNode &j = c.config();
+    if (j.get("arch").text() != "llama") throw std::runtime_error(std::string(path) + ": arch '" + j.get("arch").text() + "' is not a Llama-family model");
     qph_config cfg{};
-    cfg.hidden = (int)j["hidden_size"].integer(0); cfg.layers = (int)j["num_hidden_layers"].integer(0);
-    cfg.heads = (int)j["num_attention_heads"].integer(0); cfg.kv_heads = (int)j["num_key_value_heads"].integer(0);
-    cfg.head_dim = (int)j["head_dim"].integer(cfg.heads > 0 ? cfg.hidden / cfg.heads : 0);
-    cfg.ffn = (int)j["intermediate_size"].integer(0); cfg.vocab = (int)j["vocab_size"].integer(0);
-    cfg.rms_eps = (float)j["rms_norm_eps"].number(1e-6); cfg.rope_theta = j["rope_theta"].number(10000);
-    cfg.tied = j["tie_embeddings"].boolean(false) ? 1 : 0;
-    cfg.max_pos = (int)j["max_position_embeddings"].integer(1 << 20);
+    cfg.hidden = (int)j.get("hidden_size").int_or(0); cfg.layers = (int)j.get("num_hidden_layers").int_or(0);
+    cfg.heads = (int)j.get("num_attention_heads").int_or(0); cfg.kv_heads = (int)j.get("num_key_value_heads").int_or(0);
+    cfg.head_dim = (int)j.get("head_dim").int_or(cfg.heads > 0 ? cfg.hidden / cfg.heads : 0);
+    cfg.ffn = (int)j.get("intermediate_size").int_or(0); cfg.vocab = (int)j.get("vocab_size").int_or(0);
+    cfg.rms_eps = (float)j.get("rms_norm_eps").num_or(1e-6); cfg.rope_theta = j.get("rope_theta").num_or(10000);
+    cfg.tied = j.get("tie_embeddings").bool_or(false) ? 1 : 0;
+    cfg.max_pos = (int)j.get("max_position_embeddings").int_or(1 << 20);
     std::vector<qph_tensor> ts;
-    for (const qph::Json &e : c.manifest()["tensors"].arr) {
-      const qph::TensorView &t = c.at(e["name"].string());
+    for (const qph::JNode &e : c.manifest().get("tensors").items()) {
+      const qph::TensorView &t = c.at(e.get("name").text());
       if (t.kind == qph::Kind::F16) continue;   // 2-D f16 matrices are not on the HIP path; a required one is reported missing
       qph_tensor q{}; q.name = t.name.c_str(); q.data = t.data; q.scale = t.scale;
       if (t.shape.size() == 1) { q.rows = t.shape[0]; q.cols = 1; } else { q.rows = t.rows(); q.cols = t.cols(); }

@@ -45,8 +45,8 @@ class Container {
   Container(const Container &) = delete;
   Container &operator=(const Container &) = delete;
   int version() const { return version_; }
-  const Json &config() const { return config_; }
-  const Json &manifest() const { return manifest_; }
+  const JNode &config() const { return config_; }
+  const JNode &manifest() const { return manifest_; }
   bool has_blob(const std::string &n) const { return toc_.count(n) > 0; }
   bool is_coded(const std::string &n) const { return coded_.count(n) > 0; }
   std::vector<std::string> blob_names() const;                    // in file order
@@ -62,7 +62,7 @@ class Container {
   int version_ = 0;
   std::map<std::string, std::pair<uint64_t, uint64_t>> toc_;
   std::map<std::string, bool> coded_;
-  Json manifest_, config_;
+  JNode manifest_, config_;
   std::map<std::string, TensorView> tensors_;
   std::vector<std::vector<float>> widened_;   // storage of 1-D f16 tensors converted to f32
 };

@@ -1,160 +1,246 @@
 #include "json.hpp"
 
-#include <algorithm>
 #include <cmath>
-#include <cstdlib>
 #include <cstdio>
+#include <cstdlib>
 #include <stdexcept>
 
 namespace qph {
 
-static const Json kNullJson;
-static const std::string kEmptyStr;
-
-const Json *Json::find(const std::string &k) const {
-  if (type != Obj) return nullptr;
-  for (auto &kv : obj) if (kv.first == k) return &kv.second;
-  return nullptr;
-}
-const Json &Json::operator[](const std::string &k) const { const Json *j = find(k); return j ? *j : kNullJson; }
-Json &Json::set(const std::string &k, Json v) {
-  if (type != Obj) { type = Obj; obj.clear(); }
-  for (auto &kv : obj) if (kv.first == k) { kv.second = std::move(v); return kv.second; }
-  obj.emplace_back(k, std::move(v));
-  return obj.back().second;
-}
-const std::string &Json::string() const { return type == Str ? str : kEmptyStr; }
-
 namespace {
-class Parser {
+
+const JNode kNullNode;
+const JNode::List kNoItems;
+const std::string kNoText;
+
+// recursive-descent reader over [p, end); depth-limited so hostile input cannot exhaust the stack
+class Reader {
  public:
-  Parser(const char *p, size_t n) : p_(p), e_(p + n) {}
-  Json document() {
-    Json v = value(0); ws();
-    if (p_ != e_) fail("trailing characters");
+  Reader(const char *p, size_t n) : begin_(p), p_(p), end_(p + n) {}
+
+  JNode document() {
+    JNode v = value(0);
+    blank();
+    if (p_ != end_) fail("text after the document");
     return v;
   }
 
  private:
-  const char *p_, *e_;
-  [[noreturn]] void fail(const char *what) { throw std::runtime_error(std::string("json: ") + what); }
-  void ws() { while (p_ < e_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) p_++; }
-  bool eat(char c) { ws(); if (p_ < e_ && *p_ == c) { p_++; return true; } return false; }
-  void expect(char c) { if (!eat(c)) fail("unexpected character"); }
+  const char *begin_, *p_, *end_;
+
+  [[noreturn]] void fail(const char *what) const {
+    throw std::runtime_error(std::string("JSON: ") + what + " at offset " + std::to_string(p_ - begin_));
+  }
+  void blank() { while (p_ < end_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) p_++; }
+  bool eat(char c) { blank(); if (p_ < end_ && *p_ == c) { p_++; return true; } return false; }
+  void expect(char c, const char *what) { if (!eat(c)) fail(what); }
   bool word(const char *w) {
-    const char *q = p_; for (; *w; w++, q++) if (q >= e_ || *q != *w) return false;
-    p_ = q; return true;
+    size_t n = 0;
+    while (w[n]) n++;
+    if ((size_t)(end_ - p_) < n) return false;
+    for (size_t i = 0; i < n; i++) if (p_[i] != w[i]) return false;
+    p_ += n;
+    return true;
   }
-  static void utf8(std::string &out, uint32_t cp) {
-    if (cp < 0x80) out += (char)cp;
-    else if (cp < 0x800) { out += (char)(0xC0 | (cp >> 6)); out += (char)(0x80 | (cp & 63)); }
-    else if (cp < 0x10000) { out += (char)(0xE0 | (cp >> 12)); out += (char)(0x80 | ((cp >> 6) & 63)); out += (char)(0x80 | (cp & 63)); }
-    else { out += (char)(0xF0 | (cp >> 18)); out += (char)(0x80 | ((cp >> 12) & 63)); out += (char)(0x80 | ((cp >> 6) & 63)); out += (char)(0x80 | (cp & 63)); }
+
+  JNode value(int depth) {
+    if (depth > 64) fail("nesting too deep");
+    blank();
+    if (p_ >= end_) fail("unexpected end of text");
+    switch (*p_) {
+      case '{': return fields(depth);
+      case '[': return list(depth);
+      case '"': return JNode(text());
+      case 't': if (word("true")) return JNode(true); break;
+      case 'f': if (word("false")) return JNode(false); break;
+      case 'n': if (word("null")) return JNode(); break;
+      default: return JNode(number());
+    }
+    fail("unknown literal");
   }
-  uint32_t hex4() {
-    if (e_ - p_ < 4) fail("short \\u escape");
-    uint32_t v = 0;
-    for (int i = 0; i < 4; i++) {
-      const char c = *p_++; v <<= 4;
-      if (c >= '0' && c <= '9') v |= (uint32_t)(c - '0');
-      else if (c >= 'a' && c <= 'f') v |= (uint32_t)(c - 'a' + 10);
-      else if (c >= 'A' && c <= 'F') v |= (uint32_t)(c - 'A' + 10);
-      else fail("bad \\u escape");
+
+  JNode fields(int depth) {
+    p_++;   // '{'
+    JNode::Fields f;
+    if (eat('}')) return JNode(std::move(f));
+    do {
+      blank();
+      if (p_ >= end_ || *p_ != '"') fail("expected a member name");
+      std::string k = text();
+      expect(':', "expected ':' after a member name");
+      f.emplace_back(std::move(k), value(depth + 1));
+    } while (eat(','));
+    expect('}', "expected ',' or '}' in an object");
+    return JNode(std::move(f));
+  }
+
+  JNode list(int depth) {
+    p_++;   // '['
+    JNode::List l;
+    if (eat(']')) return JNode(std::move(l));
+    do l.push_back(value(depth + 1));
+    while (eat(','));
+    expect(']', "expected ',' or ']' in an array");
+    return JNode(std::move(l));
+  }
+
+  double number() {
+    // the JSON number grammar, checked here; the conversion itself is strtod's (locale "C" digits only)
+    const char *s = p_;
+    if (p_ < end_ && *p_ == '-') p_++;
+    auto digits = [&] { const char *d = p_; while (p_ < end_ && *p_ >= '0' && *p_ <= '9') p_++; return p_ > d; };
+    if (!digits()) fail("malformed number");
+    if (p_ < end_ && *p_ == '.') { p_++; if (!digits()) fail("malformed number"); }
+    if (p_ < end_ && (*p_ == 'e' || *p_ == 'E')) {
+      p_++;
+      if (p_ < end_ && (*p_ == '+' || *p_ == '-')) p_++;
+      if (!digits()) fail("malformed number");
+    }
+    return std::strtod(std::string(s, p_).c_str(), nullptr);
+  }
+
+  unsigned hex4() {
+    if (end_ - p_ < 4) fail("short \\u escape");
+    unsigned v = 0;
+    for (int i = 0; i < 4; i++, p_++) {
+      const char c = *p_;
+      const unsigned d = c >= '0' && c <= '9' ? c - '0' : c >= 'a' && c <= 'f' ? c - 'a' + 10 : c >= 'A' && c <= 'F' ? c - 'A' + 10 : 99;
+      if (d > 15) fail("bad hex digit in \\u escape");
+      v = v * 16 + d;
     }
     return v;
   }
+
+  static void put_utf8(std::string &s, unsigned cp) {
+    if (cp < 0x80) { s += (char)cp; return; }
+    if (cp < 0x800) { s += (char)(0xc0 | cp >> 6); s += (char)(0x80 | (cp & 0x3f)); return; }
+    if (cp < 0x10000) { s += (char)(0xe0 | cp >> 12); s += (char)(0x80 | ((cp >> 6) & 0x3f)); s += (char)(0x80 | (cp & 0x3f)); return; }
+    s += (char)(0xf0 | cp >> 18); s += (char)(0x80 | ((cp >> 12) & 0x3f));
+    s += (char)(0x80 | ((cp >> 6) & 0x3f)); s += (char)(0x80 | (cp & 0x3f));
+  }
+
   std::string text() {
+    p_++;   // opening quote
     std::string s;
-    for (;;) {
-      if (p_ >= e_) fail("unterminated string");
+    while (true) {
+      if (p_ >= end_) fail("unterminated string");
       const char c = *p_++;
       if (c == '"') return s;
+      if ((unsigned char)c < 0x20) fail("control character in a string");
       if (c != '\\') { s += c; continue; }
-      if (p_ >= e_) fail("bad escape");
-      const char x = *p_++;
-      switch (x) {
-        case '"': s += '"'; break;
-        case '\\': s += '\\'; break;
-        case '/': s += '/'; break;
+      if (p_ >= end_) fail("unterminated escape");
+      const char e = *p_++;
+      switch (e) {
+        case '"': case '\\': case '/': s += e; break;
         case 'b': s += '\b'; break;
         case 'f': s += '\f'; break;
         case 'n': s += '\n'; break;
         case 'r': s += '\r'; break;
         case 't': s += '\t'; break;
         case 'u': {
-          uint32_t cp = hex4();
-          if (cp >= 0xD800 && cp < 0xDC00 && e_ - p_ >= 6 && p_[0] == '\\' && p_[1] == 'u') {
-            p_ += 2; const uint32_t lo = hex4(); cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+          unsigned cp = hex4();
+          if (cp >= 0xd800 && cp < 0xdc00) {   // a high surrogate must pair with a low one
+            if (!word("\\u")) fail("unpaired surrogate");
+            const unsigned lo = hex4();
+            if (lo < 0xdc00 || lo >= 0xe000) fail("unpaired surrogate");
+            cp = 0x10000 + ((cp - 0xd800) << 10 | (lo - 0xdc00));
           }
-          utf8(s, cp); break;
+          put_utf8(s, cp);
+          break;
         }
-        default: fail("bad escape");
+        default: fail("unknown escape");
       }
     }
-  }
-  Json value(int depth) {
-    if (depth > 64) fail("nesting too deep");
-    ws();
-    if (p_ >= e_) fail("unexpected end");
-    const char c = *p_;
-    if (c == '{') {
-      p_++; Json o = Json::object();
-      if (eat('}')) return o;
-      do { ws(); expect('"'); std::string k = text(); expect(':'); o.obj.emplace_back(std::move(k), value(depth + 1)); } while (eat(','));
-      expect('}'); return o;
-    }
-    if (c == '[') {
-      p_++; Json a = Json::array();
-      if (eat(']')) return a;
-      do a.arr.push_back(value(depth + 1)); while (eat(','));
-      expect(']'); return a;
-    }
-    if (c == '"') { p_++; return Json(text()); }
-    if (word("true")) return Json(true);
-    if (word("false")) return Json(false);
-    if (word("null")) return Json();
-    char *end = nullptr; const std::string tok(p_, (size_t)std::min<ptrdiff_t>(e_ - p_, 64));
-    const double v = strtod(tok.c_str(), &end);
-    if (end == tok.c_str()) fail("bad value");
-    p_ += end - tok.c_str();
-    return Json(v);
   }
 };
 
-void dump_to(const Json &j, std::string &o) {
-  switch (j.type) {
-    case Json::Null: o += "null"; break;
-    case Json::Bool: o += j.b ? "true" : "false"; break;
-    case Json::Num: {
-      char buf[40];
-      if (std::isfinite(j.num) && j.num == std::floor(j.num) && std::fabs(j.num) < 9e15) snprintf(buf, sizeof buf, "%lld", (long long)j.num);
-      else snprintf(buf, sizeof buf, "%.17g", j.num);
-      o += buf; break;
+void write_text(std::string &out, const std::string &s) {
+  out += '"';
+  for (const char c : s) {
+    switch (c) {
+      case '"': out += "\\\""; break;
+      case '\\': out += "\\\\"; break;
+      case '\n': out += "\\n"; break;
+      case '\r': out += "\\r"; break;
+      case '\t': out += "\\t"; break;
+      default:
+        if ((unsigned char)c < 0x20) { char b[8]; snprintf(b, sizeof b, "\\u%04x", (unsigned)(unsigned char)c); out += b; }
+        else out += c;
     }
-    case Json::Str:
-      o += '"';
-      for (unsigned char ch : j.str) {
-        if (ch == '"') o += "\\\""; else if (ch == '\\') o += "\\\\"; else if (ch == '\n') o += "\\n";
-        else if (ch < 0x20) { char b[8]; snprintf(b, sizeof b, "\\u%04x", ch); o += b; }
-        else o += (char)ch;
-      }
-      o += '"'; break;
-    case Json::Arr:
-      o += '[';
-      for (size_t i = 0; i < j.arr.size(); i++) { if (i) o += ','; dump_to(j.arr[i], o); }
-      o += ']'; break;
-    case Json::Obj:
-      o += '{';
-      for (size_t i = 0; i < j.obj.size(); i++) {
-        if (i) o += ',';
-        dump_to(Json(j.obj[i].first), o); o += ':'; dump_to(j.obj[i].second, o);
-      }
-      o += '}'; break;
   }
+  out += '"';
 }
+
+void write_number(std::string &out, double v) {
+  char b[40];
+  if (!std::isfinite(v)) { out += "null"; return; }   // JSON has no inf / nan
+  if (v == std::floor(v) && std::fabs(v) < 9007199254740992.0) snprintf(b, sizeof b, "%.0f", v);
+  else snprintf(b, sizeof b, "%.17g", v);   // round-trips every double
+  out += b;
+}
+
 }  // namespace
 
-Json Json::parse(const char *p, size_t n) { return Parser(p, n).document(); }
-std::string Json::dump() const { std::string o; dump_to(*this, o); return o; }
+const JNode *JNode::find(std::string_view key) const {
+  const Fields *f = std::get_if<Fields>(&v_);
+  if (!f) return nullptr;
+  for (const auto &kv : *f) if (kv.first == key) return &kv.second;
+  return nullptr;
+}
+const JNode &JNode::get(std::string_view key) const { const JNode *n = find(key); return n ? *n : kNullNode; }
+const JNode::List &JNode::items() const { const List *l = std::get_if<List>(&v_); return l ? *l : kNoItems; }
+size_t JNode::size() const {
+  if (const List *l = std::get_if<List>(&v_)) return l->size();
+  if (const Fields *f = std::get_if<Fields>(&v_)) return f->size();
+  return 0;
+}
+const std::string &JNode::text() const { const std::string *s = std::get_if<std::string>(&v_); return s ? *s : kNoText; }
+
+JNode &JNode::put(std::string key, JNode v) {
+  if (is_null()) v_ = Fields{};
+  Fields *f = std::get_if<Fields>(&v_);
+  if (!f) throw std::runtime_error("JSON: put on a node that is not an object");
+  for (auto &kv : *f)
+    if (kv.first == key) { kv.second = std::move(v); return kv.second; }
+  f->emplace_back(std::move(key), std::move(v));
+  return f->back().second;
+}
+JNode &JNode::append(JNode v) {
+  if (is_null()) v_ = List{};
+  List *l = std::get_if<List>(&v_);
+  if (!l) throw std::runtime_error("JSON: append on a node that is not an array");
+  l->push_back(std::move(v));
+  return l->back();
+}
+
+void JNode::write_to(std::string &out) const {
+  switch (v_.index()) {
+    case 0: out += "null"; break;
+    case 1: out += std::get<bool>(v_) ? "true" : "false"; break;
+    case 2: write_number(out, std::get<double>(v_)); break;
+    case 3: write_text(out, std::get<std::string>(v_)); break;
+    case 4: {
+      out += '[';
+      bool first = true;
+      for (const JNode &n : std::get<List>(v_)) { if (!first) out += ','; first = false; n.write_to(out); }
+      out += ']';
+      break;
+    }
+    default: {
+      out += '{';
+      bool first = true;
+      for (const auto &kv : std::get<Fields>(v_)) {
+        if (!first) out += ',';
+        first = false;
+        write_text(out, kv.first);
+        out += ':';
+        kv.second.write_to(out);
+      }
+      out += '}';
+    }
+  }
+}
+std::string JNode::serialize() const { std::string s; write_to(s); return s; }
+JNode JNode::read(const char *text, size_t n) { return Reader(text, n).document(); }
 
 }  // namespace qph

@@ -1,43 +1,62 @@
-// Minimal JSON value for QPACK manifests and model configs (manifest.json / config.json blobs).
-// Objects keep insertion order so a written manifest reads back in the same order.
+// JNode: a JSON document tree for the two small text blobs of a QPACK container (config.json, manifest.json) and for
+// the manifests this library writes (synthetic models, QPACK3 packing).
+//
+// One std::variant holds the node: null, bool, number (double), text, list, or fields.  Fields are a vector of
+// (key, node) pairs rather than a map because a written manifest must list its members, and its tensors, in the order
+// they were added.  Lookups on the wrong kind of node return neutral values (a null node, an empty list, the caller's
+// default), so reading optional config keys needs no checks; malformed text throws std::runtime_error from read().
 #pragma once
 #include <cstdint>
 #include <string>
+#include <string_view>
 #include <utility>
+#include <variant>
 #include <vector>
 
 namespace qph {
 
-struct Json {
-  enum Type { Null, Bool, Num, Str, Arr, Obj } type = Null;
-  bool b = false;
-  double num = 0;
-  std::string str;
-  std::vector<Json> arr;
-  std::vector<std::pair<std::string, Json>> obj;
+class JNode {
+ public:
+  using List = std::vector<JNode>;
+  using Fields = std::vector<std::pair<std::string, JNode>>;
 
-  Json() = default;
-  Json(bool v) : type(Bool), b(v) {}
-  Json(int v) : type(Num), num(v) {}
-  Json(int64_t v) : type(Num), num((double)v) {}
-  Json(double v) : type(Num), num(v) {}
-  Json(const char *s) : type(Str), str(s) {}
-  Json(std::string s) : type(Str), str(std::move(s)) {}
-  static Json array() { Json j; j.type = Arr; return j; }
-  static Json object() { Json j; j.type = Obj; return j; }
+  JNode() = default;
+  JNode(bool v) : v_(v) {}
+  JNode(int v) : v_((double)v) {}
+  JNode(int64_t v) : v_((double)v) {}
+  JNode(uint64_t v) : v_((double)v) {}
+  JNode(double v) : v_(v) {}
+  JNode(const char *s) : v_(std::string(s)) {}
+  JNode(std::string s) : v_(std::move(s)) {}
+  JNode(List l) : v_(std::move(l)) {}
+  JNode(Fields f) : v_(std::move(f)) {}
 
-  const Json *find(const std::string &k) const;
-  const Json &operator[](const std::string &k) const;   // a Null value when absent
-  Json &set(const std::string &k, Json v);
-  void push(Json v) { type = Arr; arr.push_back(std::move(v)); }
+  bool is_null() const { return v_.index() == 0; }
+  bool is_list() const { return std::holds_alternative<List>(v_); }
+  bool is_fields() const { return std::holds_alternative<Fields>(v_); }
 
-  double number(double def) const { return type == Num ? num : def; }
-  int64_t integer(int64_t def) const { return type == Num ? (int64_t)num : def; }
-  bool boolean(bool def) const { return type == Bool ? b : def; }
-  const std::string &string() const;
+  // member `key` of an object node: nullptr (find) or a null node (get) when absent
+  const JNode *find(std::string_view key) const;
+  const JNode &get(std::string_view key) const;
+  // elements of a list node (an empty list for any other node)
+  const List &items() const;
+  size_t size() const;
 
-  static Json parse(const char *p, size_t n);   // throws std::runtime_error on malformed input
-  std::string dump() const;
+  double num_or(double def) const { const double *d = std::get_if<double>(&v_); return d ? *d : def; }
+  int64_t int_or(int64_t def) const { const double *d = std::get_if<double>(&v_); return d ? (int64_t)*d : def; }
+  bool bool_or(bool def) const { const bool *b = std::get_if<bool>(&v_); return b ? *b : def; }
+  const std::string &text() const;   // an empty string for a non-text node
+
+  // builders: put replaces an existing member or appends one (a null node becomes an object); append adds a list element
+  JNode &put(std::string key, JNode v);
+  JNode &append(JNode v);
+
+  std::string serialize() const;
+  static JNode read(const char *text, size_t n);
+
+ private:
+  std::variant<std::monostate, bool, double, std::string, List, Fields> v_;
+  void write_to(std::string &out) const;
 };
 
 }  // namespace qph

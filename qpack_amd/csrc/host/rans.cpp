@@ -148,12 +148,12 @@ int pack(const std::string &src_path, const std::string &dst_path, int threads) 
   if (src.version() != 2) throw std::runtime_error(src_path + ": pack needs a QPACK2 file");
   struct Plan { int codec, planes; };
   std::map<std::string, Plan> plan;   // qpack-pack's classes, all selected (tools/qpack-pack.cpp:43-53)
-  for (const Json &e : src.manifest()["tensors"].arr) {
-    const std::string &k = e["kind"].string(), &b = e["blob"].string();
-    if (k == "q4") { plan[b] = {2, 1}; plan[e["scale"].string()] = {1, 2}; }
+  for (const JNode &e : src.manifest().get("tensors").items()) {
+    const std::string &k = e.get("kind").text(), &b = e.get("blob").text();
+    if (k == "q4") { plan[b] = {2, 1}; plan[e.get("scale").text()] = {1, 2}; }
     else if (k == "q8") plan[b] = {1, 1};
-    else if (k == "mxfp4") { plan[b] = {1, 1}; plan[e["scale"].string()] = {1, 1}; }
-    else if (k == "q1" || k == "q8g") { plan[b] = {1, 1}; plan[e["scale"].string()] = {1, 2}; }
+    else if (k == "mxfp4") { plan[b] = {1, 1}; plan[e.get("scale").text()] = {1, 1}; }
+    else if (k == "q1" || k == "q8g") { plan[b] = {1, 1}; plan[e.get("scale").text()] = {1, 2}; }
     else if (k == "f16") plan[b] = {1, 2};
     else if (k == "f32") plan[b] = {1, 4};
   }
@@ -186,7 +186,7 @@ int pack(const std::string &src_path, const std::string &dst_path, int threads) 
   for (auto &x : th) x.join();
   for (auto &e : errs) if (!e.empty()) throw std::runtime_error("pack: " + e);
   std::vector<std::vector<uint8_t>> coded(names.size());
-  Json enc = Json::array();
+  JNode enc = JNode(JNode::List{});
   for (size_t i = 0; i < names.size(); i++) {
     if (range[i].first == range[i].second) continue;
     size_t len; src.blob(names[i], &len);
@@ -198,12 +198,12 @@ int pack(const std::string &src_path, const std::string &dst_path, int threads) 
     } else {
       c = std::move(jobs[range[i].first].out);
     }
-    if (c.size() < len) { coded[i] = std::move(c); enc.push(Json(names[i])); }   // blobs that do not shrink stay raw
+    if (c.size() < len) { coded[i] = std::move(c); enc.append(JNode(names[i])); }   // blobs that do not shrink stay raw
   }
-  Json man = src.manifest();
-  man.set("encoded", enc);
-  man.set("format", "QPACK3");
-  const std::string mtext = man.dump();
+  JNode man = src.manifest();
+  man.put("encoded", enc);
+  man.put("format", "QPACK3");
+  const std::string mtext = man.serialize();
   std::vector<std::pair<std::string, uint64_t>> layout;
   for (size_t i = 0; i < names.size(); i++) {
     size_t len; src.blob(names[i], &len);
@@ -217,7 +217,7 @@ int pack(const std::string &src_path, const std::string &dst_path, int threads) 
     else w.write(names[i], p, len);
   }
   w.close();
-  return (int)enc.arr.size();
+  return (int)enc.size();
 }
 
 }  // namespace rans

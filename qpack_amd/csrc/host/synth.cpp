@@ -107,37 +107,42 @@ void synth_write(const SynthSpec &s, const std::string &path, int threads) {
   for (auto &t : ts) if (t.q == Q::Q4 && t.shape[1] % 32) throw std::runtime_error("synth: q4 tensor " + t.name + " needs cols % 32 == 0");
   for (auto &t : ts) if (t.q == Q::Q1 && t.shape[1] % 128) throw std::runtime_error("synth: q1 tensor " + t.name + " needs cols % 128 == 0");
 
-  Json man = Json::object(), tl = Json::array();
+  JNode man = JNode(JNode::Fields{}), tl = JNode(JNode::List{});
   std::vector<std::pair<std::string, uint64_t>> plan;
   for (size_t k = 0; k < ts.size(); k++) {
     const Plan &t = ts[k]; char bid[16]; snprintf(bid, sizeof bid, "w%04zu", k);
-    Json e = Json::object(); e.set("name", t.name);
-    Json sh = Json::array(); for (auto v : t.shape) sh.push(Json(v)); e.set("shape", sh); e.set("dtype", "float32");
+    JNode e = JNode(JNode::Fields{}); e.put("name", t.name);
+    JNode sh = JNode(JNode::List{}); for (auto v : t.shape) sh.append(JNode((int64_t)v)); e.put("shape", sh); e.put("dtype", "float32");
     const int64_t rows = t.shape[0], cols = t.shape.size() > 1 ? t.shape[1] : 1;
-    if (t.q == Q::F32) { e.set("kind", "f32"); e.set("blob", std::string(bid) + ".f32"); plan.push_back({std::string(bid) + ".f32", 4ull * rows * cols}); }
+    if (t.q == Q::F32) { e.put("kind", "f32"); e.put("blob", std::string(bid) + ".f32"); plan.push_back({std::string(bid) + ".f32", 4ull * rows * cols}); }
     else if (t.q == Q::Q8) {
-      e.set("kind", "q8"); e.set("blob", std::string(bid) + ".q8"); e.set("scale", std::string(bid) + ".scale");
+      e.put("kind", "q8"); e.put("blob", std::string(bid) + ".q8"); e.put("scale", std::string(bid) + ".scale");
       plan.push_back({std::string(bid) + ".q8", (uint64_t)(rows * cols)}); plan.push_back({std::string(bid) + ".scale", 4ull * rows});
     } else if (t.q == Q::Q1) {
-      e.set("kind", "q1"); e.set("blob", std::string(bid) + ".q1"); e.set("scale", std::string(bid) + ".scale"); e.set("group", 128);
+      e.put("kind", "q1"); e.put("blob", std::string(bid) + ".q1"); e.put("scale", std::string(bid) + ".scale"); e.put("group", 128);
       plan.push_back({std::string(bid) + ".q1", (uint64_t)(rows * cols / 8)}); plan.push_back({std::string(bid) + ".scale", 2ull * rows * (cols / 128)});
     } else {
-      e.set("kind", "q4"); e.set("blob", std::string(bid) + ".q4"); e.set("scale", std::string(bid) + ".scale"); e.set("group", 32);
+      e.put("kind", "q4"); e.put("blob", std::string(bid) + ".q4"); e.put("scale", std::string(bid) + ".scale"); e.put("group", 32);
       plan.push_back({std::string(bid) + ".q4", (uint64_t)(rows * cols / 2)}); plan.push_back({std::string(bid) + ".scale", 2ull * rows * (cols / 32)});
     }
-    tl.push(e);
+    tl.append(e);
   }
-  man.set("format", "QPACK2");
-  man.set("quant", s.mlp_q1 ? (s.more_bits ? "q1m" : "q1") : s.q4 ? (s.q4m_alt || s.more_bits ? "q4m" : "q4") : "q8");
-  man.set("tensors", tl);
-  man.set("synthetic", Json::object()); man.obj.back().second.set("seed", Json((int64_t)s.seed)); man.obj.back().second.set("std", Json((double)s.std));
-  Json cfg = Json::object();
-  cfg.set("arch", "llama"); cfg.set("model_type", s.model_type[0] ? s.model_type : "llama");
-  cfg.set("hidden_size", Json(d)); cfg.set("num_hidden_layers", s.layers); cfg.set("num_attention_heads", s.heads);
-  cfg.set("num_key_value_heads", s.kv_heads); cfg.set("head_dim", s.head_dim); cfg.set("intermediate_size", Json(ff));
-  cfg.set("vocab_size", Json(V)); cfg.set("rope_theta", s.rope_theta); cfg.set("max_position_embeddings", s.max_pos);
-  cfg.set("rms_norm_eps", (double)s.rms_eps); cfg.set("tie_embeddings", (bool)s.tied); cfg.set("qkv_bias", (bool)s.qkv_bias);
-  const std::string mj = man.dump(), cj = cfg.dump();
+  man.put("format", "QPACK2");
+  man.put("quant", s.mlp_q1 ? (s.more_bits ? "q1m" : "q1") : s.q4 ? (s.q4m_alt || s.more_bits ? "q4m" : "q4") : "q8");
+  man.put("tensors", tl);
+  {
+    JNode syn = JNode(JNode::Fields{});
+    syn.put("seed", JNode((int64_t)s.seed));
+    syn.put("std", JNode((double)s.std));
+    man.put("synthetic", syn);
+  }
+  JNode cfg = JNode(JNode::Fields{});
+  cfg.put("arch", "llama"); cfg.put("model_type", s.model_type[0] ? s.model_type : "llama");
+  cfg.put("hidden_size", JNode(d)); cfg.put("num_hidden_layers", s.layers); cfg.put("num_attention_heads", s.heads);
+  cfg.put("num_key_value_heads", s.kv_heads); cfg.put("head_dim", s.head_dim); cfg.put("intermediate_size", JNode(ff));
+  cfg.put("vocab_size", JNode(V)); cfg.put("rope_theta", s.rope_theta); cfg.put("max_position_embeddings", s.max_pos);
+  cfg.put("rms_norm_eps", (double)s.rms_eps); cfg.put("tie_embeddings", (bool)s.tied); cfg.put("qkv_bias", (bool)s.qkv_bias);
+  const std::string mj = man.serialize(), cj = cfg.serialize();
   plan.insert(plan.begin(), {"config.json", cj.size()});
   plan.insert(plan.begin(), {"manifest.json", mj.size()});
 

@@ -43,10 +43,10 @@ def test_errors_without_gpu():
 def test_bad_container_is_rejected(tmp_path):
     p = tmp_path / "bad.qpack"
     p.write_bytes(b"NOTQPACK" + b"\0" * 64)
-    with pytest.raises(qa.QphError, match="not a QPACK"):
+    with pytest.raises(qa.QphError, match="not a QPACK container"):
         qa.HipLlama.load(str(p))
     p.write_bytes(b"QPACK2\0\0" + np.uint32(1).tobytes() + b"\0" * 4 + b"x" * 56 + np.uint64(10 ** 9).tobytes() * 2)
-    with pytest.raises(qa.QphError, match="corrupt table of contents"):
+    with pytest.raises(qa.QphError, match="table of contents points outside the file"):
         qa.HipLlama.load(str(p))
 
 
@@ -125,3 +125,37 @@ def test_synthetic_policies_match_qpack_quantize(name, args, tmp_path):
     qa.write_synthetic(name, mine, seed=3)
     kinds = lambda p: {e["name"]: (e["kind"], e.get("group")) for e in O.QpackFile(p).manifest["tensors"]}   # noqa: E731
     assert kinds(mine) == kinds(out)
+
+
+def _container(path, blobs, magic=b"QPACK2\0\0"):
+    """a QPACK container written from Python (16-byte header, 72-byte entries, 64-byte aligned blobs)"""
+    n = len(blobs)
+    at = (16 + 72 * n + 63) // 64 * 64
+    head, body, offs = bytearray(magic + np.uint32(n).tobytes() + b"\0" * 4), bytearray(), []
+    for name, data in blobs:
+        offs.append(at)
+        head += name.encode().ljust(56, b"\0") + np.uint64(at).tobytes() + np.uint64(len(data)).tobytes()
+        at = (at + len(data) + 63) // 64 * 64
+    out = bytearray(head)
+    for (name, data), o in zip(blobs, offs):
+        out += b"\0" * (o - len(out)) + data
+    open(path, "wb").write(bytes(out))
+
+
+def test_config_json_reader(tmp_path):
+    """the container's JSON reader on hand-written text: whitespace, escapes (\\u0061 -> 'a', a surrogate pair),
+    exponents and nesting parse (arch decodes to "llama", so the load reaches the shape checks); malformed text is reported with
+    its offset"""
+    cfg = (b'{ "arch" : "llam\\u0061", "note": "\\ud83d\\ude00 \\"q\\"\\n", "hidden_size": 8.96e2, "nested": {"a": [1, -2.5e-3, '
+           b'true, false, null, {}]}, "num_hidden_layers": 1 }')
+    man = b'{"format": "QPACK2", "tensors": []}'
+    p = str(tmp_path / "m.qpack")
+    _container(p, [("manifest.json", man), ("config.json", cfg)])
+    with pytest.raises(qa.QphError, match="bad model config"):
+        qa.HipLlama.load(p)
+    _container(p, [("manifest.json", man), ("config.json", b'{"arch": "llama", "x": [1, 2,]}')])
+    with pytest.raises(qa.QphError, match=r"JSON: .* at offset 29"):
+        qa.HipLlama.load(p)
+    _container(p, [("manifest.json", man), ("config.json", b'{"arch": "lfm2"}')])
+    with pytest.raises(qa.QphError, match="not a Llama-family model"):
+        qa.HipLlama.load(p)
