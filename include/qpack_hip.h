@@ -151,6 +151,12 @@ int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int 
 int qph_kernel_matmul_ref(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y);
 /* The top-M selection of qph_step_topk on a host vector x[n] (parity hook; 1 <= M <= min(512, n)). */
 int qph_kernel_topk(const float *x, int n, int M, int *idx, float *val);
+/* No counterpart in the reference.  For callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the top-M of qph_kernel_topk on DEVICE buffers x[n] -> idx[M] / val[M],
+ * enqueued on `stream` (a hipStream_t; NULL = the null stream) and not waited for.  Allocates nothing: its scratch keys
+ * live in a fixed 512 KiB device array per GPU (hence n <= 262144; larger n is an error).  Calls that overlap on one
+ * GPU share that array and race. */
+int qph_topk_noalloc(const float *x, int n, int M, int *idx, float *val, void *stream);
 /* rans::decode (/root/reference/include/qpack/rans.h:101-113) of one plain or chunked blob on the GPU: blob[len] (host)
  * -> out[cap] (host, at least the blob's raw length, which *raw receives).  Errors carry the reference's messages
  * (truncated / bad frequency table / unknown codec / stream overrun).  *ms (optional) = the decode kernel's HIP-event

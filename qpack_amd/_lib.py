@@ -77,6 +77,7 @@ SIGNATURES = {
     "qph_kernel_matmul": (_I, [_I, _P, _P, _I, _I, _FP, _I, _FP]),
     "qph_kernel_matmul_ref": (_I, [_I, _P, _P, _I, _I, _FP, _I, _FP]),
     "qph_kernel_topk": (_I, [_FP, _I, _I, _IP, _FP]),
+    "qph_topk_noalloc": (_I, [_P, _I, _I, _P, _P, _P]),
     "qph_synth_write": (_I, [C.POINTER(SynthSpecC), C.c_char_p, _I]),
     "qph_load_stats_of": (_I, [C.c_void_p, C.POINTER(LoadStatsC)]),
     "qph_kernel_rans_decode": (_I, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.POINTER(C.c_int64), _FP]),

@@ -249,6 +249,14 @@ int qph_kernel_topk(const float *x, int n, int M, int *idx, float *val) {
     for (void *p : bufs) (void)hipFree(p);
   });
 }
+int qph_topk_noalloc(const float *x, int n, int M, int *idx, float *val, void *stream) {
+  QPH_API_TRY({
+    need(x, "x"); need(idx, "idx"); need(val, "val");
+    if (n <= 0 || n > 262144) throw std::invalid_argument("topk_noalloc: n must be in [1, 262144] (the size of its fixed device buffers)");
+    if (M < 1 || M > qph::kTopkMax || M > n) throw std::invalid_argument("topk_noalloc: 1 <= M <= min(512, n) required");
+    hck(qph::launch_topk_noalloc(x, n, M, idx, val, (hipStream_t)stream), "launch topk");
+  });
+}
 int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y) {
   QPH_API_TRY({
     need(q, "q"); need(scale, "scale"); need(X, "X"); need(Y, "Y");

@@ -72,6 +72,8 @@ constexpr int kTopkMax = 512;
 size_t topk_scratch_keys(int n, int M);
 hipError_t launch_topk(const float *x, int n, int M, uint64_t *buf_a, uint64_t *buf_b, int *idx, float *val,
                        hipStream_t st);
+// the same with the key buffers in a file-scope device array (no allocation): n <= 262144; device pointers; enqueued on st
+hipError_t launch_topk_noalloc(const float *x, int n, int M, int *idx, float *val, hipStream_t st);
 
 // x[0..d) = row ctl->tok of the embedding (row_f32 semantics, /root/reference/src/kernels.cpp:146-162)
 hipError_t launch_embed(const DMat &embed, const Ctl *ctl, float *x, hipStream_t st);

@@ -7,6 +7,8 @@
 // value's order-preserving unsigned image, the low word the index.  Rounds: every workgroup bitonic-sorts a chunk of
 // 4096 keys in LDS and keeps its first M; the survivors form the next round's input, until one chunk is left, whose
 // first M keys are the result.
+#include <mutex>
+
 #include "launch.hpp"
 
 namespace qph {
@@ -75,6 +77,38 @@ hipError_t launch_topk(const float *x, int n, int M, uint64_t *buf_a, uint64_t *
     std::swap(out, spare);
   }
   return hipGetLastError();
+}
+
+// ---- the top-M without allocation (qph_topk_noalloc): the key buffers live in a file-scope device array, one copy per
+// GPU, held until the process ends.  Its address comes from hipGetSymbolAddress once per device, with that device
+// current (the array's name in host code is only a stand-in: passed to a kernel it would fault).  Calls that overlap
+// on one GPU share the array and race; the array keeps the last call's keys (every round writes what the next reads,
+// so nothing needs clearing).
+constexpr int kTopkNoAllocMaxN = 262144;
+constexpr size_t kTopkNoAllocKeys = (size_t)(kTopkNoAllocMaxN / kTopkChunk) * kTopkMax;   // per buffer: 32768 keys
+static __device__ __align__(256) uint64_t scratch[2 * kTopkNoAllocKeys];                  // 512 KiB per GPU
+
+static uint64_t *scratch_ptr(int dev) {
+  static std::mutex mu;
+  static uint64_t *ptrs[64] = {};
+  if (dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    ptrs[dev] = (uint64_t *)p;
+  }
+  return ptrs[dev];
+}
+
+hipError_t launch_topk_noalloc(const float *x, int n, int M, int *idx, float *val, hipStream_t st) {
+  if (n <= 0 || n > kTopkNoAllocMaxN || M < 1 || M > kTopkMax || M > n) return hipErrorInvalidValue;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  uint64_t *base = scratch_ptr(dev);
+  if (!base) return hipErrorInvalidSymbol;
+  return launch_topk(x, n, M, base, base + kTopkNoAllocKeys, idx, val, st);
 }
 
 }  // namespace qph
