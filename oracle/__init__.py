@@ -127,6 +127,7 @@ def olib():
             "or_kcache": (C.c_void_p, [C.c_void_p]), "or_vcache": (C.c_void_p, [C.c_void_p]),
             "or_set_threads": (None, [C.c_int]),
             "or_set_order": (None, [C.c_int]),
+            "or_top_m": (C.c_int, [_FP, C.c_int, C.c_int, C.c_void_p, _FP]),
             "or_rans_raw_size": (C.c_int64, [C.c_void_p, C.c_int64]),
             "or_rans_decode": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64]),
             "or_rans_encode": (C.c_int64, [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_int64]),
@@ -223,6 +224,15 @@ def matmul(kind, q, s, X, cols=None):
     Y = np.empty((X.shape[0], rows), np.float32)
     olib().or_matmul(C.byref(m), _f(X), X.shape[0], _f(Y))
     return Y
+
+
+def top_m(x, M):
+    """the sampler's M candidates (index, value) in its order (or_top_m)"""
+    x = np.ascontiguousarray(x, np.float32)
+    idx = np.empty(M, np.int32); val = np.empty(M, np.float32)
+    if olib().or_top_m(_f(x), len(x), int(M), _p(idx), _f(val)):
+        raise ValueError("top_m: 1 <= M <= len(x) required")
+    return idx, val
 
 
 def rmsnorm(x, w, eps):
@@ -493,7 +503,8 @@ def rlib(threads=0):
             "qpref_exp_v": (None, [_FP, _FP, I]), "qpref_to_f16": (None, [_FP, P, I]),
             "qpref_row_f32": (None, [I, P, P, I, I, I, _FP]),
             "qpref_rans_encode": (I, [P, C.c_int64, I, I, P, C.c_int64, C.POINTER(C.c_int64)]),
-            "qpref_rans_decode": (I, [P, C.c_int64, P]), "qpref_rans_raw_size": (C.c_int64, [P, C.c_int64]),
+            "qpref_rans_decode": (I, [P, C.c_int64, P]),
+            "qpref_prefill_all": (I, [P, P, I, _FP, I]), "qpref_rewind": (I, [P, I]), "qpref_sampler_topk": (I, [_FP, I, I, P]), "qpref_rans_raw_size": (C.c_int64, [P, C.c_int64]),
         }
         for k, (r, a) in sig.items():
             getattr(L, k).restype = r
@@ -551,6 +562,16 @@ class Ref:
         self._ck(self.L.qpref_greedy(self.m, int(tok), n, _p(out)))
         return out
 
+    def rewind(self, pos):
+        return bool(self.L.qpref_rewind(self.m, int(pos)))
+
+    def prefill_all(self, toks, exact=True):
+        """Model::prefill_all: the logits of every position [n, vocab]; under ExactBatches when exact"""
+        toks = np.ascontiguousarray(toks, np.int32)
+        out = np.empty((len(toks), self.vocab()), np.float32)
+        self._ck(self.L.qpref_prefill_all(self.m, _p(toks), len(toks), _f(out), int(exact)))
+        return out
+
     def snapshot(self):
         n = self.L.qpref_snapshot(self.m, None, 0)
         buf = np.empty(n, np.uint8)
@@ -561,3 +582,14 @@ class Ref:
     def restore(self, s):
         buf = np.frombuffer(s, np.uint8)
         self._ck(self.L.qpref_restore(self.m, _p(buf), len(buf)))
+
+
+def ref_sampler_topk(x, M):
+    """the indices of the reference sampler's top-M candidates (Sampler::dist with top_k = M and no other filter), in its
+    order: the compiled reference's top_m + sort (/root/reference/src/sampler.cpp:12-27, :41-42)"""
+    L = rlib()
+    x = np.ascontiguousarray(x, np.float32)
+    idx = np.empty(M, np.int32)
+    if L.qpref_sampler_topk(_f(x), len(x), int(M), _p(idx)):
+        raise RuntimeError(L.qpref_error().decode())
+    return idx

@@ -573,6 +573,42 @@ int or_greedy(or_model *m, int tok, int n, int *out) {
   return n;
 }
 
+/* ------------------------------------------------------------------ sampler candidates
+ * top_m + the sort of Sampler::dist (/root/reference/src/sampler.cpp:12-27, :41-42): the M largest logits in the order
+ * value descending, lower index first among equal values.  Same steps as the reference: all V candidates when
+ * M >= V / 4; otherwise the first min(V, 4 M + 8) entries, cut to M (the threshold = the smallest kept value), then a
+ * scan of the rest for entries strictly above the threshold (scan_gt, kernels_x86.cpp:498-506), cut again whenever more
+ * than 4 M are held, a last cut to M, and the sort.  The cuts keep the M first entries of the same total order the
+ * sort uses, which is what nth_element + resize keeps. */
+typedef struct { int i; float v; } or_cand;
+static int cand_cmp(const void *pa, const void *pb) {
+  const or_cand *a = (const or_cand *)pa, *b = (const or_cand *)pb;
+  if (a->v > b->v) return -1;
+  if (b->v > a->v) return 1;
+  return a->i < b->i ? -1 : (a->i > b->i);
+}
+int or_top_m(const float *x, int V, int M, int *idx, float *val) {
+  if (V <= 0 || M < 1 || M > V) return -1;
+  or_cand *c = (or_cand *)malloc(sizeof(or_cand) * (size_t)(M >= V / 4 ? V : 4 * M + 8 + 4096));
+  int n = 0;
+  if (M >= V / 4) {
+    for (int v = 0; v < V; v++) { c[n].i = v; c[n].v = x[v]; n++; }
+  } else {
+    const int init = V < 4 * M + 8 ? V : 4 * M + 8;
+    for (int v = 0; v < init; v++) { c[n].i = v; c[n].v = x[v]; n++; }
+    qsort(c, (size_t)n, sizeof *c, cand_cmp); n = M; float thr = c[M - 1].v;
+    for (int v0 = init; v0 < V; v0 += 4096) {
+      const int v1 = v0 + 4096 < V ? v0 + 4096 : V;
+      for (int v = v0; v < v1; v++) if (x[v] > thr) { c[n].i = v; c[n].v = x[v]; n++; }
+      if (n > 4 * M) { qsort(c, (size_t)n, sizeof *c, cand_cmp); n = M; thr = c[M - 1].v; }
+    }
+  }
+  qsort(c, (size_t)n, sizeof *c, cand_cmp);
+  for (int k = 0; k < M; k++) { idx[k] = c[k].i; val[k] = c[k].v; }
+  free(c);
+  return 0;
+}
+
 /* ------------------------------------------------------------------ QPACK3 rANS (/root/reference/include/qpack/rans.h)
  * Static per-plane model: 12-bit frequencies summing to 4096, four interleaved 32-bit states (symbol i uses state i & 3),
  * byte-wise renormalisation into [2^23, 2^31).  The encoder walks the symbols backwards and the bytes are stored in

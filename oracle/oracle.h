@@ -80,6 +80,8 @@ int or_greedy(or_model *m, int tok, int n, int *out);
 uint16_t *or_kcache(or_model *m);
 uint16_t *or_vcache(or_model *m);
 void or_set_threads(int n);
+/* the sampler's top-M candidates (top_m + sort, /root/reference/src/sampler.cpp:12-27, :41-42) */
+int or_top_m(const float *x, int V, int M, int *idx, float *val);
 /* evaluation-order variants for experiments (0 = the reference's orders everywhere) */
 enum { OR_ORD_TREE_NORM = 1, OR_ORD_ROWS_PREFILL = 2, OR_ORD_ATTN_F64 = 4, OR_ORD_EXP_F64 = 8 };
 void or_set_order(int flags);

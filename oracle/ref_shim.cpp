@@ -11,6 +11,7 @@
 #include <string>
 #include <vector>
 
+#include "qpack/engine.h"
 #include "qpack/qpack.h"
 #include "qpack/rans.h"
 
@@ -23,7 +24,7 @@ void rows_q1(const uint8_t *Q, const uint16_t *S, const int16_t *xq, const float
 }}
 
 static thread_local std::string g_err;
-#define QPREF_TRY(body) try { body; return 0; } catch (std::exception &e) { g_err = e.what(); return -1; }
+#define QPREF_TRY(...) try { __VA_ARGS__; return 0; } catch (std::exception &e) { g_err = e.what(); return -1; }
 
 extern "C" {
 
@@ -57,6 +58,30 @@ int qpref_prefill(void *mp, const int *toks, int n, int want, float *out) {
   });
 }
 int qpref_greedy(void *mp, int tok, int n, int *out) { QPREF_TRY(((qp::Model *)mp)->greedy_run(tok, n, out)); }
+// Model::rewind (qpack.h:160): 1 when the model kept the first pos tokens
+int qpref_rewind(void *mp, int pos) { return ((qp::Model *)mp)->rewind(pos) ? 1 : 0; }
+// Model::prefill_all (qpack.h:152), under ExactBatches when `exact` (how Session's speculative verification calls it,
+// /root/reference/src/chat.cpp:233): n x vocab logits
+int qpref_prefill_all(void *mp, const int *toks, int n, float *out, int exact) {
+  QPREF_TRY({
+    qp::Model *m = (qp::Model *)mp;
+    if (exact) { qp::ExactBatches ex; m->prefill_all(toks, n, out); }
+    else m->prefill_all(toks, n, out);
+  });
+}
+// the sampler's candidate list for top_k = M (Sampler::dist, /root/reference/src/sampler.cpp:29-57, with no penalty,
+// temperature 1, top-p and min-p off): top_m, then the sort by value (lower index first among equal values); the
+// indices in that order
+int qpref_sampler_topk(const float *x, int V, int M, int *idx) {
+  QPREF_TRY({
+    qp::SamplerParams p; p.temperature = 1.f; p.top_k = M; p.top_p = 1.f; p.min_p = 0.f; p.repeat_penalty = 1.f; p.seed = 1;
+    qp::Sampler s(p);
+    std::vector<std::pair<int, float>> d;
+    s.dist(x, V, {}, d);
+    if ((int)d.size() != M) throw std::runtime_error("sampler returned " + std::to_string(d.size()) + " candidates");
+    for (int i = 0; i < M; i++) idx[i] = d[i].first;
+  });
+}
 
 // snapshot layout of /root/reference/src/model_llama.cpp:55-59; call with buf = nullptr to get the size
 int64_t qpref_snapshot(void *mp, uint8_t *buf, int64_t cap) {

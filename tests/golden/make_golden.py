@@ -126,6 +126,17 @@ def model_fixture(name):
         tok = int(np.argmax(l))
         stream.append(tok)
     fx.update(greedy=stream, greedy_top2_gap=gaps, decode_top5=tops, step_hash=hashes, pos_after=int(ref.pos()))
+    if not restore and n_gen >= 8:
+        # speculative verification (chat.cpp:229-233): back to the end of the prompt, then prefill_all of the first
+        # token and 7 greedy drafts under ExactBatches; logits of every position
+        p0 = len(fx["prompt"])
+        assert ref.rewind(p0)
+        seq = [fx["first_token"]] + stream[:7]
+        la = ref.prefill_all(np.array(seq, np.int32), exact=True)
+        idx = np.arange(0, V, max(1, V // 256))
+        fx["prefill_all"] = dict(pos=p0, tokens=seq, hash=[logits_hash(l) for l in la], sample_idx=idx.tolist(),
+                                 sample=[l[idx].astype(float).tolist() for l in la],
+                                 argmax=[int(np.argmax(l)) for l in la])
     if samples:
         fx["step_sample"] = samples
     ref.close()

@@ -167,3 +167,31 @@ def test_c4_prefill(exact, synth):
         assert np.all(d <= 2 * ulp + 1e-2), f"cache rows max|d| {d.max()}"
     print(f"c4: prefill logit max|d| {err.max():.3g}; cache rows max|d| K {np.abs(k.astype(np.float32) - kv['k']).max():.3g}, "
           f"V {np.abs(v.astype(np.float32) - kv['v']).max():.3g}", flush=True)
+
+
+@pytest.mark.parametrize("name", ["mini", "mini_q4m", "c1", "c2", "c3"])
+@pytest.mark.parametrize("exact", [False, True], ids=["default", "reference_order"])
+def test_prefill_all_speculative_verification(name, exact, synth):
+    """Model::prefill_all as Session's speculative verification calls it (under ExactBatches, chat.cpp:229-233): the
+    first token and 7 greedy drafts at the end of the prompt; n x vocab logits.  Reference order: every row
+    bit-identical to the reference's; default order: every row within the logit tolerance on a fixed sample, each row's
+    argmax the reference's, and every row bit-identical to this model's own decode step at that position (the
+    ExactBatches contract: prefill_all == step by step)"""
+    fx = fixture(name)
+    pa = fx["prefill_all"]
+    m, _ = start(name, fx, synth, exact)
+    assert m.pos() == pa["pos"]
+    la = m.prefill_all(np.array(pa["tokens"], np.int32))
+    assert la.shape == (8, m.vocab()) and m.pos() == pa["pos"] + 8
+    if exact:
+        assert [lhash(l) for l in la] == pa["hash"]
+    else:
+        for i, l in enumerate(la):
+            ref = np.float32(pa["sample"][i])
+            err = np.abs(l[pa["sample_idx"]] - ref)
+            assert np.all(err <= np.maximum(1e-2, 1e-3 * np.abs(ref))), f"row {i}: max|d| {err.max()}"
+        assert [int(np.argmax(l)) for l in la] == pa["argmax"]
+        assert m.rewind(pa["pos"])
+        for i, t in enumerate(pa["tokens"]):
+            np.testing.assert_array_equal(m.step(t, 1), la[i], err_msg=f"row {i} differs from the decode step")
+    m.close()

@@ -1,19 +1,19 @@
-"""Device top-M of the logits (qph_step_topk / qph_prefill_topk / qph_kernel_topk) against the definition the
-reference's sampler implements (top_m + sort, /root/reference/src/sampler.cpp:12-27, :41-42): the M largest values,
-value descending, the lower index first among equal values.  The expected order comes from a stable numpy sort on
-(-value, index), i.e. the textbook selection - exact equality is required (indices and values)."""
+"""Device top-M of the logits (qph_step_topk / qph_prefill_topk / qph_kernel_topk) against the oracle's restatement of
+the reference sampler's candidate selection (or_top_m: top_m + sort, /root/reference/src/sampler.cpp:12-27, :41-42,
+pinned in tests/test_oracle.py against the compiled reference's Sampler and a stable numpy sort on (-value, index)):
+the M largest values, value descending, the lower index first among equal values; exact equality of indices and
+values is required."""
 import numpy as np
 import pytest
 
+import oracle as O
 import qpack_amd as qa
 
 pytestmark = pytest.mark.gpu
 
 
 def expect_topk(x, M):
-    order = np.lexsort((np.arange(len(x)), -x.astype(np.float64)))   # primary key -value, then index
-    idx = order[:M].astype(np.int32)
-    return idx, x[idx]
+    return O.top_m(x, M)
 
 
 def check(x, M):

@@ -181,3 +181,38 @@ def test_model_matches_live_reference(name, tmp_path):
     body = snap[4:].view(np.uint16).reshape(L, 2, n, kvd)
     np.testing.assert_array_equal(body[:, 0], k[:, :n])
     np.testing.assert_array_equal(body[:, 1], v[:, :n])
+
+
+def _topk_cases():
+    rng = np.random.default_rng(77)
+    cases = []
+    for V, M in ((151936, 40), (128256, 512), (1000, 250), (1000, 251), (5000, 1), (8200, 64), (17, 3)):
+        cases.append((rng.standard_normal(V).astype(np.float32) * 3, M))
+    x = (np.round(rng.standard_normal(60000) * 2) / 4).astype(np.float32)   # long runs of equal values
+    x[::7] = 0.0; x[3::7] = -0.0; x[100] = np.inf; x[200] = -np.inf
+    cases += [(x, 1), (x, 40), (x, 512), (np.zeros(9000, np.float32), 33)]
+    return cases
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref/libqpref.so not built")
+def test_top_m_matches_reference_sampler():
+    """or_top_m against the compiled reference's own sampler (Sampler::dist with top_k = M) and against the textbook
+    order (a stable sort on (-value, index)), including ties, -0 / +0, infinities and M >= V / 4"""
+    for x, M in _topk_cases():
+        idx, val = O.top_m(x, M)
+        np.testing.assert_array_equal(idx, O.ref_sampler_topk(x, M))
+        np.testing.assert_array_equal(idx, np.lexsort((np.arange(len(x)), -x.astype(np.float64)))[:M])
+        np.testing.assert_array_equal(val, x[idx])
+
+
+@pytest.mark.parametrize("name", ["mini", "mini_q4m", "c1", "c2", "c3"])
+def test_fixture_prefill_all_equals_steps(name):
+    """the reference's own contract, read off its fixtures: prefill_all under ExactBatches (qpack.h:106-108, :152)
+    gives every position's logits bit-identical to stepping the same tokens (per-position hashes equal the decode
+    steps' hashes)"""
+    with open(os.path.join(GOLD, name + ".json")) as f:
+        fx = json.load(f)
+    pa = fx["prefill_all"]
+    assert pa["tokens"] == [fx["first_token"]] + fx["greedy"][:7]
+    assert pa["hash"] == fx["step_hash"][:8]
+    assert pa["argmax"] == fx["greedy"][:8]
