@@ -19,6 +19,7 @@ import argparse
 import json
 import os
 import sys
+import subprocess
 import tempfile
 import time
 
@@ -165,28 +166,32 @@ def other_config(name, seed, steps_override=None):
                          f"timed greedy tokens (context {T1}..{T2})")
 
 
-def cpu_baseline(path, threads, n_prompt=16, n_gen=16, reps=2):
-    """qpack-bench --row protocol (tools/qpack-bench.cpp:35-47) on the reference engine: reset, prefill(np), ng x step,
-    best of reps"""
-    import oracle
-    L = oracle.rlib(threads)
-    ref = oracle.Ref(path, n_prompt + n_gen + 8)
-    toks = np.array([100 + (i * 37) % 5000 for i in range(n_prompt)], np.int32)
-    pp = tg = 0.0
-    for _ in range(reps):
-        ref.reset()
-        t0 = time.time()
-        ref.prefill(toks, 1)
-        t1 = time.time()
-        for i in range(n_gen):
-            ref.step(100 + (i * 53) % 5000, 1)
-        t2 = time.time()
-        pp, tg = max(pp, n_prompt / (t1 - t0)), max(tg, n_gen / (t2 - t1))
-    used = L.qpref_threads()
-    ref.close()
-    return dict(value=round(tg, 3), unit="tokens/s", cores=used, kind="reference",
-                sample=f"reference qp::Llama (AVX2, {used} threads) on the same C3 file: prefill {n_prompt} + {n_gen} decode steps "
-                       f"(qpack-bench protocol, best of {reps}); its prefill rate {pp:.2f} tok/s")
+REF_BENCH = os.path.join(ROOT, "qpack_amd", "integration", "_build", "qpack-bench")
+
+
+def cpu_baseline(path, threads):
+    """the reference's qpack-bench (tools/qpack-bench.cpp, AVX2 engine, compiled from its sources with the HIP adapter
+    linked in but not selected: QPACK_DEVICE unset) on the same C3 file, with its own protocol (:35-62): one child
+    process per thread count, prefill np then np decode steps, best of 2 repetitions.  Two rows: min(16, cores) threads
+    on the C3 workload's 128-token prompt + 32 decode steps, and 1 thread on a bounded sample (32-token prompt + 8
+    steps; the 128-token prompt alone takes ~30 s on one core).  value = the min(16, cores)-thread decode rate."""
+    env = dict(os.environ)
+    env.pop("QPACK_DEVICE", None)
+    rows = []
+    for t, np_, ng in ((threads, 128, 32), (1, 32, 8)):
+        r = subprocess.run([REF_BENCH, "-m", path, "-p", str(np_), "-n", str(ng), "-t", str(t), "-r", "2"], env=env,
+                           capture_output=True, text=True, timeout=900, check=True)
+        line = [x for x in r.stdout.splitlines() if x.startswith("|") and not x.startswith("| model") and "---" not in x][0]
+        c = [x.strip() for x in line.strip().strip("|").split("|")]
+        rows.append(dict(threads=int(c[3]), prompt=np_, decode_steps=ng, prefill_tokens_per_s=float(c[4]),
+                         decode_tokens_per_s=float(c[5])))
+    top = rows[0]
+    return dict(value=top["decode_tokens_per_s"], unit="tokens/s", cores=top["threads"], kind="reference",
+                sample=f"reference qpack-bench (AVX2) on the same C3 file: {top['threads']} threads, {top['prompt']}-token "
+                       f"prompt + {top['decode_steps']} decode steps, best of 2 (prefill {top['prefill_tokens_per_s']} tok/s); "
+                       f"1 thread: {rows[1]['prefill_tokens_per_s']} tok/s prefill, {rows[1]['decode_tokens_per_s']} tok/s "
+                       f"decode ({rows[1]['prompt']}-token prompt + {rows[1]['decode_steps']} steps)",
+                rows=rows)
 
 
 def qpack3_cpu_decode(path3, threads):
@@ -389,13 +394,12 @@ def main():
 
     cpu = None
     if not a.no_cpu_baseline:
-        import oracle
-        if oracle.ref_available():
+        if os.path.exists(REF_BENCH):
             t = time.time()
             cpu = cpu_baseline(path, min(16, os.cpu_count() or 1))
-            log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads ({time.time() - t:.1f}s)")
+            log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads; rows {cpu['rows']} ({time.time() - t:.1f}s)")
         else:
-            log("cpu baseline skipped: oracle/_ref/libqpref.so is not built")
+            log("cpu baseline skipped: qpack_amd/integration/_build/qpack-bench is not built")
     if tmpdir:
         os.remove(path)
         os.rmdir(tmpdir)
