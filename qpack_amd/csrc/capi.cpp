@@ -270,21 +270,23 @@ int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int 
     try {
       void *dq = alloc(qb), *ds = alloc(sb);
       float *dx = (float *)alloc(4ull * B * cols), *dy = (float *)alloc(4ull * B * rows), *dxb = (float *)alloc(4ull * B * nb);
+      const int ldbt = (B + 63) / 64 * 64;
+      float *dxbt = (float *)alloc(4ull * ldbt * nb);
       int8_t *dxh = (int8_t *)alloc((size_t)B * cols), *dxl = (int8_t *)alloc((size_t)B * cols);
       int *dxg = (int *)alloc(4ull * B * ldg);
       hck(hipMemcpy(dq, q, qb, hipMemcpyHostToDevice), "upload q");
       hck(hipMemcpy(ds, scale, sb, hipMemcpyHostToDevice), "upload scale");
       hck(hipMemcpy(dx, X, 4ull * B * cols, hipMemcpyHostToDevice), "upload X");
       qph::PfQuantArgs qa{}; qa.x = dx; qa.ldx = cols; qa.cols = cols; qa.xh = dxh; qa.xl = dxl; qa.ldq = cols; qa.xb = dxb; qa.ldb = nb;
-      qa.xg = dxg; qa.ldg = ldg;
+      qa.xg = dxg; qa.ldg = ldg; qa.xbt = dxbt; qa.ldbt = ldbt;
       hck(qph::launch_pf_quant(qph::PRO_QUANT, qa, B, nullptr), "launch quant");
       qph::GemmArgs ga{}; ga.kind = kind == QPH_Q8 ? qph::MK_Q8 : qph::MK_Q4; ga.w = (const int8_t *)dq; ga.scale = (const float *)ds;
       ga.rows = rows; ga.cols = cols; ga.xh = dxh; ga.xl = dxl; ga.xb = dxb; ga.ntok = B; ga.ldq = cols; ga.ldb = nb;
-      ga.xg = dxg; ga.ldg = ldg; ga.y = dy; ga.ldy = rows;
+      ga.xg = dxg; ga.ldg = ldg; ga.y = dy; ga.ldy = rows; ga.xbt = dxbt; ga.ldbt = ldbt;
       if (kind == QPH_Q8) {
-        int *dws = (int *)alloc(4ull * rows * nb);
+        int *dws = (int *)alloc(4ull * qph::ws_pitch(rows) * nb);
         hck(qph::launch_rowsum_q8((const int8_t *)dq, rows, cols, dws, nullptr), "launch rowsum");
-        ga.wsum = dws; ga.ldw = nb;
+        ga.wsum = dws;
       } else {
         int *dns = (int *)alloc(4ull * rows * G); float *dsc = (float *)alloc(4ull * rows * G);
         hck(qph::launch_q4_prep((const uint8_t *)dq, (const uint16_t *)ds, rows, cols, dns, dsc, nullptr), "launch q4 prep");

@@ -115,6 +115,7 @@ struct PfQuantArgs {
   int cols;
   int8_t *xh, *xl; int ldq;
   float *xb; int ldb;
+  float *xbt; int ldbt;   // optional: the block scales block-major [cols / 128][ldbt]
   int *xg; int ldg;   // optional: sum of q per 32-column group [B][ldg] (the q4 product needs it)
 };
 hipError_t launch_pf_quant(int pro, const PfQuantArgs &a, int B, hipStream_t st);
@@ -131,10 +132,11 @@ constexpr int kGemmMaxSeg = 3;
 struct GemmArgs {
   int kind;
   const int8_t *w; const float *scale; int rows, cols;
-  const int *wsum; int ldw;   // q8: 128 x the row sums per 128-column block (k_rowsum_q8), [rows][ldw]
+  const int *wsum;   // q8: 128 x the row sums per 128-column block (k_rowsum_q8), [cols / 128][ws_pitch(rows)]
   const int *q4ns; const float *q4sc;
   const int *xg; int ldg;
   const int8_t *xh, *xl; const float *xb; int ntok, ldq, ldb;
+  const float *xbt; int ldbt;   // q8: the block scales again, block-major [cols / 128][ldbt] (ldbt % 4 == 0, >= ntok)
   float *y; int ldy;
   const float *bias;
   int resid;
@@ -147,8 +149,12 @@ struct GemmArgs {
   // segment fields replacing w / scale / wsum / q4ns / q4sc / bias / y / ldy / rows; each starts on a fresh row tile
   int nseg;
   GemmSeg seg[kGemmMaxSeg];
+  int dbg;   // measurement switches of the 32 x 32 q8 kernel (QPH_G2_DBG; results are wrong when set): 1 no compute,
+             // 2 no loads past the first two stages, 4 no barriers, 8 no shift-add / fp32 steps
 };
 size_t gemm_lds_bytes();
+// row pitch of the block-major row sums: rows rounded up to 64 (16-byte loads of 4 rows stay inside a block's run)
+__host__ __device__ inline int ws_pitch(int rows) { return (rows + 63) & ~63; }
 // out[row][block] = sum of W[row] over each 128-column block
 hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipStream_t st);
 // q4 rows: per (block, group, row) the sum of the nibbles and the f32 scale, group-major within each 128-column block

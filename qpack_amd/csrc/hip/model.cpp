@@ -142,7 +142,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     for (Layer &ly : layers_)
       for (DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd}) {
         if (m->kind == MK_Q8) {
-          int *rs = (int *)dalloc(4ull * m->rows * (m->cols / 128));
+          int *rs = (int *)dalloc(4ull * ws_pitch(m->rows) * (m->cols / 128));
           QPH_CK(launch_rowsum_q8((const int8_t *)m->q, m->rows, m->cols, rs, st_));
           m->rs = rs;
         } else {
@@ -162,6 +162,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     pf_g_ = (float *)dalloc(4 * B * ff);
     pf_xh_ = (int8_t *)dalloc(B * pf_ldq_); pf_xl_ = (int8_t *)dalloc(B * pf_ldq_);
     pf_xb_ = (float *)dalloc(4 * B * (pf_ldq_ / 128 + 1));
+    pf_ldbt_ = (int)(B + 63) / 64 * 64;
+    pf_xbt_ = (float *)dalloc(4ull * pf_ldbt_ * (pf_ldq_ / 128 + 1));
     pf_ldg_ = (pf_ldq_ / 32 + 3) / 4 * 4;
     pf_xg_ = (int *)dalloc(4 * B * pf_ldg_);
     pf_tok_ = (int *)dalloc(4 * B);
@@ -382,11 +384,12 @@ void HipLlama::prefill_batched(const int *toks, int n) {
   auto quant = [&](int pro, const float *x, int ldx, const float *w, int cols, int B) {
     PfQuantArgs a{}; a.x = x; a.ldx = ldx; a.norm_w = w; a.eps = eps; a.cols = cols;
     a.xh = pf_xh_; a.xl = pf_xl_; a.ldq = pf_ldq_; a.xb = pf_xb_; a.ldb = nb_ld; a.xg = pf_xg_; a.ldg = pf_ldg_;
+    a.xbt = pf_xbt_; a.ldbt = pf_ldbt_;
     QPH_CK(launch_pf_quant(pro, a, B, st_));
   };
   auto gemm = [&](const DMat &m, float *y, int ldy, const float *bias, bool resid, int B, const float *gate = nullptr) {
     GemmArgs a{}; a.kind = m.kind; a.w = (const int8_t *)m.q; a.scale = (const float *)m.s; a.rows = m.rows; a.cols = m.cols;
-    a.wsum = m.rs; a.ldw = m.cols / 128; a.q4ns = m.q4ns; a.q4sc = m.q4sc; a.xg = pf_xg_; a.ldg = pf_ldg_;
+    a.wsum = m.rs; a.xbt = pf_xbt_; a.ldbt = pf_ldbt_; a.q4ns = m.q4ns; a.q4sc = m.q4sc; a.xg = pf_xg_; a.ldg = pf_ldg_;
     a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld;
     a.y = y; a.ldy = ldy; a.bias = bias; a.resid = resid ? 1 : 0; a.gate = gate;
     QPH_CK(launch_gemm(a, st_));
@@ -401,7 +404,7 @@ void HipLlama::prefill_batched(const int *toks, int n) {
       int j = i + 1;
       while (j < 3 && m[j]->kind == m[i]->kind && m[j]->cols == m[i]->cols) j++;
       if (j - i == 1 || (m[i]->kind != MK_Q8 && m[i]->kind != MK_Q4)) { gemm(*m[i], y[i], ld[i], bias[i], false, B); i++; continue; }
-      GemmArgs a{}; a.kind = m[i]->kind; a.cols = m[i]->cols; a.ldw = a.cols / 128; a.xg = pf_xg_; a.ldg = pf_ldg_;
+      GemmArgs a{}; a.kind = m[i]->kind; a.cols = m[i]->cols; a.xbt = pf_xbt_; a.ldbt = pf_ldbt_; a.xg = pf_xg_; a.ldg = pf_ldg_;
       a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld;
       a.nseg = j - i;
       for (int s = i; s < j; s++)
@@ -433,7 +436,7 @@ void HipLlama::prefill_batched(const int *toks, int n) {
       if (ly.wg.kind == MK_Q8 && ly.wu.kind == MK_Q8) {   // gate and up in one launch, only h = silu(gate) * up stored
         GemmArgs a{}; a.kind = MK_Q8; a.w = (const int8_t *)ly.wg.q; a.scale = (const float *)ly.wg.s; a.wsum = ly.wg.rs;
         a.w2 = (const int8_t *)ly.wu.q; a.scale2 = (const float *)ly.wu.s; a.wsum2 = ly.wu.rs;
-        a.rows = ff; a.cols = d; a.ldw = d / 128; a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B;
+        a.rows = ff; a.cols = d; a.xbt = pf_xbt_; a.ldbt = pf_ldbt_; a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B;
         a.ldq = pf_ldq_; a.ldb = nb_ld; a.y = pf_g_; a.ldy = ff;
         QPH_CK(launch_gemm(a, st_));
       } else {

@@ -104,7 +104,8 @@ class HipLlama {
   bool pf_ok_ = false;
   int pf_cap_ = 0, pf_ldq_ = 0, pf_ldg_ = 0;
   float *pf_x_ = nullptr, *pf_q_ = nullptr, *pf_k_ = nullptr, *pf_v_ = nullptr, *pf_att_ = nullptr, *pf_g_ = nullptr;
-  float *pf_xb_ = nullptr;
+  float *pf_xb_ = nullptr, *pf_xbt_ = nullptr;   // block scales token-major [B][nb], block-major [nb][pf_ldbt_]
+  int pf_ldbt_ = 0;
   int8_t *pf_xh_ = nullptr, *pf_xl_ = nullptr;
   int *pf_tok_ = nullptr, *pf_xg_ = nullptr;
   void prefill_batched(const int *toks, int n);

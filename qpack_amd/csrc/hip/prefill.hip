@@ -12,6 +12,7 @@
 //     blocks in order, y = acc * scale[row]; every prompt token's projection is therefore bit-identical to a decode
 //     step's (the reference's own batched mm_q8 sums lane partials in another float order, within the logit tolerance).
 #include <math.h>
+#include <stdlib.h>
 
 #include <algorithm>
 
@@ -21,6 +22,7 @@
 namespace qph {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------------------ embeddings of a token batch
 __global__ __launch_bounds__(256) void k_pf_embed(DMat e, const int *toks, float *X, int ldx) {
@@ -50,6 +52,8 @@ __global__ __launch_bounds__(1024) void k_pf_quant(PfQuantArgs a) {
     *(uint4 *)(xl + c) = make_uint4(l.x ^ 0x80808080u, l.y ^ 0x80808080u, l.z ^ 0x80808080u, l.w ^ 0x80808080u);
   }
   for (int b = threadIdx.x; b < nb; b += blockDim.x) a.xb[(size_t)t * a.ldb + b] = av.bs[b];
+  if (a.xbt)
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) a.xbt[(size_t)b * a.ldbt + t] = av.bs[b];
   if (a.xg)   // sum of q per 32-column group (the q4 product's nibble-offset correction)
     for (int g = threadIdx.x; g < cols / 32; g += blockDim.x) a.xg[(size_t)t * a.ldg + g] = av.gsum[g];
 }
@@ -117,13 +121,13 @@ __device__ __forceinline__ float lds_read4o(uint32_t addr) {
   return r;
 }
 
-// 128 x the sum of each weight row over each 128-column block: out[row][block] (exact int32; the product's lo
-// accumulators start at this value, isum = 256 hi + lo + 128 sum(W))
+// 128 x the sum of each weight row over each 128-column block, block-major: out[block][ws_pitch(rows)] (exact int32;
+// isum = 256 hi + lo + 128 sum(W))
 __global__ __launch_bounds__(256) void k_rowsum_q8(const int8_t *w, int rows, int cols, int *out) {
-  const int nb = cols / kQB;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)rows * nb) return;
-  const v4i *p = (const v4i *)(w + (i / nb) * cols + (i % nb) * kQB);
+  if (i >= (int64_t)rows * (cols / kQB)) return;
+  const int row = (int)(i % rows), blk = (int)(i / rows);
+  const v4i *p = (const v4i *)(w + (size_t)row * cols + (size_t)blk * kQB);
   int s = 0;
 #pragma unroll
   for (int k = 0; k < 8; k++) {
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(256) void k_rowsum_q8(const int8_t *w, int rows, in
     s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
     s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
   }
-  out[i] = 128 * s;
+  out[(size_t)blk * ws_pitch(rows) + row] = 128 * s;
 }
 hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipStream_t st) {
   if (cols % kQB || rows <= 0) return hipErrorInvalidValue;
@@ -250,14 +254,15 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
   const int half = wave & 1;
   const bool sums = (wave & 2) != 0;
   const int *wsm = paired && half ? a.wsum2 : a.wsum;
-  const char *esrc = sums ? (const char *)(wsm + (size_t)min(r0 + (paired ? 0 : 64 * half) + lane, a.rows - 1) * a.ldw)
+  const char *esrc = sums ? (const char *)(wsm + min(r0 + (paired ? 0 : 64 * half) + lane, a.rows - 1))
                           : (const char *)(a.xb + (size_t)min(t0 + 64 * half + lane, a.ntok - 1) * a.ldb);
+  const size_t estep = sums ? 4 * (size_t)ws_pitch(a.rows) : 4;   // bytes per block
   const int edst = 3 * 128 * 128 + (sums ? 512 : 0) + 256 * half;
   auto issue = [&](int kb) {
     char *st = smem + (size_t)(kb % kGStages) * kGStage;
 #pragma unroll
     for (int j = 0; j < 6; j++) dma16(src[j] + kb * kQB, st + dst[j]);
-    dma4(esrc + 4 * kb, st + edst);
+    dma4(esrc + kb * estep, st + edst);
   };
 
   float acc[4][2][4];
@@ -407,6 +412,284 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
       if (t >= a.ntok) continue;
       gemm_store4(a, a.y + (size_t)t * a.ldy, r0 + wr * 64 + mi * 16 + 4 * lg,
                   make_float4(acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]), true);
+    }
+}
+
+// ------------------------------------------------------------------ int8 MFMA matrix product (q8), 32 x 32 tiles
+// Workgroup tile: 256 weight rows x 128 tokens, 8 waves (two per SIMD) in a 4 x 2 grid of 64 rows x 64 tokens, each a
+// 2 x 2 grid of v_mfma_i32_32x32x32_i8 tiles.  Per 128-column block a tile's one int32 accumulator T takes the hi plane
+// over the block's four 32-deep steps, then T = 256 T + 128 sum(W) (one shift-add), then the lo plane on top: T is the
+// block's exact isum = 256 hi + lo + 128 sum(W), and acc = fma(bs, (float) T, acc) is rows_q8's fp32 step - the same
+// arithmetic, bit for bit, as the 16 x 16 product and the decode matrix-vector product.
+// K advances in 64-column stages through a 4-slot ring of direct global->LDS loads, two stages ahead.
+//   stage: weights [256 rows][64 B], hi plane [128 tokens][64 B], lo plane likewise, the rows' block sums [256] and the
+//   tokens' block scales [128] of the stage's block.  The four 16-byte segments of a 64-byte row are XOR-swizzled by
+//   (row bit 2, row bit 1 ^ row bit 3), so the 32 rows of a fragment read spread over the 64 banks.
+//   fragments: lane l reads A = W[row l % 32][16 (l / 32) + 0..15] and B = plane[token l % 32][16 (l / 32) + 0..15]
+//   within the 32-deep step; C lane l holds rows 8 (r / 4) + 4 (l / 32) + r % 4 (r = 0..15) of token l % 32.
+constexpr int kG2M = 256, kG2N = 128, kG2Slots = 4, kG2Waves = 8;
+constexpr int kG2XH = 256 * 64, kG2XL = kG2XH + 128 * 64, kG2WS = kG2XL + 128 * 64, kG2BS = kG2WS + 1024;
+constexpr int kG2Stage = kG2BS + 1024;   // 34816 bytes (the block scales' second 512 bytes unused)
+constexpr int kG2GX = 132;                  // gate hand-off row pitch (floats)
+size_t gemm2_lds_bytes() { return (size_t)kG2Slots * kG2Stage; }
+static_assert(kG2N * kG2GX * 4 <= kG2Slots * kG2Stage, "gate hand-off fits in the ring");
+
+__device__ __forceinline__ int g2_swz(int r) { return (((r >> 2) & 1) << 1) | (((r >> 1) ^ (r >> 3)) & 1); }
+
+#define G2_WAIT(n, ...) asm volatile("s_waitcnt lgkmcnt(" #n ")" : __VA_ARGS__)
+
+__global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 1, wc = wave & 1;   // rows 64 wr, tokens 64 wc of the tile
+  const bool paired = a.w2 != nullptr;       // rows 0-127 of the tile from the gate matrix, 128-255 the same up rows
+  const int RT = paired ? kG2M / 2 : kG2M;
+  int r0, t0;
+  {
+    // XCD-aware tile order, as in the 16 x 16 product
+    const int ntt = gridDim.x, nrt = gridDim.y, n = ntt * nrt, lin = blockIdx.y * gridDim.x + blockIdx.x;
+    const int xcd = lin & 7, k = lin >> 3;
+    if (ntt % 8 == 0) {
+      const int tn = ntt >> 3;
+      r0 = (k / tn) * RT; t0 = (xcd * tn + k % tn) * kG2N;
+    } else {
+      const int base = n >> 3, rem = n & 7;
+      const int tile = xcd * base + min(xcd, rem) + k;
+      r0 = (tile / ntt) * RT; t0 = (tile % ntt) * kG2N;
+    }
+  }
+  r0 = gemm_segment(a, r0, RT);
+  const int nb = a.cols / kQB, nst = 2 * nb;
+
+  // DMA sources: 32 1-KiB row groups per stage (16 of weights, 8 per plane; 16 rows each), 4 to a wave; the lane
+  // fetches the logical segment that belongs at physical segment lane % 4 of row lane / 4
+  const int drow = lane >> 2, dseg = (lane & 3) ^ g2_swz(drow);
+  const int8_t *src[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int q = wave * 4 + j;
+    if (q < 16) {
+      const int row = 16 * q + drow;
+      const int8_t *wm = paired && row >= 128 ? a.w2 : a.w;
+      src[j] = wm + (size_t)min(r0 + (paired ? (row & 127) : row), a.rows - 1) * a.cols + dseg * 16;
+    } else {
+      const int tok = 16 * (q & 7) + drow;
+      src[j] = (q < 24 ? a.xh : a.xl) + (size_t)min(t0 + tok, a.ntok - 1) * a.ldq + dseg * 16;
+    }
+  }
+  // once per block, with its first stage: wave 0 the tile's 256 row sums (16 bytes = 4 rows a lane), wave 1 the 128
+  // token scales (lanes 32-63 repeat lanes 0-31 into the unused half), both from the block-major copies
+  const int pitch = ws_pitch(a.rows);
+  const char *esrc = nullptr;
+  size_t estep = 0;
+  if (wave == 0) {
+    const int row = 4 * lane;
+    const int *wsm = paired && row >= 128 ? a.wsum2 : a.wsum;
+    esrc = (const char *)(wsm + min(r0 + (paired ? (row & 127) : row), pitch - 4));
+    estep = 4 * (size_t)pitch;
+  } else if (wave == 1) {
+    esrc = (const char *)(a.xbt + min(t0 + 4 * (lane & 31), a.ldbt - 4));
+    estep = 4 * (size_t)a.ldbt;
+  }
+  auto issue = [&](int s) {
+    char *st = smem + (size_t)(s % kG2Slots) * kG2Stage;
+#pragma unroll
+    for (int j = 0; j < 4; j++) dma16(src[j] + 64 * s, st + (wave * 4 + j) * 1024);
+    if (wave < 2 && !(s & 1)) dma16(esrc + (s >> 1) * estep, st + (wave ? kG2BS : kG2WS));
+  };
+  // stage s's loads (this wave's, then everyone's) have landed, and every wave is done with stage s - 1, so the
+  // slot of stage s - 2 is refilled with stage s + 2
+  auto stage_sync = [&](int s) {
+    if (s + 1 >= nst) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (wave < 2 && (s & 1)) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");   // stage s + 1 carries the extras
+    else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    if (!(a.dbg & 4)) __builtin_amdgcn_s_barrier();
+    if (s + 2 < nst && !(a.dbg & 2)) issue(s + 2);
+  };
+
+  // per-lane LDS offsets: fragment row / token lane % 32, logical segment 2 step + lane / 32, physical ^ swizzle
+  const int fr = lane & 31, fh = lane >> 5, fsw = g2_swz(fr);
+  const uint32_t o0 = fr * 64 + ((fh ^ fsw) << 4), o1 = fr * 64 + (((2 | fh) ^ fsw) << 4);
+  const uint32_t ra0 = 64 * wr * 64 + o0, ra1 = 64 * wr * 64 + o1;   // + 2048 mi
+  const uint32_t rb0 = 64 * wc * 64 + o0, rb1 = 64 * wc * 64 + o1;   // + plane + 2048 ni
+  const uint32_t rws = kG2WS + (64 * wr + 4 * fh) * 4;               // + 128 mi + 32 j
+  const uint32_t rbs = kG2BS + (64 * wc + fr) * 4;                   // + 128 ni
+  const uint32_t sbase = lds_addr(smem);
+
+  float acc[2][2][16];
+#pragma unroll
+  for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
+  v16i T[2][2];
+  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+  issue(0);
+  issue(1);
+  for (int b = 0; b < nb; b++) {
+    const int s0 = 2 * b, s1 = s0 + 1;
+    if (a.dbg & 1) { stage_sync(s0); stage_sync(s1); continue; }
+    const uint32_t st0 = sbase + (uint32_t)((s0 % kG2Slots) * kG2Stage), st1 = sbase + (uint32_t)((s1 % kG2Slots) * kG2Stage);
+    // ---- hi plane, steps 0 and 1 (stage s0)
+    stage_sync(s0);
+    {
+      v4i A0 = lds_read16o<0>(st0 + ra0), A1 = lds_read16o<2048>(st0 + ra0);
+      v4i B0 = lds_read16o<kG2XH>(st0 + rb0), B1 = lds_read16o<kG2XH + 2048>(st0 + rb0);
+      v4i C0 = lds_read16o<0>(st0 + ra1), C1 = lds_read16o<2048>(st0 + ra1);
+      v4i D0 = lds_read16o<kG2XH>(st0 + rb1), D1 = lds_read16o<kG2XH + 2048>(st0 + rb1);
+      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, zero, 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, zero, 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, zero, 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, zero, 0, 0, 0);
+      G2_WAIT(0, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
+    }
+    // ---- hi plane, steps 2 and 3 (stage s1); the shift-add with the row sums; lo plane, steps 0-3; fp32 step
+    stage_sync(s1);
+    {
+      v4i A0 = lds_read16o<0>(st1 + ra0), A1 = lds_read16o<2048>(st1 + ra0);
+      v4i B0 = lds_read16o<kG2XH>(st1 + rb0), B1 = lds_read16o<kG2XH + 2048>(st1 + rb0);
+      v4i C0 = lds_read16o<0>(st1 + ra1), C1 = lds_read16o<2048>(st1 + ra1);
+      v4i D0 = lds_read16o<kG2XH>(st1 + rb1), D1 = lds_read16o<kG2XH + 2048>(st1 + rb1);
+      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, T[1][1], 0, 0, 0);
+      v4i W0 = lds_read16o<0>(st0 + rws), W1 = lds_read16o<32>(st0 + rws), W2 = lds_read16o<64>(st0 + rws),
+          W3 = lds_read16o<96>(st0 + rws);
+      G2_WAIT(4, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
+      v4i X0 = lds_read16o<128>(st0 + rws), X1 = lds_read16o<160>(st0 + rws), X2 = lds_read16o<192>(st0 + rws),
+          X3 = lds_read16o<224>(st0 + rws);
+      // lo step 0 (stage s0, still intact: its slot is refilled only after the next barrier)
+      A0 = lds_read16o<0>(st0 + ra0); A1 = lds_read16o<2048>(st0 + ra0);
+      B0 = lds_read16o<kG2XL>(st0 + rb0); B1 = lds_read16o<kG2XL + 2048>(st0 + rb0);
+      G2_WAIT(8, "+v"(W0), "+v"(W1), "+v"(W2), "+v"(W3));
+      if (!(a.dbg & 8)) {
+        const v4i w[4] = {W0, W1, W2, W3};
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          T[0][0][r] = T[0][0][r] * 256 + w[r >> 2][r & 3];
+          T[0][1][r] = T[0][1][r] * 256 + w[r >> 2][r & 3];
+        }
+      }
+      G2_WAIT(4, "+v"(X0), "+v"(X1), "+v"(X2), "+v"(X3));
+      if (!(a.dbg & 8)) {
+        const v4i w[4] = {X0, X1, X2, X3};
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          T[1][0][r] = T[1][0][r] * 256 + w[r >> 2][r & 3];
+          T[1][1][r] = T[1][1][r] * 256 + w[r >> 2][r & 3];
+        }
+      }
+      C0 = lds_read16o<0>(st0 + ra1); C1 = lds_read16o<2048>(st0 + ra1);
+      D0 = lds_read16o<kG2XL>(st0 + rb1); D1 = lds_read16o<kG2XL + 2048>(st0 + rb1);
+      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, T[1][1], 0, 0, 0);
+      A0 = lds_read16o<0>(st1 + ra0); A1 = lds_read16o<2048>(st1 + ra0);
+      B0 = lds_read16o<kG2XL>(st1 + rb0); B1 = lds_read16o<kG2XL + 2048>(st1 + rb0);
+      G2_WAIT(4, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
+      C0 = lds_read16o<0>(st1 + ra1); C1 = lds_read16o<2048>(st1 + ra1);
+      D0 = lds_read16o<kG2XL>(st1 + rb1); D1 = lds_read16o<kG2XL + 2048>(st1 + rb1);
+      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, T[1][1], 0, 0, 0);
+      float bs0 = lds_read4o<0>(st0 + rbs), bs1 = lds_read4o<128>(st0 + rbs);
+      G2_WAIT(2, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
+      G2_WAIT(0, "+v"(bs0), "+v"(bs1));
+      if (!(a.dbg & 8))
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          acc[mi][0][r] = __builtin_fmaf(bs0, (float)T[mi][0][r], acc[mi][0][r]);
+          acc[mi][1][r] = __builtin_fmaf(bs1, (float)T[mi][1][r], acc[mi][1][r]);
+        }
+    }
+  }
+
+  if (paired) {
+    // the gate waves (rows 0-127) hand gate = acc * scale to the up waves through LDS ([128 tokens][132 floats] over
+    // the ring, free once everyone is past the loop); the up waves store y = silu(gate) * (acc * scale2)
+    __syncthreads();
+    float *gx = (float *)smem;
+    auto scaled = [&](const float *sc, int rb, const float *v) {
+      float4 o;
+      if (rb + 3 < a.rows) {
+        const float4 s = *(const float4 *)(sc + rb);
+        o = make_float4(v[0] * s.x, v[1] * s.y, v[2] * s.z, v[3] * s.w);
+      } else {
+        o = make_float4(v[0] * sc[min(rb, a.rows - 1)], v[1] * sc[min(rb + 1, a.rows - 1)], v[2] * sc[min(rb + 2, a.rows - 1)],
+                        v[3] * sc[min(rb + 3, a.rows - 1)]);
+      }
+      return o;
+    };
+    if (wr < 2)
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int lrow = 64 * wr + 32 * mi + 8 * j + 4 * fh, tok = 64 * wc + 32 * ni + fr;
+            *(float4 *)(gx + tok * kG2GX + lrow) = scaled(a.scale, r0 + lrow, &acc[mi][ni][4 * j]);
+          }
+    __syncthreads();
+    if (wr >= 2)
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+          const int tok = 64 * wc + 32 * ni + fr, t = t0 + tok;
+          if (t >= a.ntok) continue;
+          float *yt = a.y + (size_t)t * a.ldy;
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int lrow = 64 * (wr - 2) + 32 * mi + 8 * j + 4 * fh, rb = r0 + lrow;
+            const float4 g = *(const float4 *)(gx + tok * kG2GX + lrow);
+            const float4 u = scaled(a.scale2, rb, &acc[mi][ni][4 * j]);
+            const float h[4] = {silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w)};
+            if (rb + 3 < a.rows && (a.ldy & 3) == 0) *(float4 *)(yt + rb) = make_float4(h[0], h[1], h[2], h[3]);
+            else
+#pragma unroll
+              for (int i = 0; i < 4; i++) if (rb + i < a.rows) yt[rb + i] = h[i];
+          }
+        }
+    return;
+  }
+#pragma unroll
+  for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+      const int t = t0 + 64 * wc + 32 * ni + fr;
+      if (t >= a.ntok) continue;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        gemm_store4(a, a.y + (size_t)t * a.ldy, r0 + 64 * wr + 32 * mi + 8 * j + 4 * fh,
+                    make_float4(acc[mi][ni][4 * j], acc[mi][ni][4 * j + 1], acc[mi][ni][4 * j + 2], acc[mi][ni][4 * j + 3]), true);
     }
 }
 
@@ -628,33 +911,57 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
     }
 }
 
+// q8: which product kernel.  The 32 x 32 one does twice a 16 x 16 workgroup's work ~12 % faster, so it wins unless its
+// fewer, larger workgroups leave CUs idle: compare ceil(n2 / CUs) x 1.76 with ceil(2 n2 / CUs) rounds (n2 = its
+// workgroup count).  QPH_GEMM=1 / 2 forces the 32 x 32 / 16 x 16 kernel.
+static bool gemm_use_32x32(int row_tiles32, int token_tiles32) {
+  const char *fe = getenv("QPH_GEMM");   // read per launch: tests switch it between calls
+  const int force = fe ? atoi(fe) : 0;
+  if (force == 1 || force == 2) return force == 1;
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 256;
+    return std::max(1, n);
+  }();
+  const long n2 = (long)row_tiles32 * token_tiles32;
+  return (double)((n2 + cus - 1) / cus) * 1.76 < (double)((2 * n2 + cus - 1) / cus);
+}
+
 hipError_t launch_gemm(const GemmArgs &a0, hipStream_t st) {
   if (a0.ntok <= 0) return hipSuccess;
   GemmArgs a = a0;
-  int tiles;
-  const int rt = a.w2 ? kGM / 2 : kGM;
+  { static const int dbg = [] { const char *e = getenv("QPH_G2_DBG"); return e ? atoi(e) : 0; }(); a.dbg = dbg; }
+  // row tiles of each kernel (a pair of gate / up matrices: half-height tiles of each)
+  auto row_tiles = [&](int big) {
+    const int rt = big ? (a.w2 ? kG2M / 2 : kG2M) : (a.w2 ? kGM / 2 : kGM);
+    if (a.nseg < 2) return (a.rows + rt - 1) / rt;
+    int t = 0;
+    for (int s = 0; s < a.nseg && s < kGemmMaxSeg; s++) t += (a.seg[s].rows + rt - 1) / rt;
+    return t;
+  };
   if (a.nseg > 1) {
     // the first matrix also stands in the launch's own fields, so the checks below cover every segment's pointers
     if (a.nseg > kGemmMaxSeg || a.w2 || a.resid || a.gate) return hipErrorInvalidValue;
-    tiles = 0;
     for (int s = 0; s < a.nseg; s++) {
       const GemmSeg &g = a.seg[s];
       if (g.rows <= 0 || !g.w || !g.scale || !g.y || (a.kind == MK_Q8 ? !g.wsum : (!g.q4ns || !g.q4sc))) return hipErrorInvalidValue;
-      tiles += (g.rows + rt - 1) / rt;
     }
     const GemmSeg &g = a.seg[0];
     a.w = g.w; a.scale = g.scale; a.wsum = g.wsum; a.q4ns = g.q4ns; a.q4sc = g.q4sc; a.bias = g.bias; a.y = g.y;
     a.rows = g.rows; a.ldy = g.ldy;
   } else {
     a.nseg = 0;
-    tiles = (a.rows + rt - 1) / rt;
   }
+  const bool big = a.kind == MK_Q8 && a.xbt && gemm_use_32x32(row_tiles(1), (a.ntok + kG2N - 1) / kG2N);
+  const int tiles = row_tiles(big);
   if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
-  const dim3 grid((a.ntok + kGN - 1) / kGN, tiles);
+  const dim3 grid((a.ntok + (big ? kG2N : kGN) - 1) / (big ? kG2N : kGN), tiles);
   if (a.w2 && (a.kind != MK_Q8 || !a.scale2 || !a.wsum2 || a.resid || a.bias || a.gate)) return hipErrorInvalidValue;
   if (a.kind == MK_Q8) {
-    if (!a.wsum || a.ldw < a.cols / kQB) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
+    if (!a.wsum) return hipErrorInvalidValue;
+    if (big && (!a.xbt || a.ldbt % 4 || a.ldbt < a.ntok)) return hipErrorInvalidValue;
+    if (big) hipLaunchKernelGGL(k_gemm2_q8, grid, dim3(64 * kG2Waves), gemm2_lds_bytes(), st, a);
+    else hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
   } else if (a.kind == MK_Q4) {
     if (!a.q4ns || !a.q4sc || !a.xg || a.ldg < a.cols / 32 || a.ldg % 4) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_gemm_q4, grid, dim3(64 * kGWaves), (size_t)kGStages * kG4Stage, st, a);

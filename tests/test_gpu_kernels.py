@@ -89,14 +89,17 @@ def test_matvec_q1_exact_sums(rows, cols):
 @pytest.mark.parametrize("rows,cols,B", [(1000, 4096, 200), (256, 896, 129), (300, 14336, 17), (7, 128, 1), (4864, 896, 64),
                                          (130, 512, 1024), (300, 896, 2048),
                                          (130, 512, 300)])
-def test_matmul_q8_rows_equal_decode_arithmetic(rows, cols, B):
-    """batched prefill product (int8 MFMA, two activation planes): every token's row bit-identical to rows_q8 on that
-    token's quantised activation - the decode step's arithmetic; ragged row / token counts exercise the tile edges"""
+@pytest.mark.parametrize("kernel", ["16x16", "32x32"])
+def test_matmul_q8_rows_equal_decode_arithmetic(rows, cols, B, kernel, monkeypatch):
+    """batched prefill product (int8 MFMA, two activation planes), each of the two q8 kernels forced (QPH_GEMM): every
+    token's row bit-identical to rows_q8 on that token's quantised activation - the decode step's arithmetic; ragged
+    row / token counts exercise the tile edges"""
+    monkeypatch.setenv("QPH_GEMM", "1" if kernel == "32x32" else "2")
     rng = np.random.default_rng(rows * 13 + cols + B)
     q, s = q8_matrix(rng, rows, cols)
     X = np.stack([act_vector(rng, cols) * rng.uniform(0.1, 10) for _ in range(B)]).astype(np.float32)
     X[B // 2] = 0                                   # an all-zero token
-    print(f"q8 matmul rows={rows} cols={cols} B={B}", flush=True)
+    print(f"q8 matmul {kernel} rows={rows} cols={cols} B={B}", flush=True)
     Y = qa.kernel_matmul(q, s, X)
     for b in range(B):
         xq, bs = O.quant_act(X[b])
