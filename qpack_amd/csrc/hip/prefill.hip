@@ -459,7 +459,7 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
     }
   }
   r0 = gemm_segment(a, r0, RT);
-  const int nb = a.cols / kQB, nst = 2 * nb;
+  const int nb = a.cols / kQB;
 
   // DMA sources: 32 1-KiB row groups per stage (16 of weights, 8 per plane; 16 rows each), 4 to a wave; the lane
   // fetches the logical segment that belongs at physical segment lane % 4 of row lane / 4
@@ -497,15 +497,7 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
     for (int j = 0; j < 4; j++) dma16(src[j] + 64 * s, st + (wave * 4 + j) * 1024);
     if (wave < 2 && !(s & 1)) dma16(esrc + (s >> 1) * estep, st + (wave ? kG2BS : kG2WS));
   };
-  // stage s's loads (this wave's, then everyone's) have landed, and every wave is done with stage s - 1, so the
-  // slot of stage s - 2 is refilled with stage s + 2
-  auto stage_sync = [&](int s) {
-    if (s + 1 >= nst) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    else if (wave < 2 && (s & 1)) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");   // stage s + 1 carries the extras
-    else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    if (!(a.dbg & 4)) __builtin_amdgcn_s_barrier();
-    if (s + 2 < nst && !(a.dbg & 2)) issue(s + 2);
-  };
+
 
   // per-lane LDS offsets: fragment row / token lane % 32, logical segment 2 step + lane / 32, physical ^ swizzle
   const int fr = lane & 31, fh = lane >> 5, fsw = g2_swz(fr);
@@ -523,113 +515,30 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
     for (int ni = 0; ni < 2; ni++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
-  v16i T[2][2];
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  v16i T[2][2] = {{zero, zero}, {zero, zero}};
+  v4i A0[4], A1[4], f0a, f0b, f1a, f1b, f2a, f2b, w0, w1, w2, w3, x0, x1, x2, x3;
+  float nb0 = 0.f, nb1 = 0.f, pb0 = 0.f, pb1 = 0.f;   // token scales of this block / of the previous one
 
+  // one block per iteration: its two stages have landed (every wave's loads: the barrier), every wave is done with
+  // the previous block, whose two slots now take the next block
   issue(0);
   issue(1);
   for (int b = 0; b < nb; b++) {
-    const int s0 = 2 * b, s1 = s0 + 1;
-    if (a.dbg & 1) { stage_sync(s0); stage_sync(s1); continue; }
-    const uint32_t st0 = sbase + (uint32_t)((s0 % kG2Slots) * kG2Stage), st1 = sbase + (uint32_t)((s1 % kG2Slots) * kG2Stage);
-    // ---- hi plane, steps 0 and 1 (stage s0)
-    stage_sync(s0);
-    {
-      v4i A0 = lds_read16o<0>(st0 + ra0), A1 = lds_read16o<2048>(st0 + ra0);
-      v4i B0 = lds_read16o<kG2XH>(st0 + rb0), B1 = lds_read16o<kG2XH + 2048>(st0 + rb0);
-      v4i C0 = lds_read16o<0>(st0 + ra1), C1 = lds_read16o<2048>(st0 + ra1);
-      v4i D0 = lds_read16o<kG2XH>(st0 + rb1), D1 = lds_read16o<kG2XH + 2048>(st0 + rb1);
-      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, zero, 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, zero, 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, zero, 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, zero, 0, 0, 0);
-      G2_WAIT(0, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
-    }
-    // ---- hi plane, steps 2 and 3 (stage s1); the shift-add with the row sums; lo plane, steps 0-3; fp32 step
-    stage_sync(s1);
-    {
-      v4i A0 = lds_read16o<0>(st1 + ra0), A1 = lds_read16o<2048>(st1 + ra0);
-      v4i B0 = lds_read16o<kG2XH>(st1 + rb0), B1 = lds_read16o<kG2XH + 2048>(st1 + rb0);
-      v4i C0 = lds_read16o<0>(st1 + ra1), C1 = lds_read16o<2048>(st1 + ra1);
-      v4i D0 = lds_read16o<kG2XH>(st1 + rb1), D1 = lds_read16o<kG2XH + 2048>(st1 + rb1);
-      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, T[0][0], 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, T[0][1], 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, T[1][0], 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, T[1][1], 0, 0, 0);
-      v4i W0 = lds_read16o<0>(st0 + rws), W1 = lds_read16o<32>(st0 + rws), W2 = lds_read16o<64>(st0 + rws),
-          W3 = lds_read16o<96>(st0 + rws);
-      G2_WAIT(4, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
-      v4i X0 = lds_read16o<128>(st0 + rws), X1 = lds_read16o<160>(st0 + rws), X2 = lds_read16o<192>(st0 + rws),
-          X3 = lds_read16o<224>(st0 + rws);
-      // lo step 0 (stage s0, still intact: its slot is refilled only after the next barrier)
-      A0 = lds_read16o<0>(st0 + ra0); A1 = lds_read16o<2048>(st0 + ra0);
-      B0 = lds_read16o<kG2XL>(st0 + rb0); B1 = lds_read16o<kG2XL + 2048>(st0 + rb0);
-      G2_WAIT(8, "+v"(W0), "+v"(W1), "+v"(W2), "+v"(W3));
-      if (!(a.dbg & 8)) {
-        const v4i w[4] = {W0, W1, W2, W3};
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          T[0][0][r] = T[0][0][r] * 256 + w[r >> 2][r & 3];
-          T[0][1][r] = T[0][1][r] * 256 + w[r >> 2][r & 3];
-        }
-      }
-      G2_WAIT(4, "+v"(X0), "+v"(X1), "+v"(X2), "+v"(X3));
-      if (!(a.dbg & 8)) {
-        const v4i w[4] = {X0, X1, X2, X3};
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          T[1][0][r] = T[1][0][r] * 256 + w[r >> 2][r & 3];
-          T[1][1][r] = T[1][1][r] * 256 + w[r >> 2][r & 3];
-        }
-      }
-      C0 = lds_read16o<0>(st0 + ra1); C1 = lds_read16o<2048>(st0 + ra1);
-      D0 = lds_read16o<kG2XL>(st0 + rb1); D1 = lds_read16o<kG2XL + 2048>(st0 + rb1);
-      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, T[0][0], 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, T[0][1], 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, T[1][0], 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, T[1][1], 0, 0, 0);
-      A0 = lds_read16o<0>(st1 + ra0); A1 = lds_read16o<2048>(st1 + ra0);
-      B0 = lds_read16o<kG2XL>(st1 + rb0); B1 = lds_read16o<kG2XL + 2048>(st1 + rb0);
-      G2_WAIT(4, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
-      C0 = lds_read16o<0>(st1 + ra1); C1 = lds_read16o<2048>(st1 + ra1);
-      D0 = lds_read16o<kG2XL>(st1 + rb1); D1 = lds_read16o<kG2XL + 2048>(st1 + rb1);
-      G2_WAIT(4, "+v"(A0), "+v"(A1), "+v"(B0), "+v"(B1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, T[0][0], 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B1, T[0][1], 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B0, T[1][0], 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, T[1][1], 0, 0, 0);
-      float bs0 = lds_read4o<0>(st0 + rbs), bs1 = lds_read4o<128>(st0 + rbs);
-      G2_WAIT(2, "+v"(C0), "+v"(C1), "+v"(D0), "+v"(D1));
-      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D0, T[0][0], 0, 0, 0);
-      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C0, D1, T[0][1], 0, 0, 0);
-      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D0, T[1][0], 0, 0, 0);
-      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(C1, D1, T[1][1], 0, 0, 0);
-      G2_WAIT(0, "+v"(bs0), "+v"(bs1));
-      if (!(a.dbg & 8))
-#pragma unroll
-      for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          acc[mi][0][r] = __builtin_fmaf(bs0, (float)T[mi][0][r], acc[mi][0][r]);
-          acc[mi][1][r] = __builtin_fmaf(bs1, (float)T[mi][1][r], acc[mi][1][r]);
-        }
-    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (!(a.dbg & 4)) __builtin_amdgcn_s_barrier();
+    if (b + 1 < nb && !(a.dbg & 2)) { issue(2 * b + 2); issue(2 * b + 3); }
+    const uint32_t stA = sbase + (uint32_t)(((2 * b) % kG2Slots) * kG2Stage), stB = stA + kG2Stage;
+    if (a.dbg & 1) continue;
+#include "gemm2_loop.inc"
+    pb0 = nb0; pb1 = nb1;
   }
+  // the last block's fp32 step of rows mi1 (the loop defers it under the next block's first MFMAs)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      acc[1][0][r] = __builtin_fmaf(pb0, (float)T[1][0][r], acc[1][0][r]);
+      acc[1][1][r] = __builtin_fmaf(pb1, (float)T[1][1][r], acc[1][1][r]);
+    }
 
   if (paired) {
     // the gate waves (rows 0-127) hand gate = acc * scale to the up waves through LDS ([128 tokens][132 floats] over
