@@ -44,12 +44,12 @@ def wait(*names):
 
 
 def RA(ks, mi):
-    return f"lds_read16o<{mi * 2048}>({'stA' if ks < 2 else 'stB'} + {'ra1' if ks & 1 else 'ra0'})"
+    return f"lds_read16o<{mi * 4096}>(st + ra[{ks}])"
 
 
 def RB(plane, ks, ni):
     base = "kG2XH" if plane == "h" else "kG2XL"
-    return f"lds_read16o<{base} + {ni * 2048}>({'stA' if ks < 2 else 'stB'} + {'rb1' if ks & 1 else 'rb0'})"
+    return f"lds_read16o<{base} + {ni * 4096}>(st + rb[{ks}])"
 
 
 def fp32_step(t, half, bs):
@@ -89,13 +89,13 @@ def valu_q4(ks):
 def extras_ws(mi, reg):
     def f():
         for j in range(4):
-            read(f"{reg}{j}", f"lds_read16o<{128 * mi + 32 * j}>(stA + rws)")
+            read(f"{reg}{j}", f"lds_read16o<{128 * mi + 32 * j}>(st + rws)")
     return f
 
 
 def extras_bs():
-    read("nb0", "lds_read4o<0>(stA + rbs)")
-    read("nb1", "lds_read4o<128>(stA + rbs)")
+    read("nb0", "lds_read4o<0>(st + rbs)")
+    read("nb1", "lds_read4o<128>(st + rbs)")
 
 
 quarters = [

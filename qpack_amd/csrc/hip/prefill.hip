@@ -427,14 +427,19 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
 //   (row bit 2, row bit 1 ^ row bit 3), so the 32 rows of a fragment read spread over the 64 banks.
 //   fragments: lane l reads A = W[row l % 32][16 (l / 32) + 0..15] and B = plane[token l % 32][16 (l / 32) + 0..15]
 //   within the 32-deep step; C lane l holds rows 8 (r / 4) + 4 (l / 32) + r % 4 (r = 0..15) of token l % 32.
-constexpr int kG2M = 256, kG2N = 128, kG2Slots = 4, kG2Waves = 8;
-constexpr int kG2XH = 256 * 64, kG2XL = kG2XH + 128 * 64, kG2WS = kG2XL + 128 * 64, kG2BS = kG2WS + 1024;
-constexpr int kG2Stage = kG2BS + 1024;   // 34816 bytes (the block scales' second 512 bytes unused)
-constexpr int kG2GX = 132;                  // gate hand-off row pitch (floats)
+constexpr int kG2M = 256, kG2N = 128, kG2Slots = 2, kG2Waves = 8;
+// stage = one 128-column block: the rows' block sums [256] and the tokens' block scales [128] first (small constant
+// offsets for their reads), then weights [256 rows][128 B], hi plane [128 tokens][128 B], lo plane likewise
+constexpr int kG2WS = 0, kG2BS = 1024, kG2W = 2048, kG2XH = kG2W + 256 * 128, kG2XL = kG2XH + 128 * 128;
+constexpr int kG2Stage = kG2XL + 128 * 128;   // 67584 bytes (the block scales' second 512 bytes unused)
+constexpr int kG2GX = 132;                    // gate hand-off row pitch (floats)
 size_t gemm2_lds_bytes() { return (size_t)kG2Slots * kG2Stage; }
 static_assert(kG2N * kG2GX * 4 <= kG2Slots * kG2Stage, "gate hand-off fits in the ring");
+static_assert(kG2XL + 4096 + 16 < 65536, "fragment offsets fit the ds_read offset field");
 
-__device__ __forceinline__ int g2_swz(int r) { return (((r >> 2) & 1) << 1) | (((r >> 1) ^ (r >> 3)) & 1); }
+// physical 16-byte segment of logical segment s in 128-byte row r: s ^ g2_swz(r).  The 8 rows of a 128-byte (32-bank)
+// read phase and the 8 same-parity rows of a 256-byte (64-bank) phase all land on distinct segments.
+__device__ __forceinline__ int g2_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
 #define G2_WAIT(n, ...) asm volatile("s_waitcnt lgkmcnt(" #n ")" : __VA_ARGS__)
 
@@ -461,24 +466,22 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
   r0 = gemm_segment(a, r0, RT);
   const int nb = a.cols / kQB;
 
-  // DMA sources: 32 1-KiB row groups per stage (16 of weights, 8 per plane; 16 rows each), 4 to a wave; the lane
-  // fetches the logical segment that belongs at physical segment lane % 4 of row lane / 4
-  const int drow = lane >> 2, dseg = (lane & 3) ^ g2_swz(drow);
-  const int8_t *src[4];
+  // DMA sources: 64 1-KiB row groups per stage (32 of weights, 16 per plane; 8 rows of 128 B each), 8 to a wave; the
+  // lane fetches the logical segment that belongs at physical segment lane % 8 of row lane / 8
+  const int8_t *src[8];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int q = wave * 4 + j;
-    if (q < 16) {
-      const int row = 16 * q + drow;
+  for (int j = 0; j < 8; j++) {
+    const int q = wave * 8 + j, row = 8 * (q & 31) + (lane >> 3), seg = (lane & 7) ^ g2_swz(row);
+    if (q < 32) {
       const int8_t *wm = paired && row >= 128 ? a.w2 : a.w;
-      src[j] = wm + (size_t)min(r0 + (paired ? (row & 127) : row), a.rows - 1) * a.cols + dseg * 16;
+      src[j] = wm + (size_t)min(r0 + (paired ? (row & 127) : row), a.rows - 1) * a.cols + seg * 16;
     } else {
-      const int tok = 16 * (q & 7) + drow;
-      src[j] = (q < 24 ? a.xh : a.xl) + (size_t)min(t0 + tok, a.ntok - 1) * a.ldq + dseg * 16;
+      const int tok = row & 127;
+      src[j] = (q < 48 ? a.xh : a.xl) + (size_t)min(t0 + tok, a.ntok - 1) * a.ldq + seg * 16;
     }
   }
-  // once per block, with its first stage: wave 0 the tile's 256 row sums (16 bytes = 4 rows a lane), wave 1 the 128
-  // token scales (lanes 32-63 repeat lanes 0-31 into the unused half), both from the block-major copies
+  // with each block: wave 0 the tile's 256 row sums (16 bytes = 4 rows a lane), wave 1 the 128 token scales (lanes
+  // 32-63 repeat lanes 0-31 into the unused half), both from the block-major copies
   const int pitch = ws_pitch(a.rows);
   const char *esrc = nullptr;
   size_t estep = 0;
@@ -491,21 +494,24 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
     esrc = (const char *)(a.xbt + min(t0 + 4 * (lane & 31), a.ldbt - 4));
     estep = 4 * (size_t)a.ldbt;
   }
-  auto issue = [&](int s) {
-    char *st = smem + (size_t)(s % kG2Slots) * kG2Stage;
+  auto issue = [&](int b) {
+    char *st = smem + (size_t)(b % kG2Slots) * kG2Stage;
 #pragma unroll
-    for (int j = 0; j < 4; j++) dma16(src[j] + 64 * s, st + (wave * 4 + j) * 1024);
-    if (wave < 2 && !(s & 1)) dma16(esrc + (s >> 1) * estep, st + (wave ? kG2BS : kG2WS));
+    for (int j = 0; j < 8; j++) dma16(src[j] + kQB * b, st + kG2W + (wave * 8 + j) * 1024);
+    if (wave < 2) dma16(esrc + b * estep, st + (wave ? kG2BS : kG2WS));
   };
 
-
-  // per-lane LDS offsets: fragment row / token lane % 32, logical segment 2 step + lane / 32, physical ^ swizzle
+  // per-lane LDS offsets of step ks: fragment row / token lane % 32, logical segment 2 ks + lane / 32, swizzled
   const int fr = lane & 31, fh = lane >> 5, fsw = g2_swz(fr);
-  const uint32_t o0 = fr * 64 + ((fh ^ fsw) << 4), o1 = fr * 64 + (((2 | fh) ^ fsw) << 4);
-  const uint32_t ra0 = 64 * wr * 64 + o0, ra1 = 64 * wr * 64 + o1;   // + 2048 mi
-  const uint32_t rb0 = 64 * wc * 64 + o0, rb1 = 64 * wc * 64 + o1;   // + plane + 2048 ni
-  const uint32_t rws = kG2WS + (64 * wr + 4 * fh) * 4;               // + 128 mi + 32 j
-  const uint32_t rbs = kG2BS + (64 * wc + fr) * 4;                   // + 128 ni
+  uint32_t ra[4], rb[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) {
+    const uint32_t o = fr * 128 + (((2 * ks + fh) ^ fsw) << 4);
+    ra[ks] = kG2W + 64 * wr * 128 + o;   // + 4096 mi
+    rb[ks] = 64 * wc * 128 + o;          // + plane + 4096 ni
+  }
+  const uint32_t rws = kG2WS + (64 * wr + 4 * fh) * 4;   // + 128 mi + 32 j
+  const uint32_t rbs = kG2BS + (64 * wc + fr) * 4;       // + 128 ni
   const uint32_t sbase = lds_addr(smem);
 
   float acc[2][2][16];
@@ -520,15 +526,14 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
   v4i A0[4], A1[4], f0a, f0b, f1a, f1b, f2a, f2b, w0, w1, w2, w3, x0, x1, x2, x3;
   float nb0 = 0.f, nb1 = 0.f, pb0 = 0.f, pb1 = 0.f;   // token scales of this block / of the previous one
 
-  // one block per iteration: its two stages have landed (every wave's loads: the barrier), every wave is done with
-  // the previous block, whose two slots now take the next block
+  // one block per iteration: it has landed (every wave's loads: the barrier), every wave is done with the previous
+  // block, whose slot now takes the next one
   issue(0);
-  issue(1);
   for (int b = 0; b < nb; b++) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (!(a.dbg & 4)) __builtin_amdgcn_s_barrier();
-    if (b + 1 < nb && !(a.dbg & 2)) { issue(2 * b + 2); issue(2 * b + 3); }
-    const uint32_t stA = sbase + (uint32_t)(((2 * b) % kG2Slots) * kG2Stage), stB = stA + kG2Stage;
+    if (b + 1 < nb && !(a.dbg & 2)) issue(b + 1);
+    const uint32_t st = sbase + (uint32_t)((b % kG2Slots) * kG2Stage);
     if (a.dbg & 1) continue;
 #include "gemm2_loop.inc"
     pb0 = nb0; pb1 = nb1;
