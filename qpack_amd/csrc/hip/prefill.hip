@@ -825,9 +825,10 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
     }
 }
 
-// q8: which product kernel.  The 32 x 32 one does twice a 16 x 16 workgroup's work ~12 % faster, so it wins unless its
-// fewer, larger workgroups leave CUs idle: compare ceil(n2 / CUs) x 1.76 with ceil(2 n2 / CUs) rounds (n2 = its
-// workgroup count).  QPH_GEMM=1 / 2 forces the 32 x 32 / 16 x 16 kernel.
+// q8: which product kernel.  A 32 x 32 workgroup does twice a 16 x 16 one's work in ~1.45 x its time (C4 shapes on
+// MI355X: 2 x 14336 x 4096 578 vs 707 us, 4096 x 4096 173 vs 215, 6144 x 4096 152 vs 160), so it wins unless its fewer,
+// larger workgroups leave CUs idle: ceil(n2 / CUs) x 1.45 against ceil(2 n2 / CUs) rounds (n2 = its workgroup count).
+// QPH_GEMM=1 / 2 forces the 32 x 32 / 16 x 16 kernel.
 static bool gemm_use_32x32(int row_tiles32, int token_tiles32) {
   const char *fe = getenv("QPH_GEMM");   // read per launch: tests switch it between calls
   const int force = fe ? atoi(fe) : 0;
@@ -838,7 +839,7 @@ static bool gemm_use_32x32(int row_tiles32, int token_tiles32) {
     return std::max(1, n);
   }();
   const long n2 = (long)row_tiles32 * token_tiles32;
-  return (double)((n2 + cus - 1) / cus) * 1.76 < (double)((2 * n2 + cus - 1) / cus);
+  return (double)((n2 + cus - 1) / cus) * 1.45 < (double)((2 * n2 + cus - 1) / cus);
 }
 
 hipError_t launch_gemm(const GemmArgs &a0, hipStream_t st) {
