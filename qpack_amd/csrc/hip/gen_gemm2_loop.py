@@ -104,42 +104,93 @@ quarters = [
     Quarter("Q3: lo plane of rows mi0 || shift-add of rows mi1", 0, "l", False, valu_q3, extras_ws(1, "x")),
     Quarter("Q4: lo plane of rows mi1 || fp32 step of rows mi0", 1, "l", False, valu_q4, extras_bs),
 ]
-steps = [(q, ks) for q in quarters for ks in range(4)]   # 16 steps in order
-bset = [f"f{i}" for i in range(LOOK + 1)]
 
 
-def regs_of(i):
-    q, ks = steps[i]
-    s = bset[i % (LOOK + 1)]
-    a = f"A{q.mi}[{ks}]"
-    return a, f"{s}a", f"{s}b"
+def schedule_halves():
+    """the four quarters above: 8 MFMAs on one row half per step pair; token fragments read once per row half"""
+    steps = [(q, ks) for q in quarters for ks in range(4)]
+    bset = [f"f{i}" for i in range(LOOK + 1)]
+
+    def regs_of(i):
+        q, ks = steps[i]
+        s_ = bset[i % (LOOK + 1)]
+        return f"A{q.mi}[{ks}]", f"{s_}a", f"{s_}b"
+
+    def issue_step(i):
+        q, ks = steps[i]
+        if ks == 0 and q.extras:
+            q.extras()
+        a, b0, b1 = regs_of(i)
+        if q.read_a:
+            read(a, RA(ks, q.mi))
+        read(b0, RB(q.plane, ks, 0))
+        read(b1, RB(q.plane, ks, 1))
+
+    for i in range(LOOK):
+        issue_step(i)
+    for i, (q, ks) in enumerate(steps):
+        if ks == 0:
+            emit(f"// ---- {q.title}")
+        if i + LOOK < len(steps):
+            issue_step(i + LOOK)
+        a, b0, b1 = regs_of(i)
+        wait(*((a,) if q.read_a else ()), b0, b1)
+        t0, t1 = f"T[{q.mi}][0]", f"T[{q.mi}][1]"
+        first = q.plane == "h" and ks == 0
+        emit(f"{t0} = __builtin_amdgcn_mfma_i32_32x32x32_i8({a}, {b0}, {'zero' if first else t0}, 0, 0, 0);")
+        emit(f"{t1} = __builtin_amdgcn_mfma_i32_32x32x32_i8({a}, {b1}, {'zero' if first else t1}, 0, 0, 0);")
+        q.valu(ks)
 
 
-def issue_step(i):
-    q, ks = steps[i]
-    if ks == 0 and q.extras:
-        q.extras()
-    a, b0, b1 = regs_of(i)
-    if q.read_a:
-        read(a, RA(ks, q.mi))
-    read(b0, RB(q.plane, ks, 0))
-    read(b1, RB(q.plane, ks, 1))
+def schedule_steps():
+    """4 MFMAs (all four tiles) per step, every fragment read once per plane (A held from hi to lo); the VALU steps
+    staggered by tile pair: the shift-add of row half mi0 under the last hi MFMAs of mi1 and the first lo MFMAs, the
+    fp32 step of mi0 under the last lo MFMAs of mi1, that of mi1 under the next block's first hi MFMAs"""
+    LOOK = 1   # a step is 4 MFMAs; two steps of reads (16) would pass the 15-read limit with the row sums
+    steps = [("h", ks) for ks in range(4)] + [("l", ks) for ks in range(4)]
+    bset = [f"f{i}" for i in range(LOOK + 1)]
+
+    def issue_step(i):
+        plane, ks = steps[i]
+        if i == 4:
+            extras_ws(0, "w")()
+            extras_ws(1, "x")()
+        if i == 7:
+            extras_bs()
+        s_ = bset[i % (LOOK + 1)]
+        if plane == "h":
+            read(f"A0[{ks}]", RA(ks, 0)); read(f"A1[{ks}]", RA(ks, 1))
+        read(f"{s_}a", RB(plane, ks, 0)); read(f"{s_}b", RB(plane, ks, 1))
+
+    for i in range(LOOK):
+        issue_step(i)
+    for i, (plane, ks) in enumerate(steps):
+        if i + LOOK < len(steps):
+            issue_step(i + LOOK)
+        s_ = bset[i % (LOOK + 1)]
+        b0, b1 = f"{s_}a", f"{s_}b"
+        wait(*((f"A0[{ks}]", f"A1[{ks}]") if plane == "h" else ()), b0, b1)
+        first = plane == "h" and ks == 0
+        for mi in (0, 1):
+            if plane == "l" and ks == 0:   # the shift-add of this row half just before its first lo MFMAs
+                shift_add(f"T{mi}0", "w" if mi == 0 else "x")
+                shift_add(f"T{mi}1", "w" if mi == 0 else "x")
+            for ni, b in ((0, b0), (1, b1)):
+                t = f"T[{mi}][{ni}]"
+                emit(f"{t} = __builtin_amdgcn_mfma_i32_32x32x32_i8(A{mi}[{ks}], {b}, {'zero' if first else t}, 0, 0, 0);")
+            if plane == "h" and ks == 0 and mi == 0:   # the previous block's fp32 step of mi1 before its first hi MFMA
+                for half in (0, 1):
+                    fp32_step("T10", half, "pb0")
+                for half in (0, 1):
+                    fp32_step("T11", half, "pb1")
+        if plane == "l" and ks == 3:   # this block's fp32 step of mi0 under the last MFMAs of mi1
+            for half in (0, 1):
+                fp32_step("T00", half, "nb0")
+            for half in (0, 1):
+                fp32_step("T01", half, "nb1")
 
 
-for i in range(LOOK):
-    issue_step(i)
-for i, (q, ks) in enumerate(steps):
-    if ks == 0:
-        emit(f"// ---- {q.title}")
-    if i + LOOK < len(steps):
-        issue_step(i + LOOK)
-    a, b0, b1 = regs_of(i)
-    wait(*((a,) if q.read_a else ()), b0, b1)
-    t0, t1 = f"T[{q.mi}][0]", f"T[{q.mi}][1]"
-    first = q.plane == "h" and ks == 0
-    emit(f"{t0} = __builtin_amdgcn_mfma_i32_32x32x32_i8({a}, {b0}, {'zero' if first else t0}, 0, 0, 0);")
-    emit(f"{t1} = __builtin_amdgcn_mfma_i32_32x32x32_i8({a}, {b1}, {'zero' if first else t1}, 0, 0, 0);")
-    q.valu(ks)
+(schedule_halves if len(sys.argv) > 1 and sys.argv[1] == "halves" else schedule_steps)()
 assert not issued, issued
 
 sys.stdout.write("// generated by gen_gemm2_loop.py (the schedule and its lgkmcnt waits) - edit it there\n" + "\n".join(out) + "\n")
