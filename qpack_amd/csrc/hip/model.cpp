@@ -677,7 +677,9 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   if (iters <= 0) iters = 1;
   // consecutive launches walk the layers, as the token loop does, so no launch finds its weights in the
   // 256 MiB last-level cache from the previous one
-  const int L = cfg_.layers, d = cfg_.hidden, cap = 1 << 20;
+  // QPH_TK_LAYERS (measurement hook): walk only that many layers, so repeated launches find their weights cached
+  const char *tkl = getenv("QPH_TK_LAYERS");
+  const int L = tkl ? std::max(1, std::min(cfg_.layers, atoi(tkl))) : cfg_.layers, d = cfg_.hidden, cap = 1 << 20;
   int li = 0;
   const float eps = cfg_.rms_eps;
   write_ctl(0, std::min(pos_, ctx_ - 1));
