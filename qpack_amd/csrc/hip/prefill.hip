@@ -921,11 +921,14 @@ hipError_t launch_pf_rope(const PfRopeArgs &a, int B, hipStream_t st) {
 // 32-position blocks through LDS (K as stored, V transposed), with an online softmax per token:
 //   scores  S^T[p][t] = K[p] . q[t] on v_mfma_f32_16x16x32_f16: A = K rows (exact fp16), B = q^T; q is fp32, so it
 //           enters as hi + lo halves (hi = f16(q), lo = f16(q - hi)) - two MFMAs, products exact, fp32 accumulation;
-//           scaled by 1/sqrt(hd) like the reference;
+//           q is pre-scaled by log2(e) / sqrt(hd) (the reference's 1 / sqrt(hd), in base-2 units);
 //   values  O^T[d][t] += V^T[d][p] P^T[p][t], P split into hi + lo halves the same way; the C layout of S^T
 //           (lane l: token l % 16, positions 4 (l / 16) + i of each 16-block) is the B layout the value MFMA needs once
 //           its k index runs over those 8 positions, so P never leaves the registers;
-//   softmax each lane keeps its token's running max and sum (reduced over the 4 lanes holding that token).
+//   softmax each lane keeps its token's running max and sum (reduced over the 4 lanes holding that token); the
+//           exponentials are the hardware exp2 (v_exp_f32, ~1 ulp) instead of the reference's exp256 polynomial
+//           (kernels_x86.cpp:406-417): a float-order difference within the logit tolerance, like the rest of this
+//           kernel's order (the reference-order mode has its own kernel, k_ex_pf_attn).
 constexpr int kPfKB = 32;      // cache positions per block
 constexpr int kPfAttnWaves = 8;   // units (16-token tile, query head) per workgroup, one per wave: they share the K / V
 template <int HD>
@@ -959,7 +962,9 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   const int wg_last = a.p0 + min((ulast / rep) * 16 + 15, a.ntok - 1);
   const int nkb = wg_last / kPfKB + 1;
 
-  // q^T fragments: lane holds q[t][32 s + 8 lg + 0..7] as hi / lo halves
+  // q^T fragments: lane holds q[t][32 s + 8 lg + 0..7] as hi / lo halves, pre-scaled by log2(e) / sqrt(hd) so the
+  // scores come out in base-2 units for the hardware exp2 (v_exp_f32)
+  const float qscale = 1.4426950408889634f / sqrtf((float)HD);
   h8 qh[HD / 32], ql[HD / 32];
   {
     const float *qt = a.q + (size_t)(tok_ok ? t : 0) * a.ldq + head * HD;
@@ -967,7 +972,7 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
     for (int s = 0; s < HD / 32; s++) {
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float x = tok_ok ? qt[32 * s + 8 * lg + j] : 0.f;
+        const float x = tok_ok ? qt[32 * s + 8 * lg + j] * qscale : 0.f;
         const _Float16 h = (_Float16)x;
         qh[s][j] = h; ql[s][j] = (_Float16)(x - (float)h);
       }
@@ -977,7 +982,6 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
 #pragma unroll
   for (int d = 0; d < DT; d++) o[d] = (f4){0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
-  const float scl = 1.f / sqrtf((float)HD);
   const uint16_t *kg = a.kc + g * HD, *vg = a.vc + g * HD;
 
   // piece i of a block: position (tid + NT i) / (HD / 8), dims 8 ((tid + NT i) % (HD / 8)) + 0..7 (threads past the
@@ -1043,18 +1047,21 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int p = pb + 16 * mt + 4 * lg + i;
-        const float x = (tok_ok && p <= ptok) ? sc[mt][i] * scl : -INFINITY;
+        const float x = (tok_ok && p <= ptok) ? sc[mt][i] : -INFINITY;
         sv[4 * mt + i] = x; bm = fmaxf(bm, x);
       }
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float mn = fmaxf(m, bm);
-    const float corr = m == -INFINITY ? 0.f : exp_poly(m - mn);
+    // exp2 of -inf is 0: masked scores need no select; a token with no valid position yet (only tokens past the
+    // batch, never stored) keeps mn = -inf, replaced by 0 so no -inf - -inf appears
+    const float mz = mn == -INFINITY ? 0.f : mn;
+    const float corr = __builtin_amdgcn_exp2f(m - mz);
     float rs = 0.f;
     h8 ph, pl;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const float pv = sv[j] == -INFINITY ? 0.f : exp_poly(sv[j] - mn);
+      const float pv = __builtin_amdgcn_exp2f(sv[j] - mz);
       rs += pv;
       const _Float16 h = (_Float16)pv;
       ph[j] = h; pl[j] = (_Float16)(pv - (float)h);
