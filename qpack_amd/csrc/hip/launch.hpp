@@ -145,6 +145,10 @@ struct GemmArgs {
   // optional (q8): a second matrix of the same shape (the up matrix, with w / scale / wsum the gate's): one launch
   // computes both products for each 64-row tile and stores only y = silu(gate product) * (up product)
   const int8_t *w2; const float *scale2; const int *wsum2;
+  // optional (with w2, 32 x 32 kernel only, rows % 128 == 0): instead of y, the SwiGLU output quantised for the next
+  // product - planes oh / ol [ntok][ldq], block scales ob [ntok][ldb] and obt [rows / 128][ldbt] (the quantiser's
+  // arithmetic: every 128-row tile of the pair is one quantisation block of each token)
+  int8_t *oh, *ol; float *ob, *obt;
   // optional: nseg (2 .. kGemmMaxSeg) matrices of this kind and column count over the same activations (q / k / v), the
   // segment fields replacing w / scale / wsum / q4ns / q4sc / bias / y / ldy / rows; each starts on a fresh row tile
   int nseg;
@@ -160,6 +164,8 @@ hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipSt
 // q4 rows: per (block, group, row) the sum of the nibbles and the f32 scale, group-major within each 128-column block
 hipError_t launch_q4_prep(const uint8_t *w, const uint16_t *sc, int rows, int cols, int *out_ns, float *out_sc, hipStream_t st);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st);
+// whether launch_gemm runs this q8 launch on the 32 x 32 kernel (the one that can quantise a SwiGLU pair's output)
+bool gemm_uses_32x32(const GemmArgs &a);
 // token t of the batch at position p0 + t: RoPE on q [t][ldq] (in place) and k, fp16 k / v rows into the caches
 struct PfRopeArgs {
   float *q; int ldq;

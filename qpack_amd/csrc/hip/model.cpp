@@ -161,9 +161,12 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     pf_k_ = (float *)dalloc(4 * B * kvd_); pf_v_ = (float *)dalloc(4 * B * kvd_);
     pf_g_ = (float *)dalloc(4 * B * ff);
     pf_xh_ = (int8_t *)dalloc(B * pf_ldq_); pf_xl_ = (int8_t *)dalloc(B * pf_ldq_);
+    pf_xh2_ = (int8_t *)dalloc(B * pf_ldq_); pf_xl2_ = (int8_t *)dalloc(B * pf_ldq_);   // the SwiGLU output, quantised
     pf_xb_ = (float *)dalloc(4 * B * (pf_ldq_ / 128 + 1));
     pf_ldbt_ = (int)(B + 63) / 64 * 64;
     pf_xbt_ = (float *)dalloc(4ull * pf_ldbt_ * (pf_ldq_ / 128 + 1));
+    pf_xb2_ = (float *)dalloc(4 * B * (pf_ldq_ / 128 + 1));
+    pf_xbt2_ = (float *)dalloc(4ull * pf_ldbt_ * (pf_ldq_ / 128 + 1));
     pf_ldg_ = (pf_ldq_ / 32 + 3) / 4 * 4;
     pf_xg_ = (int *)dalloc(4 * B * pf_ldg_);
     pf_tok_ = (int *)dalloc(4 * B);
@@ -433,18 +436,28 @@ void HipLlama::prefill_batched(const int *toks, int n) {
       quant(PRO_QUANT, pf_att_, qd_, nullptr, qd_, B);
       gemm(ly.wo, pf_x_, d, nullptr, true, B);
       quant(PRO_NORM, pf_x_, d, ly.fn, d, B);
+      bool fused = false;   // h = silu(gate) * up quantised by the product's store, straight into the second planes
       if (ly.wg.kind == MK_Q8 && ly.wu.kind == MK_Q8) {   // gate and up in one launch, only h = silu(gate) * up stored
         GemmArgs a{}; a.kind = MK_Q8; a.w = (const int8_t *)ly.wg.q; a.scale = (const float *)ly.wg.s; a.wsum = ly.wg.rs;
         a.w2 = (const int8_t *)ly.wu.q; a.scale2 = (const float *)ly.wu.s; a.wsum2 = ly.wu.rs;
         a.rows = ff; a.cols = d; a.xbt = pf_xbt_; a.ldbt = pf_ldbt_; a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B;
         a.ldq = pf_ldq_; a.ldb = nb_ld; a.y = pf_g_; a.ldy = ff;
+        fused = ly.wd.kind == MK_Q8 && ff % 128 == 0 && gemm_uses_32x32(a);
+        if (fused) { a.oh = pf_xh2_; a.ol = pf_xl2_; a.ob = pf_xb2_; a.obt = pf_xbt2_; }
         QPH_CK(launch_gemm(a, st_));
       } else {
         gemm(ly.wg, pf_g_, ff, nullptr, false, B);
         gemm(ly.wu, pf_g_, ff, nullptr, false, B, pf_g_);   // h = silu(gate) * up, in place over the gate product
       }
-      quant(PRO_QUANT, pf_g_, ff, nullptr, ff, B);
-      gemm(ly.wd, pf_x_, d, nullptr, true, B);
+      if (fused) {
+        GemmArgs a{}; a.kind = MK_Q8; a.w = (const int8_t *)ly.wd.q; a.scale = (const float *)ly.wd.s; a.rows = ly.wd.rows;
+        a.cols = ly.wd.cols; a.wsum = ly.wd.rs; a.xbt = pf_xbt2_; a.ldbt = pf_ldbt_; a.xh = pf_xh2_; a.xl = pf_xl2_;
+        a.xb = pf_xb2_; a.ntok = B; a.ldq = pf_ldq_; a.ldb = nb_ld; a.y = pf_x_; a.ldy = d; a.resid = 1;
+        QPH_CK(launch_gemm(a, st_));
+      } else {
+        quant(PRO_QUANT, pf_g_, ff, nullptr, ff, B);
+        gemm(ly.wd, pf_x_, d, nullptr, true, B);
+      }
     }
     pos_ += B;
   }

@@ -107,6 +107,8 @@ class HipLlama {
   float *pf_xb_ = nullptr, *pf_xbt_ = nullptr;   // block scales token-major [B][nb], block-major [nb][pf_ldbt_]
   int pf_ldbt_ = 0;
   int8_t *pf_xh_ = nullptr, *pf_xl_ = nullptr;
+  int8_t *pf_xh2_ = nullptr, *pf_xl2_ = nullptr;   // second planes: the SwiGLU output quantised by the gate / up store
+  float *pf_xb2_ = nullptr, *pf_xbt2_ = nullptr;
   int *pf_tok_ = nullptr, *pf_xg_ = nullptr;
   void prefill_batched(const int *toks, int n);
 

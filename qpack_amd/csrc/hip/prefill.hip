@@ -434,7 +434,7 @@ constexpr int kG2WS = 0, kG2BS = 1024, kG2W = 2048, kG2XH = kG2W + 256 * 128, kG
 constexpr int kG2Stage = kG2XL + 128 * 128;   // 67584 bytes (the block scales' second 512 bytes unused)
 constexpr int kG2GX = 132;                    // gate hand-off row pitch (floats)
 size_t gemm2_lds_bytes() { return (size_t)kG2Slots * kG2Stage; }
-static_assert(kG2N * kG2GX * 4 <= kG2Slots * kG2Stage, "gate hand-off fits in the ring");
+static_assert(kG2N * kG2GX * 4 + 2 * kG2N * 4 <= kG2Slots * kG2Stage, "gate hand-off and block maxima fit in the ring");
 static_assert(kG2XL + 4096 + 16 < 65536, "fragment offsets fit the ds_read offset field");
 
 // physical 16-byte segment of logical segment s in 128-byte row r: s ^ g2_swz(r).  The 8 rows of a 128-byte (32-bank)
@@ -523,7 +523,8 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
       for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   v16i T[2][2] = {{zero, zero}, {zero, zero}};
-  v4i A0[4], A1[4], f0a, f0b, f1a, f1b, f2a, f2b, w0, w1, w2, w3, x0, x1, x2, x3;
+  v4i A0[4], A1[4], f0a, f0b, f1a, f1b, w0, w1, w2, w3, x0, x1, x2, x3;
+  [[maybe_unused]] v4i f2a, f2b;   // the staggered-halves schedule's third fragment pair
   float nb0 = 0.f, nb1 = 0.f, pb0 = 0.f, pb1 = 0.f;   // token scales of this block / of the previous one
 
   // one block per iteration: it has landed (every wave's loads: the barrier), every wave is done with the previous
@@ -547,9 +548,12 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
 
   if (paired) {
     // the gate waves (rows 0-127) hand gate = acc * scale to the up waves through LDS ([128 tokens][132 floats] over
-    // the ring, free once everyone is past the loop); the up waves store y = silu(gate) * (acc * scale2)
+    // the ring, free once everyone is past the loop); the up waves form h = silu(gate) * (acc * scale2) and store it,
+    // or (a.oh) quantise it: the tile's 128 rows are one 128-column block of each token's h, so the block max needs
+    // only this workgroup (the two up waves of a token column meet in LDS)
     __syncthreads();
     float *gx = (float *)smem;
+    float *red = gx + kG2N * kG2GX;   // [2 up waves][128 tokens] block maxima
     auto scaled = [&](const float *sc, int rb, const float *v) {
       float4 o;
       if (rb + 3 < a.rows) {
@@ -572,26 +576,86 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
             *(float4 *)(gx + tok * kG2GX + lrow) = scaled(a.scale, r0 + lrow, &acc[mi][ni][4 * j]);
           }
     __syncthreads();
-    if (wr >= 2)
+    if (wr >= 2) {
+      // h in place of the up accumulators
 #pragma unroll
       for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-          const int tok = 64 * wc + 32 * ni + fr, t = t0 + tok;
-          if (t >= a.ntok) continue;
-          float *yt = a.y + (size_t)t * a.ldy;
+        for (int ni = 0; ni < 2; ni++)
 #pragma unroll
           for (int j = 0; j < 4; j++) {
-            const int lrow = 64 * (wr - 2) + 32 * mi + 8 * j + 4 * fh, rb = r0 + lrow;
+            const int lrow = 64 * (wr - 2) + 32 * mi + 8 * j + 4 * fh, tok = 64 * wc + 32 * ni + fr;
             const float4 g = *(const float4 *)(gx + tok * kG2GX + lrow);
-            const float4 u = scaled(a.scale2, rb, &acc[mi][ni][4 * j]);
-            const float h[4] = {silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w)};
-            if (rb + 3 < a.rows && (a.ldy & 3) == 0) *(float4 *)(yt + rb) = make_float4(h[0], h[1], h[2], h[3]);
-            else
-#pragma unroll
-              for (int i = 0; i < 4; i++) if (rb + i < a.rows) yt[rb + i] = h[i];
+            const float4 u = scaled(a.scale2, r0 + lrow, &acc[mi][ni][4 * j]);
+            acc[mi][ni][4 * j] = silu_mul(g.x, u.x); acc[mi][ni][4 * j + 1] = silu_mul(g.y, u.y);
+            acc[mi][ni][4 * j + 2] = silu_mul(g.z, u.z); acc[mi][ni][4 * j + 3] = silu_mul(g.w, u.w);
           }
+    }
+    if (!a.oh) {
+      if (wr >= 2)
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+          for (int ni = 0; ni < 2; ni++) {
+            const int t = t0 + 64 * wc + 32 * ni + fr;
+            if (t >= a.ntok) continue;
+            float *yt = a.y + (size_t)t * a.ldy;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const int rb = r0 + 64 * (wr - 2) + 32 * mi + 8 * j + 4 * fh;
+              const float *h = &acc[mi][ni][4 * j];
+              if (rb + 3 < a.rows && (a.ldy & 3) == 0) *(float4 *)(yt + rb) = make_float4(h[0], h[1], h[2], h[3]);
+              else
+#pragma unroll
+                for (int i = 0; i < 4; i++) if (rb + i < a.rows) yt[rb + i] = h[i];
+            }
+          }
+      return;
+    }
+    // quantise (quant_rows, kernels.cpp:17-31, as k_pf_quant: mx = max |h| over the block, isx = mx > 0 ? 32767 / mx
+    // : 0, bs = mx / 32767, q = rint(h * isx), planes hi = q >> 8, lo = (q & 255) ^ 0x80)
+    if (wr >= 2)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++) {
+        float m = 0.f;
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) m = fmaxf(m, fabsf(acc[mi][ni][r]));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        if (fh == 0) red[(wr - 2) * kG2N + 64 * wc + 32 * ni + fr] = m;
+      }
+    __syncthreads();
+    if (wr < 2) return;
+    const int blk = r0 / kQB;
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+      const int tok = 64 * wc + 32 * ni + fr, t = t0 + tok;
+      if (t >= a.ntok) continue;
+      const float m = fmaxf(red[tok], red[kG2N + tok]);
+      const float isx = m > 0 ? kActMax / m : 0.f;
+      if (wr == 2 && fh == 0) {
+        const float bs = m / kActMax;
+        a.ob[(size_t)t * a.ldb + blk] = bs;
+        a.obt[(size_t)blk * a.ldbt + t] = bs;
+      }
+      int8_t *oh = a.oh + (size_t)t * a.ldq, *ol = a.ol + (size_t)t * a.ldq;
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int rb = r0 + 64 * (wr - 2) + 32 * mi + 8 * j + 4 * fh;
+          uint32_t hh = 0, ll = 0;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int q = (int)__builtin_rintf(acc[mi][ni][4 * j + i] * isx);
+            hh |= (uint32_t)((q >> 8) & 0xff) << (8 * i);
+            ll |= (uint32_t)((q & 0xff) ^ 0x80) << (8 * i);
+          }
+          *(uint32_t *)(oh + rb) = hh;
+          *(uint32_t *)(ol + rb) = ll;
         }
+    }
     return;
   }
 #pragma unroll
@@ -842,18 +906,26 @@ static bool gemm_use_32x32(int row_tiles32, int token_tiles32) {
   return (double)((n2 + cus - 1) / cus) * 1.45 < (double)((2 * n2 + cus - 1) / cus);
 }
 
+// row tiles of a launch for a tile height (a gate / up pair: half-height tiles of each matrix)
+static int gemm_row_tiles(const GemmArgs &a, bool big) {
+  const int rt = big ? (a.w2 ? kG2M / 2 : kG2M) : (a.w2 ? kGM / 2 : kGM);
+  if (a.nseg < 2) return (a.rows + rt - 1) / rt;
+  int t = 0;
+  for (int s = 0; s < a.nseg && s < kGemmMaxSeg; s++) t += (a.seg[s].rows + rt - 1) / rt;
+  return t;
+}
+bool gemm_uses_32x32(const GemmArgs &a) {
+  return a.kind == MK_Q8 && a.xbt && a.ntok > 0 && gemm_use_32x32(gemm_row_tiles(a, true), (a.ntok + kG2N - 1) / kG2N);
+}
+
 hipError_t launch_gemm(const GemmArgs &a0, hipStream_t st) {
   if (a0.ntok <= 0) return hipSuccess;
   GemmArgs a = a0;
   { static const int dbg = [] { const char *e = getenv("QPH_G2_DBG"); return e ? atoi(e) : 0; }(); a.dbg = dbg; }
-  // row tiles of each kernel (a pair of gate / up matrices: half-height tiles of each)
-  auto row_tiles = [&](int big) {
-    const int rt = big ? (a.w2 ? kG2M / 2 : kG2M) : (a.w2 ? kGM / 2 : kGM);
-    if (a.nseg < 2) return (a.rows + rt - 1) / rt;
-    int t = 0;
-    for (int s = 0; s < a.nseg && s < kGemmMaxSeg; s++) t += (a.seg[s].rows + rt - 1) / rt;
-    return t;
-  };
+  const bool big = gemm_uses_32x32(a0);
+  const int tiles = gemm_row_tiles(a0, big);
+  if (a.oh && (!big || !a.w2 || a.rows % kQB || !a.ol || !a.ob || !a.obt || a.ldbt % 4 || a.ldbt < a.ntok))
+    return hipErrorInvalidValue;   // quantised output: the 32 x 32 kernel's gate / up pair, whole 128-row blocks
   if (a.nseg > 1) {
     // the first matrix also stands in the launch's own fields, so the checks below cover every segment's pointers
     if (a.nseg > kGemmMaxSeg || a.w2 || a.resid || a.gate) return hipErrorInvalidValue;
@@ -867,8 +939,6 @@ hipError_t launch_gemm(const GemmArgs &a0, hipStream_t st) {
   } else {
     a.nseg = 0;
   }
-  const bool big = a.kind == MK_Q8 && a.xbt && gemm_use_32x32(row_tiles(1), (a.ntok + kG2N - 1) / kG2N);
-  const int tiles = row_tiles(big);
   if (a.cols % kQB || a.rows <= 0 || a.ldq % 16 || a.ldq < a.cols || a.ldb < a.cols / kQB) return hipErrorInvalidValue;
   const dim3 grid((a.ntok + (big ? kG2N : kGN) - 1) / (big ? kG2N : kGN), tiles);
   if (a.w2 && (a.kind != MK_Q8 || !a.scale2 || !a.wsum2 || a.resid || a.bias || a.gate)) return hipErrorInvalidValue;
