@@ -154,7 +154,7 @@ struct GemmArgs {
   int nseg;
   GemmSeg seg[kGemmMaxSeg];
   int dbg;   // measurement switches of the 32 x 32 q8 kernel (QPH_G2_DBG; results are wrong when set): 1 no compute,
-             // 2 no loads past the first two stages, 4 no barriers, 8 no shift-add / fp32 steps
+             // 2 no loads after the first block, 4 no barriers
 };
 size_t gemm_lds_bytes();
 // row pitch of the block-major row sums: rows rounded up to 64 (16-byte loads of 4 rows stay inside a block's run)
