@@ -999,17 +999,18 @@ hipError_t launch_pf_rope(const PfRopeArgs &a, int B, hipStream_t st) {
 //           exponentials are the hardware exp2 (v_exp_f32, ~1 ulp) instead of the reference's exp256 polynomial
 //           (kernels_x86.cpp:406-417): a float-order difference within the logit tolerance, like the rest of this
 //           kernel's order (the reference-order mode has its own kernel, k_ex_pf_attn).
-constexpr int kPfKB = 32;      // cache positions per block
+constexpr int kPfKB = 64;      // cache positions per block (two 32-deep value steps)
 constexpr int kPfAttnWaves = 8;   // units (16-token tile, query head) per workgroup, one per wave: they share the K / V
 template <int HD>
 __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
-  constexpr int KS = HD + 8, VS = kPfKB + 8, DT = HD / 16;   // VS: transposed rows of 20 dwords (see the V stores)
+  constexpr int KS = HD + 8, VS = kPfKB + 8, DT = HD / 16;   // VS: transposed rows of 36 dwords (see the V stores)
+  constexpr int NH = kPfKB / 32, NM = kPfKB / 16;              // 32-position value steps, 16-position score tiles
   constexpr int NT = kPfAttnWaves * 64;
   constexpr int NPC = kPfKB * (HD / 8);                        // 16-byte pieces of K (and of V) per block
   constexpr int NP = (NPC + NT - 1) / NT;                      // ... per thread
-  static_assert(NPC % 64 == 0, "whole waves of pieces");
+  static_assert(NPC % NT == 0, "every thread holds NP whole pieces (the shuffles below see whole waves)");
   __shared__ __align__(16) uint16_t ks[kPfKB * KS];
   __shared__ __align__(16) uint16_t vt[HD * VS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
@@ -1054,54 +1055,55 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   float m = -INFINITY, l = 0.f;
   const uint16_t *kg = a.kc + g * HD, *vg = a.vc + g * HD;
 
-  // piece i of a block: position (tid + NT i) / (HD / 8), dims 8 ((tid + NT i) % (HD / 8)) + 0..7 (threads past the
-  // NPC pieces idle); the next block's pieces are loaded while the current one is computed
-  uint4 kr[NP], vr[NP];
+  // piece i of a block: position (tid + NT i) / (HD / 8), dims 8 ((tid + NT i) % (HD / 8)) + 0..7; the next block's
+  // pieces are loaded while the current one is computed (named registers, not an array: a two-entry array indexed in the rolled-up loop ended in scratch)
+  static_assert(NP == 1 || NP == 2, "one or two pieces per thread");
+  uint4 kr0, vr0, kr1, vr1;
+  auto load_piece = [&](int pb, int i, uint4 &k, uint4 &v) {
+    const int c = tid + NT * i, pos = pb + c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+    const int pc = pos <= wg_last ? pos : wg_last;   // rows past the last one re-read it (masked out)
+    k = *(const uint4 *)(kg + (size_t)pc * kvd + d0);
+    v = *(const uint4 *)(vg + (size_t)pc * kvd + d0);
+  };
   auto load_block = [&](int pb) {
-#pragma unroll
-    for (int i = 0; i < NP; i++) {
-      const int c = tid + NT * i, pos = pb + c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-      if (c >= NPC) break;
-      const int pc = pos <= wg_last ? pos : wg_last;   // rows past the last one re-read it (masked out)
-      kr[i] = *(const uint4 *)(kg + (size_t)pc * kvd + d0);
-      vr[i] = *(const uint4 *)(vg + (size_t)pc * kvd + d0);
-    }
+    load_piece(pb, 0, kr0, vr0);
+    if (NP == 2) load_piece(pb, 1, kr1, vr1);
+  };
+  // K as stored; V transposed: the lane HD / 8 away holds position p ^ 1 with the same dims, the two swap halves so
+  // the even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each writes
+  // four (p even, p odd) pairs as 32-bit words
+  auto store_piece = [&](int i, const uint4 &k, const uint4 &vrr) {
+    const int c = tid + NT * i, p = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+    *(uint4 *)(ks + p * KS + d0) = k;
+    const uint32_t vv[4] = {vrr.x, vrr.y, vrr.z, vrr.w};
+    const bool ev = (p & 1) == 0;
+    const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, 64);
+    const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, 64);
+    const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
+    const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
+    // dword (p / 2) of the row, XOR 2 (d0 / 8 mod 8): without it the lanes' rows, 8 apart, land on a few banks only;
+    // with the padded rows and the swizzle (even, so the pairs the reads take stay adjacent) both the stores and the
+    // V^T fragment reads below spread over the banks
+    const int sw = 2 * ((d0 >> 3) & 7);
+    uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ sw);
+    w[0] = (lo_x & 0xffffu) | (hi_x << 16);
+    w[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
+    w[VS] = (lo_y & 0xffffu) | (hi_y << 16);
+    w[3 * VS / 2] = (lo_y >> 16) | (hi_y & 0xffff0000u);
   };
   load_block(0);
   for (int kb = 0; kb < nkb; kb++) {
     const int pb = kb * kPfKB;
     __syncthreads();   // the previous block's LDS reads are done
-    // K as stored; V transposed: the lane HD / 8 away holds position p ^ 1 with the same dims, the two swap halves so
-    // the even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each
-    // writes four (p even, p odd) pairs as 32-bit words
-#pragma unroll
-    for (int i = 0; i < NP; i++) {
-      const int c = tid + NT * i, p = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-      if (c >= NPC) break;   // wave-uniform (NPC is a multiple of 64): the shuffles below see whole waves
-      *(uint4 *)(ks + p * KS + d0) = kr[i];
-      const uint32_t vv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-      const bool ev = (p & 1) == 0;
-      const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, 64);
-      const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, 64);
-      const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
-      const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-      // dword (p / 2) of the row, XOR 2 (d0 / 8 mod 8): without it the lanes' rows, 8 apart, land on a few banks only;
-      // with 20-dword rows and the swizzle (even, so the pairs the reads take stay adjacent) both the stores and the
-      // V^T fragment reads below spread over the banks
-      const int sw = 2 * ((d0 >> 3) & 7);
-      uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ sw);
-      w[0] = (lo_x & 0xffffu) | (hi_x << 16);
-      w[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
-      w[VS] = (lo_y & 0xffffu) | (hi_y << 16);
-      w[3 * VS / 2] = (lo_y >> 16) | (hi_y & 0xffff0000u);
-    }
+    store_piece(0, kr0, vr0);
+    if (NP == 2) store_piece(1, kr1, vr1);
     __syncthreads();
     if (kb + 1 < nkb) load_block(pb + kPfKB);
     if (!live || pb > wave_last) continue;
-    // scores of the two 16-position halves
-    f4 sc[2];
+    // scores of the block's 16-position tiles
+    f4 sc[NM];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
+    for (int mt = 0; mt < NM; mt++) {
       sc[mt] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < HD / 32; s++) {
@@ -1111,9 +1113,9 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
       }
     }
     // online softmax for token t over positions pb + 16 mt + 4 lg + i
-    float sv[8], bm = -INFINITY;
+    float sv[4 * NM], bm = -INFINITY;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < NM; mt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int p = pb + 16 * mt + 4 * lg + i;
@@ -1128,13 +1130,13 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
     const float mz = mn == -INFINITY ? 0.f : mn;
     const float corr = __builtin_amdgcn_exp2f(m - mz);
     float rs = 0.f;
-    h8 ph, pl;
+    h8 ph[NH], pl[NH];   // value step hs: positions 32 hs + 4 lg + 0..3 and 32 hs + 16 + 4 lg + 0..3
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < 4 * NM; j++) {
       const float pv = __builtin_amdgcn_exp2f(sv[j] - mz);
       rs += pv;
       const _Float16 h = (_Float16)pv;
-      ph[j] = h; pl[j] = (_Float16)(pv - (float)h);
+      ph[j / 8][j % 8] = h; pl[j / 8][j % 8] = (_Float16)(pv - (float)h);
     }
     rs += __shfl_xor(rs, 16, 64);
     rs += __shfl_xor(rs, 32, 64);
@@ -1143,14 +1145,18 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
 #pragma unroll
     for (int d = 0; d < DT; d++) {
       o[d] *= corr;
-      // V^T fragment: dim 16 d + lr, positions 4 lg + 0..3 and 16 + 4 lg + 0..3 (the k order of ph / pl)
-      const int row = 16 * d + lr, sw = 2 * ((row >> 3) & 7);   // the writes' swizzle
+      // V^T fragment of step hs: dim 16 d + lr, positions 32 hs + 4 lg + 0..3 and 32 hs + 16 + 4 lg + 0..3 (the k order
+      // of ph / pl); the writes' swizzle XORs the low four bits of the dword index only
+      const int row = 16 * d + lr, sw = 2 * ((row >> 3) & 7);
       const uint32_t *vr = (const uint32_t *)(vt + row * VS);
-      const uint2 v0 = *(const uint2 *)(vr + ((2 * lg) ^ sw)), v1 = *(const uint2 *)(vr + ((8 + 2 * lg) ^ sw));
-      const uint4 vv = make_uint4(v0.x, v0.y, v1.x, v1.y);
-      const h8 vf = __builtin_bit_cast(h8, vv);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
+#pragma unroll
+      for (int hs = 0; hs < NH; hs++) {
+        const uint2 v0 = *(const uint2 *)(vr + 16 * hs + ((2 * lg) ^ sw)), v1 = *(const uint2 *)(vr + 16 * hs + ((8 + 2 * lg) ^ sw));
+        const uint4 vv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        const h8 vf = __builtin_bit_cast(h8, vv);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[hs], o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[hs], o[d], 0, 0, 0);
+      }
     }
   }
   if (!tok_ok) return;
