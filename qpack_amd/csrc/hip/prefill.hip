@@ -147,6 +147,8 @@ hipError_t launch_rowsum_q8(const int8_t *w, int rows, int cols, int *out, hipSt
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + exp_poly(0.f - g)) * u; }   // kernels_x86.cpp:427-431
+// silu_mul's first half: silu_mul(g, u) == silu_f(g) * u, the same operations in the same order
+__device__ __forceinline__ float silu_f(float g) { return g / (1.f + exp_poly(0.f - g)); }
 
 // rows rb .. rb + 3 of token row yt (the MFMA C layout gives a lane four consecutive rows of one token): y = v (* row
 // scale when `scaled`), then y += the residual, y = that + bias, or y = silu(gate) * that; one 16-byte access where the
@@ -547,8 +549,9 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
     }
 
   if (paired) {
-    // the gate waves (rows 0-127) hand gate = acc * scale to the up waves through LDS ([128 tokens][132 floats] over
-    // the ring, free once everyone is past the loop); the up waves form h = silu(gate) * (acc * scale2) and store it,
+    // the gate waves (rows 0-127) hand silu(gate), gate = acc * scale, to the up waves through LDS ([128 tokens][132
+    // floats] over the ring, free once everyone is past the loop); the up waves form h = silu(gate) * (acc * scale2)
+    // (silu_mul's operations, split between the two wave groups) and store it,
     // or (a.oh) quantise it: the tile's 128 rows are one 128-column block of each token's h, so the block max needs
     // only this workgroup (the two up waves of a token column meet in LDS)
     __syncthreads();
@@ -573,7 +576,8 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; j++) {
             const int lrow = 64 * wr + 32 * mi + 8 * j + 4 * fh, tok = 64 * wc + 32 * ni + fr;
-            *(float4 *)(gx + tok * kG2GX + lrow) = scaled(a.scale, r0 + lrow, &acc[mi][ni][4 * j]);
+            const float4 g = scaled(a.scale, r0 + lrow, &acc[mi][ni][4 * j]);
+            *(float4 *)(gx + tok * kG2GX + lrow) = make_float4(silu_f(g.x), silu_f(g.y), silu_f(g.z), silu_f(g.w));
           }
     __syncthreads();
     if (wr >= 2) {
@@ -587,8 +591,8 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
             const int lrow = 64 * (wr - 2) + 32 * mi + 8 * j + 4 * fh, tok = 64 * wc + 32 * ni + fr;
             const float4 g = *(const float4 *)(gx + tok * kG2GX + lrow);
             const float4 u = scaled(a.scale2, r0 + lrow, &acc[mi][ni][4 * j]);
-            acc[mi][ni][4 * j] = silu_mul(g.x, u.x); acc[mi][ni][4 * j + 1] = silu_mul(g.y, u.y);
-            acc[mi][ni][4 * j + 2] = silu_mul(g.z, u.z); acc[mi][ni][4 * j + 3] = silu_mul(g.w, u.w);
+            acc[mi][ni][4 * j] = g.x * u.x; acc[mi][ni][4 * j + 1] = g.y * u.y;   // g = silu(gate), from the gate waves
+            acc[mi][ni][4 * j + 2] = g.z * u.z; acc[mi][ni][4 * j + 3] = g.w * u.w;
           }
     }
     if (!a.oh) {
