@@ -153,6 +153,7 @@ struct GemmArgs {
   // segment fields replacing w / scale / wsum / q4ns / q4sc / bias / y / ldy / rows; each starts on a fresh row tile
   int nseg;
   GemmSeg seg[kGemmMaxSeg];
+  int tile0;   // first row tile of this launch (a launch split over the two q8 kernels; set by launch_gemm)
   int dbg;   // measurement switches of the 32 x 32 q8 kernel (QPH_G2_DBG; results are wrong when set): 1 no compute,
              // 2 no loads after the first block, 4 no barriers
 };

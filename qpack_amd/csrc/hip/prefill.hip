@@ -231,7 +231,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GemmArgs a) {
       r0 = (tile / ntt) * RT; t0 = (tile % ntt) * kGN;
     }
   }
-  r0 = gemm_segment(a, r0, RT);
+  r0 = gemm_segment(a, r0 + a.tile0 * RT, RT);
   const int nb = a.cols / kQB;
 
   // this lane's DMA sources.  Per stage the 48 1-KiB row groups (16 each of weights, hi plane, lo plane; 8 rows per
@@ -465,7 +465,7 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
       r0 = (tile / ntt) * RT; t0 = (tile % ntt) * kG2N;
     }
   }
-  r0 = gemm_segment(a, r0, RT);
+  r0 = gemm_segment(a, r0 + a.tile0 * RT, RT);
   const int nb = a.cols / kQB;
 
   // DMA sources: 64 1-KiB row groups per stage (32 of weights, 16 per plane; 8 rows of 128 B each), 8 to a wave; the
@@ -739,7 +739,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
       r0 = (tile / ntt) * kGM; t0 = (tile % ntt) * kGN;
     }
   }
-  r0 = gemm_segment(a, r0, kGM);
+  r0 = gemm_segment(a, r0 + a.tile0 * kGM, kGM);
   const int nb = a.cols / kQB, rb = a.cols / 2;   // packed bytes per row
   // DMA jobs per stage (64 wave instructions, 8 per wave; jobs 60..63 repeat 0..3 byte for byte):
   //   0..7 packed weights (16 rows x 64 B each), 8..23 hi plane, 24..39 lo plane (8 rows x 128 B each),
@@ -897,17 +897,26 @@ __global__ __launch_bounds__(512) void k_gemm_q4(GemmArgs a) {
 // MI355X: 2 x 14336 x 4096 578 vs 707 us, 4096 x 4096 173 vs 215, 6144 x 4096 152 vs 160), so it wins unless its fewer,
 // larger workgroups leave CUs idle: ceil(n2 / CUs) x 1.45 against ceil(2 n2 / CUs) rounds (n2 = its workgroup count).
 // QPH_GEMM=1 / 2 forces the 32 x 32 / 16 x 16 kernel.
-static bool gemm_use_32x32(int row_tiles32, int token_tiles32) {
-  const char *fe = getenv("QPH_GEMM");   // read per launch: tests switch it between calls
-  const int force = fe ? atoi(fe) : 0;
-  if (force == 1 || force == 2) return force == 1;
+static int gemm_forced() {   // QPH_GEMM, read per launch: tests switch it between calls
+  const char *fe = getenv("QPH_GEMM");
+  const int f = fe ? atoi(fe) : 0;
+  return f == 1 || f == 2 ? f : 0;
+}
+static int gemm_cus() {
+  if (const char *e = getenv("QPH_GEMM_CUS")) return std::max(1, atoi(e));   // test hook: the choice for another CU count
   static const int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 256;
     return std::max(1, n);
   }();
+  return cus;
+}
+static double gemm_rounds(long wgs) { return (double)((wgs + gemm_cus() - 1) / gemm_cus()); }
+constexpr double kG2Cost = 1.45;   // a 32 x 32 round in 16 x 16 rounds
+static bool gemm_use_32x32(int row_tiles32, int token_tiles32) {
+  if (const int f = gemm_forced()) return f == 1;
   const long n2 = (long)row_tiles32 * token_tiles32;
-  return (double)((n2 + cus - 1) / cus) * 1.45 < (double)((2 * n2 + cus - 1) / cus);
+  return gemm_rounds(n2) * kG2Cost < gemm_rounds(2 * n2);
 }
 
 // row tiles of a launch for a tile height (a gate / up pair: half-height tiles of each matrix)
@@ -926,6 +935,7 @@ hipError_t launch_gemm(const GemmArgs &a0, hipStream_t st) {
   if (a0.ntok <= 0) return hipSuccess;
   GemmArgs a = a0;
   { static const int dbg = [] { const char *e = getenv("QPH_G2_DBG"); return e ? atoi(e) : 0; }(); a.dbg = dbg; }
+  if (a0.tile0) return hipErrorInvalidValue;   // set only here
   const bool big = gemm_uses_32x32(a0);
   const int tiles = gemm_row_tiles(a0, big);
   if (a.oh && (!big || !a.w2 || a.rows % kQB || !a.ol || !a.ob || !a.obt || a.ldbt % 4 || a.ldbt < a.ntok))
@@ -949,8 +959,33 @@ hipError_t launch_gemm(const GemmArgs &a0, hipStream_t st) {
   if (a.kind == MK_Q8) {
     if (!a.wsum) return hipErrorInvalidValue;
     if (big && (!a.xbt || a.ldbt % 4 || a.ldbt < a.ntok)) return hipErrorInvalidValue;
-    if (big) hipLaunchKernelGGL(k_gemm2_q8, grid, dim3(64 * kG2Waves), gemm2_lds_bytes(), st, a);
-    else hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
+    // a segment launch whose 32 x 32 grid would end in a part-filled round: its first segments on the 32 x 32 kernel,
+    // the rest on the 16 x 16 one, when that takes fewer rounds (C4 q / k / v: q alone fills one 32 x 32 round, k + v
+    // one 16 x 16 round)
+    int split = 0, t32 = 0, t16 = 0, t16_0 = 0;
+    if (big && a.nseg > 1 && a.tile0 == 0 && !gemm_forced()) {
+      const int tt = grid.x;
+      double best = gemm_rounds((long)tiles * tt) * kG2Cost;
+      for (int s = 1; s < a.nseg; s++) {
+        int f32 = 0, f16 = 0, r16 = 0;
+        for (int i = 0; i < a.nseg; i++) {
+          if (i < s) { f32 += (a.seg[i].rows + kG2M - 1) / kG2M; f16 += (a.seg[i].rows + kGM - 1) / kGM; }
+          else r16 += (a.seg[i].rows + kGM - 1) / kGM;
+        }
+        const double c = gemm_rounds((long)f32 * tt) * kG2Cost + gemm_rounds((long)r16 * tt);
+        if (c < best) { best = c; split = s; t32 = f32; t16 = r16; t16_0 = f16; }
+      }
+    }
+    if (split) {
+      hipLaunchKernelGGL(k_gemm2_q8, dim3(grid.x, t32), dim3(64 * kG2Waves), gemm2_lds_bytes(), st, a);
+      GemmArgs b = a;
+      b.tile0 = t16_0;
+      hipLaunchKernelGGL(k_gemm_q8, dim3(grid.x, t16), dim3(64 * kGWaves), gemm_lds_bytes(), st, b);
+    } else if (big) {
+      hipLaunchKernelGGL(k_gemm2_q8, grid, dim3(64 * kG2Waves), gemm2_lds_bytes(), st, a);
+    } else {
+      hipLaunchKernelGGL(k_gemm_q8, grid, dim3(64 * kGWaves), gemm_lds_bytes(), st, a);
+    }
   } else if (a.kind == MK_Q4) {
     if (!a.q4ns || !a.q4sc || !a.xg || a.ldg < a.cols / 32 || a.ldg % 4) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_gemm_q4, grid, dim3(64 * kGWaves), (size_t)kGStages * kG4Stage, st, a);

@@ -159,19 +159,25 @@ def test_prefill_q8_kernels_agree(cfg, synth, monkeypatch):
     """the two q8 prompt-product kernels (16 x 16 and 32 x 32 MFMA tiles, forced with QPH_GEMM=2 / 1) carry out the
     same arithmetic: a 300-token prompt gives bit-identical logits and cache rows with either, the 32 x 32 kernel then
     running every product of the prompt (the q / k / v segments with bias, wo / down into the residual, the gate / up
-    pair with SwiGLU)"""
+    pair with SwiGLU and its quantised store); and so does the launcher's own choice for 8 CUs, which splits the
+    q / k / v launch over both kernels"""
     path = synth(cfg)
     toks = np.random.default_rng(17).integers(0, qa.CONFIGS[cfg].vocab, 300).astype(np.int32)
     out = []
-    for k in ("2", "1"):
-        monkeypatch.setenv("QPH_GEMM", k)
+    for k in ("2", "1", "auto8"):
+        if k == "auto8":   # the launcher's own choice for 8 CUs: q / k / v split over both kernels
+            monkeypatch.delenv("QPH_GEMM")
+            monkeypatch.setenv("QPH_GEMM_CUS", "8")
+        else:
+            monkeypatch.setenv("QPH_GEMM", k)
         print(f"{cfg}: 300-token prompt, QPH_GEMM={k}", flush=True)
         gpu = qa.HipLlama.load(path, max_ctx=320)
         lg = gpu.prefill(toks, 1)
         out.append((lg, gpu.snapshot()))
         gpu.close()
-    np.testing.assert_array_equal(out[0][0], out[1][0])
-    assert out[0][1] == out[1][1], "cache rows differ between the two kernels"
+    for o in out[1:]:
+        np.testing.assert_array_equal(out[0][0], o[0])
+        assert out[0][1] == o[1], "cache rows differ between the kernels"
 
 
 def kv_snapshot(k, v):
