@@ -174,6 +174,7 @@ struct PfRopeArgs {
   const float *cos_t, *sin_t;
   uint16_t *kc, *vc;
   int p0, nh, nkv, hd;
+  int skip_q;   // q is rotated by the attention kernel instead
 };
 hipError_t launch_pf_rope(const PfRopeArgs &a, int B, hipStream_t st);
 // causal attention of the batch's (rotated) queries over cache positions [0, p0 + t] -> att [t][lda]
@@ -182,6 +183,11 @@ struct PfAttnArgs {
   const uint16_t *kc, *vc;
   float *att; int lda;
   int ntok, p0, nh, nkv, hd;
+  // optional: q not yet rotated - the kernel applies RoPE (k_pf_rope's arithmetic) as it loads q
+  const float *cos_t, *sin_t;
+  // optional (hd 128, one head = one 128-column block): the output quantised for the wo product instead of att -
+  // planes oh / ol [ntok][ldo], block scales ob [ntok][ldb] and obt [nh][ldbt] (the quantiser's arithmetic)
+  int8_t *oh, *ol; float *ob, *obt; int ldo, ldb, ldbt;
 };
 hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st);
 

@@ -382,6 +382,9 @@ void HipLlama::prefill(const int *toks, int n, int want, float *out) {
 // causal attention -> quantise -> wo product into the residual -> RMSNorm + quantise -> gate product, up product
 // with SwiGLU in its store -> quantise -> down product into the residual.  Leaves the last token's hidden state in x_.
 void HipLlama::prefill_batched(const int *toks, int n) {
+  // QPH_PF_UNFUSED=bits (test hook): 1 q's RoPE, 2 the attention output's quantisation, 4 the SwiGLU output's
+  // quantisation as launches of their own, for bit-for-bit comparisons with the fused kernels
+  const int unfused = getenv("QPH_PF_UNFUSED") ? atoi(getenv("QPH_PF_UNFUSED")) : 0;
   const int d = cfg_.hidden, ff = cfg_.ffn, nb_ld = pf_ldq_ / 128 + 1;
   const float eps = cfg_.rms_eps;
   auto quant = [&](int pro, const float *x, int ldx, const float *w, int cols, int B) {
@@ -427,13 +430,20 @@ void HipLlama::prefill_batched(const int *toks, int n) {
       uint16_t *kc = kc_ + (size_t)l * ctx_ * kvd_, *vc = vc_ + (size_t)l * ctx_ * kvd_;
       quant(PRO_NORM, pf_x_, d, ly.an, d, B);
       gemm_qkv(ly, B);
+      // q's RoPE happens in the attention kernel; at head dim 128 (one head = one quantisation block) that kernel also
+      // quantises its output for a q8 wo
       PfRopeArgs r{}; r.q = pf_q_; r.ldq = qd_; r.k = pf_k_; r.v = pf_v_; r.ldk = kvd_; r.cos_t = cos_; r.sin_t = sin_;
-      r.kc = kc; r.vc = vc; r.p0 = p0; r.nh = cfg_.heads; r.nkv = cfg_.kv_heads; r.hd = cfg_.head_dim;
+      r.kc = kc; r.vc = vc; r.p0 = p0; r.nh = cfg_.heads; r.nkv = cfg_.kv_heads; r.hd = cfg_.head_dim; r.skip_q = !(unfused & 1);
       QPH_CK(launch_pf_rope(r, B, st_));
       PfAttnArgs t{}; t.q = pf_q_; t.ldq = qd_; t.kc = kc; t.vc = vc; t.att = pf_att_; t.lda = qd_;
       t.ntok = B; t.p0 = p0; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
+      if (!(unfused & 1)) { t.cos_t = cos_; t.sin_t = sin_; }
+      const bool att_q = !(unfused & 2) && cfg_.head_dim == 128 && ly.wo.kind == MK_Q8;
+      if (att_q) {
+        t.oh = pf_xh_; t.ol = pf_xl_; t.ob = pf_xb_; t.obt = pf_xbt_; t.ldo = pf_ldq_; t.ldb = nb_ld; t.ldbt = pf_ldbt_;
+      }
       QPH_CK(launch_pf_attn(t, st_));
-      quant(PRO_QUANT, pf_att_, qd_, nullptr, qd_, B);
+      if (!att_q) quant(PRO_QUANT, pf_att_, qd_, nullptr, qd_, B);
       gemm(ly.wo, pf_x_, d, nullptr, true, B);
       quant(PRO_NORM, pf_x_, d, ly.fn, d, B);
       bool fused = false;   // h = silu(gate) * up quantised by the product's store, straight into the second planes
@@ -442,7 +452,7 @@ void HipLlama::prefill_batched(const int *toks, int n) {
         a.w2 = (const int8_t *)ly.wu.q; a.scale2 = (const float *)ly.wu.s; a.wsum2 = ly.wu.rs;
         a.rows = ff; a.cols = d; a.xbt = pf_xbt_; a.ldbt = pf_ldbt_; a.xh = pf_xh_; a.xl = pf_xl_; a.xb = pf_xb_; a.ntok = B;
         a.ldq = pf_ldq_; a.ldb = nb_ld; a.y = pf_g_; a.ldy = ff;
-        fused = ly.wd.kind == MK_Q8 && ff % 128 == 0 && gemm_uses_32x32(a);
+        fused = !(unfused & 4) && ly.wd.kind == MK_Q8 && ff % 128 == 0 && gemm_uses_32x32(a);
         if (fused) { a.oh = pf_xh2_; a.ol = pf_xl2_; a.ob = pf_xb2_; a.obt = pf_xbt2_; }
         QPH_CK(launch_gemm(a, st_));
       } else {

@@ -1002,7 +1002,7 @@ __global__ __launch_bounds__(256) void k_pf_rope(PfRopeArgs a) {
   const int t = blockIdx.x, pos = a.p0 + t, half = a.hd / 2, kvd = a.nkv * a.hd;
   const float *cs = a.cos_t + (size_t)pos * half, *sn = a.sin_t + (size_t)pos * half;
   float *q = a.q + (size_t)t * a.ldq;
-  for (int e = threadIdx.x; e < a.nh * half; e += blockDim.x) {
+  for (int e = threadIdx.x; e < (a.skip_q ? 0 : a.nh * half); e += blockDim.x) {
     const int h = e / half, i = e % half;
     float *qh = q + h * a.hd; const float x0 = qh[i], x1 = qh[i + half];
     qh[i] = __builtin_fmaf(x0, cs[i], -(x1 * sn[i]));
@@ -1078,11 +1078,31 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   h8 qh[HD / 32], ql[HD / 32];
   {
     const float *qt = a.q + (size_t)(tok_ok ? t : 0) * a.ldq + head * HD;
+    float qv[HD / 32][8];
+#pragma unroll
+    for (int s = 0; s < HD / 32; s++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) qv[s][j] = tok_ok ? qt[32 * s + 8 * lg + j] : 0.f;
+    if (a.cos_t) {
+      // RoPE here (k_pf_rope's arithmetic): dims d and d + hd / 2 of a rotate-half pair sit in this lane's steps s and
+      // s + hd / 64
+      const int pos = tok_ok ? ptok : 0;   // tokens past the batch: any row of the table (their q is 0)
+      const float *cs = a.cos_t + (size_t)pos * (HD / 2), *sn = a.sin_t + (size_t)pos * (HD / 2);
+#pragma unroll
+      for (int s = 0; s < HD / 64; s++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int i = 32 * s + 8 * lg + j;
+          const float x0 = qv[s][j], x1 = qv[s + HD / 64][j], c = cs[i], si = sn[i];
+          qv[s][j] = __builtin_fmaf(x0, c, -(x1 * si));
+          qv[s + HD / 64][j] = __builtin_fmaf(x1, c, x0 * si);
+        }
+    }
 #pragma unroll
     for (int s = 0; s < HD / 32; s++) {
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float x = tok_ok ? qt[32 * s + 8 * lg + j] * qscale : 0.f;
+        const float x = qv[s][j] * qscale;
         const _Float16 h = (_Float16)x;
         qh[s][j] = h; ql[s][j] = (_Float16)(x - (float)h);
       }
@@ -1198,8 +1218,39 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
       }
     }
   }
-  if (!tok_ok) return;
+  if (!tok_ok) return;   // a token's four lanes (lr, l ^ 16, l ^ 32, l ^ 48) leave together
   const float inv = 1.f / l;
+  if (HD == kQB && a.oh) {
+    // quantise the head (one 128-column block; quant_rows as k_pf_quant: mx = max |v|, isx = mx > 0 ? 32767 / mx : 0,
+    // bs = mx / 32767, q = rint(v * isx), planes hi = q >> 8, lo = (q & 255) ^ 0x80)
+    float v[DT][4], mx = 0.f;
+#pragma unroll
+    for (int d = 0; d < DT; d++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) { v[d][i] = o[d][i] * inv; mx = fmaxf(mx, fabsf(v[d][i])); }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float isx = mx > 0 ? kActMax / mx : 0.f;
+    if (lg == 0) {
+      const float bs = mx / kActMax;
+      a.ob[(size_t)t * a.ldb + head] = bs;
+      a.obt[(size_t)head * a.ldbt + t] = bs;
+    }
+    int8_t *oh = a.oh + (size_t)t * a.ldo + head * HD, *ol = a.ol + (size_t)t * a.ldo + head * HD;
+#pragma unroll
+    for (int d = 0; d < DT; d++) {
+      uint32_t hh = 0, ll = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int q = (int)__builtin_rintf(v[d][i] * isx);
+        hh |= (uint32_t)((q >> 8) & 0xff) << (8 * i);
+        ll |= (uint32_t)((q & 0xff) ^ 0x80) << (8 * i);
+      }
+      *(uint32_t *)(oh + 16 * d + 4 * lg) = hh;
+      *(uint32_t *)(ol + 16 * d + 4 * lg) = ll;
+    }
+    return;
+  }
   float *out = a.att + (size_t)t * a.lda + head * HD;
 #pragma unroll
   for (int d = 0; d < DT; d++)
@@ -1207,7 +1258,8 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
 }
 hipError_t launch_pf_attn(const PfAttnArgs &a, hipStream_t st) {
   if (a.ntok <= 0) return hipSuccess;
-  if (a.nh % a.nkv || (a.hd != 64 && a.hd != 128) || a.lda % 4) return hipErrorInvalidValue;
+  if (a.nh % a.nkv || (a.hd != 64 && a.hd != 128) || a.lda % 4 || (a.cos_t && !a.sin_t)) return hipErrorInvalidValue;
+  if (a.oh && (a.hd != kQB || !a.ol || !a.ob || !a.obt || a.ldo % 4 || a.ldbt < a.ntok)) return hipErrorInvalidValue;
   const int units = (a.ntok + 15) / 16 * (a.nh / a.nkv);
   const dim3 grid((units + kPfAttnWaves - 1) / kPfAttnWaves, a.nkv);
   if (a.hd == 128) hipLaunchKernelGGL(k_pf_attn<128>, grid, dim3(kPfAttnWaves * 64), 0, st, a);

@@ -160,14 +160,17 @@ def test_prefill_q8_kernels_agree(cfg, synth, monkeypatch):
     same arithmetic: a 300-token prompt gives bit-identical logits and cache rows with either, the 32 x 32 kernel then
     running every product of the prompt (the q / k / v segments with bias, wo / down into the residual, the gate / up
     pair with SwiGLU and its quantised store); and so does the launcher's own choice for 8 CUs, which splits the
-    q / k / v launch over both kernels"""
+    q / k / v launch over both kernels, and the prompt with no fusions (QPH_PF_UNFUSED: q rotated by k_pf_rope, the
+    attention and SwiGLU outputs quantised by k_pf_quant)"""
     path = synth(cfg)
     toks = np.random.default_rng(17).integers(0, qa.CONFIGS[cfg].vocab, 300).astype(np.int32)
     out = []
-    for k in ("2", "1", "auto8"):
+    for k in ("2", "1", "auto8", "unfused"):
         if k == "auto8":   # the launcher's own choice for 8 CUs: q / k / v split over both kernels
             monkeypatch.delenv("QPH_GEMM")
             monkeypatch.setenv("QPH_GEMM_CUS", "8")
+        elif k == "unfused":   # q's RoPE and the output quantisations as launches of their own
+            monkeypatch.setenv("QPH_PF_UNFUSED", "7")
         else:
             monkeypatch.setenv("QPH_GEMM", k)
         print(f"{cfg}: 300-token prompt, QPH_GEMM={k}", flush=True)
