@@ -1,6 +1,8 @@
 """GPU parity of the whole token loop (qp::Model surface over the C ABI) against the oracle on small seeded models.
 
-Bar (the parity contract of this path): logits within max-abs 1e-2 and relative 1e-3 of the reference, identical greedy streams.
+Bar (the parity contract of this path's default order): logits within max-abs 1e-2 and relative 1e-3 of the reference,
+identical greedy streams (up to a reference near-tie where a file's stream meets one: assert_greedy_agrees).  The
+reference-order mode is checked bit for bit in test_gpu_golden.py.
 """
 import os
 
@@ -18,6 +20,24 @@ ATOL, RTOL = 1e-2, 1e-3
 def close(a, b):
     err = np.abs(a - b)
     return float(err.max()), bool(np.all(err <= np.maximum(ATOL, RTOL * np.abs(b))))
+
+
+def assert_greedy_agrees(gpu, orc, tok, n, err):
+    """the device greedy chain (gpu.greedy_run) against the oracle's greedy steps: identical tokens up to the first
+    oracle step whose top-2 gap is below tie = 20 x the measured logit error - the default order's contract (a float
+    order of its own, within the tolerance; the reference-order mode is the bit-exact one), as in test_gpu_golden"""
+    g = gpu.greedy_run(tok, n)
+    tie = max(20 * err, 1e-5)
+    for i in range(n):
+        lo = orc.step(tok, 1)
+        want = int(np.argmax(lo))
+        if int(g[i]) != want:
+            top = np.sort(lo)[-2:]
+            gap = float(top[1] - top[0])
+            assert gap < tie, f"greedy step {i}: {int(g[i])} vs the oracle's {want}, its top-2 gap {gap:.3g} >= {tie:.3g}"
+            print(f"greedy agrees for {i}/{n} steps, then a near-tie (oracle gap {gap:.3g} < {tie:.3g})", flush=True)
+            return
+        tok = want
 
 
 @pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_q4", "mini_q4m", "mini_q1", "mini_q1m", "mini_q4mb", "mini_q4h",
@@ -228,7 +248,7 @@ REF_QUANT = os.path.join(os.path.dirname(O.REF_LIB), "qpack-quantize")
                                       ("mini128", ["--type", "q4", "--q4-head"]), ("mini_q4m", ["--type", "q4m"])])
 def test_files_of_the_reference_quantiser(src, args, synth, tmp_path):
     """files written by the reference's own qpack-quantize (q1 MLP, q1 with q4 attention, q4 head, q4m policy) from a
-    synthetic q8 / q4m model: logits within the bar and identical greedy streams against the oracle"""
+    synthetic q8 / q4m model: logits within the bar and the greedy stream against the oracle's up to a near-tie"""
     import subprocess
     path = str(tmp_path / "rq.qpack")
     subprocess.run([REF_QUANT, synth(src), path] + args, check=True, capture_output=True)
@@ -240,7 +260,8 @@ def test_files_of_the_reference_quantiser(src, args, synth, tmp_path):
     lg, lo = gpu.prefill(toks, 1), orc.prefill(toks, 1)
     err, ok = close(lg, lo)
     assert ok, f"prefill logits max|d| {err}"
-    np.testing.assert_array_equal(gpu.greedy_run(int(np.argmax(lg)), 32), orc.greedy_run(int(np.argmax(lo)), 32))
+    assert int(np.argmax(lg)) == int(np.argmax(lo))
+    assert_greedy_agrees(gpu, orc, int(np.argmax(lo)), 32, err)
     gpu.close(); orc.close()
 
 
