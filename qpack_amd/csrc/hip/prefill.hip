@@ -1140,10 +1140,11 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
     const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, 64);
     const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
     const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-    // dword (p / 2) of the row, XOR 2 (d0 / 8 mod 8): without it the lanes' rows, 8 apart, land on a few banks only;
-    // with the padded rows and the swizzle (even, so the pairs the reads take stay adjacent) both the stores and the
-    // V^T fragment reads below spread over the banks
-    const int sw = 2 * ((d0 >> 3) & 7);
+    // dword (p / 2) of the row, XOR 2 (d0 / 16 mod 8) (even, so the pairs the reads take stay adjacent; a lane's rows
+    // d0 .. d0 + 7 share it): with 36-dword rows both these stores and the V^T fragment reads below hit 64 distinct
+    // banks per instruction (a bank model of both patterns over 32-47-dword rows and five swizzles chose it; XOR
+    // 2 (d0 / 8 mod 8) left every store 2-way conflicted)
+    const int sw = 2 * ((d0 >> 4) & 7);
     uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ sw);
     w[0] = (lo_x & 0xffffu) | (hi_x << 16);
     w[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
@@ -1206,7 +1207,7 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
       o[d] *= corr;
       // V^T fragment of step hs: dim 16 d + lr, positions 32 hs + 4 lg + 0..3 and 32 hs + 16 + 4 lg + 0..3 (the k order
       // of ph / pl); the writes' swizzle XORs the low four bits of the dword index only
-      const int row = 16 * d + lr, sw = 2 * ((row >> 3) & 7);
+      const int row = 16 * d + lr, sw = 2 * ((row >> 4) & 7);
       const uint32_t *vr = (const uint32_t *)(vt + row * VS);
 #pragma unroll
       for (int hs = 0; hs < NH; hs++) {
