@@ -527,6 +527,7 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
   v16i T[2][2] = {{zero, zero}, {zero, zero}};
   v4i A0[4], A1[4], f0a, f0b, f1a, f1b, w0, w1, w2, w3, x0, x1, x2, x3;
   [[maybe_unused]] v4i f2a, f2b;   // the staggered-halves schedule's third fragment pair
+  [[maybe_unused]] v4i bq[4];   // the eighths / pairs schedules' token fragments (rolling)
   float nb0 = 0.f, nb1 = 0.f, pb0 = 0.f, pb1 = 0.f;   // token scales of this block / of the previous one
 
   // one block per iteration: it has landed (every wave's loads: the barrier), every wave is done with the previous
@@ -541,12 +542,10 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
 #include "gemm2_loop.inc"
     pb0 = nb0; pb1 = nb1;
   }
-  // the last block's fp32 step of rows mi1 (the loop defers it under the next block's first MFMAs)
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      acc[1][0][r] = __builtin_fmaf(pb0, (float)T[1][0][r], acc[1][0][r]);
-      acc[1][1][r] = __builtin_fmaf(pb1, (float)T[1][1][r], acc[1][1][r]);
-    }
+  // the last block's deferred fp32 steps (the loop runs them under the next block's first MFMAs)
+#define G2_TAIL
+#include "gemm2_loop.inc"
+#undef G2_TAIL
 
   if (paired) {
     // the gate waves (rows 0-127) hand silu(gate), gate = acc * scale, to the up waves through LDS ([128 tokens][132

@@ -51,8 +51,8 @@ def check_schedule(text):
 
 
 def test_schedule_waits_cover_every_use():
-    check_schedule(generate())
-    check_schedule(generate("halves"))
+    for name in ("pairs", "eighths", "steps", "halves"):
+        check_schedule(generate(name))
 
 
 def test_checker_catches_a_missing_wait():
