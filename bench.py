@@ -324,6 +324,13 @@ def main():
         ks, kb = m.time_kernel(which, a.kernel_iters)
         others[name] = dict(us=round(ks * 1e3, 2), mbytes=round(kb / 1e6, 3), gbs=round(kb / (ks / 1e3) / 1e9, 1))
         log(f"  {name}: {ks * 1e3:.2f} us, {kb / 1e6:.2f} MB -> {kb / (ks / 1e3) / 1e9:.0f} GB/s")
+    if m.pos() <= 1024:   # the fused attention + wo kernel the token loop runs at these contexts (q8 wo shapes)
+        try:
+            ks, kb = m.time_kernel(6, a.kernel_iters)
+            others["attn_wo"] = dict(us=round(ks * 1e3, 2), mbytes=round(kb / 1e6, 3), gbs=round(kb / (ks / 1e3) / 1e9, 1))
+            log(f"  attn_wo (fused): {ks * 1e3:.2f} us, {kb / 1e6:.2f} MB -> {kb / (ks / 1e3) / 1e9:.0f} GB/s")
+        except RuntimeError:
+            pass
 
     prefill = None
     if not a.no_prefill:

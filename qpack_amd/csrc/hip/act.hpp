@@ -48,9 +48,66 @@ struct ActRegs {
   float4 x[2][4];
   float4 w[2][4];
 };
+// PRO_NORM_SUM: the input is x + y, y the sum of np <= kMaxParts partial vectors `pstride` floats apart, and workgroup
+// 0 stores that input to xsum.  When the workgroup has at least two threads per 16-column piece, nsets = min(np,
+// threads / pieces) sets of `pieces` threads share the partials (set s adds parts s, s + nsets, ... in order; sets
+// 1 .. nsets - 1 hand their sums to set 0 through scr, [nsets - 1][cols] floats), so every load goes out at once:
+// y = (S_0 + S_1) + ... ; otherwise the owners add the parts one by one, y = ((p_0 + p_1) + p_2) + ...
+constexpr int kMaxParts = 8;
+__host__ __device__ inline int act_part_sets(int cols, int threads, int np) {
+  const int pieces = cols / kQB * 8;
+  return 2 * pieces <= threads ? (np < threads / pieces ? np : threads / pieces) : 1;
+}
+__device__ __forceinline__ void f4add(float4 &a, const float4 &b) { a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w; }
+// sets path (act_part_sets >= 2, one pass): thread t % pieces owns columns 16 (t % pieces) .. + 15 (the set-0 thread)
+__device__ inline void act_load_sum_sets(const float *x, const float *w, int cols, ActRegs &r, const float *part, int np,
+                                         size_t pstride, float *xsum, float *scr, int nsets) {
+  const int pieces = cols / kQB * 8, t = threadIdx.x, set = t / pieces, c0 = (t % pieces) * 16;
+  if (set == 0)
+#pragma unroll
+    for (int k = 0; k < 4; k++) { r.x[0][k] = *(const float4 *)(x + c0 + 4 * k); r.w[0][k] = *(const float4 *)(w + c0 + 4 * k); }
+  float4 y[4];
+  if (set < nsets) {
+    constexpr int Q = kMaxParts / 2;   // parts per set (nsets >= 2)
+    float4 v[Q][4];
+#pragma unroll
+    for (int q = 0; q < Q; q++)
+      if (set + q * nsets < np)
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[q][k] = *(const float4 *)(part + (set + q * nsets) * pstride + c0 + 4 * k);
+#pragma unroll
+    for (int k = 0; k < 4; k++) y[k] = v[0][k];
+#pragma unroll
+    for (int q = 1; q < Q; q++)
+      if (set + q * nsets < np)
+#pragma unroll
+        for (int k = 0; k < 4; k++) f4add(y[k], v[q][k]);
+    if (set > 0)
+#pragma unroll
+      for (int k = 0; k < 4; k++) *(float4 *)(scr + (set - 1) * cols + c0 + 4 * k) = y[k];
+  }
+  __syncthreads();
+  if (set == 0) {
+    for (int s = 1; s < nsets; s++)
+#pragma unroll
+      for (int k = 0; k < 4; k++) f4add(y[k], *(const float4 *)(scr + (s - 1) * cols + c0 + 4 * k));
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      f4add(r.x[0][k], y[k]);
+      if (blockIdx.x == 0) *(float4 *)(xsum + c0 + 4 * k) = r.x[0][k];
+    }
+  }
+  __syncthreads();   // scr is the block-sum area act_build uses next
+}
+
 template <int PRO>
-__device__ __forceinline__ void act_load(const float *x, const float *w, int cols, ActRegs &r) {
+__device__ __forceinline__ void act_load(const float *x, const float *w, int cols, ActRegs &r, const float *part = nullptr,
+                                         int np = 0, size_t pstride = 0, float *xsum = nullptr, float *scr = nullptr) {
   const int nb = cols / kQB, per = (int)blockDim.x / 8, sub = threadIdx.x & 7;
+  if (PRO == PRO_NORM_SUM) {
+    const int nsets = act_part_sets(cols, (int)blockDim.x, np);
+    if (nsets >= 2) { act_load_sum_sets(x, w, cols, r, part, np, pstride, xsum, scr, nsets); return; }
+  }
 #pragma unroll
   for (int p = 0; p < 2; p++) {
     const int b = p * per + (int)(threadIdx.x >> 3);
@@ -59,10 +116,29 @@ __device__ __forceinline__ void act_load(const float *x, const float *w, int col
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         r.x[p][k] = *(const float4 *)(x + c0 + 4 * k);
-        if (PRO == PRO_NORM) r.w[p][k] = *(const float4 *)(w + c0 + 4 * k);
+        if (PRO != PRO_QUANT) r.w[p][k] = *(const float4 *)(w + c0 + 4 * k);
       }
     }
   }
+  if (PRO == PRO_NORM_SUM)   // the owners add the parts one by one
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int b = p * per + (int)(threadIdx.x >> 3);
+      if (b < nb) {
+        const int c0 = b * kQB + sub * 16;
+        float4 y[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) y[k] = *(const float4 *)(part + c0 + 4 * k);
+        for (int j = 1; j < np; j++)
+#pragma unroll
+          for (int k = 0; k < 4; k++) f4add(y[k], *(const float4 *)(part + j * pstride + c0 + 4 * k));
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          f4add(r.x[p][k], y[k]);
+          if (blockIdx.x == 0) *(float4 *)(xsum + c0 + 4 * k) = r.x[p][k];
+        }
+      }
+    }
 }
 __device__ __forceinline__ float f4get(const float4 &v, int j) { return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w)); }
 
@@ -73,7 +149,7 @@ template <int PRO, bool CM = false>
 __device__ void act_build(const ActRegs &r, float eps, int cols, const ActView &a) {
   const int nb = cols / kQB, per = (int)blockDim.x / 8, sub = threadIdx.x & 7;
   float inv = 1.f;
-  if (PRO == PRO_NORM) {
+  if (PRO != PRO_QUANT) {
     float *bss = (float *)a.sums;   // block sums of squares; the sums area is free until the main loop
 #pragma unroll
     for (int p = 0; p < 2; p++) {
@@ -108,7 +184,7 @@ __device__ void act_build(const ActRegs &r, float eps, int cols, const ActView &
 #pragma unroll
       for (int k = 0; k < 16; k++) {
         v[k] = f4get(r.x[p][k >> 2], k & 3);
-        if (PRO == PRO_NORM) v[k] = v[k] * inv * f4get(r.w[p][k >> 2], k & 3);
+        if (PRO != PRO_QUANT) v[k] = v[k] * inv * f4get(r.w[p][k >> 2], k & 3);
       }
       float m = 0;
 #pragma unroll

@@ -62,10 +62,13 @@ __device__ __forceinline__ UnitGeo<NS> unit_geo(const MvArgs &a, int u, int cols
   g.rowbytes = m0.kind == MK_Q8 ? cols : m0.kind == MK_Q4 ? cols / 2 : cols / 8;
   const int sgroups = m0.kind == MK_Q1 ? cols / 128 : cols / 32;   // fp16 scales per row (q4, q1)
   g.nch = (g.rowbytes + 1023) >> 10;
+  const bool rope = EPI == EPI_STORE && NS == 2 && (seg == 0 ? a.rope[0] : (seg == 1 ? a.rope[1] : a.rope[2]));
+  const int H = a.hd / 2;
 #pragma unroll
   for (int s = 0; s < NS; s++) {
     const DMat m = (EPI == EPI_SWIGLU && s == 1) ? a.m[1] : m0;
-    const int r = EPI == EPI_SWIGLU ? (u - u0) : (u - u0) * NS + s;
+    const int lu = u - u0;
+    const int r = EPI == EPI_SWIGLU ? lu : (rope ? (lu / H) * a.hd + lu % H + s * H : lu * NS + s);
     g.row[s] = r;
     const int rc = r < m.rows ? r : m.rows - 1;
     g.p[s] = (const uint8_t *)m.q + (size_t)rc * g.rowbytes;
@@ -116,7 +119,8 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 
   ActRegs ar;
   const int dm = a.dbg_mode;
-  if (!(dm & 2)) act_load<PRO>(a.x, a.norm_w, cols, ar);
+  const int pos = EPI == EPI_STORE && NS == 2 && a.ctl ? a.ctl->pos : 0;   // RoPE / cache position
+  if (!(dm & 2)) act_load<PRO>(a.x, a.norm_w, cols, ar, a.part, a.nparts, a.pstride, a.xsum, (float *)av.sums);
 
   uint4 wr[D][NS];
   uint16_t sr[D][NS];
@@ -311,14 +315,32 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
       }
     }
     const bool store = live && row < og.rows;
-    if (EPI == EPI_SWIGLU) {
+    if (EPI == EPI_STORE && NS == 2 && a.ctl) {
+      // RoPE of q / k rows (the partner row of the pair sits in the next lane) and the fp16 cache rows
+      const int sg = og.seg;
+      const float *const bias_seg = sg == 0 ? a.bias[0] : (sg == 1 ? a.bias[1] : a.bias[2]);
+      float y = v;
+      if (store && bias_seg) y = y + bias_seg[row];
+      const float yo = __shfl_xor(y, 1, kWave);
+      const bool rope = sg == 0 ? a.rope[0] : (sg == 1 ? a.rope[1] : a.rope[2]);
+      uint16_t *const cache = sg == 0 ? a.cache[0] : (sg == 1 ? a.cache[1] : a.cache[2]);
+      if (store) {
+        if (rope) {
+          const int H = a.hd / 2, i = row % H;
+          const float cs = a.cos_t[(size_t)pos * H + i], sn = a.sin_t[(size_t)pos * H + i];
+          y = s == 0 ? __builtin_fmaf(y, cs, -(yo * sn)) : __builtin_fmaf(y, cs, yo * sn);
+        }
+        (sg == 0 ? a.out[0] : (sg == 1 ? a.out[1] : a.out[2]))[row] = y;
+        if (cache) cache[(size_t)pos * a.cache_ld + row] = f32_to_half_bits(y);
+      }
+    } else if (EPI == EPI_SWIGLU) {
       const float up = __shfl_xor(v, 1, kWave);   // slot 1 (up) sits in the lane after slot 0 (gate)
       if (store && s == 0) a.out[0][row] = v / (1.f + exp_poly(0.f - v)) * up;   // silu_mul, kernels_x86.cpp:427-431
     } else if (store) {
       float *const out_seg = og.seg == 0 ? a.out[0] : (og.seg == 1 ? a.out[1] : a.out[2]);
       const float *const bias_seg = og.seg == 0 ? a.bias[0] : (og.seg == 1 ? a.bias[1] : a.bias[2]);
       if (EPI == EPI_STORE) { float y = v; if (bias_seg) y = y + bias_seg[row]; out_seg[row] = y; }
-      else if (EPI == EPI_RESID) a.out[0][row] = a.out[0][row] + v;
+      else if (EPI == EPI_RESID) a.out[0][row] = (a.resid_in ? a.resid_in[row] : a.out[0][row]) + v;
       else { a.out[0][row] = v; if (better(v, row, best_v, best_i)) { best_v = v; best_i = row; } }
     }
   }
@@ -342,7 +364,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 // rows per unit: SwiGLU units are one gate/up row pair; large matrices stream 2 rows per unit (the activation LDS reads
 // serve both), small ones 1 row so every wave gets an equal share
 static int mv_ns(const MvArgs &a, int epi, int waves) {
-  if (epi == EPI_SWIGLU) return 2;
+  if (epi == EPI_SWIGLU || (epi == EPI_STORE && a.ctl)) return 2;   // SwiGLU pairs; RoPE pairs (q / k / v)
   int rows = 0;
   for (int s = 0; s < a.nseg; s++) rows += a.m[s].rows;
   return rows >= 4 * waves ? 2 : 1;
@@ -396,7 +418,12 @@ static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
     a.upw = up8 > up4 ? up8 : up4;
   }
   const int nbp = ((cols / kQB) + 3) / 4 * 4;
-  const size_t lds = mv_lds_bytes(cols, w, a.upw * NS * (KIND == MK_Q8 || KIND == MK_MIX ? nbp : 1));
+  size_t lds = mv_lds_bytes(cols, w, a.upw * NS * (KIND == MK_Q8 || KIND == MK_MIX ? nbp : 1));
+  if (PRO == PRO_NORM_SUM) {   // the partial sets' hand-over area at the sums offset
+    if (a.nparts < 1 || a.nparts > kMaxParts) return hipErrorInvalidValue;
+    const int ns = act_part_sets(cols, w * 64, a.nparts);
+    lds = std::max(lds, mv_lds_bytes(cols, w, 0) - 4 * (size_t)nbp + 4 * (size_t)(ns - 1) * cols);
+  }
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   const bool dbg = a.dbg_sums || a.dbg_xq || a.dbg_bs;
   if (dbg) {
@@ -415,6 +442,7 @@ static hipError_t launch_mv_k(int pro, int epi, const MvArgs &a, int ns, int gri
   QPH_MV(PRO_QUANT, EPI_ARGMAX)
 #undef QPH_MV
   if (pro == PRO_NORM && epi == EPI_SWIGLU) return launch_mv_t<PRO_NORM, EPI_SWIGLU, 2, KIND>(a, grid_cap, st);
+  if (pro == PRO_NORM_SUM && epi == EPI_SWIGLU) return launch_mv_t<PRO_NORM_SUM, EPI_SWIGLU, 2, KIND>(a, grid_cap, st);
   return hipErrorInvalidValue;
 }
 MvConfig g_mv_config;
@@ -424,6 +452,11 @@ MvConfig g_mv_config;
 hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStream_t st) {
   const int cols = a.m[0].cols;
   if (cols % kQB || cols > 32768) return hipErrorInvalidValue;
+  if (a.ctl) {   // RoPE / cache rows: the decode q / k / v launch
+    if (epi != EPI_STORE || a.hd < 2 || a.hd % 2 || !a.cos_t || !a.sin_t) return hipErrorInvalidValue;
+    for (int s = 0; s < a.nseg; s++)
+      if ((a.rope[s] && a.m[s].rows % a.hd) || (!a.rope[s] && a.m[s].rows % 2)) return hipErrorInvalidValue;
+  }
   const int nseg = epi == EPI_SWIGLU ? 1 : a.nseg;
   bool has8 = false, has4 = false, has1 = false;
   for (int s = 0; s < nseg; s++) { has8 |= a.m[s].kind == MK_Q8; has4 |= a.m[s].kind == MK_Q4; has1 |= a.m[s].kind == MK_Q1; }
@@ -432,7 +465,10 @@ hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStr
     MvArgs b = a; b.nseg = 0;
     for (int k : {(int)MK_Q8, (int)MK_Q4})
       for (int s = 0; s < nseg; s++)
-        if (a.m[s].kind == k) { b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s]; b.nseg++; }
+        if (a.m[s].kind == k) {
+          b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s];
+          b.rope[b.nseg] = a.rope[s]; b.cache[b.nseg] = a.cache[s]; b.nseg++;
+        }
     const int ns = mv_ns(b, epi, g_mv_config.cus * 16);
     if (pro == PRO_NORM) return ns == 2 ? launch_mv_t<PRO_NORM, EPI_STORE, 2, MK_MIX>(b, grid_cap, st)
                                         : launch_mv_t<PRO_NORM, EPI_STORE, 1, MK_MIX>(b, grid_cap, st);
@@ -442,7 +478,10 @@ hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStr
   for (int k : {(int)MK_Q8, (int)MK_Q4, (int)MK_Q1}) {
     MvArgs b = a; b.nseg = 0;
     for (int s = 0; s < nseg; s++)
-      if (a.m[s].kind == k) { b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s]; b.nseg++; }
+      if (a.m[s].kind == k) {
+        b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s];
+        b.rope[b.nseg] = a.rope[s]; b.cache[b.nseg] = a.cache[s]; b.nseg++;
+      }
     if (!b.nseg) continue;
     if (epi == EPI_SWIGLU) { b.m[1] = a.m[1]; b.nseg = 1; b.seg_tile0[0] = 0; b.seg_tile0[1] = a.m[0].rows; }
     if (b.nseg != nseg && (b.dbg_sums || epi == EPI_ARGMAX)) return hipErrorInvalidValue;
@@ -483,9 +522,8 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 // needed; beyond that S_eff = min(grid.y, ceil(T / 64)) splits.  Split s takes positions [s T / S_eff, (s + 1) T /
 // S_eff); the waves take contiguous runs of whole blocks, streamed straight from HBM with the next block's loads in
 // flight.
-// The workgroup applies RoPE to its rep query heads (rotate-half with the reference's contraction
-// a' = fma(a, cos, -(b sin)), b' = fma(b, cos, a sin), model_llama.cpp:176); the workgroup owning the current position
-// writes the rotated k and the v row into the cache as fp16 (round to nearest even, to_f16) and uses its LDS copy.
+// The queries arrive rotated and the current position's k / v rows are already in the cache: the q / k / v matvec's
+// epilogue applies RoPE and writes the fp16 rows (EPI_STORE with MvArgs::rope / cache).
 // Per wave (MFMA, see attn_split): scores S^T = K q^T, an online softmax per head, values O^T += V^T P^T; the wave
 // partials merge in LDS; with several splits the last one to finish (a per-group counter, which that workgroup
 // resets) merges the split partials in split order - the merge of model_llama.cpp:160-165:
@@ -498,7 +536,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // output and (max, sum) to a.part (waves 0 .. nact - 1 hold positions; ored rows HS floats apart)
 template <int HD, int REP, int NW, int HS>
 __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s, int S, int ys, int nact,
-                                                const float (*wm)[REP], const float (*wl)[REP], const float (*ored)[REP][HS]) {
+                                                const float (*wm)[REP], const float (*wl)[REP], const float (*ored)[REP][HS],
+                                                float *lout) {
   __shared__ float fwv[NW][REP], mlv[REP][2];
   // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M).  Wave 0 holds every
   // (wave w, head j) pair, lane 8 w + j (NW, REP <= 8), and reduces over w with xor shuffles of 8, 16 and 32
@@ -530,7 +569,8 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
     const float M = mlv[j][0], L = mlv[j][1];
     if (S == 1) {
       const float li = 1.f / L;
-      *(float4 *)(a.att + (size_t)(g * REP + j) * HD + i) = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
+      float *dst = lout ? lout + j * HD + i : a.att + (size_t)(g * REP + j) * HD + i;
+      *(float4 *)dst = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
     } else {
       // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback; the
       // caller's s_waitcnt vmcnt(0) before the arrival counter covers them.
@@ -588,8 +628,11 @@ __device__ __forceinline__ void mf_load_v(const uint16_t *vc, int kvd, int g, in
   }
 }
 
-template <int HD, int REP>
-__device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
+// lout: with S == 1, the normalised heads go to this LDS array [REP][HD] instead of a.att; mid() runs once the waves'
+// partials are in LDS, before their merge (the block loop's registers are free by then)
+struct AttnNoMid { __device__ void operator()() const {} };
+template <int HD, int REP, typename Mid = AttnNoMid>
+__device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float *lout = nullptr, const Mid &mid = Mid()) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   // LDS rows padded so the MFMA-layout accesses (16 heads / dims apart per lane) spread over the banks
@@ -598,8 +641,6 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
   __shared__ __align__(16) float qs[REP][QS];
   __shared__ float wm[NW][REP], wl[NW][REP];
   __shared__ __align__(16) float ored[NW][REP][QS];
-  __shared__ __align__(16) uint16_t knew[HD];
-  __shared__ __align__(16) uint16_t vnew[HD];
   __shared__ __align__(16) uint16_t vt[NW][HD * VS];
   const int pos = a.ctl->pos, T = pos + 1;
   const int kvd = a.nkv * HD;
@@ -615,25 +656,9 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
     mf_load_k<HD>(a.kc, kvd, g, wt0, wt1, lane, ka);
     mf_load_v<HD>(a.vc, kvd, g, wt0, wt1, lane, vb);
   }
-  const float *cs = a.cos_t + (size_t)pos * HALF, *sn = a.sin_t + (size_t)pos * HALF;
-  for (int e = threadIdx.x; e < REP * HALF; e += blockDim.x) {
-    const int j = e / HALF, i = e % HALF; const float *qh = a.q + (size_t)(g * REP + j) * HD;
-    const float x0 = qh[i], x1 = qh[i + HALF];
-    qs[j][i] = __builtin_fmaf(x0, cs[i], -(x1 * sn[i]));
-    qs[j][i + HALF] = __builtin_fmaf(x1, cs[i], x0 * sn[i]);
-  }
-  if (t0 <= pos && pos < t1) {
-    for (int i = threadIdx.x; i < HALF; i += blockDim.x) {
-      const float *kh = a.k + (size_t)g * HD; const float x0 = kh[i], x1 = kh[i + HALF];
-      const uint16_t k0 = f32_to_half_bits(__builtin_fmaf(x0, cs[i], -(x1 * sn[i])));
-      const uint16_t k1 = f32_to_half_bits(__builtin_fmaf(x1, cs[i], x0 * sn[i]));
-      knew[i] = k0; knew[i + HALF] = k1;
-      a.kc[(size_t)pos * kvd + g * HD + i] = k0; a.kc[(size_t)pos * kvd + g * HD + i + HALF] = k1;
-    }
-    for (int i = threadIdx.x; i < HD; i += blockDim.x) {
-      const uint16_t v = float_to_half_bits(a.v[(size_t)g * HD + i]);
-      vnew[i] = v; a.vc[(size_t)pos * kvd + g * HD + i] = v;
-    }
+  for (int e = threadIdx.x; e < REP * HD / 4; e += blockDim.x) {   // the group's rotated heads, 4 dims per thread
+    const int j = e / (HD / 4), i = 4 * (e % (HD / 4));
+    *(float4 *)&qs[j][i] = *(const float4 *)(a.q + (size_t)(g * REP + j) * HD + i);
   }
   __syncthreads();
   // q^T fragments: lane holds head lr (zero past REP), dims 32 s + 8 lg + 0..7, as hi / lo halves
@@ -659,14 +684,14 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
   // one block: V -> LDS, then the next block's loads (V into the same registers, K into the other set), then the
   // scores from this block's K registers
   auto block = [&](MfK<HD> &kcur, MfK<HD> &knxt, int tb) {
-    // V -> LDS transposed (this wave's tile; the current position's row from LDS).  Piece i of lane l holds position
+    // V -> LDS transposed (this wave's tile).  Piece i of lane l holds position
     // p, dims d0 .. d0 + 7; the lane HD / 8 away holds position p ^ 1, same dims.  The two swap halves so that the
     // even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each writes
     // four (p even, p odd) pairs of its dims as 32-bit words.
 #pragma unroll
     for (int i = 0; i < NV; i++) {
       const int c = lane + 64 * i, p = c / (HD / 8), d0 = 8 * (c % (HD / 8));
-      const u32x4 vv = tb + p == pos ? *(const u32x4 *)(vnew + d0) : vb.v[i];
+      const u32x4 vv = vb.v[i];
       const bool ev = (p & 1) == 0;
       const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, kWave);
       const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, kWave);
@@ -690,11 +715,9 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
 #pragma unroll
     for (int mt = 0; mt < 2; mt++) {
       sc[mt] = (f4){0.f, 0.f, 0.f, 0.f};
-      const bool cur = tb + 16 * mt + lr == pos;
 #pragma unroll
       for (int k = 0; k < KS; k++) {
-        const u32x4 kw = cur ? *(const u32x4 *)(knew + 32 * k + 8 * lg) : kcur.k[mt][k];
-        const h8 kf = __builtin_bit_cast(h8, kw);
+        const h8 kf = __builtin_bit_cast(h8, kcur.k[mt][k]);
         sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[k], sc[mt], 0, 0, 0);
         sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[k], sc[mt], 0, 0, 0);
       }
@@ -755,8 +778,9 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys) {
 #pragma unroll
     for (int d = 0; d < DT; d++) *(float4 *)&ored[wave][lr][16 * d + 4 * lg] = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
   }
+  mid();
   __syncthreads();
-  attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored);
+  attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored, lout);
 }
 
 // One workgroup merges every head of group g over S < kAttnParMerge splits, in one round of loads: P threads share
@@ -910,7 +934,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
       while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < S && ++spins < lim)
         __builtin_amdgcn_s_sleep(1);
     rank = r < 0 ? -1 : r;
-    late = spins >= lim;
+    late = spins >= lim || (a.force_late && r >= 0 && r < MG - 1);
     if (late && a.status) *(volatile int *)a.status = 1;   // the step's outputs are invalid: the host raises an error
   }
   __syncthreads();
@@ -943,6 +967,141 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
   QPH_ATT(64, 1) QPH_ATT(64, 2) QPH_ATT(64, 3) QPH_ATT(64, 4) QPH_ATT(64, 5) QPH_ATT(64, 6) QPH_ATT(64, 7) QPH_ATT(64, 8)
   QPH_ATT(128, 1) QPH_ATT(128, 2) QPH_ATT(128, 3) QPH_ATT(128, 4) QPH_ATT(128, 5) QPH_ATT(128, 6) QPH_ATT(128, 7) QPH_ATT(128, 8)
 #undef QPH_ATT
+  return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------ decode attention fused with the wo product
+// Workgroup (kv group g, row chunk c) of grid (nkv, rc), 8 waves:
+//   1. computes the group's attention over the whole context with attn_split (one split, output to LDS);
+//   2. once the waves' partials are in LDS (before their merge) issues the loads of its wo tile - rows [c R, c R + R)
+//      x the group's columns [g CG, g CG + CG), CG = REP * HD - into registers (NL 16-byte pieces per thread; piece
+//      p = thread + 512 i is row p / (CG / 16), bytes 16 (p % (CG / 16)) of the row's slice);
+//   3. quantises the REP * HD outputs with quant_rows' arithmetic, every 128 columns one block (act_build's
+//      expressions: the same planes and scales as the wo matvec's prologue builds from att for these blocks);
+//   4. forms the exact int32 block sums (the matvec's two-plane dot products and 8-lane sums) and, one thread per row,
+//      rows_q8's fp32 chain over the group's blocks, acc = fma(bs[b], sum[b], acc) (kernels_x86.cpp:57-69), times the
+//      row scale: part[g][row].  No workgroup waits for another; the next kernel sums the groups' parts.
+template <int HD, int REP, int NL>
+__global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoArgs w) {
+  constexpr int NT = kAttnMfWaves * 64, CG = REP * HD, PPR = CG / 16, NBG = CG / kQB;
+  static_assert(CG % kQB == 0, "a group's columns are whole quantisation blocks");
+  __shared__ __align__(16) float ao[REP * HD];
+  __shared__ __align__(16) int8_t xh[CG];
+  __shared__ __align__(16) uint8_t xl[CG];
+  __shared__ float bsl[NBG];
+  __shared__ int lsl[NBG];
+  __shared__ int isl[NT * NL / 8];   // block sums [row in tile][NBG]
+  const int g = blockIdx.x, c = blockIdx.y, d = w.wo.rows, cols = w.wo.cols;
+  const int r0 = c * w.R, R = min(w.R, d - r0);
+  const int8_t *wq = (const int8_t *)w.wo.q + (size_t)g * CG;
+  uint64_t t0 = 0, t1 = 0, t2 = 0;
+  if (w.stamps) t0 = __builtin_amdgcn_s_memrealtime();
+  uint4 wr[NL];
+  auto issue = [&]() {
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int p = threadIdx.x + NT * i, lr = p / PPR, c16 = p % PPR;
+      const int row = lr < R ? r0 + lr : r0;   // past the tile: row r0 (< d: chunks are never empty), not used
+      wr[i] = *(const uint4 *)(wq + (size_t)row * cols + 16 * c16);
+    }
+  };
+  attn_split<HD, REP>(a, g, 0, 1, 1, ao, issue);
+  __syncthreads();
+  if (w.stamps) t1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x < 8 * NBG) {   // eight lanes per block, 16 columns each (act_build's arithmetic)
+    const int b = threadIdx.x >> 3, sub = threadIdx.x & 7, c0 = b * kQB + sub * 16;
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float4 t = *(const float4 *)(ao + c0 + 4 * k);
+      v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+    }
+    float m = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) m = fmaxf(m, fabsf(v[k]));
+    m = max8_f(m);
+    const float isx = m > 0 ? kActMax / m : 0.f;
+    if (sub == 0) bsl[b] = m / kActMax;
+    uint32_t hw[4], lw[4]; int ls = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      uint32_t hh = 0, ll = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int q = (int)__builtin_rintf(v[4 * k + j] * isx);
+        hh |= (uint32_t)((q >> 8) & 0xff) << (8 * j);
+        ll |= (uint32_t)(q & 0xff) << (8 * j);
+        ls += q & 0xff;
+      }
+      hw[k] = hh; lw[k] = ll;
+    }
+    *(uint4 *)(xh + c0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(xl + c0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    ls = sum8_i(ls);
+    if (sub == 0) lsl[b] = ls;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    const int p = threadIdx.x + NT * i, lr = p / PPR, c16 = p % PPR;
+    const uint4 h = *(const uint4 *)(xh + 16 * c16), l = *(const uint4 *)(xl + 16 * c16);
+    const uint4 ww = wr[i];
+    int A = __builtin_amdgcn_sdot4((int)ww.x, (int)h.x, 0, false);
+    A = __builtin_amdgcn_sdot4((int)ww.y, (int)h.y, A, false);
+    A = __builtin_amdgcn_sdot4((int)ww.z, (int)h.z, A, false);
+    A = __builtin_amdgcn_sdot4((int)ww.w, (int)h.w, A, false);
+    uint32_t B = __builtin_amdgcn_udot4(ww.x ^ 0x80808080u, l.x, 0u, false);
+    B = __builtin_amdgcn_udot4(ww.y ^ 0x80808080u, l.y, B, false);
+    B = __builtin_amdgcn_udot4(ww.z ^ 0x80808080u, l.z, B, false);
+    B = __builtin_amdgcn_udot4(ww.w ^ 0x80808080u, l.w, B, false);
+    const int sum = sum8_i(A * 256 + (int)B);
+    if ((lane & 7) == 0 && lr < R) isl[lr * NBG + (c16 >> 3)] = sum - 128 * lsl[c16 >> 3];
+  }
+  __syncthreads();
+  if (w.stamps) t2 = __builtin_amdgcn_s_memrealtime();
+  for (int lr = threadIdx.x; lr < R; lr += NT) {
+    float ch = 0.f;
+#pragma unroll
+    for (int b = 0; b < NBG; b++) ch = __builtin_fmaf(bsl[b], (float)isl[lr * NBG + b], ch);
+    const int row = r0 + lr;
+    w.part[(size_t)g * d + row] = ch * ((const float *)w.wo.s)[row];
+  }
+  if (w.stamps && threadIdx.x == 0) {
+    uint64_t *o = w.stamps + 4 * (blockIdx.y * gridDim.x + blockIdx.x);
+    o[0] = t0; o[1] = t1; o[2] = t2; o[3] = __builtin_amdgcn_s_memrealtime();
+  }
+}
+
+bool attn_wo_fits(int hd, int nh, int nkv, const DMat &wo, int cus, int *rc, int *nl) {
+  if (wo.kind != MK_Q8 || nh % nkv || (hd != 64 && hd != 128)) return false;
+  const int rep = nh / nkv, cg = rep * hd;
+  if (cg % kQB || rep > 8 || wo.cols != nh * hd || wo.rows < 1) return false;
+  // about one workgroup per CU; every chunk non-empty (rc = ceil(rows / R))
+  for (int c = std::max(1, std::min(wo.rows, cus / nkv)); c <= wo.rows; c++) {
+    const int R = (wo.rows + c - 1) / c, pieces = R * (cg / 16), need = (pieces + kAttnMfWaves * 64 - 1) / (kAttnMfWaves * 64);
+    if (need <= 16) { *rc = (wo.rows + R - 1) / R; *nl = need <= 4 ? 4 : need <= 8 ? 8 : 16; return true; }
+  }
+  return false;
+}
+
+hipError_t launch_attn_wo(const AttnArgs &a, AwoArgs w, hipStream_t st) {
+  int rc = 0, nl = 0;
+  if (!attn_wo_fits(a.hd, a.nh, a.nkv, w.wo, g_mv_config.cus, &rc, &nl)) return hipErrorInvalidValue;
+  w.R = (w.wo.rows + rc - 1) / rc;
+  if ((size_t)(rc - 1) * w.R >= (size_t)w.wo.rows) return hipErrorInvalidValue;
+  const dim3 grid(a.nkv, rc);
+  const int rep = a.nh / a.nkv;
+#define QPH_AWO(HD, R, NL)                                                                                          \
+  if (a.hd == HD && rep == R && nl == NL) {                                                                         \
+    hipLaunchKernelGGL((k_attn_wo<HD, R, NL>), grid, dim3(kAttnMfWaves * 64), 0, st, a, w);                         \
+    return hipGetLastError();                                                                                       \
+  }
+#define QPH_AWO3(HD, R) QPH_AWO(HD, R, 4) QPH_AWO(HD, R, 8) QPH_AWO(HD, R, 16)
+  QPH_AWO3(64, 2) QPH_AWO3(64, 4) QPH_AWO3(64, 6) QPH_AWO3(64, 8)
+  QPH_AWO3(128, 1) QPH_AWO3(128, 2) QPH_AWO3(128, 3) QPH_AWO3(128, 4) QPH_AWO3(128, 5) QPH_AWO3(128, 6) QPH_AWO3(128, 7) QPH_AWO3(128, 8)
+#undef QPH_AWO3
+#undef QPH_AWO
   return hipErrorInvalidValue;
 }
 

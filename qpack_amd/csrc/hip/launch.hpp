@@ -22,11 +22,12 @@ namespace qph {
 enum Prologue : int {
   PRO_QUANT = 0,   // quantise x as is (wo input, down input, test hook)
   PRO_NORM = 1,    // RMSNorm(x) * w, then quantise (qkv, gate/up, output head)
+  PRO_NORM_SUM = 2,   // the same on x + the sum of nparts partial vectors (gate/up after the fused attention + wo)
 };
 // what a matvec kernel does with each finished row value y = W x
 enum Epilogue : int {
   EPI_STORE = 0,    // out[seg][row] = y (+ bias[seg][row])          up to 3 segments (q / k / v)
-  EPI_RESID = 1,    // out[0][row] += y                             (wo, down: residual stream)
+  EPI_RESID = 1,    // out[0][row] = in[row] + y, in = resid_in or out[0] (wo, down: residual stream)
   EPI_SWIGLU = 2,   // out[0][row] = silu(y_gate) * y_up            (segments 0 = gate, 1 = up, same rows)
   EPI_ARGMAX = 3,   // out[0][row] = y and one (max, index) per workgroup into amax (output head)
 };
@@ -49,6 +50,18 @@ struct MvArgs {
   // set by the launcher for one launch over q8 and q4 segments (MK_MIX): the q8 segments come first, their units are
   // [0, mix_u8), and waves gw < mix_w8 take them; the other waves take the q4 units
   int mix_w8, mix_u8;
+  // PRO_NORM_SUM: partial vectors part[j * pstride + c], j < nparts (added to x in order); workgroup 0 stores the sum
+  const float *part; int nparts; size_t pstride; float *xsum;
+  const float *resid_in;   // EPI_RESID: the residual input when it is not out[0]
+  // EPI_STORE (q / k / v of the decode step; needs 2-row units): segment s with rope[s] pairs rows i and i + hd / 2 of
+  // each head in a unit and rotates them after the bias (model_llama.cpp:176: a' = fma(a, cos, -(b sin)),
+  // b' = fma(b, cos, a sin), tables at position ctl->pos); a segment with cache[s] also writes its (rotated) row as
+  // fp16 into cache[s] at position ctl->pos (row stride cache_ld)
+  int rope[3];
+  uint16_t *cache[3];
+  int cache_ld, hd;
+  const float *cos_t, *sin_t;
+  const Ctl *ctl;
 };
 
 // The matvec kernel runs one workgroup of up to 16 waves per CU; every wave streams its own units of 1 or 2 rows
@@ -81,9 +94,8 @@ hipError_t launch_embed(const DMat &embed, const Ctl *ctl, float *x, hipStream_t
 hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, float *out, hipStream_t st);
 
 struct AttnArgs {
-  const float *q, *k, *v;      // this step's projections (bias added, RoPE not yet applied)
-  uint16_t *kc, *vc;           // this layer's fp16 caches [ctx][kvd]
-  const float *cos_t, *sin_t;  // RoPE tables [ctx][hd / 2]
+  const float *q;              // this step's queries, RoPE applied (the q / k / v matvec's epilogue)
+  uint16_t *kc, *vc;           // this layer's fp16 caches [ctx][kvd], the current position's rows already written
   const Ctl *ctl;
   float *part;                 // unnormalised outputs [nh][splits][hd], then (max, sum) [nh][splits][2]
   int *counters;               // [2 nkv] zero: arrivals and finished mergers per group; the last merger resets both
@@ -94,8 +106,24 @@ struct AttnArgs {
   int split_pos;               // beyond: S = min(max_chunks, ceil(T / split_pos)) (0: 64)
   int *status;                 // optional (host-visible): set to 1 when a merger's bounded wait for the partials ran out
   int spin_limit;              // the bound of that wait in polls (0: 1 << 22)
+  int force_late;              // test hook: every merger that would wait gives up at once (the error path, forced)
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+// Decode attention fused with the wo product (q8 wo, REP * hd a multiple of 128): grid (nkv, rc); workgroup (g, c)
+// computes kv group g's attention over the whole context (no splits) and, for wo rows [c R, c R + R), the product over
+// the group's columns: part[g][row] = (rows_q8's fp32 block chain over the group's blocks) * scale[row].  The next
+// kernel adds x + sum_g part[g] in group order (PRO_NORM_SUM).  The attention's part / counters / max_chunks fields are
+// unused.
+struct AwoArgs {
+  DMat wo;      // q8 [d][nh * hd]
+  float *part;  // [nkv][d] per-group partial products
+  int R;        // rows per chunk (set by the launcher)
+  uint64_t *stamps;   // measurement only (optional): per workgroup realtime at start, after the attention, after the
+                      // weights arrived, at the end
+};
+// whether the fused kernel takes this shape; rc = row chunks (grid.y), nl = 16-byte weight pieces per thread
+bool attn_wo_fits(int hd, int nh, int nkv, const DMat &wo, int cus, int *rc, int *nl);
+hipError_t launch_attn_wo(const AttnArgs &a, AwoArgs w, hipStream_t st);
 
 // greedy pick over the head's per-workgroup (max, index) pairs; advances ctl (tok = pick, pos += 1, n_out += 1) and
 // writes the pick to out_tokens[ctl->n_out]

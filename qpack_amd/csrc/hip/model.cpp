@@ -115,6 +115,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   if (const char *e = getenv("QPH_ATTN_SPLIT_POS")) attn_split_pos_ = std::max(0, atoi(e));
   // test hook: the bound of a merger's wait for the other splits (the failure path forced from the host)
   if (const char *e = getenv("QPH_ATTN_SPIN")) attn_spin_ = std::max(0, atoi(e));
+  attn_force_late_ = getenv("QPH_ATTN_FORCE_LATE") != nullptr;   // test hook: the same failure without the race
   counters_ = (int *)dalloc(8ull * nkv);
   const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
   kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
@@ -124,6 +125,18 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   h_ = (float *)dalloc(4ull * ff); logits_ = (float *)dalloc(4ull * V);
   part_ = (float *)dalloc(4ull * nh * max_chunks_ * (hd + 2));
   QPH_CK(hipMemset(counters_, 0, 8ull * nkv));
+  {  // decode attention fused with wo (q8 wo on every layer, a group's heads whole 128-column blocks), short contexts
+    int rc = 0, nl = 0;
+    bool ok = !layers_.empty();
+    for (const Layer &ly : layers_) ok = ok && attn_wo_fits(hd, nh, nkv, ly.wo, g_mv_config.cus, &rc, &nl);
+    const char *e = getenv("QPH_AWO_MAX");   // longest context (positions) that takes the fused kernel; 0: never
+    awo_max_ = ok ? (e ? std::max(0, atoi(e)) : kAwoMaxDefault) : 0;
+    if (awo_max_ > 0) {
+      awo_rc_ = rc;
+      awo_part_ = (float *)dalloc(4ull * nkv * d);
+      xs_ = (float *)dalloc(4ull * d);
+    }
+  }
   head_grid_ = cus_ * 4;
   amax_ = (float2 *)dalloc(sizeof(float2) * head_grid_);
   {  // partials of workgroups a smaller launch does not use must never win the pick
@@ -201,7 +214,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
 
 HipLlama::~HipLlama() {
   if (st_) (void)hipStreamSynchronize(st_);
-  for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_, g_ex_state_, g_ex_logits_, g_ex_greedy_})
+  for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_, g_ex_state_, g_ex_logits_, g_ex_greedy_, g_fs_state_,
+                           g_fs_logits_, g_fs_greedy_})
     if (g) (void)hipGraphExecDestroy(g);
   for (void *p : allocs_) (void)hipFree(p);
   if (hctl_) (void)hipHostFree(hctl_);
@@ -212,25 +226,42 @@ HipLlama::~HipLlama() {
   if (st_) (void)hipStreamDestroy(st_);
 }
 
+// the decode q / k / v launch's epilogue: RoPE on q and k at ctl->pos, fp16 k / v rows into this layer's caches
+void HipLlama::qkv_rope(MvArgs &a, uint16_t *kc, uint16_t *vc) const {
+  a.rope[0] = a.rope[1] = 1; a.rope[2] = 0;
+  a.cache[0] = nullptr; a.cache[1] = kc; a.cache[2] = vc;
+  a.cache_ld = kvd_; a.hd = cfg_.head_dim; a.cos_t = cos_; a.sin_t = sin_; a.ctl = ctl_;
+}
+
 void HipLlama::enqueue_layer(int l) {
   const Layer &ly = layers_[l];
   const int cap = 1 << 20;
   const float eps = cfg_.rms_eps;
-  {  // RMSNorm + q/k/v (+ bias)
+  uint16_t *kc = kc_ + (size_t)l * ctx_ * kvd_, *vc = vc_ + (size_t)l * ctx_ * kvd_;
+  {  // RMSNorm + q/k/v (+ bias), RoPE on q / k, fp16 k / v rows into the caches
     MvArgs a{}; a.m[0] = ly.wq; a.m[1] = ly.wk; a.m[2] = ly.wv; a.nseg = 3; a.x = x_; a.norm_w = ly.an; a.eps = eps;
     a.out[0] = q_; a.out[1] = k_; a.out[2] = v_; a.bias[0] = ly.bq; a.bias[1] = ly.bk; a.bias[2] = ly.bv;
+    qkv_rope(a, kc, vc);
     mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_NORM, EPI_STORE, a, cap, st_));
   }
-  {  // RoPE, fp16 KV append, split-K attention, merge
-    AttnArgs a{}; a.q = q_; a.k = k_; a.v = v_;
-    a.kc = kc_ + (size_t)l * ctx_ * kvd_; a.vc = vc_ + (size_t)l * ctx_ * kvd_;
-    a.cos_t = cos_; a.sin_t = sin_; a.ctl = ctl_; a.part = part_; a.att = att_;
-    a.nh = cfg_.heads; a.nkv = cfg_.kv_heads; a.hd = cfg_.head_dim; a.max_chunks = max_chunks_; a.counters = counters_;
-    a.single_max = attn_single_; a.split_pos = attn_split_pos_; a.status = dstatus_; a.spin_limit = attn_spin_;
-    QPH_CK(launch_attention(a, st_));
-  }
-  {  // wo + residual
-    MvArgs a{}; a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = x_;
+  AttnArgs at{}; at.q = q_; at.kc = kc; at.vc = vc; at.ctl = ctl_; at.part = part_; at.att = att_;
+  at.nh = cfg_.heads; at.nkv = cfg_.kv_heads; at.hd = cfg_.head_dim; at.max_chunks = max_chunks_; at.counters = counters_;
+  at.single_max = attn_single_; at.split_pos = attn_split_pos_; at.status = dstatus_; at.spin_limit = attn_spin_;
+  at.force_late = attn_force_late_;
+  if (fuse_) {
+    // RoPE, fp16 KV append, attention and the wo product per kv group in one launch; the group partials are added to
+    // the residual stream by the gate / up prologue (x + sum of parts, also stored to xs_), down adds into x_ from xs_
+    AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_;
+    QPH_CK(launch_attn_wo(at, w, st_));
+    MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
+    a.part = awo_part_; a.nparts = cfg_.kv_heads; a.pstride = (size_t)cfg_.hidden; a.xsum = xs_;
+    mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM_SUM, EPI_SWIGLU, a, cap, st_));
+    MvArgs b{}; b.m[0] = ly.wd; b.nseg = 1; b.x = h_; b.out[0] = x_; b.resid_in = xs_;
+    mv_plan(b, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, b, cap, st_));
+    return;
+  } else {
+    QPH_CK(launch_attention(at, st_));   // RoPE, fp16 KV append, split-K attention, merge
+    MvArgs a{}; a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = x_;   // wo + residual
     mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_));
   }
   {  // RMSNorm + gate / up + SwiGLU
@@ -269,12 +300,15 @@ void HipLlama::enqueue_step(int parts) {
   if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
 }
 
-hipGraphExec_t HipLlama::capture(int parts) {
+hipGraphExec_t HipLlama::capture(int parts, bool fused) {
   hipGraph_t g = nullptr; hipGraphExec_t ge = nullptr;
+  fuse_ = fused;
   QPH_CK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
   try {
     enqueue_step(parts);
+    fuse_ = false;
   } catch (...) {
+    fuse_ = false;
     (void)hipStreamEndCapture(st_, &g);
     if (g) (void)hipGraphDestroy(g);
     throw;
@@ -295,16 +329,23 @@ void HipLlama::build_graphs() {
   g_state_ = capture(0);
   g_logits_ = capture(1);
   g_greedy_ = capture(2);
+  if (awo_max_ > 0) { g_fs_state_ = capture(0, true); g_fs_logits_ = capture(1, true); g_fs_greedy_ = capture(2, true); }
 }
 
-void HipLlama::run_step(int parts) {
+// pos: the position this step writes (its context is pos + 1 positions); contexts up to awo_max_ take the fused
+// attention + wo kernel
+void HipLlama::run_step(int parts, int pos) {
+  const bool fused = !order_ && pos + 1 <= awo_max_;
   if (use_graphs_) {
     hipGraphExec_t g = order_ ? (parts == 0 ? g_ex_state_ : parts == 1 ? g_ex_logits_ : g_ex_greedy_)
-                              : (parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_);
+                       : fused ? (parts == 0 ? g_fs_state_ : parts == 1 ? g_fs_logits_ : g_fs_greedy_)
+                               : (parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_);
     QPH_CK(hipGraphLaunch(g, st_));
     return;
   }
+  fuse_ = fused;
   enqueue_step(parts);
+  fuse_ = false;
 }
 
 // Called after every wait for the stream: a decode attention merger whose bounded wait for the other splits' partials
@@ -334,10 +375,10 @@ void HipLlama::step(int tok, int want, float *out) {
   if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
   write_ctl(tok, pos_);
   if (want == 1 || want == 3) {   // 3 (internal): logits left on the device
-    run_step(1);
+    run_step(1, pos_);
     if (want == 1) QPH_CK(hipMemcpyAsync(hout_, logits_, 4ull * cfg_.vocab, hipMemcpyDeviceToHost, st_));
   } else {
-    run_step(0);
+    run_step(0, pos_);
     if (want == 2) {
       if (order_) ex_norm(x_, fnorm_, xn_, 1, cfg_.hidden);
       else QPH_CK(launch_rmsnorm(x_, fnorm_, cfg_.hidden, cfg_.rms_eps, xn_, st_));
@@ -499,7 +540,7 @@ int HipLlama::greedy_run(int tok, int n, int *out) {
   if (n <= 0) return 0;
   if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
   write_ctl(tok, pos_);
-  for (int i = 0; i < n; i++) run_step(2);
+  for (int i = 0; i < n; i++) run_step(2, pos_ + i);
   QPH_CK(hipMemcpyAsync(htok_, out_tok_, 4ull * n, hipMemcpyDeviceToHost, st_));
   { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
   memcpy(out, htok_, 4ull * n);
@@ -681,7 +722,7 @@ float HipLlama::time_greedy(int tok, int n) {
   QPH_CK(hipEventCreate(&e0)); QPH_CK(hipEventCreate(&e1));
   write_ctl(tok, pos_);
   QPH_CK(hipEventRecord(e0, st_));
-  for (int i = 0; i < n; i++) run_step(2);
+  for (int i = 0; i < n; i++) run_step(2, pos_ + i);
   QPH_CK(hipEventRecord(e1, st_));
   QPH_CK(hipEventSynchronize(e1)); check_status();
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
@@ -706,6 +747,10 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   int li = 0;
   const float eps = cfg_.rms_eps;
   write_ctl(0, std::min(pos_, ctx_ - 1));
+  // QPH_AWO_STAMPS=file (measurement hook): the fused attention + wo kernel's per-workgroup realtime stamps of the
+  // last timed launch, written to that file as text
+  const char *stf = which == 6 ? getenv("QPH_AWO_STAMPS") : nullptr;
+  uint64_t *stamps = stf ? (uint64_t *)dalloc(4 * 8 * 4096) : nullptr;
   const char *dme = getenv("QPH_MV_DBG");
   const int dmode = dme ? atoi(dme) : 0;
   auto launch = [&]() {
@@ -722,14 +767,28 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); break;
       case 2:
         a.m[0] = ly.wq; a.m[1] = ly.wk; a.m[2] = ly.wv; a.nseg = 3; a.x = x_; a.norm_w = ly.an; a.eps = eps;
-        a.out[0] = q_; a.out[1] = k_; a.out[2] = v_;
+        a.out[0] = q_; a.out[1] = k_; a.out[2] = v_; a.bias[0] = ly.bq; a.bias[1] = ly.bk; a.bias[2] = ly.bv;
+        qkv_rope(a, kc_, vc_);
         mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_NORM, EPI_STORE, a, cap, st_)); break;
       case 3:
         a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = xn_;
         mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); break;
       case 4: enqueue_head(); break;
+      case 6: {   // fused attention + wo
+        AttnArgs t{}; t.q = q_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
+        t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
+        AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_;
+        if (!awo_part_) throw std::runtime_error("time_kernel: the fused attention + wo kernel does not take this model");
+        w.stamps = stamps;
+        QPH_CK(launch_attn_wo(t, w, st_)); break;
+      }
+      case 7:   // gate / up after the fused attention + wo: x + the group parts
+        if (!awo_part_) throw std::runtime_error("time_kernel: the fused attention + wo kernel does not take this model");
+        a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
+        a.part = awo_part_; a.nparts = cfg_.kv_heads; a.pstride = (size_t)d; a.xsum = xs_;
+        mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM_SUM, EPI_SWIGLU, a, cap, st_)); break;
       case 5: {
-        AttnArgs t{}; t.q = q_; t.k = k_; t.v = v_; t.kc = kc_; t.vc = vc_; t.cos_t = cos_; t.sin_t = sin_; t.ctl = ctl_;
+        AttnArgs t{}; t.q = q_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         t.max_chunks = max_chunks_; t.counters = counters_; t.single_max = attn_single_; t.split_pos = attn_split_pos_;
         t.status = dstatus_; t.spin_limit = attn_spin_;
@@ -748,6 +807,8 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
       case 3: sum += mat_bytes(ly.wo); break;
       case 4: sum += mat_bytes(head_) + 4.0 * d + 4.0 * cfg_.vocab; break;
       case 5: sum += 4.0 * (double)(pos_ + 1) * kvd_; break;
+      case 6: sum += 4.0 * (double)(pos_ + 1) * kvd_ + mat_bytes(ly.wo); break;
+      case 7: sum += mat_bytes(ly.wg) + mat_bytes(ly.wu) + 4.0 * d * (1 + cfg_.kv_heads); break;
       default: throw std::runtime_error("time_kernel: unknown kernel id");
     }
   }
@@ -761,6 +822,16 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   QPH_CK(hipEventSynchronize(e1)); check_status();
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
+  if (stamps) {
+    std::vector<uint64_t> h(4 * 4096);
+    QPH_CK(hipMemcpy(h.data(), stamps, h.size() * 8, hipMemcpyDeviceToHost));
+    if (FILE *f = fopen(stf, "w")) {
+      for (int i = 0; i < cfg_.kv_heads * awo_rc_; i++)
+        fprintf(f, "%llu %llu %llu %llu\n", (unsigned long long)h[4 * i], (unsigned long long)h[4 * i + 1],
+                (unsigned long long)h[4 * i + 2], (unsigned long long)h[4 * i + 3]);
+      fclose(f);
+    }
+  }
   return ms / iters;
 }
 

@@ -58,6 +58,7 @@ class HipLlama {
   int ctx_ = 0, kvd_ = 0, qd_ = 0, max_chunks_ = 1, cus_ = 256, head_grid_ = 0;
   int *counters_ = nullptr;
   int attn_single_ = 0, attn_split_pos_ = 0, attn_spin_ = 0;   // attention split policy (0: the kernel's defaults)
+  bool attn_force_late_ = false;
   int pos_ = 0;
   unsigned slot_ = 0;
   hipStream_t st_ = nullptr;
@@ -86,8 +87,15 @@ class HipLlama {
   int *hstatus_ = nullptr, *dstatus_ = nullptr;   // attention status word: mapped pinned host memory, its device alias
   void topk_to_host(int M, int *idx, float *val);
   hipGraphExec_t g_state_ = nullptr, g_logits_ = nullptr, g_greedy_ = nullptr;
+  // decode attention fused with wo (launch_attn_wo) for contexts up to awo_max_ positions (0: not used) and its graphs
+  static constexpr int kAwoMaxDefault = 1024;
+  int awo_max_ = 0, awo_rc_ = 0;
+  bool fuse_ = false;   // enqueue_layer: the fused kernel (set around a capture or a direct enqueue)
+  float *awo_part_ = nullptr;   // [nkv][d] per-group partial wo products
+  float *xs_ = nullptr;         // x + the attention block's output (written by the gate / up prologue)
+  hipGraphExec_t g_fs_state_ = nullptr, g_fs_logits_ = nullptr, g_fs_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
-  void run_step(int parts);
+  void run_step(int parts, int pos);
   // reference-order mode (exact.hip)
   int order_ = 0, ex_ncmax_ = 0;
   float *ex_qr_ = nullptr, *ex_part_ = nullptr, *ex_u_ = nullptr, *ex_xn_ = nullptr;
@@ -118,9 +126,10 @@ class HipLlama {
   void *place(const void *src, int64_t coded, size_t bytes, const char *name);
   void enqueue_layers();
   void enqueue_layer(int l);
+  void qkv_rope(MvArgs &a, uint16_t *kc, uint16_t *vc) const;
   void enqueue_head();
   void build_graphs();
-  hipGraphExec_t capture(int parts);
+  hipGraphExec_t capture(int parts, bool fused = false);
   void check_status();
   void write_ctl(int tok, int pos);
 };

@@ -266,9 +266,9 @@ def test_files_of_the_reference_quantiser(src, args, synth, tmp_path):
 
 
 def test_attention_merge_timeout_is_an_error(synth, monkeypatch):
-    """the decode attention's failure path, forced from the host: with the mergers' bounded wait cut to one poll
-    (QPH_ATTN_SPIN=1, read at load) a merger gives up, writes NaN and sets the status word; the call raises instead of
-    returning those outputs, the split counters are cleared, and every kernel still runs to completion (a fresh model
+    """the decode attention's failure path, forced from the host (QPH_ATTN_FORCE_LATE, read at load: every merger
+    that would wait gives up at once, as when its bounded wait runs out): it writes NaN and sets the status word; the
+    call raises instead of returning those outputs, the split counters are cleared, and every kernel still runs to completion (a fresh model
     at the same context decodes normally afterwards)"""
     cfg, T = "mini_r7", 1500   # 24 splits per kv group, 7 heads per group: the parallel merge with waiting mergers
     path = synth(cfg)
@@ -278,9 +278,9 @@ def test_attention_merge_timeout_is_an_error(synth, monkeypatch):
     k = rng.standard_normal((shape.layers, T, kvd)).astype(np.float16)
     v = rng.standard_normal((shape.layers, T, kvd)).astype(np.float16)
     snap = kv_snapshot(k, v)
-    monkeypatch.setenv("QPH_ATTN_SPIN", "1")
+    monkeypatch.setenv("QPH_ATTN_FORCE_LATE", "1")
     bad = qa.HipLlama.load(path, max_ctx=T + 64)
-    monkeypatch.delenv("QPH_ATTN_SPIN")
+    monkeypatch.delenv("QPH_ATTN_FORCE_LATE")
     bad.restore(snap)
     with pytest.raises(qa.QphError, match="timed out"):
         bad.step(5, 1)
@@ -317,3 +317,39 @@ def test_graph_replays_with_device_logits(synth):
         np.testing.assert_array_equal(val, lg[order])
     assert a.pos() == b.pos() == 32 + 600
     a.close(); b.close()
+
+
+@pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_odd", "mini_r7h"])
+def test_fused_attention_wo(cfg, synth, monkeypatch):
+    """decode attention fused with the wo product and residual (k_attn_wo, contexts up to QPH_AWO_MAX positions)
+    against the oracle and against the split attention + wo matvec launches, across the threshold (fused up to 100
+    positions, split beyond), then greedy chains of both against the oracle's"""
+    path = synth(cfg)
+    monkeypatch.setenv("QPH_AWO_MAX", "100")
+    fused = qa.HipLlama.load(path, max_ctx=192)
+    monkeypatch.setenv("QPH_AWO_MAX", "0")
+    split = qa.HipLlama.load(path, max_ctx=192)
+    monkeypatch.delenv("QPH_AWO_MAX")
+    orc = O.Oracle(path, max_ctx=192)
+    rng = np.random.default_rng(21)
+    toks = rng.integers(0, fused.vocab(), 60).astype(np.int32)
+    print(f"{cfg}: fused attention + wo, prompt 60, steps to 110", flush=True)
+    for m in (fused, split):
+        m.prefill(toks, 0)
+    lo = orc.prefill(toks, 1)
+    for t in rng.integers(0, fused.vocab(), 50):
+        a, b, c = fused.step(int(t), 1), split.step(int(t), 1), orc.step(int(t), 1)
+        err, ok = close(a, c)
+        assert ok, f"fused step at {fused.pos()}: logits max|d| {err} against the oracle"
+        err, ok = close(b, c)
+        assert ok, f"split step at {split.pos()}: logits max|d| {err} against the oracle"
+        lo = c
+    # greedy from position 70 (fused for the first 30 steps, then split)
+    for m in (fused, split):
+        assert m.rewind(70)
+    orc.set_pos(70)
+    tok = int(np.argmax(lo))
+    o = orc.greedy_run(tok, 40)
+    np.testing.assert_array_equal(fused.greedy_run(tok, 40), o)
+    np.testing.assert_array_equal(split.greedy_run(tok, 40), o)
+    fused.close(); split.close(); orc.close()
