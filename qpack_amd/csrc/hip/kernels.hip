@@ -332,6 +332,12 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
         }
         (sg == 0 ? a.out[0] : (sg == 1 ? a.out[1] : a.out[2]))[row] = y;
         if (cache) cache[(size_t)pos * a.cache_ld + row] = f32_to_half_bits(y);
+        uint16_t *const q16 = sg == 0 ? a.q16[0] : (sg == 1 ? a.q16[1] : a.q16[2]);
+        if (q16) {   // the attention's MFMA operand halves: hi = f16(y), lo = f16(y - hi)
+          const _Float16 h = (_Float16)y;
+          q16[row] = __builtin_bit_cast(uint16_t, h);
+          q16[og.rows + row] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)h));
+        }
       }
     } else if (EPI == EPI_SWIGLU) {
       const float up = __shfl_xor(v, 1, kWave);   // slot 1 (up) sits in the lane after slot 0 (gate)
@@ -467,7 +473,7 @@ hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStr
       for (int s = 0; s < nseg; s++)
         if (a.m[s].kind == k) {
           b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s];
-          b.rope[b.nseg] = a.rope[s]; b.cache[b.nseg] = a.cache[s]; b.nseg++;
+          b.rope[b.nseg] = a.rope[s]; b.cache[b.nseg] = a.cache[s]; b.q16[b.nseg] = a.q16[s]; b.nseg++;
         }
     const int ns = mv_ns(b, epi, g_mv_config.cus * 16);
     if (pro == PRO_NORM) return ns == 2 ? launch_mv_t<PRO_NORM, EPI_STORE, 2, MK_MIX>(b, grid_cap, st)
@@ -480,7 +486,7 @@ hipError_t launch_matvec(int pro, int epi, const MvArgs &a, int grid_cap, hipStr
     for (int s = 0; s < nseg; s++)
       if (a.m[s].kind == k) {
         b.m[b.nseg] = a.m[s]; b.out[b.nseg] = a.out[s]; b.bias[b.nseg] = a.bias[s];
-        b.rope[b.nseg] = a.rope[s]; b.cache[b.nseg] = a.cache[s]; b.nseg++;
+        b.rope[b.nseg] = a.rope[s]; b.cache[b.nseg] = a.cache[s]; b.q16[b.nseg] = a.q16[s]; b.nseg++;
       }
     if (!b.nseg) continue;
     if (epi == EPI_SWIGLU) { b.m[1] = a.m[1]; b.nseg = 1; b.seg_tile0[0] = 0; b.seg_tile0[1] = a.m[0].rows; }
@@ -608,13 +614,13 @@ struct MfV {   // V of one block: HD / 16 16-byte pieces, piece i = position (la
   static constexpr int NV = HD / 16;
   u32x4 v[NV];
 };
-// rows past te read row tb instead (finite values, masked out of the softmax)
+// rows at or past te (the cache allocation) read row tb instead
 template <int HD>
 __device__ __forceinline__ void mf_load_k(const uint16_t *kc, int kvd, int g, int tb, int te, int lane, MfK<HD> &b) {
   const int lr = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < 2; mt++) {
-    const int t = tb + 16 * mt + lr, tc = t < te ? t : tb;
+    const int t = tb + 16 * mt + lr, tc = t < te ? t : te - 1;
 #pragma unroll
     for (int s = 0; s < MfK<HD>::KS; s++) b.k[mt][s] = *(const u32x4 *)(kc + (size_t)tc * kvd + g * HD + 32 * s + 8 * lg);
   }
@@ -623,57 +629,54 @@ template <int HD>
 __device__ __forceinline__ void mf_load_v(const uint16_t *vc, int kvd, int g, int tb, int te, int lane, MfV<HD> &b) {
 #pragma unroll
   for (int i = 0; i < MfV<HD>::NV; i++) {
-    const int c = lane + 64 * i, t = tb + c / (HD / 8), tc = t < te ? t : tb;
+    const int c = lane + 64 * i, t = tb + c / (HD / 8), tc = t < te ? t : te - 1;
     b.v[i] = *(const u32x4 *)(vc + (size_t)tc * kvd + g * HD + 8 * (c % (HD / 8)));
   }
 }
 
 // lout: with S == 1, the normalised heads go to this LDS array [REP][HD] instead of a.att; mid() runs once the waves'
-// partials are in LDS, before their merge (the block loop's registers are free by then)
+// partials are in LDS, before their merge (the block loop's registers are free by then).  ONE: S == 1 is known before
+// the position is: each wave's first block (positions 32 w ..) is loaded before ctl->pos arrives.
 struct AttnNoMid { __device__ void operator()() const {} };
-template <int HD, int REP, typename Mid = AttnNoMid>
+template <int HD, int REP, bool ONE = false, typename Mid = AttnNoMid>
 __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float *lout = nullptr, const Mid &mid = Mid()) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   // LDS rows padded so the MFMA-layout accesses (16 heads / dims apart per lane) spread over the banks
   constexpr int NW = kAttnMfWaves, HALF = HD / 2, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 8;   // VS: rows of 20 dwords
   constexpr int QS = HD + 4;
-  __shared__ __align__(16) float qs[REP][QS];
   __shared__ float wm[NW][REP], wl[NW][REP];
   __shared__ __align__(16) float ored[NW][REP][QS];
   __shared__ __align__(16) uint16_t vt[NW][HD * VS];
-  const int pos = a.ctl->pos, T = pos + 1;
   const int kvd = a.nkv * HD;
-  const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
-  // waves take contiguous runs of whole 32-position blocks (waves without a block idle)
-  const int nblk = (t1 - t0 + kAttnMfBlk - 1) / kAttnMfBlk, bpw = (nblk + NW - 1) / NW;
-  const int wt0 = min(t1, t0 + kAttnMfBlk * wave * bpw), wt1 = min(t1, t0 + kAttnMfBlk * (wave + 1) * bpw);
-  const int nact = (nblk + bpw - 1) / bpw;
   MfK<HD> ka, kb;
   MfV<HD> vb;
-  if (wt0 < wt1) {   // the first block goes out before anything else
-    mf_load_k<HD>(a.kc, kvd, g, wt0, wt1, lane, ka);
-    mf_load_v<HD>(a.vc, kvd, g, wt0, wt1, lane, vb);
+  // positions past the context or the split are loaded from rows below a.ctx (in the allocation) and masked: their
+  // scores become -inf and their V pieces zero
+  if (ONE) {
+    mf_load_k<HD>(a.kc, kvd, g, kAttnMfBlk * wave, a.ctx, lane, ka);
+    mf_load_v<HD>(a.vc, kvd, g, kAttnMfBlk * wave, a.ctx, lane, vb);
   }
-  for (int e = threadIdx.x; e < REP * HD / 4; e += blockDim.x) {   // the group's rotated heads, 4 dims per thread
-    const int j = e / (HD / 4), i = 4 * (e % (HD / 4));
-    *(float4 *)&qs[j][i] = *(const float4 *)(a.q + (size_t)(g * REP + j) * HD + i);
-  }
-  __syncthreads();
-  // q^T fragments: lane holds head lr (zero past REP), dims 32 s + 8 lg + 0..7, as hi / lo halves
+  // q^T fragments straight from the q / k / v epilogue's fp16 planes (hi = f16(q), lo = f16(q - hi)): lane holds head
+  // lr (zero past REP), dims 32 k + 8 lg + 0..7
   h8 qh[KS], ql[KS];
+  {
+    const uint16_t *qp = a.q16 + (size_t)(g * REP + (lr < REP ? lr : 0)) * HD + 8 * lg;
 #pragma unroll
-  for (int k = 0; k < KS; k++) {
-    const float *qr = qs[lr < REP ? lr : 0] + 32 * k + 8 * lg;
-    const float4 x0 = *(const float4 *)qr, x1 = *(const float4 *)(qr + 4);
-    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float x = lr < REP ? xs[e] : 0.f;
-      const _Float16 h = (_Float16)x;
-      qh[k][e] = h; ql[k][e] = (_Float16)(x - (float)h);
+    for (int k = 0; k < KS; k++) {
+      u32x4 h = *(const u32x4 *)(qp + 32 * k), lo = *(const u32x4 *)(qp + (size_t)a.nh * HD + 32 * k);
+      if (lr >= REP) h = lo = (u32x4){0u, 0u, 0u, 0u};
+      qh[k] = __builtin_bit_cast(h8, h); ql[k] = __builtin_bit_cast(h8, lo);
     }
+  }
+  const int pos = a.ctl->pos, T = pos + 1;
+  const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
+  // wave w takes blocks w, w + NW, ... of the split's 32-position blocks (waves without a block idle)
+  const int nblk = (t1 - t0 + kAttnMfBlk - 1) / kAttnMfBlk, nact = min(nblk, NW);
+  if (!ONE && wave < nblk) {
+    mf_load_k<HD>(a.kc, kvd, g, t0 + kAttnMfBlk * wave, a.ctx, lane, ka);
+    mf_load_v<HD>(a.vc, kvd, g, t0 + kAttnMfBlk * wave, a.ctx, lane, vb);
   }
   const float scl = 1.f / sqrtf((float)HD);
   f4 o[DT];
@@ -691,7 +694,7 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
 #pragma unroll
     for (int i = 0; i < NV; i++) {
       const int c = lane + 64 * i, p = c / (HD / 8), d0 = 8 * (c % (HD / 8));
-      const u32x4 vv = vb.v[i];
+      const u32x4 vv = tb + p < t1 ? vb.v[i] : (u32x4){0u, 0u, 0u, 0u};
       const bool ev = (p & 1) == 0;
       const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, kWave);
       const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, kWave);
@@ -706,9 +709,9 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
       wr[VS] = (lo_y & 0xffffu) | (hi_y << 16);
       wr[3 * VS / 2] = (lo_y >> 16) | (hi_y & 0xffff0000u);
     }
-    if (tb + kAttnMfBlk < wt1) {
-      mf_load_v<HD>(a.vc, kvd, g, tb + kAttnMfBlk, wt1, lane, vb);
-      mf_load_k<HD>(a.kc, kvd, g, tb + kAttnMfBlk, wt1, lane, knxt);
+    if (tb + NW * kAttnMfBlk < t1) {
+      mf_load_v<HD>(a.vc, kvd, g, tb + NW * kAttnMfBlk, a.ctx, lane, vb);
+      mf_load_k<HD>(a.kc, kvd, g, tb + NW * kAttnMfBlk, a.ctx, lane, knxt);
     }
     // scores of the two 16-position tiles
     f4 sc[2];
@@ -728,7 +731,7 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float x = tb + 16 * mt + 4 * lg + i < wt1 ? sc[mt][i] * scl : -INFINITY;
+        const float x = tb + 16 * mt + 4 * lg + i < t1 ? sc[mt][i] * scl : -INFINITY;
         sv[4 * mt + i] = x; bm = fmaxf(bm, x);
       }
     bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
@@ -767,10 +770,10 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
-  for (int tb = wt0; tb < wt1; tb += 2 * kAttnMfBlk) {
+  for (int tb = t0 + kAttnMfBlk * wave; tb < t1; tb += 2 * NW * kAttnMfBlk) {
     block(ka, kb, tb);
-    if (tb + kAttnMfBlk >= wt1) break;
-    block(kb, ka, tb + kAttnMfBlk);
+    if (tb + NW * kAttnMfBlk >= t1) break;
+    block(kb, ka, tb + NW * kAttnMfBlk);
   }
   // this wave's (m, l, o) -> LDS: lane holds head lr, dims 16 d + 4 lg + i
   if (lr < REP) {
@@ -1005,7 +1008,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
       wr[i] = *(const uint4 *)(wq + (size_t)row * cols + 16 * c16);
     }
   };
-  attn_split<HD, REP>(a, g, 0, 1, 1, ao, issue);
+  attn_split<HD, REP, true>(a, g, 0, 1, 1, ao, issue);
   __syncthreads();
   if (w.stamps) t1 = __builtin_amdgcn_s_memrealtime();
   if (threadIdx.x < 8 * NBG) {   // eight lanes per block, 16 columns each (act_build's arithmetic)

@@ -62,6 +62,7 @@ struct MvArgs {
   int cache_ld, hd;
   const float *cos_t, *sin_t;
   const Ctl *ctl;
+  uint16_t *q16[3];   // optional per segment (q): its rotated rows also as fp16 hi [rows] then lo = f16(y - hi) [rows]
 };
 
 // The matvec kernel runs one workgroup of up to 16 waves per CU; every wave streams its own units of 1 or 2 rows
@@ -95,6 +96,8 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int n, float eps, floa
 
 struct AttnArgs {
   const float *q;              // this step's queries, RoPE applied (the q / k / v matvec's epilogue)
+  const uint16_t *q16;         // the same as fp16 hi [nh * hd] then lo [nh * hd] halves (MvArgs::q16)
+  int ctx;                     // positions allocated in the caches (loads stay below it)
   uint16_t *kc, *vc;           // this layer's fp16 caches [ctx][kvd], the current position's rows already written
   const Ctl *ctl;
   float *part;                 // unnormalised outputs [nh][splits][hd], then (max, sum) [nh][splits][2]

@@ -124,6 +124,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   k_ = (float *)dalloc(4ull * kvd_); v_ = (float *)dalloc(4ull * kvd_); att_ = (float *)dalloc(4ull * qd_);
   h_ = (float *)dalloc(4ull * ff); logits_ = (float *)dalloc(4ull * V);
   part_ = (float *)dalloc(4ull * nh * max_chunks_ * (hd + 2));
+  q16_ = (uint16_t *)dalloc(4ull * qd_);
   QPH_CK(hipMemset(counters_, 0, 8ull * nkv));
   {  // decode attention fused with wo (q8 wo on every layer, a group's heads whole 128-column blocks), short contexts
     int rc = 0, nl = 0;
@@ -231,6 +232,7 @@ void HipLlama::qkv_rope(MvArgs &a, uint16_t *kc, uint16_t *vc) const {
   a.rope[0] = a.rope[1] = 1; a.rope[2] = 0;
   a.cache[0] = nullptr; a.cache[1] = kc; a.cache[2] = vc;
   a.cache_ld = kvd_; a.hd = cfg_.head_dim; a.cos_t = cos_; a.sin_t = sin_; a.ctl = ctl_;
+  a.q16[0] = q16_; a.q16[1] = a.q16[2] = nullptr;
 }
 
 void HipLlama::enqueue_layer(int l) {
@@ -244,7 +246,8 @@ void HipLlama::enqueue_layer(int l) {
     qkv_rope(a, kc, vc);
     mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_NORM, EPI_STORE, a, cap, st_));
   }
-  AttnArgs at{}; at.q = q_; at.kc = kc; at.vc = vc; at.ctl = ctl_; at.part = part_; at.att = att_;
+  AttnArgs at{}; at.q = q_; at.q16 = q16_; at.ctx = ctx_; at.kc = kc; at.vc = vc; at.ctl = ctl_; at.part = part_;
+  at.att = att_;
   at.nh = cfg_.heads; at.nkv = cfg_.kv_heads; at.hd = cfg_.head_dim; at.max_chunks = max_chunks_; at.counters = counters_;
   at.single_max = attn_single_; at.split_pos = attn_split_pos_; at.status = dstatus_; at.spin_limit = attn_spin_;
   at.force_late = attn_force_late_;
@@ -775,7 +778,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); break;
       case 4: enqueue_head(); break;
       case 6: {   // fused attention + wo
-        AttnArgs t{}; t.q = q_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
+        AttnArgs t{}; t.q = q_; t.q16 = q16_; t.ctx = ctx_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_;
         if (!awo_part_) throw std::runtime_error("time_kernel: the fused attention + wo kernel does not take this model");
@@ -788,7 +791,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         a.part = awo_part_; a.nparts = cfg_.kv_heads; a.pstride = (size_t)d; a.xsum = xs_;
         mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM_SUM, EPI_SWIGLU, a, cap, st_)); break;
       case 5: {
-        AttnArgs t{}; t.q = q_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
+        AttnArgs t{}; t.q = q_; t.q16 = q16_; t.ctx = ctx_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         t.max_chunks = max_chunks_; t.counters = counters_; t.single_max = attn_single_; t.split_pos = attn_split_pos_;
         t.status = dstatus_; t.spin_limit = attn_spin_;

@@ -71,6 +71,7 @@ class HipLlama {
   // device state
   float *x_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr, *h_ = nullptr, *xn_ = nullptr;
   float *logits_ = nullptr, *part_ = nullptr, *cos_ = nullptr, *sin_ = nullptr;
+  uint16_t *q16_ = nullptr;   // rotated q as fp16 hi / lo halves (the decode attention's operand)
   float2 *amax_ = nullptr;
   Ctl *ctl_ = nullptr;
   int *out_tok_ = nullptr;
