@@ -6,9 +6,10 @@ SwiGLU 14336, vocab 128256, untied head), seeded N(0, 0.02) random-init weights 
   decode  - 128-token prompt, `--warmup` untimed greedy tokens, then exactly `--steps` greedy tokens timed (device
             argmax feeds the next step; HIP events on the model's stream, host clock around it)
   prefill - one `--prefill-tokens` prompt (C4), host clock around qph_prefill
-Roofline: the dominant decode kernel (fused RMSNorm + gate/up + SwiGLU matvec, ~47 % of the step's bytes), launched
-alone over the 32 layers in turn and timed with HIP events on the model's stream; achieved = its algorithmic bytes /
-mean duration.  traffic = its HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (committed summary under
+Roofline: the dominant decode kernel (fused RMSNorm + gate/up + SwiGLU matvec, ~47 % of the step's bytes) in the form
+the token loop runs it at the timed contexts - after the fused attention + wo kernel it also adds that kernel's kv-group
+partials to the residual stream (PRO_NORM_SUM) - launched alone over the 32 layers in turn and timed with HIP events on
+the model's stream; achieved = its algorithmic bytes / mean duration.  traffic = its HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (committed summary under
 profiles/, produced by --profile runs and --pmc-summary).
 CPU baseline: the reference engine compiled from its own sources (oracle/_ref/libqpref.so, AVX2) on the same file,
 on the host cores, qpack-bench protocol on a bounded sample.
@@ -29,8 +30,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-DOMINANT = "k_matvec<1, 2, 2, 1, false>"   # PRO_NORM, EPI_SWIGLU, 2 rows per unit, q8
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_matvec_norm_swiglu_q8_c3_traffic.md")
+# the token loop's gate / up kernel: PRO_NORM_SUM (after the fused attention + wo) or PRO_NORM; EPI_SWIGLU, 2 rows per
+# unit, q8 - its rocprofv3 name, time_kernel id and the committed counter summary
+DOMINANT = {"sum": ("k_matvec<2, 2, 2, 1, false>", 7, "k_matvec_normsum_swiglu_q8_c3_traffic.md",
+                    "k_matvec<PRO_NORM_SUM,EPI_SWIGLU> (x + the 8 kv-group partials of the fused attention + wo, "
+                    "RMSNorm, gate/up, SwiGLU; 2 x 14336 x 4096 q8; launches walk the 32 layers)"),
+            "norm": ("k_matvec<1, 2, 2, 1, false>", 0, "k_matvec_norm_swiglu_q8_c3_traffic.md",
+                     "k_matvec<PRO_NORM,EPI_SWIGLU> (fused RMSNorm + gate/up + SwiGLU, 2 x 14336 x 4096 q8; launches "
+                     "walk the 32 layers)")}
 COPY_BYTES = 1 << 29                         # calibration copy: 512 MiB read + 512 MiB written
 METRIC = "batch-1 decode tokens/s + % HBM peak; prefill tokens/s (8B-shape q8)"
 
@@ -103,10 +110,10 @@ def pmc_summary(csv_path, kernel_sub, copy_sub="k_copy"):
             for c, (k, cp) in acc.items()}
 
 
-def read_traffic():
+def read_traffic(name):
     """HBM bytes per launch of the dominant kernel, from the committed counter summary (line 'traffic_bytes: N')"""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
             for line in f:
                 if line.startswith("traffic_bytes:"):
                     return int(float(line.split(":", 1)[1]))
@@ -255,6 +262,9 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="launch kernels one by one (no HIP graphs) so a profiler sees every dispatch, and run a "
                          "calibration copy of known size for the byte counters")
+    ap.add_argument("--dominant", choices=sorted(DOMINANT), default="sum",
+                    help="which gate / up kernel --pmc-summary reads (the token loop runs 'sum' at contexts up to 1024 "
+                         "on q8 models whose kv groups are whole 128-column blocks)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the dominant kernel's per-launch HBM traffic from two rocprofv3 --pmc runs "
                          "(FETCH_SIZE, WRITE_SIZE) of --profile, scaled by the calibration copy; no GPU work")
@@ -263,7 +273,7 @@ def main():
         scale_note = []
         total = 0.0
         for path, ctr in zip(a.pmc_summary, ("FETCH_SIZE", "WRITE_SIZE")):
-            k, cp, nk, ncp = pmc_summary(path, DOMINANT)[ctr]
+            k, cp, nk, ncp = pmc_summary(path, DOMINANT[a.dominant][0])[ctr]
             f = (COPY_BYTES / 1024) / cp            # counter reads KiB; the copy moves COPY_BYTES each way
             total += k * 1024 * f
             scale_note.append(f"{ctr}: kernel {k:.1f} KiB/dispatch over {nk} dispatches; copy {cp:.1f} KiB/dispatch "
@@ -316,11 +326,17 @@ def main():
 
     if a.profile:
         calibration_copy()
-    kms, kbytes = m.time_kernel(0, a.kernel_iters)
+    dom = "sum"
+    try:
+        kms, kbytes = m.time_kernel(DOMINANT[dom][1], a.kernel_iters)
+    except RuntimeError:   # a model the fused attention + wo kernel does not take
+        dom = "norm"
+        kms, kbytes = m.time_kernel(DOMINANT[dom][1], a.kernel_iters)
     k_gbs = kbytes / (kms / 1e3) / 1e9
-    log(f"dominant kernel (layer-0 gate/up matvec): {kms * 1e3:.2f} us, {kbytes / 1e6:.1f} MB -> {k_gbs:.0f} GB/s")
+    log(f"dominant kernel ({DOMINANT[dom][0]}): {kms * 1e3:.2f} us, {kbytes / 1e6:.1f} MB -> {k_gbs:.0f} GB/s")
     others = {}
-    for which, name in [(1, "down"), (2, "qkv"), (3, "wo"), (4, "head"), (5, "attention")]:
+    plain = [(0, "gate_up_plain")] if dom == "sum" else []   # the same product without the partials, for comparison
+    for which, name in [(1, "down"), (2, "qkv"), (3, "wo"), (4, "head"), (5, "attention")] + plain:
         ks, kb = m.time_kernel(which, a.kernel_iters)
         others[name] = dict(us=round(ks * 1e3, 2), mbytes=round(kb / 1e6, 3), gbs=round(kb / (ks / 1e3) / 1e9, 1))
         log(f"  {name}: {ks * 1e3:.2f} us, {kb / 1e6:.2f} MB -> {kb / (ks / 1e3) / 1e9:.0f} GB/s")
@@ -424,9 +440,8 @@ def main():
         "step_roofline": {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4), "bytes_per_token": round(sb)},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "kernel": "k_matvec<PRO_NORM,EPI_SWIGLU> (fused RMSNorm + gate/up + SwiGLU, 2 x 14336 x 4096 q8; "
-                               "launches walk the 32 layers)",
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(DOMINANT[dom][2]),
+                     "kernel": DOMINANT[dom][3],
                      "bytes_per_launch": round(kbytes), "us_per_launch": round(kms * 1e3, 2)},
         "kernels": others,
         "prefill": prefill,

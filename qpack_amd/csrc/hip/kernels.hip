@@ -431,6 +431,7 @@ static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
     lds = std::max(lds, mv_lds_bytes(cols, w, 0) - 4 * (size_t)nbp + 4 * (size_t)(ns - 1) * cols);
   }
   if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (a.plan_only) return hipSuccess;
   const bool dbg = a.dbg_sums || a.dbg_xq || a.dbg_bs;
   if (dbg) {
     if (PRO != PRO_QUANT || EPI != EPI_STORE || KIND == MK_MIX) return hipErrorInvalidValue;

@@ -129,7 +129,14 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   {  // decode attention fused with wo (q8 wo on every layer, a group's heads whole 128-column blocks), short contexts
     int rc = 0, nl = 0;
     bool ok = !layers_.empty();
-    for (const Layer &ly : layers_) ok = ok && attn_wo_fits(hd, nh, nkv, ly.wo, g_mv_config.cus, &rc, &nl);
+    for (const Layer &ly : layers_) {
+      ok = ok && attn_wo_fits(hd, nh, nkv, ly.wo, g_mv_config.cus, &rc, &nl);
+      // the gate / up launch that adds the group partials (their LDS staging must fit)
+      MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.part = x_; a.nparts = nkv; a.pstride = (size_t)d;
+      a.plan_only = 1;
+      mv_plan(a, EPI_SWIGLU);
+      ok = ok && launch_matvec(PRO_NORM_SUM, EPI_SWIGLU, a, 1 << 20, st_) == hipSuccess;
+    }
     const char *e = getenv("QPH_AWO_MAX");   // longest context (positions) that takes the fused kernel; 0: never
     awo_max_ = ok ? (e ? std::max(0, atoi(e)) : kAwoMaxDefault) : 0;
     if (awo_max_ > 0) {
