@@ -119,6 +119,8 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 
   ActRegs ar;
   const int dm = a.dbg_mode;
+  uint64_t ts0 = 0, ts1 = 0, ts2 = 0;
+  if (a.stamps) ts0 = __builtin_amdgcn_s_memrealtime();
   const int pos = EPI == EPI_STORE && NS == 2 && a.ctl ? a.ctl->pos : 0;   // RoPE / cache position
   if (!(dm & 2)) act_load<PRO>(a.x, a.norm_w, cols, ar, a.part, a.nparts, a.pstride, a.xsum, (float *)av.sums);
 
@@ -145,6 +147,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 
   if (!(dm & 2)) act_build<PRO, KIND == MK_Q1>(ar, a.eps, cols, av);
   else __syncthreads();
+  if (a.stamps) ts1 = __builtin_amdgcn_s_memrealtime();
   if (DBG && blockIdx.x == 0) {
     for (int c = threadIdx.x; c < cols; c += blockDim.x) {
       const int at = KIND == MK_Q1 ? (((c & 127) >> 4) * nb + (c >> 7)) * 16 + (c & 15) : c;   // q1: chunk-major planes
@@ -279,6 +282,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (a.stamps) ts2 = __builtin_amdgcn_s_memrealtime();
   if (dm & 4) return;   // timing: no epilogue
 
   // epilogue: lane j finishes (unit j / NS, row slot j % NS)
@@ -364,6 +368,10 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
       for (int w = 1; w < WAVES; w++) if (better(rv[w], ri[w], bv, bi)) { bv = rv[w]; bi = ri[w]; }
       a.amax[blockIdx.x] = make_float2(bv, __builtin_bit_cast(float, bi));
     }
+  }
+  if (a.stamps && lane == 0) {   // measurement: per wave, realtime at start, after the prologue, after the loop, at the end
+    uint64_t *o = a.stamps + 4 * ((size_t)blockIdx.x * WAVES + wave);
+    o[0] = ts0; o[1] = ts1; o[2] = ts2; o[3] = __builtin_amdgcn_s_memrealtime();
   }
 }
 

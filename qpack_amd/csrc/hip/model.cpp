@@ -763,11 +763,16 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   uint64_t *stamps = stf ? (uint64_t *)dalloc(4 * 8 * 4096) : nullptr;
   const char *dme = getenv("QPH_MV_DBG");
   const int dmode = dme ? atoi(dme) : 0;
+  // QPH_MV_STAMPS=file (measurement hook): the matvec's per-wave realtime stamps of the last timed launch, as text
+  const char *mvs = which <= 4 || which == 7 ? getenv("QPH_MV_STAMPS") : nullptr;
+  uint64_t *mv_stamps = mvs ? (uint64_t *)dalloc(4 * 8 * 65536) : nullptr;
+  if (mv_stamps) QPH_CK(hipMemset(mv_stamps, 0, 4 * 8 * 65536));
   auto launch = [&]() {
     const Layer &ly = layers_[li];
     li = li + 1 == L ? 0 : li + 1;
     MvArgs a{};
     a.dbg_mode = dmode;
+    a.stamps = mv_stamps;
     switch (which) {
       case 0:
         a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
@@ -832,6 +837,16 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   QPH_CK(hipEventSynchronize(e1)); check_status();
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
+  if (mv_stamps) {
+    std::vector<uint64_t> h(4 * 65536);
+    QPH_CK(hipMemcpy(h.data(), mv_stamps, h.size() * 8, hipMemcpyDeviceToHost));
+    if (FILE *f = fopen(mvs, "w")) {
+      for (int i = 0; i < 65536 && h[4 * i]; i++)
+        fprintf(f, "%llu %llu %llu %llu\n", (unsigned long long)h[4 * i], (unsigned long long)h[4 * i + 1],
+                (unsigned long long)h[4 * i + 2], (unsigned long long)h[4 * i + 3]);
+      fclose(f);
+    }
+  }
   if (stamps) {
     std::vector<uint64_t> h(4 * 4096);
     QPH_CK(hipMemcpy(h.data(), stamps, h.size() * 8, hipMemcpyDeviceToHost));
