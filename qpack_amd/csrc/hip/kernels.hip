@@ -922,11 +922,20 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * NW * 64 / HD, sp = a.split_pos > 0 ? a.split_pos : 64;
   const int S = T <= smax ? 1 : min((int)gridDim.y, (T + sp - 1) / sp);
   if (s >= S) return;
+  uint64_t st0 = 0, st1 = 0, st2 = 0;   // measurement (a.stamps): start, partials stored, rank known
+  if (a.stamps) st0 = __builtin_amdgcn_s_memrealtime();
   attn_split<HD, REP>(a, g, s, S, gridDim.y);
   if (S == 1) return;
   // this thread's coherent stores have completed before the workgroup's counter bump
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  if (a.stamps) st1 = __builtin_amdgcn_s_memrealtime();
+  auto stamp = [&](int merger) {
+    if (a.stamps && threadIdx.x == 0) {
+      uint64_t *o = a.stamps + 5 * ((size_t)blockIdx.y * gridDim.x + blockIdx.x);
+      o[0] = st0; o[1] = st1; o[2] = st2; o[3] = __builtin_amdgcn_s_memrealtime(); o[4] = merger;
+    }
+  };
   // The last MG splits to arrive merge the S partials of the group's heads (model_llama.cpp:160-165: M = max m_c,
   // f_c = exp(m_c - M), L = sum l_c f_c, O = sum f_c o_c / L): from kAttnParMerge splits up MG = min(REP, S), head j
   // by merger j % MG, each head's loads in one round; below, the merge is short and the last arrival does it alone
@@ -950,12 +959,14 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
     if (late && a.status) *(volatile int *)a.status = 1;   // the step's outputs are invalid: the host raises an error
   }
   __syncthreads();
+  if (a.stamps) st2 = __builtin_amdgcn_s_memrealtime();
   const int r = rank;
-  if (r < 0) return;
+  if (r < 0) { stamp(0); return; }
   // The partials were written through to memory by other workgroups before their counter bumps; they are read with
   // coherent loads (no acquire fence: that is an L2 invalidate, far slower).
   if (S < kAttnParMerge) {
     attn_merge_all<HD, REP, NW>(a, g, S);
+    stamp(1);
     return;
   }
   // this merger no longer reads the arrivals; the round trip overlaps the merge
@@ -965,6 +976,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
     __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  stamp(1);
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {

@@ -112,6 +112,8 @@ struct AttnArgs {
   int *status;                 // optional (host-visible): set to 1 when a merger's bounded wait for the partials ran out
   int spin_limit;              // the bound of that wait in polls (0: 1 << 22)
   int force_late;              // test hook: every merger that would wait gives up at once (the error path, forced)
+  uint64_t *stamps;            // measurement only (optional): per workgroup of k_attention 5 words - realtime at start,
+                               // partials stored, merge rank known, end, and 1 if it merged
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 // Decode attention fused with the wo product (q8 wo, REP * hd a multiple of 128): grid (nkv, rc); workgroup (g, c)

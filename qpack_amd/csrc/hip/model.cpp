@@ -759,8 +759,9 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
   write_ctl(0, std::min(pos_, ctx_ - 1));
   // QPH_AWO_STAMPS=file (measurement hook): the fused attention + wo kernel's per-workgroup realtime stamps of the
   // last timed launch, written to that file as text
-  const char *stf = which == 6 ? getenv("QPH_AWO_STAMPS") : nullptr;
-  uint64_t *stamps = stf ? (uint64_t *)dalloc(4 * 8 * 4096) : nullptr;
+  const char *stf = which == 6 ? getenv("QPH_AWO_STAMPS") : which == 5 ? getenv("QPH_ATTN_STAMPS") : nullptr;
+  uint64_t *stamps = stf ? (uint64_t *)dalloc(5 * 8 * 4096) : nullptr;
+  if (stamps) QPH_CK(hipMemset(stamps, 0, 5 * 8 * 4096));
   const char *dme = getenv("QPH_MV_DBG");
   const int dmode = dme ? atoi(dme) : 0;
   // QPH_MV_STAMPS=file (measurement hook): the matvec's per-wave realtime stamps of the last timed launch, as text
@@ -806,7 +807,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         AttnArgs t{}; t.q = q_; t.q16 = q16_; t.ctx = ctx_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         t.max_chunks = max_chunks_; t.counters = counters_; t.single_max = attn_single_; t.split_pos = attn_split_pos_;
-        t.status = dstatus_; t.spin_limit = attn_spin_;
+        t.status = dstatus_; t.spin_limit = attn_spin_; t.stamps = stamps;
         QPH_CK(launch_attention(t, st_)); break;
       }
       default: throw std::runtime_error("time_kernel: unknown kernel id");
@@ -848,12 +849,18 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
     }
   }
   if (stamps) {
-    std::vector<uint64_t> h(4 * 4096);
+    std::vector<uint64_t> h(5 * 4096);
     QPH_CK(hipMemcpy(h.data(), stamps, h.size() * 8, hipMemcpyDeviceToHost));
     if (FILE *f = fopen(stf, "w")) {
-      for (int i = 0; i < cfg_.kv_heads * awo_rc_; i++)
-        fprintf(f, "%llu %llu %llu %llu\n", (unsigned long long)h[4 * i], (unsigned long long)h[4 * i + 1],
-                (unsigned long long)h[4 * i + 2], (unsigned long long)h[4 * i + 3]);
+      if (which == 6)
+        for (int i = 0; i < cfg_.kv_heads * awo_rc_; i++)
+          fprintf(f, "%llu %llu %llu %llu\n", (unsigned long long)h[4 * i], (unsigned long long)h[4 * i + 1],
+                  (unsigned long long)h[4 * i + 2], (unsigned long long)h[4 * i + 3]);
+      else
+        for (int i = 0; i < cfg_.kv_heads * max_chunks_ && 5 * i + 4 < (int)h.size(); i++)
+          if (h[5 * i])
+            fprintf(f, "%llu %llu %llu %llu %llu\n", (unsigned long long)h[5 * i], (unsigned long long)h[5 * i + 1],
+                    (unsigned long long)h[5 * i + 2], (unsigned long long)h[5 * i + 3], (unsigned long long)h[5 * i + 4]);
       fclose(f);
     }
   }
