@@ -1129,6 +1129,137 @@ hipError_t launch_attn_wo(const AttnArgs &a, AwoArgs w, hipStream_t st) {
   return hipErrorInvalidValue;
 }
 
+// ------------------------------------------------------------------ every group's attention + whole wo rows
+// For models whose kv groups are not whole 128-column blocks (C1: 7 heads of 64 per group) at contexts where the
+// attention runs one split per group: workgroup c of rc computes every group's attention in turn (attn_split, one
+// split, into LDS), quantises the whole attention vector (the wo matvec prologue's blocks), loads wo rows
+// [cR, cR + R) whole - issued while the last group's partials merge - and finishes them as the wo matvec does: the
+// exact int32 block sums, rows_q8's fp32 chain over all blocks in order (kernels_x86.cpp:57-69), the row scale and
+// x[row] += y.  The same arithmetic as k_attention with one split per group followed by the wo matvec, bit for bit;
+// the next kernels are unchanged.
+constexpr int kAwoRowsMaxCols = 2048, kAwoRowsMaxGroups = 2;
+template <int HD, int REP, int NL>
+__global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo_rows(AttnArgs a, AwoArgs w) {
+  constexpr int NT = kAttnMfWaves * 64;
+  __shared__ __align__(16) float ao[kAwoRowsMaxCols];
+  __shared__ __align__(16) int8_t xh[kAwoRowsMaxCols];
+  __shared__ __align__(16) uint8_t xl[kAwoRowsMaxCols];
+  __shared__ float bsl[kAwoRowsMaxCols / kQB];
+  __shared__ int lsl[kAwoRowsMaxCols / kQB];
+  __shared__ int isl[NT * NL / 8];   // block sums [row in tile][nb]
+  const int c = blockIdx.x, d = w.wo.rows, cols = w.wo.cols, nb = cols / kQB, ppr = cols / 16;
+  const int r0 = c * w.R, R = min(w.R, d - r0);
+  const int8_t *wq = (const int8_t *)w.wo.q;
+  uint4 wr[NL];
+  auto issue = [&]() {
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int p = threadIdx.x + NT * i, lr = p / ppr, c16 = p % ppr;
+      const int row = lr < R ? r0 + lr : r0;   // past the tile: row r0 (chunks are never empty), not used
+      wr[i] = *(const uint4 *)(wq + (size_t)row * cols + 16 * c16);
+    }
+  };
+  bool last = false;
+  auto mid = [&]() { if (last) issue(); };   // one attn_split instantiation (its LDS arrays are per instantiation)
+  for (int g = 0; g < a.nkv; g++) {
+    last = g + 1 == a.nkv;
+    attn_split<HD, REP, true>(a, g, 0, 1, 1, ao + g * REP * HD, mid);
+    __syncthreads();
+  }
+  if (threadIdx.x < 8 * nb) {   // eight lanes per block, 16 columns each (act_build's arithmetic)
+    const int b = threadIdx.x >> 3, sub = threadIdx.x & 7, c0 = b * kQB + sub * 16;
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float4 t = *(const float4 *)(ao + c0 + 4 * k);
+      v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+    }
+    float m = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) m = fmaxf(m, fabsf(v[k]));
+    m = max8_f(m);
+    const float isx = m > 0 ? kActMax / m : 0.f;
+    if (sub == 0) bsl[b] = m / kActMax;
+    uint32_t hw[4], lw[4]; int ls = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      uint32_t hh = 0, ll = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int q = (int)__builtin_rintf(v[4 * k + j] * isx);
+        hh |= (uint32_t)((q >> 8) & 0xff) << (8 * j);
+        ll |= (uint32_t)(q & 0xff) << (8 * j);
+        ls += q & 0xff;
+      }
+      hw[k] = hh; lw[k] = ll;
+    }
+    *(uint4 *)(xh + c0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(xl + c0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    ls = sum8_i(ls);
+    if (sub == 0) lsl[b] = ls;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    const int p = threadIdx.x + NT * i, lr = p / ppr, c16 = p % ppr;
+    const uint4 h = *(const uint4 *)(xh + 16 * c16), l = *(const uint4 *)(xl + 16 * c16);
+    const uint4 ww = wr[i];
+    int A = __builtin_amdgcn_sdot4((int)ww.x, (int)h.x, 0, false);
+    A = __builtin_amdgcn_sdot4((int)ww.y, (int)h.y, A, false);
+    A = __builtin_amdgcn_sdot4((int)ww.z, (int)h.z, A, false);
+    A = __builtin_amdgcn_sdot4((int)ww.w, (int)h.w, A, false);
+    uint32_t B = __builtin_amdgcn_udot4(ww.x ^ 0x80808080u, l.x, 0u, false);
+    B = __builtin_amdgcn_udot4(ww.y ^ 0x80808080u, l.y, B, false);
+    B = __builtin_amdgcn_udot4(ww.z ^ 0x80808080u, l.z, B, false);
+    B = __builtin_amdgcn_udot4(ww.w ^ 0x80808080u, l.w, B, false);
+    const int sum = sum8_i(A * 256 + (int)B);
+    if ((lane & 7) == 0 && lr < R) isl[lr * nb + (c16 >> 3)] = sum - 128 * lsl[c16 >> 3];
+  }
+  __syncthreads();
+  for (int lr = threadIdx.x; lr < R; lr += NT) {
+    float ch = 0.f;
+    for (int b = 0; b < nb; b++) ch = __builtin_fmaf(bsl[b], (float)isl[lr * nb + b], ch);
+    const int row = r0 + lr;
+    float y = ch * ((const float *)w.wo.s)[row];
+    asm volatile("" : "+v"(y));   // y rounded on its own, then added (rows_q8's y, then x += y): no fma contraction
+    w.x[row] = w.x[row] + y;
+  }
+}
+
+int attn_single_max(int hd) { return kAttnMfBlk * kAttnMfWaves * 64 / hd; }
+
+bool attn_wo_rows_fits(int hd, int nh, int nkv, const DMat &wo, int cus, int *rc, int *nl) {
+  if (wo.kind != MK_Q8 || nh % nkv || hd != 64 || nkv > kAwoRowsMaxGroups) return false;
+  const int rep = nh / nkv, cols = nh * hd;
+  if (rep > 8 || wo.cols != cols || cols % kQB || cols > kAwoRowsMaxCols || wo.rows < 1) return false;
+  const int c = std::max(1, std::min(wo.rows, cus)), R = (wo.rows + c - 1) / c, pieces = R * (cols / 16);
+  const int need = (pieces + kAttnMfWaves * 64 - 1) / (kAttnMfWaves * 64);
+  if (need > 4) return false;
+  *rc = (wo.rows + R - 1) / R; *nl = need <= 1 ? 1 : need <= 2 ? 2 : 4;
+  return true;
+}
+
+hipError_t launch_attn_wo_rows(const AttnArgs &a, AwoArgs w, hipStream_t st) {
+  int rc = 0, nl = 0;
+  if (!attn_wo_rows_fits(a.hd, a.nh, a.nkv, w.wo, g_mv_config.cus, &rc, &nl) || !w.x) return hipErrorInvalidValue;
+  w.R = (w.wo.rows + rc - 1) / rc;
+  if ((size_t)(rc - 1) * w.R >= (size_t)w.wo.rows) return hipErrorInvalidValue;
+  const int rep = a.nh / a.nkv;
+#define QPH_AWR(HD, R, NL)                                                                                          \
+  if (a.hd == HD && rep == R && nl == NL) {                                                                         \
+    hipLaunchKernelGGL((k_attn_wo_rows<HD, R, NL>), dim3(rc), dim3(kAttnMfWaves * 64), 0, st, a, w);                \
+    return hipGetLastError();                                                                                       \
+  }
+#define QPH_AWR3(HD, R) QPH_AWR(HD, R, 1) QPH_AWR(HD, R, 2) QPH_AWR(HD, R, 4)
+  // head dim 64 only: at 128 a group's heads are always whole 128-column blocks (k_attn_wo takes the model)
+  QPH_AWR3(64, 1) QPH_AWR3(64, 2) QPH_AWR3(64, 3) QPH_AWR3(64, 4) QPH_AWR3(64, 5) QPH_AWR3(64, 6) QPH_AWR3(64, 7)
+  QPH_AWR3(64, 8)
+#undef QPH_AWR3
+#undef QPH_AWR
+  return hipErrorInvalidValue;
+}
+
 // ------------------------------------------------------------------ greedy pick
 __global__ __launch_bounds__(kThreads) void k_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens) {
   constexpr int NW = kThreads / kWave;

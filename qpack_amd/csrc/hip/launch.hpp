@@ -124,6 +124,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 struct AwoArgs {
   DMat wo;      // q8 [d][nh * hd]
   float *part;  // [nkv][d] per-group partial products
+  float *x;     // k_attn_wo_rows: the residual stream [d] (x += wo . att)
   int R;        // rows per chunk (set by the launcher)
   uint64_t *stamps;   // measurement only (optional): per workgroup realtime at start, after the attention, after the
                       // weights arrived, at the end
@@ -131,6 +132,13 @@ struct AwoArgs {
 // whether the fused kernel takes this shape; rc = row chunks (grid.y), nl = 16-byte weight pieces per thread
 bool attn_wo_fits(int hd, int nh, int nkv, const DMat &wo, int cus, int *rc, int *nl);
 hipError_t launch_attn_wo(const AttnArgs &a, AwoArgs w, hipStream_t st);
+// Every group's attention (one split each) and whole wo rows with the residual add, for q8 wo with at most 2 kv groups
+// and nh * hd <= 2048 (groups that are not whole 128-column blocks, e.g. 7 heads of 64): grid rc; bit-identical to
+// k_attention with one split per group followed by the wo matvec (EPI_RESID)
+bool attn_wo_rows_fits(int hd, int nh, int nkv, const DMat &wo, int cus, int *rc, int *nl);
+// the longest context k_attention runs as one split per kv group by default (64 KiB of K and V per group)
+int attn_single_max(int hd);
+hipError_t launch_attn_wo_rows(const AttnArgs &a, AwoArgs w, hipStream_t st);
 
 // greedy pick over the head's per-workgroup (max, index) pairs; advances ctl (tok = pick, pos += 1, n_out += 1) and
 // writes the pick to out_tokens[ctl->n_out]

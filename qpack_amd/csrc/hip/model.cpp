@@ -126,9 +126,11 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   part_ = (float *)dalloc(4ull * nh * max_chunks_ * (hd + 2));
   q16_ = (uint16_t *)dalloc(4ull * qd_);
   QPH_CK(hipMemset(counters_, 0, 8ull * nkv));
-  {  // decode attention fused with wo (q8 wo on every layer, a group's heads whole 128-column blocks), short contexts
+  {  // decode attention fused with wo (q8 wo on every layer), short contexts: per kv group with the partials summed by
+     // gate / up (a group's heads whole 128-column blocks), else every group in each workgroup with whole wo rows
     int rc = 0, nl = 0;
-    bool ok = !layers_.empty();
+    bool ok = !layers_.empty(), rows_ok = !layers_.empty();
+    for (const Layer &ly : layers_) rows_ok = rows_ok && attn_wo_rows_fits(hd, nh, nkv, ly.wo, g_mv_config.cus, &rc, &nl);
     for (const Layer &ly : layers_) {
       ok = ok && attn_wo_fits(hd, nh, nkv, ly.wo, g_mv_config.cus, &rc, &nl);
       // the gate / up launch that adds the group partials (their LDS staging must fit)
@@ -138,8 +140,11 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
       ok = ok && launch_matvec(PRO_NORM_SUM, EPI_SWIGLU, a, 1 << 20, st_) == hipSuccess;
     }
     const char *e = getenv("QPH_AWO_MAX");   // longest context (positions) that takes the fused kernel; 0: never
-    awo_max_ = ok ? (e ? std::max(0, atoi(e)) : kAwoMaxDefault) : 0;
-    if (awo_max_ > 0) {
+    awo_rows_ = !ok && rows_ok;
+    // the rows kernel: up to the contexts where the split attention also runs one split per group (bit-identical)
+    const int dflt = ok ? kAwoMaxDefault : awo_rows_ ? (attn_single_ > 0 ? attn_single_ : attn_single_max(hd)) : 0;
+    awo_max_ = ok || awo_rows_ ? (e ? std::max(0, atoi(e)) : dflt) : 0;
+    if (awo_max_ > 0 && !awo_rows_) {
       awo_rc_ = rc;
       awo_part_ = (float *)dalloc(4ull * nkv * d);
       xs_ = (float *)dalloc(4ull * d);
@@ -258,7 +263,10 @@ void HipLlama::enqueue_layer(int l) {
   at.nh = cfg_.heads; at.nkv = cfg_.kv_heads; at.hd = cfg_.head_dim; at.max_chunks = max_chunks_; at.counters = counters_;
   at.single_max = attn_single_; at.split_pos = attn_split_pos_; at.status = dstatus_; at.spin_limit = attn_spin_;
   at.force_late = attn_force_late_;
-  if (fuse_) {
+  if (fuse_ && awo_rows_) {   // every group's attention and whole wo rows + residual in one launch
+    AwoArgs w{}; w.wo = ly.wo; w.x = x_;
+    QPH_CK(launch_attn_wo_rows(at, w, st_));
+  } else if (fuse_) {
     // RoPE, fp16 KV append, attention and the wo product per kv group in one launch; the group partials are added to
     // the residual stream by the gate / up prologue (x + sum of parts, also stored to xs_), down adds into x_ from xs_
     AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_;
@@ -793,7 +801,8 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
       case 6: {   // fused attention + wo
         AttnArgs t{}; t.q = q_; t.q16 = q16_; t.ctx = ctx_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
-        AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_;
+        AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_; w.x = xn_;
+        if (awo_rows_) { QPH_CK(launch_attn_wo_rows(t, w, st_)); break; }
         if (!awo_part_) throw std::runtime_error("time_kernel: the fused attention + wo kernel does not take this model");
         w.stamps = stamps;
         QPH_CK(launch_attn_wo(t, w, st_)); break;

@@ -91,6 +91,7 @@ class HipLlama {
   // decode attention fused with wo (launch_attn_wo) for contexts up to awo_max_ positions (0: not used) and its graphs
   static constexpr int kAwoMaxDefault = 1024;
   int awo_max_ = 0, awo_rc_ = 0;
+  bool awo_rows_ = false;   // the fused kernel is k_attn_wo_rows (every group per workgroup, whole rows, x += y)
   bool fuse_ = false;   // enqueue_layer: the fused kernel (set around a capture or a direct enqueue)
   float *awo_part_ = nullptr;   // [nkv][d] per-group partial wo products
   float *xs_ = nullptr;         // x + the attention block's output (written by the gate / up prologue)

@@ -319,11 +319,13 @@ def test_graph_replays_with_device_logits(synth):
     a.close(); b.close()
 
 
-@pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_odd", "mini_r7h"])
+@pytest.mark.parametrize("cfg", ["mini", "mini128", "mini_odd", "mini_r7h", "mini_r7"])
 def test_fused_attention_wo(cfg, synth, monkeypatch):
-    """decode attention fused with the wo product and residual (k_attn_wo, contexts up to QPH_AWO_MAX positions)
-    against the oracle and against the split attention + wo matvec launches, across the threshold (fused up to 100
-    positions, split beyond), then greedy chains of both against the oracle's"""
+    """decode attention fused with the wo product and residual (contexts up to QPH_AWO_MAX positions) against the
+    oracle and against the split attention + wo matvec launches, across the threshold (fused up to 100 positions,
+    split beyond), then greedy chains of both against the oracle's.  k_attn_wo (per kv group, partials summed by
+    gate / up) for groups of whole 128-column blocks; k_attn_wo_rows (every group, whole rows) for mini_r7's groups of
+    7 heads of 64, whose logits must equal the split launches' bit for bit"""
     path = synth(cfg)
     monkeypatch.setenv("QPH_AWO_MAX", "100")
     fused = qa.HipLlama.load(path, max_ctx=192)
@@ -337,8 +339,11 @@ def test_fused_attention_wo(cfg, synth, monkeypatch):
     for m in (fused, split):
         m.prefill(toks, 0)
     lo = orc.prefill(toks, 1)
+    rows = cfg == "mini_r7"   # 7 heads of 64 per group: k_attn_wo_rows, bit-identical to the split launches
     for t in rng.integers(0, fused.vocab(), 50):
         a, b, c = fused.step(int(t), 1), split.step(int(t), 1), orc.step(int(t), 1)
+        if rows:
+            np.testing.assert_array_equal(a, b)
         err, ok = close(a, c)
         assert ok, f"fused step at {fused.pos()}: logits max|d| {err} against the oracle"
         err, ok = close(b, c)
