@@ -7,9 +7,9 @@ SwiGLU 14336, vocab 128256, untied head), seeded N(0, 0.02) random-init weights 
             argmax feeds the next step; HIP events on the model's stream, host clock around it)
   prefill - one `--prefill-tokens` prompt (C4), host clock around qph_prefill
 Roofline: the dominant decode kernel (fused RMSNorm + gate/up + SwiGLU matvec, ~47 % of the step's bytes) in the form
-the token loop runs it at the timed contexts - after the fused attention + wo kernel it also adds that kernel's kv-group
-partials to the residual stream (PRO_NORM_SUM) - launched alone over the 32 layers in turn and timed with HIP events on
-the model's stream; achieved = its algorithmic bytes / mean duration.  traffic = its HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (committed summary under
+the token loop runs it at the timed contexts (PRO_NORM: the fused attention + wo kernel has already added its kv-group
+partials to the residual stream; with QPH_AWO_SUM=0 this kernel adds them, PRO_NORM_SUM) launched alone over the 32
+layers in turn and timed with HIP events on the model's stream; achieved = its algorithmic bytes / mean duration.  traffic = its HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (committed summary under
 profiles/, produced by --profile runs and --pmc-summary).
 CPU baseline: the reference engine compiled from its own sources (oracle/_ref/libqpref.so, AVX2) on the same file,
 on the host cores, qpack-bench protocol on a bounded sample.
@@ -30,7 +30,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# the token loop's gate / up kernel: PRO_NORM_SUM (after the fused attention + wo) or PRO_NORM; EPI_SWIGLU, 2 rows per
+# the token loop's gate / up kernel: PRO_NORM, or PRO_NORM_SUM (QPH_AWO_SUM=0: it adds the fused attention + wo
+# kernel's group partials); EPI_SWIGLU, 2 rows per
 # unit, q8 - its rocprofv3 name, time_kernel id and the committed counter summary
 DOMINANT = {"sum": ("k_matvec<2, 2, 2, 1, false>", 7, "k_matvec_normsum_swiglu_q8_c3_traffic.md",
                     "k_matvec<PRO_NORM_SUM,EPI_SWIGLU> (x + the 8 kv-group partials of the fused attention + wo, "
@@ -262,7 +263,7 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="launch kernels one by one (no HIP graphs) so a profiler sees every dispatch, and run a "
                          "calibration copy of known size for the byte counters")
-    ap.add_argument("--dominant", choices=sorted(DOMINANT), default="sum",
+    ap.add_argument("--dominant", choices=sorted(DOMINANT), default="norm",
                     help="which gate / up kernel --pmc-summary reads (the token loop runs 'sum' at contexts up to 1024 "
                          "on q8 models whose kv groups are whole 128-column blocks)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -326,7 +327,7 @@ def main():
 
     if a.profile:
         calibration_copy()
-    dom = "sum"
+    dom = "sum" if os.environ.get("QPH_AWO_SUM") == "0" else "norm"
     try:
         kms, kbytes = m.time_kernel(DOMINANT[dom][1], a.kernel_iters)
     except RuntimeError:   # a model the fused attention + wo kernel does not take

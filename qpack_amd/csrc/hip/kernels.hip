@@ -1005,6 +1005,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 //   4. forms the exact int32 block sums (the matvec's two-plane dot products and 8-lane sums) and, one thread per row,
 //      rows_q8's fp32 chain over the group's blocks, acc = fma(bs[b], sum[b], acc) (kernels_x86.cpp:57-69), times the
 //      row scale: part[g][row].  No workgroup waits for another; the next kernel sums the groups' parts.
+constexpr int kAwoMaxGroups = 8;    // kv groups the last arrival adds up (AwoArgs::counters)
 template <int HD, int REP, int NL>
 __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoArgs w) {
   constexpr int NT = kAttnMfWaves * 64, CG = REP * HD, PPR = CG / 16, NBG = CG / kQB;
@@ -1089,7 +1090,42 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
 #pragma unroll
     for (int b = 0; b < NBG; b++) ch = __builtin_fmaf(bsl[b], (float)isl[lr * NBG + b], ch);
     const int row = r0 + lr;
-    w.part[(size_t)g * d + row] = ch * ((const float *)w.wo.s)[row];
+    const float y = ch * ((const float *)w.wo.s)[row];
+    float *dst = w.part + (size_t)g * d + row;
+    if (w.counters) asm volatile("global_store_dword %0, %1, off sc1" ::"v"(dst), "v"(y) : "memory");
+    else *dst = y;
+  }
+  if (w.counters) {
+    // the last of the chunk's nkv workgroups to arrive adds the groups' parts to the residual stream:
+    // x[row] += ((p_0 + p_1) + ...) + p_{nkv-1}.  The parts went through to memory (coherent stores, drained before the
+    // counter bump) and are read back with coherent loads; the last arrival resets the counter for the next launch.
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int n = __hip_atomic_fetch_add(w.counters + c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = n == (int)gridDim.x - 1;
+      if (last) __hip_atomic_store(w.counters + c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (last)
+      for (int lr = threadIdx.x; lr < R; lr += NT) {
+        const int row = r0 + lr, ng = (int)gridDim.x;
+        float p[kAwoMaxGroups];
+#pragma unroll
+        for (int j = 0; j < kAwoMaxGroups; j++) {   // clamped in range; unused ones are not summed
+          const float *src = w.part + (size_t)(j < ng ? j : 0) * d + row;
+          asm volatile("global_load_dword %0, %1, off sc1" : "=v"(p[j]) : "v"(src));
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < kAwoMaxGroups; j++) asm volatile("" : "+v"(p[j]));   // used only after the wait
+        float y = p[0];
+#pragma unroll
+        for (int j = 1; j < kAwoMaxGroups; j++)
+          if (j < ng) y += p[j];
+        w.x[row] += y;
+      }
   }
   if (w.stamps && threadIdx.x == 0) {
     uint64_t *o = w.stamps + 4 * (blockIdx.y * gridDim.x + blockIdx.x);
@@ -1098,7 +1134,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
 }
 
 bool attn_wo_fits(int hd, int nh, int nkv, const DMat &wo, int cus, int *rc, int *nl) {
-  if (wo.kind != MK_Q8 || nh % nkv || (hd != 64 && hd != 128)) return false;
+  if (wo.kind != MK_Q8 || nkv > kAwoMaxGroups || nh % nkv || (hd != 64 && hd != 128)) return false;
   const int rep = nh / nkv, cg = rep * hd;
   if (cg % kQB || rep > 8 || wo.cols != nh * hd || wo.rows < 1) return false;
   // about one workgroup per CU; every chunk non-empty (rc = ceil(rows / R))

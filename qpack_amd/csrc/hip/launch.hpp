@@ -124,7 +124,9 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 struct AwoArgs {
   DMat wo;      // q8 [d][nh * hd]
   float *part;  // [nkv][d] per-group partial products
-  float *x;     // k_attn_wo_rows: the residual stream [d] (x += wo . att)
+  float *x;     // k_attn_wo_rows, and k_attn_wo with counters: the residual stream [d] (x += wo . att)
+  int *counters;   // k_attn_wo: [row chunks] arrival counters, zero before the first launch (each launch leaves them
+                   // zero); when set, the chunk's last workgroup adds the group parts to x, else the next kernel does
   int R;        // rows per chunk (set by the launcher)
   uint64_t *stamps;   // measurement only (optional): per workgroup realtime at start, after the attention, after the
                       // weights arrived, at the end

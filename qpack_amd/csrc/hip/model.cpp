@@ -131,8 +131,12 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     int rc = 0, nl = 0;
     bool ok = !layers_.empty(), rows_ok = !layers_.empty();
     for (const Layer &ly : layers_) rows_ok = rows_ok && attn_wo_rows_fits(hd, nh, nkv, ly.wo, g_mv_config.cus, &rc, &nl);
+    // QPH_AWO_SUM=0: the gate / up prologue adds the group parts instead of k_attn_wo's last arrivals
+    const char *es = getenv("QPH_AWO_SUM");
+    awo_sum_ = !(es && atoi(es) == 0);
     for (const Layer &ly : layers_) {
       ok = ok && attn_wo_fits(hd, nh, nkv, ly.wo, g_mv_config.cus, &rc, &nl);
+      if (awo_sum_) continue;
       // the gate / up launch that adds the group partials (their LDS staging must fit)
       MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.part = x_; a.nparts = nkv; a.pstride = (size_t)d;
       a.plan_only = 1;
@@ -148,6 +152,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
       awo_rc_ = rc;
       awo_part_ = (float *)dalloc(4ull * nkv * d);
       xs_ = (float *)dalloc(4ull * d);
+      awo_cnt_ = (int *)dalloc(4ull * rc);
+      QPH_CK(hipMemset(awo_cnt_, 0, 4ull * rc));
     }
   }
   head_grid_ = cus_ * 4;
@@ -266,6 +272,11 @@ void HipLlama::enqueue_layer(int l) {
   if (fuse_ && awo_rows_) {   // every group's attention and whole wo rows + residual in one launch
     AwoArgs w{}; w.wo = ly.wo; w.x = x_;
     QPH_CK(launch_attn_wo_rows(at, w, st_));
+  } else if (fuse_ && awo_sum_) {
+    // attention and the wo product per kv group in one launch; each row chunk's last workgroup adds the group parts
+    // to the residual stream
+    AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_; w.x = x_; w.counters = awo_cnt_;
+    QPH_CK(launch_attn_wo(at, w, st_));
   } else if (fuse_) {
     // RoPE, fp16 KV append, attention and the wo product per kv group in one launch; the group partials are added to
     // the residual stream by the gate / up prologue (x + sum of parts, also stored to xs_), down adds into x_ from xs_
@@ -805,6 +816,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         if (awo_rows_) { QPH_CK(launch_attn_wo_rows(t, w, st_)); break; }
         if (!awo_part_) throw std::runtime_error("time_kernel: the fused attention + wo kernel does not take this model");
         w.stamps = stamps;
+        if (awo_sum_) w.counters = awo_cnt_;   // adds into xn_ (scratch)
         QPH_CK(launch_attn_wo(t, w, st_)); break;
       }
       case 7:   // gate / up after the fused attention + wo: x + the group parts

@@ -95,6 +95,8 @@ class HipLlama {
   bool fuse_ = false;   // enqueue_layer: the fused kernel (set around a capture or a direct enqueue)
   float *awo_part_ = nullptr;   // [nkv][d] per-group partial wo products
   float *xs_ = nullptr;         // x + the attention block's output (written by the gate / up prologue)
+  int *awo_cnt_ = nullptr;      // [row chunks] k_attn_wo arrival counters: its last arrivals add the parts to x
+  bool awo_sum_ = false;        // the group parts are added by k_attn_wo (else by the gate / up prologue)
   hipGraphExec_t g_fs_state_ = nullptr, g_fs_logits_ = nullptr, g_fs_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
   void run_step(int parts, int pos);

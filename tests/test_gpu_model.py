@@ -325,36 +325,45 @@ def test_fused_attention_wo(cfg, synth, monkeypatch):
     oracle and against the split attention + wo matvec launches, across the threshold (fused up to 100 positions,
     split beyond), then greedy chains of both against the oracle's.  k_attn_wo (per kv group, partials summed by
     gate / up) for groups of whole 128-column blocks; k_attn_wo_rows (every group, whole rows) for mini_r7's groups of
-    7 heads of 64, whose logits must equal the split launches' bit for bit"""
+    7 heads of 64, whose logits must equal the split launches' bit for bit.  k_attn_wo's group partials are added to the
+    residual stream by each row chunk's last workgroup (default) or by the gate / up prologue (QPH_AWO_SUM=0): both
+    forms are checked"""
     path = synth(cfg)
+    rows = cfg == "mini_r7"   # 7 heads of 64 per group: k_attn_wo_rows, bit-identical to the split launches
     monkeypatch.setenv("QPH_AWO_MAX", "100")
-    fused = qa.HipLlama.load(path, max_ctx=192)
+    models = [qa.HipLlama.load(path, max_ctx=192)]
+    if not rows:
+        monkeypatch.setenv("QPH_AWO_SUM", "0")
+        models.append(qa.HipLlama.load(path, max_ctx=192))
+        monkeypatch.delenv("QPH_AWO_SUM")
     monkeypatch.setenv("QPH_AWO_MAX", "0")
     split = qa.HipLlama.load(path, max_ctx=192)
     monkeypatch.delenv("QPH_AWO_MAX")
     orc = O.Oracle(path, max_ctx=192)
     rng = np.random.default_rng(21)
-    toks = rng.integers(0, fused.vocab(), 60).astype(np.int32)
-    print(f"{cfg}: fused attention + wo, prompt 60, steps to 110", flush=True)
-    for m in (fused, split):
+    toks = rng.integers(0, split.vocab(), 60).astype(np.int32)
+    print(f"{cfg}: fused attention + wo ({len(models)} forms), prompt 60, steps to 110", flush=True)
+    for m in models + [split]:
         m.prefill(toks, 0)
     lo = orc.prefill(toks, 1)
-    rows = cfg == "mini_r7"   # 7 heads of 64 per group: k_attn_wo_rows, bit-identical to the split launches
-    for t in rng.integers(0, fused.vocab(), 50):
-        a, b, c = fused.step(int(t), 1), split.step(int(t), 1), orc.step(int(t), 1)
-        if rows:
-            np.testing.assert_array_equal(a, b)
-        err, ok = close(a, c)
-        assert ok, f"fused step at {fused.pos()}: logits max|d| {err} against the oracle"
+    for t in rng.integers(0, split.vocab(), 50):
+        b, c = split.step(int(t), 1), orc.step(int(t), 1)
         err, ok = close(b, c)
         assert ok, f"split step at {split.pos()}: logits max|d| {err} against the oracle"
+        for i, m in enumerate(models):
+            a = m.step(int(t), 1)
+            if rows:
+                np.testing.assert_array_equal(a, b)
+            err, ok = close(a, c)
+            assert ok, f"fused form {i} step at {m.pos()}: logits max|d| {err} against the oracle"
         lo = c
     # greedy from position 70 (fused for the first 30 steps, then split)
-    for m in (fused, split):
+    for m in models + [split]:
         assert m.rewind(70)
     orc.set_pos(70)
     tok = int(np.argmax(lo))
     o = orc.greedy_run(tok, 40)
-    np.testing.assert_array_equal(fused.greedy_run(tok, 40), o)
-    np.testing.assert_array_equal(split.greedy_run(tok, 40), o)
-    fused.close(); split.close(); orc.close()
+    for m in models + [split]:
+        np.testing.assert_array_equal(m.greedy_run(tok, 40), o)
+        m.close()
+    orc.close()
