@@ -295,6 +295,11 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
 #pragma unroll
     for (int t = 1; t < NS; t++) if (s == t) { row = og.row[t]; scl = og.sc[t]; }
     float v = 0.f;
+    // the row scale and the residual are loaded before the chain, so their round trips overlap it
+    const bool store = live && row < og.rows;
+    const float sc_pre = live && isq8 ? *scl : 0.f;
+    float res_pre = 0.f;
+    if (EPI == EPI_RESID && store) res_pre = a.resid_in ? a.resid_in[row] : a.out[0][row];
     if (live) {
       if (isq8) {
         const int *ss = wsum + (u * NS + s) * av.nbp;
@@ -311,14 +316,13 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
           }
         }
         for (; b < nb; b++) ch = __builtin_fmaf(av.bs[b], (float)ss[b], ch);
-        v = ch * *scl;
+        v = ch * sc_pre;
         if (DBG && a.dbg_sums && og.seg == 0 && row < og.rows)
           for (int b = 0; b < nb; b++) a.dbg_sums[(size_t)row * nb + b] = ss[b];
       } else {
         v = wval[u * NS + s];
       }
     }
-    const bool store = live && row < og.rows;
     if (EPI == EPI_STORE && NS == 2 && a.ctl) {
       // RoPE of q / k rows (the partner row of the pair sits in the next lane) and the fp16 cache rows
       const int sg = og.seg;
@@ -350,7 +354,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
       float *const out_seg = og.seg == 0 ? a.out[0] : (og.seg == 1 ? a.out[1] : a.out[2]);
       const float *const bias_seg = og.seg == 0 ? a.bias[0] : (og.seg == 1 ? a.bias[1] : a.bias[2]);
       if (EPI == EPI_STORE) { float y = v; if (bias_seg) y = y + bias_seg[row]; out_seg[row] = y; }
-      else if (EPI == EPI_RESID) a.out[0][row] = (a.resid_in ? a.resid_in[row] : a.out[0][row]) + v;
+      else if (EPI == EPI_RESID) a.out[0][row] = res_pre + v;
       else { a.out[0][row] = v; if (better(v, row, best_v, best_i)) { best_v = v; best_i = row; } }
     }
   }
