@@ -864,14 +864,14 @@ __device__ void attn_merge_all(const AttnArgs &a, int g, int S) {
 // of 4 dims and the splits t / (HD / 4) + (NW * 256 / HD) k, all its loads issued at once; wave 0 also reduces M and L
 // over the splits (one split per lane).  late: the wait for the other splits ran out (the outputs are then NaN).
 template <int HD, int REP, int NW>
-__device__ void attn_merge_heads(const AttnArgs &a, int g, int S, int r, int MG, bool late) {
+__device__ void attn_merge_heads(const AttnArgs &a, int g, int S, int r, int MG, bool late, int ys) {
   constexpr int NCOL = HD / 4, NGRP = NW * 64 / NCOL, PER = (kAttnMaxSplits + NGRP - 1) / NGRP;
   __shared__ float Ms, Linv;
   __shared__ float4 opart[NGRP][NCOL];
   const int col = threadIdx.x % NCOL, grp = threadIdx.x / NCOL;
-  const float *mlb = a.part + (size_t)a.nh * gridDim.y * HD;
+  const float *mlb = a.part + (size_t)a.nh * ys * HD;
   for (int j = r; j < REP; j += MG) {
-    const size_t hs0 = (size_t)(g * REP + j) * gridDim.y;
+    const size_t hs0 = (size_t)(g * REP + j) * ys;
     f32x4 v[PER];
     float2 mlk[PER];
 #pragma unroll
@@ -929,7 +929,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   uint64_t st0 = 0, st1 = 0, st2 = 0;   // measurement (a.stamps): start, partials stored, rank known
   if (a.stamps) st0 = __builtin_amdgcn_s_memrealtime();
   attn_split<HD, REP>(a, g, s, S, gridDim.y);
-  if (S == 1) return;
+  if (S == 1 || (a.merge_sep && S >= kAttnParMerge)) return;   // merge_sep: k_attn_merge merges (the next launch)
   // this thread's coherent stores have completed before the workgroup's counter bump
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -975,12 +975,30 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   }
   // this merger no longer reads the arrivals; the round trip overlaps the merge
   const int d = threadIdx.x == 0 ? __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-  attn_merge_heads<HD, REP, NW>(a, g, S, r, MG, late);
+  attn_merge_heads<HD, REP, NW>(a, g, S, r, MG, late, gridDim.y);
   if (threadIdx.x == 0 && d == MG - 1) {
     __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   stamp(1);
+}
+
+// The merge of k_attention's splits as a launch of its own (AttnArgs::merge_sep, contexts of at least kAttnParMerge
+// splits): workgroup (g, j) merges head j of group g over the S splits the previous launch stored - the kernel
+// boundary orders the partials before their loads, in place of the arrival counters and the mergers' wait.
+template <int HD, int REP>
+__global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_merge(AttnArgs a) {
+  const int pos = a.ctl->pos, T = pos + 1;
+  const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * kAttnMfWaves * 64 / HD, sp = a.split_pos > 0 ? a.split_pos : 64;
+  const int S = T <= smax ? 1 : min(a.max_chunks, (T + sp - 1) / sp);
+  if (S < kAttnParMerge) return;   // k_attention merged in-kernel
+  attn_merge_heads<HD, REP, kAttnMfWaves>(a, blockIdx.x, S, blockIdx.y, REP, false, a.max_chunks);
+}
+
+int attn_long_merge_min(int hd, int single_max, int split_pos, int max_chunks) {
+  const int smax = single_max > 0 ? single_max : kAttnMfBlk * kAttnMfWaves * 64 / hd, sp = split_pos > 0 ? split_pos : 64;
+  if (max_chunks < kAttnParMerge) return 0;
+  return std::max(smax + 1, (kAttnParMerge - 1) * sp + 1);   // S = min(max_chunks, ceil(T / sp)) >= kAttnParMerge
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
@@ -990,6 +1008,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 #define QPH_ATT(HD, R)                                                                                              \
   if (a.hd == HD && rep == R) {                                                                                     \
     hipLaunchKernelGGL((k_attention<HD, R>), grid, dim3(kAttnMfWaves * 64), 0, st, a);                              \
+    if (a.merge_sep) hipLaunchKernelGGL((k_attn_merge<HD, R>), dim3(a.nkv, R), dim3(kAttnMfWaves * 64), 0, st, a);   \
     return hipGetLastError();                                                                                       \
   }
   QPH_ATT(64, 1) QPH_ATT(64, 2) QPH_ATT(64, 3) QPH_ATT(64, 4) QPH_ATT(64, 5) QPH_ATT(64, 6) QPH_ATT(64, 7) QPH_ATT(64, 8)

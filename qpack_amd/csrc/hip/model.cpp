@@ -116,6 +116,12 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   // test hook: the bound of a merger's wait for the other splits (the failure path forced from the host)
   if (const char *e = getenv("QPH_ATTN_SPIN")) attn_spin_ = std::max(0, atoi(e));
   attn_force_late_ = getenv("QPH_ATTN_FORCE_LATE") != nullptr;   // test hook: the same failure without the race
+  {  // long contexts: the splits' merge as a launch of its own (QPH_ATTN_MERGE_SEP=0: merged in-kernel, as below)
+    const char *e = getenv("QPH_ATTN_MERGE_SEP");
+    lm_min_ = e && atoi(e) == 0 ? 0 : attn_long_merge_min(hd, attn_single_, attn_split_pos_, max_chunks_);
+    if (lm_min_ > ctx_) lm_min_ = 0;
+  }
+
   counters_ = (int *)dalloc(8ull * nkv);
   const size_t kvn = (size_t)cfg.layers * ctx_ * kvd_;
   kc_ = (uint16_t *)dalloc(kvn * 2); vc_ = (uint16_t *)dalloc(kvn * 2);
@@ -234,7 +240,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
 HipLlama::~HipLlama() {
   if (st_) (void)hipStreamSynchronize(st_);
   for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_, g_ex_state_, g_ex_logits_, g_ex_greedy_, g_fs_state_,
-                           g_fs_logits_, g_fs_greedy_})
+                           g_fs_logits_, g_fs_greedy_, g_lm_state_, g_lm_logits_, g_lm_greedy_})
     if (g) (void)hipGraphExecDestroy(g);
   for (void *p : allocs_) (void)hipFree(p);
   if (hctl_) (void)hipHostFree(hctl_);
@@ -268,7 +274,7 @@ void HipLlama::enqueue_layer(int l) {
   at.att = att_;
   at.nh = cfg_.heads; at.nkv = cfg_.kv_heads; at.hd = cfg_.head_dim; at.max_chunks = max_chunks_; at.counters = counters_;
   at.single_max = attn_single_; at.split_pos = attn_split_pos_; at.status = dstatus_; at.spin_limit = attn_spin_;
-  at.force_late = attn_force_late_;
+  at.force_late = attn_force_late_; at.merge_sep = lm_;
   if (fuse_ && awo_rows_) {   // every group's attention and whole wo rows + residual in one launch
     AwoArgs w{}; w.wo = ly.wo; w.x = x_;
     QPH_CK(launch_attn_wo_rows(at, w, st_));
@@ -329,15 +335,15 @@ void HipLlama::enqueue_step(int parts) {
   if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
 }
 
-hipGraphExec_t HipLlama::capture(int parts, bool fused) {
+hipGraphExec_t HipLlama::capture(int parts, bool fused, bool long_merge) {
   hipGraph_t g = nullptr; hipGraphExec_t ge = nullptr;
-  fuse_ = fused;
+  fuse_ = fused; lm_ = long_merge;
   QPH_CK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
   try {
     enqueue_step(parts);
-    fuse_ = false;
+    fuse_ = false; lm_ = false;
   } catch (...) {
-    fuse_ = false;
+    fuse_ = false; lm_ = false;
     (void)hipStreamEndCapture(st_, &g);
     if (g) (void)hipGraphDestroy(g);
     throw;
@@ -359,22 +365,27 @@ void HipLlama::build_graphs() {
   g_logits_ = capture(1);
   g_greedy_ = capture(2);
   if (awo_max_ > 0) { g_fs_state_ = capture(0, true); g_fs_logits_ = capture(1, true); g_fs_greedy_ = capture(2, true); }
+  if (lm_min_ > 0) {
+    g_lm_state_ = capture(0, false, true); g_lm_logits_ = capture(1, false, true); g_lm_greedy_ = capture(2, false, true);
+  }
 }
 
 // pos: the position this step writes (its context is pos + 1 positions); contexts up to awo_max_ take the fused
 // attention + wo kernel
 void HipLlama::run_step(int parts, int pos) {
   const bool fused = !order_ && pos + 1 <= awo_max_;
+  const bool lm = !order_ && !fused && lm_min_ > 0 && pos + 1 >= lm_min_;
   if (use_graphs_) {
     hipGraphExec_t g = order_ ? (parts == 0 ? g_ex_state_ : parts == 1 ? g_ex_logits_ : g_ex_greedy_)
                        : fused ? (parts == 0 ? g_fs_state_ : parts == 1 ? g_fs_logits_ : g_fs_greedy_)
+                       : lm    ? (parts == 0 ? g_lm_state_ : parts == 1 ? g_lm_logits_ : g_lm_greedy_)
                                : (parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_);
     QPH_CK(hipGraphLaunch(g, st_));
     return;
   }
-  fuse_ = fused;
+  fuse_ = fused; lm_ = lm;
   enqueue_step(parts);
-  fuse_ = false;
+  fuse_ = false; lm_ = false;
 }
 
 // Called after every wait for the stream: a decode attention merger whose bounded wait for the other splits' partials
@@ -828,7 +839,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         AttnArgs t{}; t.q = q_; t.q16 = q16_; t.ctx = ctx_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         t.max_chunks = max_chunks_; t.counters = counters_; t.single_max = attn_single_; t.split_pos = attn_split_pos_;
-        t.status = dstatus_; t.spin_limit = attn_spin_; t.stamps = stamps;
+        t.status = dstatus_; t.spin_limit = attn_spin_; t.stamps = stamps; t.merge_sep = lm_min_ > 0 && pos_ + 1 >= lm_min_;
         QPH_CK(launch_attention(t, st_)); break;
       }
       default: throw std::runtime_error("time_kernel: unknown kernel id");

@@ -59,6 +59,10 @@ class HipLlama {
   int *counters_ = nullptr;
   int attn_single_ = 0, attn_split_pos_ = 0, attn_spin_ = 0;   // attention split policy (0: the kernel's defaults)
   bool attn_force_late_ = false;
+  // contexts of at least lm_min_ positions (every step >= 16 splits) merge the splits in a launch of their own
+  // (k_attn_merge; graphs g_lm_*); 0: never (QPH_ATTN_MERGE_SEP=0, or too few splits for the context window)
+  int lm_min_ = 0;
+  bool lm_ = false;   // the step being enqueued is such a step
   int pos_ = 0;
   unsigned slot_ = 0;
   hipStream_t st_ = nullptr;
@@ -98,6 +102,7 @@ class HipLlama {
   int *awo_cnt_ = nullptr;      // [row chunks] k_attn_wo arrival counters: its last arrivals add the parts to x
   bool awo_sum_ = false;        // the group parts are added by k_attn_wo (else by the gate / up prologue)
   hipGraphExec_t g_fs_state_ = nullptr, g_fs_logits_ = nullptr, g_fs_greedy_ = nullptr;
+  hipGraphExec_t g_lm_state_ = nullptr, g_lm_logits_ = nullptr, g_lm_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
   void run_step(int parts, int pos);
   // reference-order mode (exact.hip)
@@ -133,7 +138,7 @@ class HipLlama {
   void qkv_rope(MvArgs &a, uint16_t *kc, uint16_t *vc) const;
   void enqueue_head();
   void build_graphs();
-  hipGraphExec_t capture(int parts, bool fused = false);
+  hipGraphExec_t capture(int parts, bool fused = false, bool long_merge = false);
   void check_status();
   void write_ctl(int tok, int pos);
 };

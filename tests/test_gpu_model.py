@@ -240,6 +240,48 @@ def test_long_context_restore(cfg, T, synth):
     gpu.close(); orc.close()
 
 
+@pytest.mark.parametrize("cfg,T", [("mini_r7", 1500), ("mini128", 2100), ("mini_q4m", 990)])
+def test_attention_separate_merge(cfg, T, synth, monkeypatch):
+    """long contexts (every step >= 16 splits per kv group) merge the splits in a launch of their own (k_attn_merge):
+    the logits equal the in-kernel merge's (QPH_ATTN_MERGE_SEP=0) bit for bit - the same merge arithmetic - at every
+    step and in graph-replayed greedy runs, and match the oracle; a run that starts below the threshold and crosses it
+    (mini_q4m: 990 = 15 x 64 + 30 positions, the threshold 961) switches graphs on the way"""
+    path = synth(cfg)
+    shape = qa.CONFIGS[cfg]
+    kvd = shape.kv_heads * shape.head_dim
+    rng = np.random.default_rng(T + 1)
+    T0 = T - 40 if cfg == "mini_q4m" else T
+    k = rng.standard_normal((shape.layers, T0, kvd)).astype(np.float16)
+    v = rng.standard_normal((shape.layers, T0, kvd)).astype(np.float16)
+    snap = kv_snapshot(k, v)
+    sep = qa.HipLlama.load(path, max_ctx=T + 96)
+    monkeypatch.setenv("QPH_ATTN_MERGE_SEP", "0")
+    ink = qa.HipLlama.load(path, max_ctx=T + 96)
+    monkeypatch.delenv("QPH_ATTN_MERGE_SEP")
+    orc = O.Oracle(path, max_ctx=T + 96)
+    ko, vo = orc.kv_cache()
+    ko[:, :T0] = k.view(np.uint16); vo[:, :T0] = v.view(np.uint16)
+    orc.set_pos(T0)
+    for m in (sep, ink):
+        m.restore(snap)
+    print(f"{cfg}: context {T0}, separate against in-kernel merge", flush=True)
+    for i in range(50):
+        t = int(rng.integers(0, shape.vocab))
+        a, b, c = sep.step(t, 1), ink.step(t, 1), orc.step(t, 1)
+        np.testing.assert_array_equal(a, b, err_msg=f"step at {sep.pos()}")
+        err, ok = close(a, c)
+        assert ok, f"step at {sep.pos()}: logits max|d| {err}"
+    p0 = sep.pos()
+    tok = int(np.argmax(a))
+    ga = sep.greedy_run(tok, 24)
+    gb = ink.greedy_run(tok, 24)
+    np.testing.assert_array_equal(ga, gb)
+    np.testing.assert_array_equal(ga, orc.greedy_run(tok, 24))
+    assert sep.rewind(p0) and ink.rewind(p0)
+    np.testing.assert_array_equal(sep.greedy_run(tok, 24), ga)
+    sep.close(); ink.close(); orc.close()
+
+
 REF_QUANT = os.path.join(os.path.dirname(O.REF_LIB), "qpack-quantize")
 
 
@@ -279,8 +321,10 @@ def test_attention_merge_timeout_is_an_error(synth, monkeypatch):
     v = rng.standard_normal((shape.layers, T, kvd)).astype(np.float16)
     snap = kv_snapshot(k, v)
     monkeypatch.setenv("QPH_ATTN_FORCE_LATE", "1")
+    monkeypatch.setenv("QPH_ATTN_MERGE_SEP", "0")   # the in-kernel merge (the default merges long contexts in a launch)
     bad = qa.HipLlama.load(path, max_ctx=T + 64)
     monkeypatch.delenv("QPH_ATTN_FORCE_LATE")
+    monkeypatch.delenv("QPH_ATTN_MERGE_SEP")
     bad.restore(snap)
     with pytest.raises(qa.QphError, match="timed out"):
         bad.step(5, 1)
