@@ -929,7 +929,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   uint64_t st0 = 0, st1 = 0, st2 = 0;   // measurement (a.stamps): start, partials stored, rank known
   if (a.stamps) st0 = __builtin_amdgcn_s_memrealtime();
   attn_split<HD, REP>(a, g, s, S, gridDim.y);
-  if (S == 1 || (a.merge_sep && S >= kAttnParMerge)) return;   // merge_sep: k_attn_merge merges (the next launch)
+  if (S == 1 || (a.merge_sep && S >= a.merge_sep)) return;   // merge_sep: k_attn_merge merges (the next launch)
   // this thread's coherent stores have completed before the workgroup's counter bump
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -991,14 +991,14 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_merge(AttnArgs a) {
   const int pos = a.ctl->pos, T = pos + 1;
   const int smax = a.single_max > 0 ? a.single_max : kAttnMfBlk * kAttnMfWaves * 64 / HD, sp = a.split_pos > 0 ? a.split_pos : 64;
   const int S = T <= smax ? 1 : min(a.max_chunks, (T + sp - 1) / sp);
-  if (S < kAttnParMerge) return;   // k_attention merged in-kernel
+  if (S < a.merge_sep || S == 1) return;   // k_attention merged in-kernel (or had one split)
   attn_merge_heads<HD, REP, kAttnMfWaves>(a, blockIdx.x, S, blockIdx.y, REP, false, a.max_chunks);
 }
 
-int attn_long_merge_min(int hd, int single_max, int split_pos, int max_chunks) {
+int attn_long_merge_min(int hd, int single_max, int split_pos, int max_chunks, int min_splits) {
   const int smax = single_max > 0 ? single_max : kAttnMfBlk * kAttnMfWaves * 64 / hd, sp = split_pos > 0 ? split_pos : 64;
-  if (max_chunks < kAttnParMerge) return 0;
-  return std::max(smax + 1, (kAttnParMerge - 1) * sp + 1);   // S = min(max_chunks, ceil(T / sp)) >= kAttnParMerge
+  if (min_splits < 2 || max_chunks < min_splits) return 0;
+  return std::max(smax + 1, (min_splits - 1) * sp + 1);   // S = min(max_chunks, ceil(T / sp)) >= min_splits
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {

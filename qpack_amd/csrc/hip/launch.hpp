@@ -112,15 +112,15 @@ struct AttnArgs {
   int *status;                 // optional (host-visible): set to 1 when a merger's bounded wait for the partials ran out
   int spin_limit;              // the bound of that wait in polls (0: 1 << 22)
   int force_late;              // test hook: every merger that would wait gives up at once (the error path, forced)
-  int merge_sep;               // contexts of >= 16 splits: the splits only store their partials and a second launch
-                               // (k_attn_merge, one workgroup per head) merges them
+  int merge_sep;               // > 1: contexts of at least this many splits only store their partials and a second
+                               // launch (k_attn_merge, one workgroup per head) merges them
   uint64_t *stamps;            // measurement only (optional): per workgroup of k_attention 5 words - realtime at start,
                                // partials stored, merge rank known, end, and 1 if it merged
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
-// the shortest context from which every decode step runs at least 16 splits per kv group (the separate-merge form,
-// AttnArgs::merge_sep), 0 when no context does
-int attn_long_merge_min(int hd, int single_max, int split_pos, int max_chunks);
+// the shortest context from which every decode step runs at least min_splits splits per kv group (the
+// separate-merge form, AttnArgs::merge_sep), 0 when no context does
+int attn_long_merge_min(int hd, int single_max, int split_pos, int max_chunks, int min_splits);
 // Decode attention fused with the wo product (q8 wo, REP * hd a multiple of 128): grid (nkv, rc); workgroup (g, c)
 // computes kv group g's attention over the whole context (no splits) and, for wo rows [c R, c R + R), the product over
 // the group's columns: part[g][row] = (rows_q8's fp32 block chain over the group's blocks) * scale[row].  The next

@@ -116,9 +116,11 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   // test hook: the bound of a merger's wait for the other splits (the failure path forced from the host)
   if (const char *e = getenv("QPH_ATTN_SPIN")) attn_spin_ = std::max(0, atoi(e));
   attn_force_late_ = getenv("QPH_ATTN_FORCE_LATE") != nullptr;   // test hook: the same failure without the race
-  {  // long contexts: the splits' merge as a launch of its own (QPH_ATTN_MERGE_SEP=0: merged in-kernel, as below)
+  {  // long contexts: the splits' merge as a launch of its own from lm_splits_ splits (QPH_ATTN_MERGE_SEP: that
+     // threshold; 0: merged in-kernel everywhere)
     const char *e = getenv("QPH_ATTN_MERGE_SEP");
-    lm_min_ = e && atoi(e) == 0 ? 0 : attn_long_merge_min(hd, attn_single_, attn_split_pos_, max_chunks_);
+    lm_splits_ = e ? std::max(0, atoi(e)) : kLongMergeSplits;
+    lm_min_ = attn_long_merge_min(hd, attn_single_, attn_split_pos_, max_chunks_, lm_splits_);
     if (lm_min_ > ctx_) lm_min_ = 0;
   }
 
@@ -274,7 +276,7 @@ void HipLlama::enqueue_layer(int l) {
   at.att = att_;
   at.nh = cfg_.heads; at.nkv = cfg_.kv_heads; at.hd = cfg_.head_dim; at.max_chunks = max_chunks_; at.counters = counters_;
   at.single_max = attn_single_; at.split_pos = attn_split_pos_; at.status = dstatus_; at.spin_limit = attn_spin_;
-  at.force_late = attn_force_late_; at.merge_sep = lm_;
+  at.force_late = attn_force_late_; at.merge_sep = lm_ ? lm_splits_ : 0;
   if (fuse_ && awo_rows_) {   // every group's attention and whole wo rows + residual in one launch
     AwoArgs w{}; w.wo = ly.wo; w.x = x_;
     QPH_CK(launch_attn_wo_rows(at, w, st_));
@@ -839,7 +841,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         AttnArgs t{}; t.q = q_; t.q16 = q16_; t.ctx = ctx_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         t.max_chunks = max_chunks_; t.counters = counters_; t.single_max = attn_single_; t.split_pos = attn_split_pos_;
-        t.status = dstatus_; t.spin_limit = attn_spin_; t.stamps = stamps; t.merge_sep = lm_min_ > 0 && pos_ + 1 >= lm_min_;
+        t.status = dstatus_; t.spin_limit = attn_spin_; t.stamps = stamps; t.merge_sep = lm_min_ > 0 && pos_ + 1 >= lm_min_ ? lm_splits_ : 0;
         QPH_CK(launch_attention(t, st_)); break;
       }
       default: throw std::runtime_error("time_kernel: unknown kernel id");

@@ -61,7 +61,8 @@ class HipLlama {
   bool attn_force_late_ = false;
   // contexts of at least lm_min_ positions (every step >= 16 splits) merge the splits in a launch of their own
   // (k_attn_merge; graphs g_lm_*); 0: never (QPH_ATTN_MERGE_SEP=0, or too few splits for the context window)
-  int lm_min_ = 0;
+  int lm_min_ = 0, lm_splits_ = 0;
+  static constexpr int kLongMergeSplits = 16;
   bool lm_ = false;   // the step being enqueued is such a step
   int pos_ = 0;
   unsigned slot_ = 0;
