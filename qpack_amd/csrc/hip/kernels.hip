@@ -1055,7 +1055,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
     for (int i = 0; i < NL; i++) {
       const int p = threadIdx.x + NT * i, lr = p / PPR, c16 = p % PPR;
       const int row = lr < R ? r0 + lr : r0;   // past the tile: row r0 (< d: chunks are never empty), not used
-      wr[i] = *(const uint4 *)(wq + (size_t)row * cols + 16 * c16);
+      wr[i] = ld16(wq + (size_t)row * cols + 16 * c16);
     }
   };
   attn_split<HD, REP, true>(a, g, 0, 1, 1, ao, issue);
@@ -1220,7 +1220,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo_rows(AttnArgs a, 
     for (int i = 0; i < NL; i++) {
       const int p = threadIdx.x + NT * i, lr = p / ppr, c16 = p % ppr;
       const int row = lr < R ? r0 + lr : r0;   // past the tile: row r0 (chunks are never empty), not used
-      wr[i] = *(const uint4 *)(wq + (size_t)row * cols + 16 * c16);
+      wr[i] = ld16(wq + (size_t)row * cols + 16 * c16);
     }
   };
   bool last = false;
