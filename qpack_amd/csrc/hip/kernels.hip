@@ -98,7 +98,10 @@ __device__ __forceinline__ void unit_rows(const MvArgs &a, int u, int cols, cons
 // fp32 chains, scales and stores run after the loop, one lane per (unit, row).
 template <int PRO, int EPI, int NS, int KIND, bool DBG>
 __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
-  constexpr int D = 8 / NS;
+  // ring slots per wave (a slot: one 1 KiB chunk of each of the unit's NS rows); measured with the nontemporal weight
+  // loads, same box, C3 / C5 greedy tok/s: 8 / NS 486 / 480, 6 / NS 494 / 499, (4, 2) 510 / 519, (3, 2) 513 / 525,
+  // (2, 2) 512 / 524, (3, 1) 499 / 517 - more loads in flight per wave only queue behind each other
+  constexpr int D = NS == 1 ? 3 : 2;
   extern __shared__ __align__(16) char smem[];
   const int WAVES = (int)blockDim.x >> 6;
   const int cols = a.m[0].cols, G = cols / 32, nb = cols / kQB;
