@@ -416,8 +416,11 @@ static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
   }
   const int units = a.seg_tile0[a.nseg], cus = g_mv_config.cus;
   const int upc = (units + cus - 1) / cus;
-  int w = upc <= 16 ? upc : 16;
-  if (upc > 16) for (int c = 16; c >= 4; c--) if (upc % c == 0) { w = c; break; }
+  // at most 8 waves per workgroup for gate / up and the head, 16 for the rest (same-box sweep, C3 greedy: 16
+  // everywhere 513.9 tok/s, 8 for gate / up and head 521.7, 12 for all 521.1, 6 or 4 for gate / up and head ~467)
+  constexpr int WM = EPI == EPI_SWIGLU || EPI == EPI_ARGMAX ? 8 : 16;
+  int w = upc <= WM ? upc : WM;
+  if (upc > WM) for (int c = WM; c >= 4; c--) if (upc % c == 0) { w = c; break; }
   int u = (upc + w - 1) / w;                                        // units per wave
   const int cols = a.m[0].cols;
   if (cols / kQB > 2 * w * 8) { w = 16; u = (upc + 15) / 16; }     // the prologue covers 2 x (threads / 8) blocks
