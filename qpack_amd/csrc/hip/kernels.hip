@@ -197,9 +197,11 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
             B = __builtin_amdgcn_udot4(ww.z ^ 0x80808080u, l.z, B, false);
             B = __builtin_amdgcn_udot4(ww.w ^ 0x80808080u, l.w, B, false);
             const int p = sum8_i(A * 256 + (int)B);
-            if (act && (lane & 7) == 0) {
+            if (act && (lane & 7) == 0) {   // the block sum, as the float the chain takes (DBG: the int, for the hook)
               const int b = cc * 8 + (lane >> 3);
-              wsum[(ci * NS + s) * av.nbp + b] = p - 128 * av.lsum[b];
+              const int isum = p - 128 * av.lsum[b];
+              if (DBG) wsum[(ci * NS + s) * av.nbp + b] = isum;
+              else ((float *)wsum)[(ci * NS + s) * av.nbp + b] = (float)isum;
             }
           }
         } else if (isq1) {
@@ -311,19 +313,24 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
     if (live) {
       if (isq8) {
         const int *ss = wsum + (u * NS + s) * av.nbp;
+        const float *sf = (const float *)ss;
         float ch = 0.f;   // rows_q8's block order; LDS read 16 blocks at a time so the chain is not latency-bound
         int b = 0;
         for (; b + 16 <= nb; b += 16) {
-          int4 sv[4]; float4 bv[4];
-#pragma unroll
-          for (int q = 0; q < 4; q++) { sv[q] = *(const int4 *)(ss + b + 4 * q); bv[q] = *(const float4 *)(av.bs + b + 4 * q); }
+          float4 sv[4], bv[4];
 #pragma unroll
           for (int q = 0; q < 4; q++) {
-            ch = __builtin_fmaf(bv[q].x, (float)sv[q].x, ch); ch = __builtin_fmaf(bv[q].y, (float)sv[q].y, ch);
-            ch = __builtin_fmaf(bv[q].z, (float)sv[q].z, ch); ch = __builtin_fmaf(bv[q].w, (float)sv[q].w, ch);
+            if (DBG) { const int4 t = *(const int4 *)(ss + b + 4 * q); sv[q] = make_float4((float)t.x, (float)t.y, (float)t.z, (float)t.w); }
+            else sv[q] = *(const float4 *)(sf + b + 4 * q);
+            bv[q] = *(const float4 *)(av.bs + b + 4 * q);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            ch = __builtin_fmaf(bv[q].x, sv[q].x, ch); ch = __builtin_fmaf(bv[q].y, sv[q].y, ch);
+            ch = __builtin_fmaf(bv[q].z, sv[q].z, ch); ch = __builtin_fmaf(bv[q].w, sv[q].w, ch);
           }
         }
-        for (; b < nb; b++) ch = __builtin_fmaf(av.bs[b], (float)ss[b], ch);
+        for (; b < nb; b++) ch = __builtin_fmaf(av.bs[b], DBG ? (float)ss[b] : sf[b], ch);
         v = ch * sc_pre;
         if (DBG && a.dbg_sums && og.seg == 0 && row < og.rows)
           for (int b = 0; b < nb; b++) a.dbg_sums[(size_t)row * nb + b] = ss[b];
