@@ -94,7 +94,7 @@ class HipLlama {
   void topk_to_host(int M, int *idx, float *val);
   hipGraphExec_t g_state_ = nullptr, g_logits_ = nullptr, g_greedy_ = nullptr;
   // decode attention fused with wo (launch_attn_wo) for contexts up to awo_max_ positions (0: not used) and its graphs
-  static constexpr int kAwoMaxDefault = 1024;
+  static constexpr int kAwoMaxDefault = 640;   // beyond, split attention + wo is faster (same-box greedy, C3)
   int awo_max_ = 0, awo_rc_ = 0;
   bool awo_rows_ = false;   // the fused kernel is k_attn_wo_rows (every group per workgroup, whole rows, x += y)
   bool fuse_ = false;   // enqueue_layer: the fused kernel (set around a capture or a direct enqueue)
