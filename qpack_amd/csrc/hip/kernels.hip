@@ -7,9 +7,9 @@
 //     w . q = 256 (w . h) + (w + 128) . l - 128 sum(l)   (q8)     nib . q = 256 (nib . h) + nib . l   (q4, nib = q + 8)
 //     Every int32 accumulator is therefore exact and equal to the reference's _mm256_madd_epi16 sums.
 //   - Weights stream once, coalesced: lane i of a wave reads bytes [16 i, 16 i + 16) of each 1 KiB row chunk.
-//   - q8: the eight lanes of a 128-column block are summed with DPP; the block sums go to LDS and one lane per row
-//     replays rows_q8's float epilogue in block order (acc = fma(bs[b], (float)isum, acc); y = acc * scale, kernels_x86.cpp:
-//     57-69), so q8 rows are bit-identical to the reference given the same activation.
+//   - q8: the eight lanes of a 128-column block are summed with DPP; the block sums go to LDS as (float)isum and one
+//     lane per row replays rows_q8's float epilogue in block order (acc = fma(bs[b], (float)isum, acc); y = acc * scale,
+//     kernels_x86.cpp:57-69), so q8 rows are bit-identical to the reference given the same activation.
 //   - q4: one lane owns one 32-column group (16 bytes); per-group exact int32 sums, fma with f16(scale) * bs in the lane,
 //     then a fixed-order wave reduction (float order differs from rows_q4's 8-lane split: within the logit tolerance).
 // The prologue optionally fuses RMSNorm (PRO_NORM); epilogues fuse bias, residual add, SwiGLU and the argmax partials.
