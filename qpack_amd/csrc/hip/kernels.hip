@@ -767,13 +767,16 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
       }
     bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
     bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+    // e^(x - mn) as the hardware exp2 of (x - mn) log2(e) (v_exp_f32, one instruction against ~20 for expf; the
+    // default order's attention is held to the logit tolerance - the reference-order kernels keep glibc's expf)
+    constexpr float kL2E = 1.44269504088896340736f;
     const float mn = fmaxf(m, bm);
-    const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+    const float corr = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m - mn) * kL2E);
     float rs = 0.f;
     h8 ph, pl;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const float pv = sv[j] == -INFINITY ? 0.f : expf(sv[j] - mn);
+      const float pv = sv[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sv[j] - mn) * kL2E);
       rs += pv;
       const _Float16 h = (_Float16)pv;
       ph[j] = h; pl[j] = (_Float16)(pv - (float)h);
