@@ -1341,9 +1341,12 @@ hipError_t launch_attn_wo_rows(const AttnArgs &a, AwoArgs w, hipStream_t st) {
 }
 
 // ------------------------------------------------------------------ greedy pick
-__global__ __launch_bounds__(kThreads) void k_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens) {
+// embed (optional, greedy runs): the chosen token's embedding row also goes to x - the next step's input, so the
+// next greedy step needs no embedding launch of its own
+__global__ __launch_bounds__(kThreads) void k_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, DMat embed,
+                                                            float *x) {
   constexpr int NW = kThreads / kWave;
-  __shared__ float bv_s[NW]; __shared__ int bi_s[NW];
+  __shared__ float bv_s[NW]; __shared__ int bi_s[NW]; __shared__ int tok_s;
   float bv = -INFINITY; int bi = 0x7fffffff;
   for (int i = threadIdx.x; i < n; i += kThreads) {
     const float v = amax[i].x; const int idx = __builtin_bit_cast(int, amax[i].y);
@@ -1361,10 +1364,17 @@ __global__ __launch_bounds__(kThreads) void k_argmax_finish(const float2 *amax, 
     int t = bi_s[0]; if (t == 0x7fffffff) t = 0;
     out_tokens[ctl->n_out] = t;
     ctl->tok = t; ctl->pos = ctl->pos + 1; ctl->n_out = ctl->n_out + 1;
+    tok_s = t;
+  }
+  if (x) {
+    __syncthreads();
+    embed_row(embed, tok_s, x, threadIdx.x, kThreads);
   }
 }
-hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st) {
-  hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(kThreads), 0, st, amax, n, ctl, out_tokens);
+hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st, const DMat *embed,
+                                float *x) {
+  hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(kThreads), 0, st, amax, n, ctl, out_tokens, embed ? *embed : DMat{},
+                     embed ? x : nullptr);
   return hipGetLastError();
 }
 

@@ -152,7 +152,9 @@ hipError_t launch_attn_wo_rows(const AttnArgs &a, AwoArgs w, hipStream_t st);
 // dst[0..n16) = src[0..n16) in 16-byte words (counter calibration)
 hipError_t launch_copy(const void *src, void *dst, size_t n16, hipStream_t st);
 
-hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st);
+// embed / x (optional): also write the chosen token's embedding row to x (the next greedy step's input)
+hipError_t launch_argmax_finish(const float2 *amax, int n, Ctl *ctl, int *out_tokens, hipStream_t st,
+                                const DMat *embed = nullptr, float *x = nullptr);
 
 // ---- batched prompt path (prefill.hip)
 // embeddings of B token ids (device array) into X[B][ldx]

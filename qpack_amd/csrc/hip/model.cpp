@@ -324,8 +324,10 @@ void HipLlama::enqueue_head() {
 
 // one decode step in the current arithmetic order: parts 0 = layers, 1 = + output head (logits), 2 = + greedy pick
 // (ctl advances on the device)
+// parts 2 (greedy): the step starts from x already embedded (by the previous greedy step's argmax launch, or by
+// greedy_run / time_greedy before the first) and ends by embedding its own token for the next one
 void HipLlama::enqueue_step(int parts) {
-  QPH_CK(launch_embed(embed_, ctl_, x_, st_));
+  if (parts < 2) QPH_CK(launch_embed(embed_, ctl_, x_, st_));
   for (int l = 0; l < cfg_.layers; l++) {
     if (order_) ex_enqueue_layer(l);
     else enqueue_layer(l);
@@ -334,7 +336,7 @@ void HipLlama::enqueue_step(int parts) {
     if (order_) ex_enqueue_head();
     else enqueue_head();
   }
-  if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_));
+  if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_, &embed_, x_));
 }
 
 hipGraphExec_t HipLlama::capture(int parts, bool fused, bool long_merge) {
@@ -582,6 +584,7 @@ int HipLlama::greedy_run(int tok, int n, int *out) {
   if (n <= 0) return 0;
   if (tok < 0 || tok >= cfg_.vocab) throw std::runtime_error("token id out of range");
   write_ctl(tok, pos_);
+  QPH_CK(launch_embed(embed_, ctl_, x_, st_));   // the first step's input; each step embeds the next one's
   for (int i = 0; i < n; i++) run_step(2, pos_ + i);
   QPH_CK(hipMemcpyAsync(htok_, out_tok_, 4ull * n, hipMemcpyDeviceToHost, st_));
   { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
@@ -764,6 +767,7 @@ float HipLlama::time_greedy(int tok, int n) {
   QPH_CK(hipEventCreate(&e0)); QPH_CK(hipEventCreate(&e1));
   write_ctl(tok, pos_);
   QPH_CK(hipEventRecord(e0, st_));
+  QPH_CK(launch_embed(embed_, ctl_, x_, st_));   // the first step's input; each step embeds the next one's
   for (int i = 0; i < n; i++) run_step(2, pos_ + i);
   QPH_CK(hipEventRecord(e1, st_));
   QPH_CK(hipEventSynchronize(e1)); check_status();
