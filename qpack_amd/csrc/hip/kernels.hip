@@ -961,6 +961,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
       o[0] = st0; o[1] = st1; o[2] = st2; o[3] = __builtin_amdgcn_s_memrealtime(); o[4] = merger;
     }
   };
+  // (With AttnArgs::merge_sep - the default from 16 splits - the splits returned above and k_attn_merge merges.)
   // The last MG splits to arrive merge the S partials of the group's heads (model_llama.cpp:160-165: M = max m_c,
   // f_c = exp(m_c - M), L = sum l_c f_c, O = sum f_c o_c / L): from kAttnParMerge splits up MG = min(REP, S), head j
   // by merger j % MG, each head's loads in one round; below, the merge is short and the last arrival does it alone
@@ -1004,7 +1005,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attention(AttnArgs a) {
   stamp(1);
 }
 
-// The merge of k_attention's splits as a launch of its own (AttnArgs::merge_sep, contexts of at least kAttnParMerge
+// The merge of k_attention's splits as a launch of its own (AttnArgs::merge_sep: contexts of at least merge_sep
 // splits): workgroup (g, j) merges head j of group g over the S splits the previous launch stored - the kernel
 // boundary orders the partials before their loads, in place of the arrival counters and the mergers' wait.
 template <int HD, int REP>
