@@ -264,8 +264,8 @@ def main():
                     help="launch kernels one by one (no HIP graphs) so a profiler sees every dispatch, and run a "
                          "calibration copy of known size for the byte counters")
     ap.add_argument("--dominant", choices=sorted(DOMINANT), default="norm",
-                    help="which gate / up kernel --pmc-summary reads (the token loop runs 'sum' at contexts up to 1024 "
-                         "on q8 models whose kv groups are whole 128-column blocks)")
+                    help="which gate / up kernel --pmc-summary reads: 'norm' (PRO_NORM, what the token loop runs) or "
+                         "'sum' (PRO_NORM_SUM, run only under QPH_AWO_SUM=0)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the dominant kernel's per-launch HBM traffic from two rocprofv3 --pmc runs "
                          "(FETCH_SIZE, WRITE_SIZE) of --profile, scaled by the calibration copy; no GPU work")

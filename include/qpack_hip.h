@@ -12,6 +12,9 @@
  *   - A model is not re-entrant: one host thread per model at a time (the reference's contract; qpack-server serialises
  *     through a mutex, /root/reference/tools/qpack-server.cpp:31).  Each model owns one HIP stream on the current device.
  *   - Weights are copied into HBM by qph_create / qph_load; the caller's buffers (or the mmap) may be released afterwards.
+ *   - A call that fails because a decode attention merge timed out (its message says so) leaves the position at the
+ *     last point the model verified clean: the start of that call, or earlier when state-only steps (want = 0, which
+ *     do not wait for the device) ran since the last wait.  qph_pos() tells where; the cache from there on is invalid.
  */
 #ifndef QPACK_HIP_H
 #define QPACK_HIP_H

@@ -392,12 +392,15 @@ void HipLlama::run_step(int parts, int pos) {
   fuse_ = false; lm_ = false;
 }
 
-// Called after every wait for the stream: a decode attention merger whose bounded wait for the other splits' partials
-// ran out wrote NaN outputs and set the status word.  The split counters may then be stale, so they are cleared before
-// the error is raised; the position is left as it was (the caller may rewind and retry).
+// Called after every wait for the stream, with pos_ already counting every step enqueued so far: a decode attention
+// merger whose bounded wait for the other splits' partials ran out wrote NaN outputs and set the status word.  The split
+// counters may then be stale, so they are cleared before the error is raised.  The failed step may be any step since the
+// last clean check (state-only steps run up to 128 ahead of a wait), and every later step read its cache rows, so the
+// position goes back to where that check left it: the cache rows from there on are invalid, the rows before it are not.
 void HipLlama::check_status() {
-  if (!*(volatile int *)hstatus_) return;
+  if (!*(volatile int *)hstatus_) { clean_pos_ = pos_; return; }
   *(volatile int *)hstatus_ = 0;
+  pos_ = clean_pos_;
   QPH_CK(hipMemsetAsync(counters_, 0, 8ull * cfg_.kv_heads, st_));
   QPH_CK(hipStreamSynchronize(st_));
   throw std::runtime_error("decode attention: a split merge timed out waiting for its partials; this call's outputs are invalid");
@@ -587,9 +590,9 @@ int HipLlama::greedy_run(int tok, int n, int *out) {
   QPH_CK(launch_embed(embed_, ctl_, x_, st_));   // the first step's input; each step embeds the next one's
   for (int i = 0; i < n; i++) run_step(2, pos_ + i);
   QPH_CK(hipMemcpyAsync(htok_, out_tok_, 4ull * n, hipMemcpyDeviceToHost, st_));
+  pos_ += n;
   { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
   memcpy(out, htok_, 4ull * n);
-  pos_ += n;
   return n;
 }
 
@@ -600,7 +603,7 @@ void HipLlama::prefill_all(const int *toks, int n, float *logits) {
 
 void HipLlama::set_pos(int pos) {
   if (pos < 0 || pos > ctx_) throw std::runtime_error("position out of range");
-  pos_ = pos;
+  pos_ = pos; clean_pos_ = std::min(clean_pos_, pos);
 }
 
 void HipLlama::snapshot(uint8_t *buf, int64_t cap) {
@@ -621,7 +624,7 @@ void HipLlama::restore(const uint8_t *buf, int64_t n) {
   const uint8_t *p = buf + 4;
   for (int l = 0; l < cfg_.layers; l++)
     for (uint16_t *c : {kc_, vc_}) { QPH_CK(hipMemcpy(c + (size_t)l * ctx_ * kvd_, p, nb, hipMemcpyHostToDevice)); p += nb; }
-  pos_ = pos;
+  pos_ = pos; clean_pos_ = pos;
 }
 
 // ------------------------------------------------------------------ reference-order mode
@@ -770,10 +773,10 @@ float HipLlama::time_greedy(int tok, int n) {
   QPH_CK(launch_embed(embed_, ctl_, x_, st_));   // the first step's input; each step embeds the next one's
   for (int i = 0; i < n; i++) run_step(2, pos_ + i);
   QPH_CK(hipEventRecord(e1, st_));
+  pos_ += n;
   QPH_CK(hipEventSynchronize(e1)); check_status();
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
-  pos_ += n;
   return ms;
 }
 

@@ -4,6 +4,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -34,8 +35,11 @@ class HipLlama {
   // sampler's order (1 <= M <= min(kTopkMax, vocab))
   void step_topk(int tok, int M, int *idx, float *val);
   void prefill_topk(const int *toks, int n, int M, int *idx, float *val);
-  void reset() { pos_ = 0; }
-  bool rewind(int pos) { if (pos < 0 || pos > pos_) return false; pos_ = pos; return true; }
+  void reset() { pos_ = 0; clean_pos_ = 0; }
+  bool rewind(int pos) {
+    if (pos < 0 || pos > pos_) return false;
+    pos_ = pos; clean_pos_ = std::min(clean_pos_, pos); return true;
+  }
   void set_pos(int pos);
   int64_t snapshot_size() const { return 4 + 4ll * cfg_.layers * pos_ * kvd_; }
   void snapshot(uint8_t *buf, int64_t cap);
@@ -65,6 +69,7 @@ class HipLlama {
   static constexpr int kLongMergeSplits = 16;
   bool lm_ = false;   // the step being enqueued is such a step
   int pos_ = 0;
+  int clean_pos_ = 0;   // the position up to which every enqueued step has been checked clean (see check_status)
   unsigned slot_ = 0;
   hipStream_t st_ = nullptr;
   std::vector<void *> allocs_;

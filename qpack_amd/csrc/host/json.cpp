@@ -1,8 +1,11 @@
 #include "json.hpp"
 
+#include <charconv>
+#include <clocale>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <locale.h>
 #include <stdexcept>
 
 namespace qph {
@@ -85,7 +88,8 @@ class Reader {
   }
 
   double number() {
-    // the JSON number grammar, checked here; the conversion itself is strtod's (locale "C" digits only)
+    // the JSON number grammar, checked here; the conversion is std::from_chars, which ignores the process's locale
+    // (strtod would read "1.5" as 1 under a comma-decimal LC_NUMERIC)
     const char *s = p_;
     if (p_ < end_ && *p_ == '-') p_++;
     auto digits = [&] { const char *d = p_; while (p_ < end_ && *p_ >= '0' && *p_ <= '9') p_++; return p_ > d; };
@@ -96,7 +100,14 @@ class Reader {
       if (p_ < end_ && (*p_ == '+' || *p_ == '-')) p_++;
       if (!digits()) fail("malformed number");
     }
-    return std::strtod(std::string(s, p_).c_str(), nullptr);
+    double v = 0;
+    const auto r = std::from_chars(s, p_, v);
+    if (r.ec == std::errc::result_out_of_range) {   // overflow or underflow: strtod's result, in the "C" locale
+      static const locale_t c_loc = newlocale(LC_ALL_MASK, "C", (locale_t)0);
+      return strtod_l(std::string(s, p_).c_str(), nullptr, c_loc);
+    }
+    if (r.ec != std::errc() || r.ptr != p_) fail("malformed number");
+    return v;
   }
 
   unsigned hex4() {

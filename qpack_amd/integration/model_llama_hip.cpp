@@ -4,7 +4,13 @@
 // and is selected in load_model (/root/reference/src/model_llama.cpp:221-235) by QPACK_DEVICE=hip.
 //
 // Built and linked against the reference's own headers and sources by qpack_amd/integration/Makefile (the test
-// tests/test_integration.py), together with tools/qpack-bench.cpp.
+// tests/test_integration.py), together with tools/qpack-bench.cpp and the check harness adapter_check.cpp.
+//
+// QPACK3 files: the reference's Container decodes rANS-coded blobs on the CPU when it opens the file
+// (src/container.cpp:41, :94-121), and every reference caller needs that Container (config, tokenizer, file size), so
+// through this adapter the model is built from decoded blobs.  The GPU decoder serves callers of the C ABI that open
+// the file with qph_load and need no Container.
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <stdexcept>
@@ -13,6 +19,7 @@
 
 #include "qpack/qpack.h"
 #include "qpack_hip.h"
+#include "sampler_hip.hpp"
 
 namespace qp {
 namespace {
@@ -64,12 +71,12 @@ class LlamaHip : public Model {
       ts.push_back(q);
     }
     ck(qph_create(&k, ts.data(), (int)ts.size(), max_ctx, &m_));   // copies to HBM: `widened` may go afterwards
-    out_.resize((size_t)std::max(qph_vocab(m_), qph_hidden(m_)));
-  }
-  // a model whose file the library opened itself (qph_load: QPACK3 blobs decoded on the GPU); it has no Container
-  LlamaHip(qph_model *adopted, std::shared_ptr<Container> c) : m_(adopted) {
-    c_ = std::move(c);
-    if (c_) cfg_ = c_->config();
+    // QPACK_HIP_ORDER=reference: the reference CPU path's float order (logits bit-identical to make_llama's); the
+    // default order is the fast kernels', within the logit tolerance
+    if (const char *o = getenv("QPACK_HIP_ORDER")) {
+      if (!strcmp(o, "reference")) ck(qph_set_order(m_, 1));
+      else if (strcmp(o, "default")) { qph_destroy(m_); throw std::runtime_error("QPACK_HIP_ORDER: 'default' or 'reference'"); }
+    }
     out_.resize((size_t)std::max(qph_vocab(m_), qph_hidden(m_)));
   }
   ~LlamaHip() override { qph_destroy(m_); }
@@ -100,7 +107,17 @@ class LlamaHip : public Model {
     std::vector<uint8_t> b((size_t)n); ck(qph_snapshot(m_, b.data(), n)); return b;
   }
   void restore(const std::vector<uint8_t> &s) override { ck(qph_restore(m_, s.data(), (int64_t)s.size())); }
-  std::string arch() const override { return "llama:" + cfg_["model_type"].as_str(); }
+  // the reference's CUDA model marks its backend the same way (model_llama_cuda.cu:500)
+  std::string arch() const override { return "llama:" + cfg_["model_type"].as_str() + "@hip"; }
+
+  // the device top-M of the next logits (qph_step_topk): the candidates Sampler::dist would take from top_m
+  void step_topk(int token, int M, std::vector<std::pair<int, float>> &cand) {
+    std::vector<int> idx((size_t)M);
+    std::vector<float> val((size_t)M);
+    ck(qph_step_topk(m_, token, M, idx.data(), val.data()));
+    cand.resize((size_t)M);
+    for (int i = 0; i < M; i++) cand[(size_t)i] = {idx[(size_t)i], val[(size_t)i]};
+  }
 
  private:
   qph_model *m_ = nullptr;
@@ -113,12 +130,11 @@ std::unique_ptr<Model> make_llama_hip(std::shared_ptr<Container> c, int max_ctx)
   return std::unique_ptr<Model>(new LlamaHip(std::move(c), max_ctx));
 }
 
-// the file opened by the library (QPACK3 blobs decoded in HBM instead of by the Container); container() is then not
-// available on the model
-std::unique_ptr<Model> make_llama_hip_path(const std::string &path, int max_ctx) {
-  qph_model *m = nullptr;
-  ck(qph_load(path.c_str(), max_ctx, &m));
-  return std::unique_ptr<Model>(new LlamaHip(m, nullptr));
+bool hip_step_candidates(Model &m, int token, int M, std::vector<std::pair<int, float>> &cand) {
+  LlamaHip *h = dynamic_cast<LlamaHip *>(&m);
+  if (!h) return false;
+  h->step_topk(token, M, cand);
+  return true;
 }
 
 }  // namespace qp

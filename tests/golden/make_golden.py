@@ -9,7 +9,9 @@ the seed by the tests), a seeded prompt, and what the reference computes on it w
 (the default Model::greedy_run, /root/reference/include/qpack/qpack.h:143-149).  Stored: the greedy stream, the top-2 gap
 of every step, top-5 ids / logits of the prefill and of the first decode steps, and a fixed sample of the prefill logits
 with their float64 sum, and for every decode step a 64-bit hash of the float32 logits (blake2b of their bytes), so a
-path that claims the reference's arithmetic can be checked bit for bit at every step.
+path that claims the reference's arithmetic can be checked bit for bit at every step, plus (<cfg>_steps.npz) every decode
+step's float32 logits at a fixed sample of >= 512 ids, so a path in another float order is held to the logit tolerance
+at every step.
 
 Benchmark-shape fixtures: c3 (8B q8: 128-token prompt, 256 greedy tokens), c4 (8B q8: one 2048-token prompt; prefill
 logits plus fp16 K / V rows of three layers at five positions, c4_kv.npz, and a hash of every layer's cache) and c5
@@ -112,7 +114,8 @@ def model_fixture(name):
         body = np.frombuffer(snap, np.float16, offset=4).reshape(shape.layers, 2, n_prompt, kvd)
         np.savez_compressed(os.path.join(HERE, "c4_kv.npz"), layers=np.array(C4_LAYERS), pos=np.array(C4_POS),
                             k=body[C4_LAYERS][:, 0][:, C4_POS], v=body[C4_LAYERS][:, 1][:, C4_POS])
-    stream, gaps, tops, hashes, samples = [], [], [], [], {}
+    stream, gaps, tops, hashes, samples, step_rows = [], [], [], [], {}, []
+    step_idx = np.arange(0, V, max(1, V // 512))
     for i in range(n_gen):
         l = ref.step(tok, 1)
         s = np.sort(l)
@@ -123,6 +126,7 @@ def model_fixture(name):
             idx = np.arange(0, V, max(1, V // 512))
             samples[str(i)] = l[idx].astype(float).tolist()
             fx["step_sample_idx"] = idx.tolist()
+        step_rows.append(l[step_idx])
         tok = int(np.argmax(l))
         stream.append(tok)
     fx.update(greedy=stream, greedy_top2_gap=gaps, decode_top5=tops, step_hash=hashes, pos_after=int(ref.pos()))
@@ -139,6 +143,10 @@ def model_fixture(name):
                                  argmax=[int(np.argmax(l)) for l in la])
     if samples:
         fx["step_sample"] = samples
+    if step_rows:
+        # every decode step's logits on a fixed sample of >= 512 ids (float32, exact), for the default-order check
+        np.savez_compressed(os.path.join(HERE, f"{name}_steps.npz"), idx=step_idx.astype(np.int32),
+                            logits=np.stack(step_rows).astype(np.float32))
     ref.close()
     os.remove(path)
     with open(os.path.join(HERE, f"{name}.json"), "w") as f:

@@ -5,9 +5,11 @@ Two arithmetic orders are checked:
   - reference order (HipLlama.set_order(1)): every logits vector must be bit-identical to the reference's (a 64-bit hash
     of its float32 bytes per prompt and per decode step), every fp16 cache row too (C4, per-layer hashes), so the greedy
     stream is identical token for token: C1 128/128, C2 256/256, C3 256/256, C5 128/128;
-  - the default order (the fast kernels): prefill logits within max-abs 1e-2 / relative 1e-3 on a fixed sample, the
-    top-5 logits of every decode step within the same bound while the streams agree, and the greedy stream identical up
-    to the first step whose reference top-2 gap is below TIE = 20 x the measured logit error.  Reordering a float sum
+  - the default order (the fast kernels): prefill logits within max-abs 1e-2 / relative 1e-3 on a fixed sample, every
+    decode step's logits on a fixed sample of >= 512 ids (<name>_steps.npz) and its top-5 within the same bound while
+    the streams agree; the greedy stream identical for the first 128 tokens at C3 and C5 (no near-tie escape: their
+    reference streams' smallest top-2 gaps there, 1.6e-3 and 4.0e-3, are 3-8x what a reordered sum moves a logit by),
+    elsewhere up to the first step whose reference top-2 gap is below TIE = 20 x the measured logit error.  Reordering a float sum
     moves C1's logits by ~5e-4 (measured with the oracle's order variants, oracle.c OR_ORD_*), so near-ties narrower than
     that are decided by rounding order; the default order is held to the tolerance there and the reference order to bit
     equality.
@@ -83,9 +85,25 @@ def test_reference_order_bit_identical(name, synth):
     print(f"{name}: reference order, {n}/{n} steps bit-identical, greedy {n}/{n}", flush=True)
 
 
+# Configurations whose reference stream has no near-tie in its first N steps that reordering could flip (smallest top-2
+# gap: C3 1.6e-3 over its first 128 steps, C5 4.0e-3, against the ~5e-4 a reordered float sum moves a logit by): the
+# default order must reproduce the first N greedy tokens exactly, with no near-tie escape.
+HARD_GREEDY = {"c3": 128, "c5": 128}
+
+
+def step_samples(name):
+    """every decode step's reference logits at a fixed sample of ids (<name>_steps.npz), or None"""
+    p = os.path.join(GOLD, name + "_steps.npz")
+    if not os.path.exists(p):
+        return None
+    z = np.load(p)
+    return z["idx"], z["logits"]
+
+
 @pytest.mark.parametrize("name", SMALL + ["c1", "c2", "c3", "c5"])
 def test_default_order_within_tolerance(name, synth):
     fx = fixture(name)
+    samp = step_samples(name)
     m, lg = start(name, fx, synth, False)
     e = 0.0
     if lg is not None:
@@ -99,15 +117,15 @@ def test_default_order_within_tolerance(name, synth):
     stream, top_err = [], 0.0
     for i in range(len(fx["greedy"])):
         l = m.step(tok, 1)
-        if fx.get("step_sample") and str(i) in fx["step_sample"]:
-            ref = np.float32(fx["step_sample"][str(i)])
-            err = np.abs(l[fx["step_sample_idx"]] - ref)
-            assert np.all(err <= np.maximum(1e-2, 1e-3 * np.abs(ref))), f"step {i} logits max|d| {err.max()}"
-            e = max(e, float(err.max()))
         tok = int(np.argmax(l))
         stream.append(tok)
         if stream != fx["greedy"][:i + 1]:
             break   # past a divergence the inputs differ; the tolerance applies while the streams agree
+        if samp is not None:   # the logits on >= 512 sampled ids, every step
+            idx, rows = samp
+            err = np.abs(l[idx] - rows[i])
+            assert np.all(err <= np.maximum(1e-2, 1e-3 * np.abs(rows[i]))), f"step {i}: sampled logits max|d| {err.max()}"
+            e = max(e, float(err.max()))
         ids, vals = fx["decode_top5"][i]
         d = np.abs(l[ids] - np.float32(vals))
         assert np.all(d <= np.maximum(1e-2, 1e-3 * np.abs(np.float32(vals)))), f"step {i}: top-5 logits max|d| {d.max()}"
@@ -122,8 +140,13 @@ def test_default_order_within_tolerance(name, synth):
     first_tie = int(np.argmax(gaps < tie)) if np.any(gaps < tie) else len(gaps)
     print(f"{name}: default order: logit max|d| {max(e, top_err):.3g}, greedy agrees for {agree}/{len(ref_stream)} tokens, "
           f"first reference near-tie (gap < {tie:.3g}) at step {first_tie}", flush=True)
-    if agree < len(ref_stream) and agree < first_tie:
-        pytest.fail(f"greedy stream differs at step {agree} (reference top-2 gap there {gaps[agree]:.3g} > {tie:.3g})")
+    hard = HARD_GREEDY.get(name, 0)
+    if agree < hard:
+        pytest.fail(f"{name}: greedy agrees for {agree}/{len(ref_stream)} tokens; the first {hard} must be identical "
+                    f"(reference top-2 gap at step {agree}: {gaps[agree]:.3g})")
+    if agree < len(ref_stream) and agree < max(first_tie, hard):
+        pytest.fail(f"{name}: greedy agrees for {agree}/{len(ref_stream)} tokens: differs at step {agree} (reference "
+                    f"top-2 gap there {gaps[agree]:.3g} > {tie:.3g})")
 
 
 def c4_cache_rows(m, fx, layers, pos):

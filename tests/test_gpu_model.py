@@ -310,7 +310,8 @@ def test_files_of_the_reference_quantiser(src, args, synth, tmp_path):
 def test_attention_merge_timeout_is_an_error(synth, monkeypatch):
     """the decode attention's failure path, forced from the host (QPH_ATTN_FORCE_LATE, read at load: every merger
     that would wait gives up at once, as when its bounded wait runs out): it writes NaN and sets the status word; the
-    call raises instead of returning those outputs, the split counters are cleared, and every kernel still runs to completion (a fresh model
+    call raises instead of returning those outputs, the split counters are cleared, the position returns to the last
+    clean wait, and every kernel still runs to completion (a fresh model
     at the same context decodes normally afterwards)"""
     cfg, T = "mini_r7", 1500   # 24 splits per kv group, 7 heads per group: the parallel merge with waiting mergers
     path = synth(cfg)
@@ -328,8 +329,16 @@ def test_attention_merge_timeout_is_an_error(synth, monkeypatch):
     bad.restore(snap)
     with pytest.raises(qa.QphError, match="timed out"):
         bad.step(5, 1)
+    assert bad.pos() == T, "a failed step must leave the position where the call found it"
     with pytest.raises(qa.QphError, match="timed out"):
         bad.greedy_run(5, 4)
+    assert bad.pos() == T
+    # state-only steps run ahead of any wait: the failure surfaces at the next wait, and the position goes back to
+    # the last clean check (here the restore), not just one step
+    bad.step(5, 0); bad.step(6, 0)
+    with pytest.raises(qa.QphError, match="timed out"):
+        bad.step(7, 1)
+    assert bad.pos() == T
     bad.close()
     good = qa.HipLlama.load(path, max_ctx=T + 64)
     good.restore(snap)
