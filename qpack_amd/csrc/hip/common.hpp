@@ -25,12 +25,25 @@ struct DMat {
 };
 
 // device-resident decode control block: the token to embed, its position, and the greedy output cursor
-struct Ctl {
+struct Ctl {   // pos at byte offset 4 (ctl_pos_issue)
   int tok;
   int pos;
   int n_out;   // greedy tokens written so far in this run
   int pad;
 };
+// ctl->pos read through the scalar data cache: ctl_pos_issue sends the load, the value is valid after ctl_pos_wait.  A
+// vector load of it would return in order behind every vector load the wave issued before it, and the wave would wait
+// for all of them to learn the position.
+__device__ __forceinline__ int ctl_pos_issue(const Ctl *c) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x4" : "=s"(v) : "s"(c));
+  return v;
+}
+__device__ __forceinline__ int ctl_pos_wait(int v) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)::"memory");
+  return v;
+}
+
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
@@ -107,4 +120,14 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// direct global -> LDS loads (global_load_lds_dwordx4 / _dword): the wave's lanes land 16 (4) bytes each, contiguously
+// from the wave-uniform LDS base, in lane order; they count in vmcnt like any other load
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+__device__ __forceinline__ void dma16(const void *g, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glb_void_t *)g, (lds_void_t *)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glb_void_t *)g, (lds_void_t *)lds_wave_base, 4, 0, 0);
+}
 }  // namespace qph

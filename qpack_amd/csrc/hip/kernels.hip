@@ -295,10 +295,12 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   if (a.stamps) ts2 = __builtin_amdgcn_s_memrealtime();
   if (dm & 4) return;   // timing: no epilogue
 
-  // epilogue: lane j finishes (unit j / NS, row slot j % NS)
+  // epilogue: lane j finishes (unit j / NS, row slot j % NS); with the split chain, lanes 8 j .. 8 j + 7 do
+  const bool split = !DBG && EPI == EPI_RESID && KIND == MK_Q8 && a.split_chain && nmine * NS <= kWave / 8;
+  const int lpr = split ? 8 : 1, part = split ? lane & 7 : 0;
   float best_v = -INFINITY; int best_i = 0x7fffffff;
-  for (int j0 = 0; j0 < nmine * NS; j0 += kWave) {
-    const int j = j0 + lane, u = j / NS, s = j % NS;
+  for (int j0 = 0; j0 < nmine * NS; j0 += kWave / lpr) {
+    const int j = j0 + (split ? lane >> 3 : lane), u = j / NS, s = j % NS;
     const bool live = j < nmine * NS;
     const UnitGeo<NS> og = unit_geo<EPI, NS>(a, ub + gk + (live ? u : 0) * W, cols);
     int row = og.row[0]; const float *scl = og.sc[0];
@@ -306,11 +308,28 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
     for (int t = 1; t < NS; t++) if (s == t) { row = og.row[t]; scl = og.sc[t]; }
     float v = 0.f;
     // the row scale and the residual are loaded before the chain, so their round trips overlap it
-    const bool store = live && row < og.rows;
+    const bool store = live && row < og.rows && part == 0;
     const float sc_pre = live && isq8 ? *scl : 0.f;
     float res_pre = 0.f;
     if (EPI == EPI_RESID && store) res_pre = a.resid_in ? a.resid_in[row] : a.out[0][row];
-    if (live) {
+    if (split) {
+      // blocks [part nbk, (part + 1) nbk) chained in order (nbk: an eighth of the blocks rounded up to whole float4
+      // reads), then ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7))
+      const int nbk = ((nb + 31) >> 5) << 2, b0 = min(nb, part * nbk), b1 = min(nb, b0 + nbk);
+      const float *sf = (const float *)(wsum + ((live ? u : 0) * NS + s) * av.nbp);
+      float ch = 0.f;
+      int b = b0;
+      for (; b + 4 <= b1; b += 4) {
+        const float4 sv = *(const float4 *)(sf + b), bv = *(const float4 *)(av.bs + b);
+        ch = __builtin_fmaf(bv.x, sv.x, ch); ch = __builtin_fmaf(bv.y, sv.y, ch);
+        ch = __builtin_fmaf(bv.z, sv.z, ch); ch = __builtin_fmaf(bv.w, sv.w, ch);
+      }
+      for (; b < b1; b++) ch = __builtin_fmaf(av.bs[b], sf[b], ch);
+      ch += __shfl_xor(ch, 1, kWave);
+      ch += __shfl_xor(ch, 2, kWave);
+      ch += __shfl_xor(ch, 4, kWave);
+      v = ch * sc_pre;
+    } else if (live) {
       if (isq8) {
         const int *ss = wsum + (u * NS + s) * av.nbp;
         const float *sf = (const float *)ss;
@@ -573,8 +592,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // output and (max, sum) to a.part (waves 0 .. nact - 1 hold positions; ored rows HS floats apart)
 template <int HD, int REP, int NW, int HS>
 __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s, int S, int ys, int nact,
-                                                const float (*wm)[REP], const float (*wl)[REP], const float (*ored)[REP][HS],
-                                                float *lout) {
+                                                const float (*wm)[REP], const float (*wl)[REP], const float *ored,
+                                                int ows, float *lout) {
   __shared__ float fwv[NW][REP], mlv[REP][2];
   // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M).  Wave 0 holds every
   // (wave w, head j) pair, lane 8 w + j (NW, REP <= 8), and reduces over w with xor shuffles of 8, 16 and 32
@@ -599,7 +618,7 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int w = 0; w < nact; w++) {
       const float f = fwv[w][j];
-      const float4 x = *(const float4 *)&ored[w][j][i];
+      const float4 x = *(const float4 *)(ored + w * ows + j * HS + i);
       O.x = __builtin_fmaf(f, x.x, O.x); O.y = __builtin_fmaf(f, x.y, O.y);
       O.z = __builtin_fmaf(f, x.z, O.z); O.w = __builtin_fmaf(f, x.w, O.w);
     }
@@ -677,12 +696,15 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   constexpr int NW = kAttnMfWaves, HALF = HD / 2, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 8;   // VS: rows of 20 dwords
   constexpr int QS = HD + 4;
   __shared__ float wm[NW][REP], wl[NW][REP];
-  __shared__ __align__(16) float ored[NW][REP][QS];
   __shared__ __align__(16) uint16_t vt[NW][HD * VS];
+  // a wave's (unnormalised) output rows go into its own V tile once its block loop is done: [REP][QS] floats
+  static_assert(REP * QS * 4 <= HD * VS * 2, "the output rows fit in the wave's V tile");
+  constexpr int OWS = HD * VS / 2;   // floats between two waves' output rows
   const int kvd = a.nkv * HD;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
   MfK<HD> ka, kb;
   MfV<HD> vb;
+  const int pos_s = ctl_pos_issue(a.ctl);
   // positions past the context or the split are loaded from rows below a.ctx (in the allocation) and masked: their
   // scores become -inf and their V pieces zero
   if (ONE) {
@@ -693,15 +715,16 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   // lr (zero past REP), dims 32 k + 8 lg + 0..7
   h8 qh[KS], ql[KS];
   {
+    // only the lanes of the group's REP heads load (the other columns are zero): 16 / REP times fewer requests
     const uint16_t *qp = a.q16 + (size_t)(g * REP + (lr < REP ? lr : 0)) * HD + 8 * lg;
 #pragma unroll
     for (int k = 0; k < KS; k++) {
-      u32x4 h = *(const u32x4 *)(qp + 32 * k), lo = *(const u32x4 *)(qp + (size_t)a.nh * HD + 32 * k);
-      if (lr >= REP) h = lo = (u32x4){0u, 0u, 0u, 0u};
+      u32x4 h = (u32x4){0u, 0u, 0u, 0u}, lo = h;
+      if (lr < REP) { h = *(const u32x4 *)(qp + 32 * k); lo = *(const u32x4 *)(qp + (size_t)a.nh * HD + 32 * k); }
       qh[k] = __builtin_bit_cast(h8, h); ql[k] = __builtin_bit_cast(h8, lo);
     }
   }
-  const int pos = a.ctl->pos, T = pos + 1;
+  const int pos = ctl_pos_wait(pos_s), T = pos + 1;
   const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
   // wave w takes blocks w, w + NW, ... of the split's 32-position blocks (waves without a block idle)
   const int nblk = (t1 - t0 + kAttnMfBlk - 1) / kAttnMfBlk, nact = min(nblk, NW);
@@ -809,15 +832,17 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
     if (tb + NW * kAttnMfBlk >= t1) break;
     block(kb, ka, tb + NW * kAttnMfBlk);
   }
-  // this wave's (m, l, o) -> LDS: lane holds head lr, dims 16 d + 4 lg + i
+  // this wave's (m, l, o) -> LDS (its own V tile, free now): lane holds head lr, dims 16 d + 4 lg + i
+  float *ored = (float *)&vt[0][0];
   if (lr < REP) {
     if (lg == 0) { wm[wave][lr] = m; wl[wave][lr] = l; }
 #pragma unroll
-    for (int d = 0; d < DT; d++) *(float4 *)&ored[wave][lr][16 * d + 4 * lg] = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
+    for (int d = 0; d < DT; d++)
+      *(float4 *)(ored + wave * OWS + lr * QS + 16 * d + 4 * lg) = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
   }
   mid();
   __syncthreads();
-  attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored, lout);
+  attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored, OWS, lout);
 }
 
 // One workgroup merges every head of group g over S < kAttnParMerge splits, in one round of loads: P threads share

@@ -116,6 +116,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   // test hook: the bound of a merger's wait for the other splits (the failure path forced from the host)
   if (const char *e = getenv("QPH_ATTN_SPIN")) attn_spin_ = std::max(0, atoi(e));
   attn_force_late_ = getenv("QPH_ATTN_FORCE_LATE") != nullptr;   // test hook: the same failure without the race
+  if (const char *e = getenv("QPH_MV_SPLIT")) split_chain_ = atoi(e) != 0;
   {  // long contexts: the splits' merge as a launch of its own from lm_splits_ splits (QPH_ATTN_MERGE_SEP: that
      // threshold; 0: merged in-kernel everywhere)
     const char *e = getenv("QPH_ATTN_MERGE_SEP");
@@ -293,20 +294,20 @@ void HipLlama::enqueue_layer(int l) {
     MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
     a.part = awo_part_; a.nparts = cfg_.kv_heads; a.pstride = (size_t)cfg_.hidden; a.xsum = xs_;
     mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM_SUM, EPI_SWIGLU, a, cap, st_));
-    MvArgs b{}; b.m[0] = ly.wd; b.nseg = 1; b.x = h_; b.out[0] = x_; b.resid_in = xs_;
+    MvArgs b{}; b.m[0] = ly.wd; b.nseg = 1; b.x = h_; b.out[0] = x_; b.resid_in = xs_; b.split_chain = split_chain_;
     mv_plan(b, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, b, cap, st_));
     return;
   } else {
     QPH_CK(launch_attention(at, st_));   // RoPE, fp16 KV append, split-K attention, merge
-    MvArgs a{}; a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = x_;   // wo + residual
+    MvArgs a{}; a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = x_;   // wo + residual (one chain: k_attn_wo_rows gives the same bits)
     mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_));
   }
   {  // RMSNorm + gate / up + SwiGLU
     MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
     mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM, EPI_SWIGLU, a, cap, st_));
   }
-  {  // down + residual
-    MvArgs a{}; a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = x_;
+  {  // down + residual (the fp32 block chain split over eight lanes per row)
+    MvArgs a{}; a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = x_; a.split_chain = split_chain_;
     mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_));
   }
 }
@@ -817,9 +818,9 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
       case 0:
         a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
         mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM, EPI_SWIGLU, a, cap, st_)); break;
-      case 1:
-        a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = xn_;
-        mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); break;
+      case 1:   // as the token loop runs it: into a residual (scratch here), the block chain split
+        a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = xn_; a.split_chain = split_chain_;
+        mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_)); break;
       case 2:
         a.m[0] = ly.wq; a.m[1] = ly.wk; a.m[2] = ly.wv; a.nseg = 3; a.x = x_; a.norm_w = ly.an; a.eps = eps;
         a.out[0] = q_; a.out[1] = k_; a.out[2] = v_; a.bias[0] = ly.bq; a.bias[1] = ly.bk; a.bias[2] = ly.bv;

@@ -62,6 +62,7 @@ class HipLlama {
   int ctx_ = 0, kvd_ = 0, qd_ = 0, max_chunks_ = 1, cus_ = 256, head_grid_ = 0;
   int *counters_ = nullptr;
   int attn_single_ = 0, attn_split_pos_ = 0, attn_spin_ = 0;   // attention split policy (0: the kernel's defaults)
+  int split_chain_ = 1;   // EPI_RESID matvecs chain their fp32 block sums over 8 lanes per row (QPH_MV_SPLIT=0: one chain)
   bool attn_force_late_ = false;
   // contexts of at least lm_min_ positions (every step >= 16 splits) merge the splits in a launch of their own
   // (k_attn_merge; graphs g_lm_*); 0: never (QPH_ATTN_MERGE_SEP=0, or too few splits for the context window)

@@ -85,14 +85,6 @@ constexpr int kGM = 128, kGN = 128, kGStages = 3, kGWaves = 8;
 constexpr int kGStage = 3 * 128 * 128 + 128 * 4 + 128 * 4;   // bytes per stage
 size_t gemm_lds_bytes() { return (size_t)kGStages * kGStage; }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-__device__ __forceinline__ void dma16(const void *g, void *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((glb_void_t *)g, (lds_void_t *)lds_wave_base, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((glb_void_t *)g, (lds_void_t *)lds_wave_base, 4, 0, 0);
-}
 // LDS reads of DMA-filled stages, kept out of the compiler's sight: it cannot tell which stage a DMA fills and would
 // otherwise wait for every load in flight before each read.  The results are only valid after the explicit lgkmcnt
 // wait that takes them as operands, so no use can be scheduled before it.
