@@ -116,8 +116,8 @@ int qph_restore(qph_model *m, const uint8_t *buf, int64_t n);
 /* ---- arithmetic order (no reference counterpart: the reference has one CPU order).  mode 0 (default): this library's
  * kernels, logits within the reference's tolerance and exact int32 accumulators; mode 1: every floating-point operation
  * in the reference CPU path's order (kernels_x86.cpp, kernels.cpp:184-189, model_llama.cpp:66-201), so logits, caches
- * and greedy streams are bit-identical to qp::Llama's; slower (a verification mode).  Needs q8 / q4 layer matrices and
- * a q8 output head.  Takes effect for the next call; the cache contents are kept. */
+ * and greedy streams are bit-identical to qp::Llama's; slower (a verification mode).  Takes every layer kind (q8, q4,
+ * q1) and a q8 or q4 output head.  Takes effect for the next call; the cache contents are kept. */
 int qph_set_order(qph_model *m, int mode);
 
 /* ---- measurement (no reference counterpart: qpack-bench times with the host clock, tools/qpack-bench.cpp:40-47) */
@@ -149,8 +149,9 @@ int qph_kernel_matvec(int kind, const void *q, const void *scale, int rows, int 
 int qph_kernel_matmul(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y);
 
 /* The reference-order products of qph_set_order(1) on one matrix: every vector of the first B - B % 4 in the lane
- * order of mm_q8 / mm_q4 (kernels_x86.cpp:287-371), the others (and B == 1) in rows_q8 / rows_q4 order; bit-identical
- * to the reference's matmul() of the B vectors (kernels.cpp:97-143) without ExactBatches. */
+ * order of mm_q8 / mm_q4 (kernels_x86.cpp:287-371), the others (and B == 1) in rows_q8 / rows_q4 order; q1 (sign bits,
+ * fp16 scale per 128 columns) in row_q1_nt's order for every vector (kernels_x86.cpp:163-211); bit-identical to the
+ * reference's matmul() of the B vectors (kernels.cpp:97-143) without ExactBatches. */
 int qph_kernel_matmul_ref(int kind, const void *q, const void *scale, int rows, int cols, const float *X, int B, float *Y);
 /* The top-M selection of qph_step_topk on a host vector x[n] (parity hook; 1 <= M <= min(512, n)). */
 int qph_kernel_topk(const float *x, int n, int M, int *idx, float *val);

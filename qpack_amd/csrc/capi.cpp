@@ -304,10 +304,10 @@ int qph_kernel_matmul_ref(int kind, const void *q, const void *scale, int rows, 
   QPH_API_TRY({
     need(q, "q"); need(scale, "scale"); need(X, "X"); need(Y, "Y");
     if (rows <= 0 || B <= 0 || cols <= 0 || cols % 128) throw std::invalid_argument("matmul: rows, B > 0 and cols a positive multiple of 128 required");
-    if (kind != QPH_Q8 && kind != QPH_Q4) throw std::invalid_argument("matmul: kind must be QPH_Q8 or QPH_Q4");
+    if (kind != QPH_Q8 && kind != QPH_Q4 && kind != QPH_Q1) throw std::invalid_argument("matmul: kind must be QPH_Q8, QPH_Q4 or QPH_Q1");
     const int nb = cols / 128, G = cols / 32;
-    const size_t qb = kind == QPH_Q8 ? (size_t)rows * cols : (size_t)rows * cols / 2;
-    const size_t sb = kind == QPH_Q8 ? 4ull * rows : 2ull * rows * G;
+    const size_t qb = kind == QPH_Q8 ? (size_t)rows * cols : kind == QPH_Q4 ? (size_t)rows * cols / 2 : (size_t)rows * cols / 8;
+    const size_t sb = kind == QPH_Q8 ? 4ull * rows : kind == QPH_Q4 ? 2ull * rows * G : 2ull * rows * nb;
     std::vector<void *> bufs;
     auto alloc = [&](size_t n) { void *p = nullptr; hck(hipMalloc(&p, n), "hipMalloc"); bufs.push_back(p); return p; };
     try {
@@ -319,7 +319,7 @@ int qph_kernel_matmul_ref(int kind, const void *q, const void *scale, int rows, 
       hck(hipMemcpy(dx, X, 4ull * B * cols, hipMemcpyHostToDevice), "upload X");
       qph::PfQuantArgs qa{}; qa.x = dx; qa.ldx = cols; qa.cols = cols; qa.xh = dxh; qa.xl = dxl; qa.ldq = cols; qa.xb = dxb; qa.ldb = nb;
       hck(qph::launch_pf_quant(qph::PRO_QUANT, qa, B, nullptr), "launch quant");
-      qph::ExGemmArgs ga{}; ga.kind = kind == QPH_Q8 ? qph::MK_Q8 : qph::MK_Q4; ga.w = dq; ga.scale = (const float *)ds;
+      qph::ExGemmArgs ga{}; ga.kind = kind == QPH_Q8 ? qph::MK_Q8 : kind == QPH_Q4 ? qph::MK_Q4 : qph::MK_Q1; ga.w = dq; ga.scale = (const float *)ds;
       ga.s16 = (const uint16_t *)ds; ga.rows = rows; ga.cols = cols; ga.xh = dxh; ga.xl = dxl; ga.ldq = cols; ga.xb = dxb;
       ga.ldb = nb; ga.ntok = B; ga.mm_below = B - B % 4; ga.tt = B == 1 ? 1 : 16; ga.y = dy; ga.ldy = rows;
       hck(qph::launch_ex_gemm(ga, nullptr), "launch gemm");

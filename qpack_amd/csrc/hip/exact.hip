@@ -337,7 +337,33 @@ __device__ float ex_mm_q4(const uint8_t *q, const uint16_t *s, const int8_t *xh,
   return ex_hsum8(f);
 }
 
-// Y[t][r] (+ bias[r]; or Y[t][r] += when resid) for rows r of one q8 / q4 matrix and the batch's quantised vectors; the
+// rows_q1 / mm_q1 (kernels_x86.cpp:163-211: every q1 entry point runs row_q1_nt, so a vector's result does not depend
+// on its batch): per 128-column group, AVX2 lane l's exact sum over columns 16 i + 2 l and 16 i + 2 l + 1 (i = 0..7) of
+// (+1 for a set sign bit, -1 for a clear one) x the activation; lane = fma((float)sum, f16(scale) * bs[g], lane) in group
+// order; y = hsum(lanes).  cols % 128 == 0 (the q1 matrices this model takes)
+__device__ float ex_row_q1(const uint8_t *q, const uint16_t *s, const int8_t *xh, const int8_t *xl, const float *bs, int cols) {
+  float f[8];
+#pragma unroll
+  for (int l = 0; l < 8; l++) f[l] = 0.f;
+  for (int g = 0; g < cols / kQB; g++) {
+    const uint8_t *gb = q + 16 * g;
+    const float cb = h2f(s[g]) * bs[g];
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+      int sum = 0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int c = 16 * i + 2 * l;   // bits c and c + 1 of the group: byte c / 8, bits c % 8 and c % 8 + 1
+        const int b0 = (gb[c >> 3] >> (c & 7)) & 1, b1 = (gb[(c + 1) >> 3] >> ((c + 1) & 7)) & 1;
+        sum += (2 * b0 - 1) * ex_act(xh, xl, kQB * g + c) + (2 * b1 - 1) * ex_act(xh, xl, kQB * g + c + 1);
+      }
+      f[l] = __builtin_fmaf((float)sum, cb, f[l]);
+    }
+  }
+  return ex_hsum8(f);
+}
+
+// Y[t][r] (+ bias[r]; or Y[t][r] += when resid) for rows r of one q8 / q4 / q1 matrix and the batch's quantised vectors; the
 // vectors t < mm_below take the tiled order (mm_q8 / mm_q4), the others the row order.  A workgroup takes 256 / tt rows
 // x tt vectors (tt = 1 for a single vector).
 __global__ __launch_bounds__(256) void k_ex_gemm(ExGemmArgs a) {
@@ -350,10 +376,12 @@ __global__ __launch_bounds__(256) void k_ex_gemm(ExGemmArgs a) {
     const int8_t *w = (const int8_t *)a.w + (size_t)r * a.cols;
     const float sc = a.scale[r];
     y = t < a.mm_below ? ex_mm_q8(w, xh, xl, bs, a.cols, sc) : ex_row_q8(w, xh, xl, bs, a.cols, sc);
-  } else {
+  } else if (a.kind == MK_Q4) {
     const uint8_t *q = (const uint8_t *)a.w + (size_t)r * (a.cols / 2);
     const uint16_t *s = a.s16 + (size_t)r * (a.cols / 32);
     y = t < a.mm_below ? ex_mm_q4(q, s, xh, xl, bs, a.cols) : ex_row_q4(q, s, xh, xl, bs, a.cols);
+  } else {
+    y = ex_row_q1((const uint8_t *)a.w + (size_t)r * (a.cols / 8), a.s16 + (size_t)r * (a.cols / kQB), xh, xl, bs, a.cols);
   }
   float *out = a.y + (size_t)t * a.ldy + r;
   if (a.bias) y = y + a.bias[r];
@@ -362,9 +390,32 @@ __global__ __launch_bounds__(256) void k_ex_gemm(ExGemmArgs a) {
 }
 hipError_t launch_ex_gemm(const ExGemmArgs &a, hipStream_t st) {
   if (a.ntok <= 0 || a.rows <= 0) return hipSuccess;
-  if ((a.kind != MK_Q8 && a.kind != MK_Q4) || a.cols % kQB || (a.tt != 1 && a.tt != 16)) return hipErrorInvalidValue;
+  if ((a.kind != MK_Q8 && a.kind != MK_Q4 && a.kind != MK_Q1) || a.cols % kQB || (a.tt != 1 && a.tt != 16))
+    return hipErrorInvalidValue;
   const int rpb = 256 / a.tt;
   hipLaunchKernelGGL(k_ex_gemm, dim3((a.rows + rpb - 1) / rpb, (a.ntok + a.tt - 1) / a.tt), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// the greedy pick's per-workgroup partials from a logits vector (a head product that is not the argmax matvec): part b
+// of n holds the (largest value, lowest index among equals) of its chunk, the strict > scan of qpack.h:143-149
+__global__ __launch_bounds__(256) void k_ex_argmax_parts(const float *x, int V, float2 *amax) {
+  const int per = (V + gridDim.x - 1) / gridDim.x, i0 = blockIdx.x * per, i1 = min(V, i0 + per);
+  float bv = -INFINITY; int bi = 0x7fffffff;
+  for (int i = i0 + (int)threadIdx.x; i < i1; i += blockDim.x)
+    if (x[i] > bv || (x[i] == bv && i < bi)) { bv = x[i]; bi = i; }
+  __shared__ float sv[256]; __shared__ int si[256];
+  sv[threadIdx.x] = bv; si[threadIdx.x] = bi;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 256; k++)
+      if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
+    amax[blockIdx.x] = make_float2(bv, __builtin_bit_cast(float, bi));
+  }
+}
+hipError_t launch_ex_argmax_parts(const float *x, int V, float2 *amax, int nparts, hipStream_t st) {
+  if (V <= 0 || nparts <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_ex_argmax_parts, dim3(nparts), dim3(256), 0, st, x, V, amax);
   return hipGetLastError();
 }
 

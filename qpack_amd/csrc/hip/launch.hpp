@@ -293,6 +293,9 @@ struct ExGemmArgs {
   int resid;
 };
 hipError_t launch_ex_gemm(const ExGemmArgs &a, hipStream_t st);
+// per-workgroup (max, lowest index) partials of logits x[V] into amax[nparts] (what the argmax matvec leaves for
+// k_argmax_finish)
+hipError_t launch_ex_argmax_parts(const float *x, int V, float2 *amax, int nparts, hipStream_t st);
 // g = silu(g) * u on rows of n values
 hipError_t launch_ex_silu(float *g, const float *u, int n, int ld, int rows, hipStream_t st);
 

@@ -173,15 +173,17 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
   }
   ctl_ = (Ctl *)dalloc(sizeof(Ctl));
   out_tok_ = (int *)dalloc(4ull * (ctx_ + 1));
-  // batched prompt path: every layer matrix q8 or q4 (the int8 MFMA products; a model with q1 layers takes its prompts
-  // through decode steps); chunks of up to pf_cap_ tokens
+  // batched prompt path: every layer matrix q8 or q4 (the int8 MFMA products; in the default order a model with q1
+  // layers takes its prompts through decode steps); chunks of up to pf_cap_ tokens.  The prompt buffers are allocated
+  // either way: the reference-order prompt (k_ex_gemm, which takes q1 matrices too) uses them
   pf_ok_ = true;
   for (const Layer &ly : layers_)
     for (const DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd})
       pf_ok_ = pf_ok_ && (m->kind == MK_Q8 || m->kind == MK_Q4);
-  if (pf_ok_) {
+  {
     for (Layer &ly : layers_)
       for (DMat *m : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.wg, &ly.wu, &ly.wd}) {
+        if (!pf_ok_) break;   // the batched products' per-matrix sums: q8 / q4 models only
         if (m->kind == MK_Q8) {
           int *rs = (int *)dalloc(4ull * ws_pitch(m->rows) * (m->cols / 128));
           QPH_CK(launch_rowsum_q8((const int8_t *)m->q, m->rows, m->cols, rs, st_));
@@ -445,7 +447,8 @@ void HipLlama::prefill(const int *toks, int n, int want, float *out) {
   if (pos_ + n > ctx_) throw std::runtime_error("context window full (" + std::to_string(ctx_) + " tokens)");
   for (int i = 0; i < n; i++) if (toks[i] < 0 || toks[i] >= cfg_.vocab) throw std::runtime_error("token id out of range");
   const bool force_steps = getenv("QPH_PREFILL_STEPS") != nullptr;   // test hook: the decode-step path
-  if (n == 1 || !pf_ok_ || force_steps) {   // one token (the reference's n == 1 case) or q1 layers: decode steps
+  // one token (the reference's n == 1 case), or q1 layers in the default order: decode steps
+  if (n == 1 || (!pf_ok_ && !order_) || force_steps) {
     for (int i = 0; i < n; i++) step(toks[i], i + 1 == n ? want : 0, i + 1 == n ? out : nullptr);
     if (!want) { QPH_CK(hipStreamSynchronize(st_)); check_status(); }
     return;
@@ -637,8 +640,7 @@ void HipLlama::restore(const uint8_t *buf, int64_t n) {
 void HipLlama::set_order(int mode) {
   if (mode != 0 && mode != 1) throw std::runtime_error("order: mode must be 0 (default) or 1 (reference order)");
   if (mode == 1) {
-    if (!pf_ok_) throw std::runtime_error("order: reference order needs q8 / q4 layer matrices");
-    if (head_.kind != MK_Q8) throw std::runtime_error("order: reference order needs a q8 output head");
+    if (head_.kind != MK_Q8 && head_.kind != MK_Q4) throw std::runtime_error("order: reference order needs a q8 or q4 output head");
     if (!ex_part_) {
       ex_ncmax_ = (ctx_ + 63) / 64;
       ex_part_ = (float *)dalloc(4ull * cfg_.heads * ex_ncmax_ * (cfg_.head_dim + 2));
@@ -725,9 +727,14 @@ void HipLlama::ex_enqueue_layer(int l) {
 
 void HipLlama::ex_enqueue_head() {
   ex_norm(x_, fnorm_, xn_, 1, cfg_.hidden);
-  MvArgs a{}; a.m[0] = head_; a.nseg = 1; a.x = xn_; a.out[0] = logits_; a.amax = amax_;
-  mv_plan(a, EPI_ARGMAX);
-  QPH_CK(launch_matvec(PRO_QUANT, EPI_ARGMAX, a, head_grid_, st_));
+  if (head_.kind == MK_Q8) {   // rows_q8 (the argmax matvec's order) with the greedy pick's partials
+    MvArgs a{}; a.m[0] = head_; a.nseg = 1; a.x = xn_; a.out[0] = logits_; a.amax = amax_;
+    mv_plan(a, EPI_ARGMAX);
+    QPH_CK(launch_matvec(PRO_QUANT, EPI_ARGMAX, a, head_grid_, st_));
+  } else {   // a q4 head (--q4-head files): rows_q4's order, then the partials from the logits
+    ex_product(head_, xn_, cfg_.hidden, 1, 0, logits_, 0, nullptr, false, false);
+    QPH_CK(launch_ex_argmax_parts(logits_, cfg_.vocab, amax_, head_grid_, st_));
+  }
 }
 
 // the prompt in the reference's batches of 64 tokens (model_llama.cpp:66-130)

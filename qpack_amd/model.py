@@ -184,15 +184,15 @@ def kernel_matvec(kind, q, scale, x):
 def kernel_matmul(q, scale, X, kind=None, order=0):
     """the product's batched prefill kernels on one matrix: Y[B, rows] = X[B, cols] W^T (qph_kernel_matmul); q8 (int8
     q, f32 scale) or q4 (packed u8 q, fp16-bits scale per 32 columns); order=1: the reference-order products
-    (qph_kernel_matmul_ref)"""
-    from ._lib import QPH_Q4, QPH_Q8
+    (qph_kernel_matmul_ref), which also take kind=QPH_Q1 (sign bits [rows][cols / 8], fp16-bits scale per 128 columns)"""
+    from ._lib import QPH_Q1, QPH_Q4, QPH_Q8
     if kind is None:
         kind = QPH_Q8 if q.dtype == np.int8 else QPH_Q4
     q = np.ascontiguousarray(q)
     scale = np.ascontiguousarray(scale)
     X = np.ascontiguousarray(X, dtype=np.float32)
     rows = q.shape[0]
-    cols = q.shape[1] if kind == QPH_Q8 else 2 * q.shape[1]
+    cols = q.shape[1] if kind == QPH_Q8 else 2 * q.shape[1] if kind == QPH_Q4 else 8 * q.shape[1]
     B = X.shape[0]
     assert X.shape[1] == cols
     Y = np.empty((B, rows), np.float32)

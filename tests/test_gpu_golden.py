@@ -27,8 +27,6 @@ pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 SMALL = ["mini", "mini128", "mini_q4", "mini_q4m", "mini_q1", "mini_q1m", "mini_q4mb", "mini_q4h"]
-# q1 layers and q4 heads have no reference-order kernels (their reference orders are not on the benchmark path)
-NO_EXACT = {"mini_q1", "mini_q1m", "mini_q4h"}
 
 
 def fixture(name):
@@ -61,8 +59,6 @@ def start(name, fx, synth, exact):
 
 @pytest.mark.parametrize("name", SMALL + ["c1", "c2", "c3", "c5"])
 def test_reference_order_bit_identical(name, synth):
-    if name in NO_EXACT:
-        pytest.skip("no reference-order kernels for q1 layers / a q4 head")
     fx = fixture(name)
     m, lg = start(name, fx, synth, True)
     if lg is not None:

@@ -151,8 +151,15 @@ def test_matmul_reference_order_bit_exact(kind, rows, cols, B):
 
 
 def test_matmul_reference_order_golden():
-    """the same products on the reference's own outputs (tests/golden/kernels.npz: its matmul of 6 vectors)"""
+    """the same products on the reference's own outputs (tests/golden/kernels.npz: its matmul of 6 vectors, and its
+    matvec of one): q8, q4, and q1 (the reference order's q1 products, rows_q1 / mm_q1)"""
+    from qpack_amd._lib import QPH_Q1
     g = np.load(__file__.replace("test_gpu_kernels.py", "golden/kernels.npz"))
     for key in ("q8_48x1024", "q8_33x896", "q4_48x1024", "q4_33x896"):
         Y = qa.kernel_matmul(g[key + "_q"], g[key + "_s"], g[key + "_X"], order=1)
         np.testing.assert_array_equal(Y, g[key + "_Y"], err_msg=key)
+    for key in ("q1_48x1024", "q1_33x896"):   # cols % 128 == 0 (the q1 matrices a model takes)
+        Y = qa.kernel_matmul(g[key + "_q"], g[key + "_s"], g[key + "_X"], kind=QPH_Q1, order=1)
+        np.testing.assert_array_equal(Y, g[key + "_Y"], err_msg=key)
+        y = qa.kernel_matmul(g[key + "_q"], g[key + "_s"], g[key + "_x"][None, :], kind=QPH_Q1, order=1)
+        np.testing.assert_array_equal(y[0], g[key + "_y"], err_msg=key + " matvec")
