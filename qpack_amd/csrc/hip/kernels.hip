@@ -295,13 +295,16 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
   if (a.stamps) ts2 = __builtin_amdgcn_s_memrealtime();
   if (dm & 4) return;   // timing: no epilogue
 
-  // epilogue: lane j finishes (unit j / NS, row slot j % NS); with the split chain, lanes 8 j .. 8 j + 7 do
-  const bool split = !DBG && EPI == EPI_RESID && KIND == MK_Q8 && a.split_chain && nmine * NS <= kWave / 8;
-  const int lpr = split ? 8 : 1, part = split ? lane & 7 : 0;
+  // epilogue: lane j finishes (unit j / NS, row slot j % NS); with the split chain, lanes lpr j .. lpr j + lpr - 1 do
+  // (lpr lanes per row: 8, or 4 / 2 where the wave's rows need more lanes)
+  const int nrows = nmine * NS;
+  const bool split = !DBG && (EPI == EPI_RESID || EPI == EPI_SWIGLU) && KIND == MK_Q8 && a.split_chain && nrows <= kWave / 2;
+  const int lpr = !split ? 1 : nrows <= kWave / 8 ? 8 : nrows <= kWave / 4 ? 4 : 2;
+  const int lsh = lpr == 8 ? 3 : lpr == 4 ? 2 : lpr == 2 ? 1 : 0, part = lane & (lpr - 1);
   float best_v = -INFINITY; int best_i = 0x7fffffff;
-  for (int j0 = 0; j0 < nmine * NS; j0 += kWave / lpr) {
-    const int j = j0 + (split ? lane >> 3 : lane), u = j / NS, s = j % NS;
-    const bool live = j < nmine * NS;
+  for (int j0 = 0; j0 < nrows; j0 += kWave / lpr) {
+    const int j = j0 + (lane >> lsh), u = j / NS, s = j % NS;
+    const bool live = j < nrows;
     const UnitGeo<NS> og = unit_geo<EPI, NS>(a, ub + gk + (live ? u : 0) * W, cols);
     int row = og.row[0]; const float *scl = og.sc[0];
 #pragma unroll
@@ -313,9 +316,9 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
     float res_pre = 0.f;
     if (EPI == EPI_RESID && store) res_pre = a.resid_in ? a.resid_in[row] : a.out[0][row];
     if (split) {
-      // blocks [part nbk, (part + 1) nbk) chained in order (nbk: an eighth of the blocks rounded up to whole float4
-      // reads), then ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7))
-      const int nbk = ((nb + 31) >> 5) << 2, b0 = min(nb, part * nbk), b1 = min(nb, b0 + nbk);
+      // blocks [part nbk, (part + 1) nbk) chained in order (nbk: 1 / lpr of the blocks rounded up to whole float4
+      // reads), then the lane partials summed pairwise: ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)) for lpr 8
+      const int nbk = ((nb + 4 * lpr - 1) / (4 * lpr)) * 4, b0 = min(nb, part * nbk), b1 = min(nb, b0 + nbk);
       const float *sf = (const float *)(wsum + ((live ? u : 0) * NS + s) * av.nbp);
       float ch = 0.f;
       int b = b0;
@@ -325,9 +328,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
         ch = __builtin_fmaf(bv.z, sv.z, ch); ch = __builtin_fmaf(bv.w, sv.w, ch);
       }
       for (; b < b1; b++) ch = __builtin_fmaf(av.bs[b], sf[b], ch);
-      ch += __shfl_xor(ch, 1, kWave);
-      ch += __shfl_xor(ch, 2, kWave);
-      ch += __shfl_xor(ch, 4, kWave);
+      for (int o = 1; o < lpr; o <<= 1) ch += __shfl_xor(ch, o, kWave);
       v = ch * sc_pre;
     } else if (live) {
       if (isq8) {
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
         }
       }
     } else if (EPI == EPI_SWIGLU) {
-      const float up = __shfl_xor(v, 1, kWave);   // slot 1 (up) sits in the lane after slot 0 (gate)
+      const float up = __shfl_xor(v, lpr, kWave);   // slot 1 (up) sits in the lanes after slot 0 (gate)
       if (store && s == 0) a.out[0][row] = v / (1.f + exp_poly(0.f - v)) * up;   // silu_mul, kernels_x86.cpp:427-431
     } else if (store) {
       float *const out_seg = og.seg == 0 ? a.out[0] : (og.seg == 1 ? a.out[1] : a.out[2]);

@@ -65,9 +65,10 @@ struct MvArgs {
   const float *cos_t, *sin_t;
   const Ctl *ctl;
   uint16_t *q16[3];   // optional per segment (q): its rotated rows also as fp16 hi [rows] then lo = f16(y - hi) [rows]
-  // EPI_RESID, q8, at most 8 rows per wave (the decode step's down product): eight lanes per row each chain an eighth
-  // of the blocks, then a fixed pairwise sum - another fp32 order than rows_q8's single chain (the int32 block sums
-  // stay exact), a sixth of its dependent latency (down at the 8B shape: a 112-block chain)
+  // EPI_RESID / EPI_SWIGLU, q8, at most 32 rows per wave (the decode step's down and gate / up products): 8, 4 or 2
+  // lanes per row (as the wave's rows allow) each chain a contiguous share of the blocks, then a fixed pairwise sum -
+  // another fp32 order than rows_q8's single chain (the int32 block sums stay exact), a fraction of its dependent
+  // latency (down at the 8B shape: a 112-block chain)
   int split_chain;
 };
 

@@ -294,7 +294,7 @@ void HipLlama::enqueue_layer(int l) {
     AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_;
     QPH_CK(launch_attn_wo(at, w, st_));
     MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
-    a.part = awo_part_; a.nparts = cfg_.kv_heads; a.pstride = (size_t)cfg_.hidden; a.xsum = xs_;
+    a.part = awo_part_; a.nparts = cfg_.kv_heads; a.pstride = (size_t)cfg_.hidden; a.xsum = xs_; a.split_chain = split_chain_;
     mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM_SUM, EPI_SWIGLU, a, cap, st_));
     MvArgs b{}; b.m[0] = ly.wd; b.nseg = 1; b.x = h_; b.out[0] = x_; b.resid_in = xs_; b.split_chain = split_chain_;
     mv_plan(b, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, b, cap, st_));
@@ -306,6 +306,7 @@ void HipLlama::enqueue_layer(int l) {
   }
   {  // RMSNorm + gate / up + SwiGLU
     MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
+    a.split_chain = split_chain_;
     mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM, EPI_SWIGLU, a, cap, st_));
   }
   {  // down + residual (the fp32 block chain split over eight lanes per row)
@@ -824,6 +825,7 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
     switch (which) {
       case 0:
         a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
+        a.split_chain = split_chain_;
         mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM, EPI_SWIGLU, a, cap, st_)); break;
       case 1:   // as the token loop runs it: into a residual (scratch here), the block chain split
         a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = xn_; a.split_chain = split_chain_;
