@@ -707,8 +707,10 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   MfV<HD> vb;
   const int pos_s = ctl_pos_issue(a.ctl);
   // positions past the context or the split are loaded from rows below a.ctx (in the allocation) and masked: their
-  // scores become -inf and their V pieces zero
-  if (ONE) {
+  // scores become -inf and their V pieces zero.  ONE: the first a.early waves (all when 0) load their first block now;
+  // the host sets a.early to the blocks the step's context can need, so no wave loads a block past it
+  const bool early = ONE && (a.early <= 0 || wave < a.early);
+  if (early) {
     mf_load_k<HD>(a.kc, kvd, g, kAttnMfBlk * wave, a.ctx, lane, ka);
     mf_load_v<HD>(a.vc, kvd, g, kAttnMfBlk * wave, a.ctx, lane, vb);
   }
@@ -729,7 +731,7 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   const int t0 = (int)((int64_t)s * T / S), t1 = (int)((int64_t)(s + 1) * T / S);
   // wave w takes blocks w, w + NW, ... of the split's 32-position blocks (waves without a block idle)
   const int nblk = (t1 - t0 + kAttnMfBlk - 1) / kAttnMfBlk, nact = min(nblk, NW);
-  if (!ONE && wave < nblk) {
+  if (!early && wave < nblk) {
     mf_load_k<HD>(a.kc, kvd, g, t0 + kAttnMfBlk * wave, a.ctx, lane, ka);
     mf_load_v<HD>(a.vc, kvd, g, t0 + kAttnMfBlk * wave, a.ctx, lane, vb);
   }

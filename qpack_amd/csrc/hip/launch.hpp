@@ -117,6 +117,8 @@ struct AttnArgs {
   int *status;                 // optional (host-visible): set to 1 when a merger's bounded wait for the partials ran out
   int spin_limit;              // the bound of that wait in polls (0: 1 << 22)
   int force_late;              // test hook: every merger that would wait gives up at once (the error path, forced)
+  int early;                   // one-split kernels (k_attn_wo, k_attn_wo_rows): the waves that load their first block before
+                               // the context is known (0: all); the others load theirs, if they have one, once it is
   int merge_sep;               // > 1: contexts of at least this many splits only store their partials and a second
                                // launch (k_attn_merge, one workgroup per head) merges them
   uint64_t *stamps;            // measurement only (optional): per workgroup of k_attention 5 words - realtime at start,

@@ -244,9 +244,12 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
 
 HipLlama::~HipLlama() {
   if (st_) (void)hipStreamSynchronize(st_);
-  for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_, g_ex_state_, g_ex_logits_, g_ex_greedy_, g_fs_state_,
-                           g_fs_logits_, g_fs_greedy_, g_lm_state_, g_lm_logits_, g_lm_greedy_})
+  for (hipGraphExec_t g : {g_state_, g_logits_, g_greedy_, g_ex_state_, g_ex_logits_, g_ex_greedy_, g_lm_state_,
+                           g_lm_logits_, g_lm_greedy_})
     if (g) (void)hipGraphExecDestroy(g);
+  for (auto &set : g_fs_)
+    for (hipGraphExec_t g : set)
+      if (g) (void)hipGraphExecDestroy(g);
   for (void *p : allocs_) (void)hipFree(p);
   if (hctl_) (void)hipHostFree(hctl_);
   if (hout_) (void)hipHostFree(hout_);
@@ -279,7 +282,7 @@ void HipLlama::enqueue_layer(int l) {
   at.att = att_;
   at.nh = cfg_.heads; at.nkv = cfg_.kv_heads; at.hd = cfg_.head_dim; at.max_chunks = max_chunks_; at.counters = counters_;
   at.single_max = attn_single_; at.split_pos = attn_split_pos_; at.status = dstatus_; at.spin_limit = attn_spin_;
-  at.force_late = attn_force_late_; at.merge_sep = lm_ ? lm_splits_ : 0;
+  at.force_late = attn_force_late_; at.merge_sep = lm_ ? lm_splits_ : 0; at.early = fuse_ ? early_ : 0;
   if (fuse_ && awo_rows_) {   // every group's attention and whole wo rows + residual in one launch
     AwoArgs w{}; w.wo = ly.wo; w.x = x_;
     QPH_CK(launch_attn_wo_rows(at, w, st_));
@@ -343,9 +346,9 @@ void HipLlama::enqueue_step(int parts) {
   if (parts >= 2) QPH_CK(launch_argmax_finish(amax_, head_grid_, ctl_, out_tok_, st_, &embed_, x_));
 }
 
-hipGraphExec_t HipLlama::capture(int parts, bool fused, bool long_merge) {
+hipGraphExec_t HipLlama::capture(int parts, bool fused, bool long_merge, int early) {
   hipGraph_t g = nullptr; hipGraphExec_t ge = nullptr;
-  fuse_ = fused; lm_ = long_merge;
+  fuse_ = fused; lm_ = long_merge; early_ = early;
   QPH_CK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
   try {
     enqueue_step(parts);
@@ -372,7 +375,11 @@ void HipLlama::build_graphs() {
   g_state_ = capture(0);
   g_logits_ = capture(1);
   g_greedy_ = capture(2);
-  if (awo_max_ > 0) { g_fs_state_ = capture(0, true); g_fs_logits_ = capture(1, true); g_fs_greedy_ = capture(2, true); }
+  if (awo_max_ > 0)
+    for (int e = 1; e <= kEarlyMax; e++) {
+      if (32 * (e - 1) >= awo_max_) break;   // no fused context needs this many early blocks
+      for (int p = 0; p < 3; p++) g_fs_[e][p] = capture(p, true, false, e);
+    }
   if (lm_min_ > 0) {
     g_lm_state_ = capture(0, false, true); g_lm_logits_ = capture(1, false, true); g_lm_greedy_ = capture(2, false, true);
   }
@@ -385,15 +392,15 @@ void HipLlama::run_step(int parts, int pos) {
   const bool lm = !order_ && !fused && lm_min_ > 0 && pos + 1 >= lm_min_;
   if (use_graphs_) {
     hipGraphExec_t g = order_ ? (parts == 0 ? g_ex_state_ : parts == 1 ? g_ex_logits_ : g_ex_greedy_)
-                       : fused ? (parts == 0 ? g_fs_state_ : parts == 1 ? g_fs_logits_ : g_fs_greedy_)
+                       : fused ? g_fs_[early_for(pos)][parts]
                        : lm    ? (parts == 0 ? g_lm_state_ : parts == 1 ? g_lm_logits_ : g_lm_greedy_)
                                : (parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_);
     QPH_CK(hipGraphLaunch(g, st_));
     return;
   }
-  fuse_ = fused; lm_ = lm;
+  fuse_ = fused; lm_ = lm; early_ = fused ? early_for(pos) : 0;
   enqueue_step(parts);
-  fuse_ = false; lm_ = false;
+  fuse_ = false; lm_ = false; early_ = 0;
 }
 
 // Called after every wait for the stream, with pos_ already counting every step enqueued so far: a decode attention
@@ -839,8 +846,9 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
         a.m[0] = ly.wo; a.nseg = 1; a.x = att_; a.out[0] = xn_;
         mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_QUANT, EPI_STORE, a, cap, st_)); break;
       case 4: enqueue_head(); break;
-      case 6: {   // fused attention + wo
+      case 6: {   // fused attention + wo (QPH_AWO_EARLY: the early-load count, else the position's)
         AttnArgs t{}; t.q = q_; t.q16 = q16_; t.ctx = ctx_; t.kc = kc_; t.vc = vc_; t.ctl = ctl_;
+        t.early = getenv("QPH_AWO_EARLY") ? atoi(getenv("QPH_AWO_EARLY")) : early_for(std::min(pos_, ctx_ - 1));
         t.part = part_; t.att = att_; t.nh = cfg_.heads; t.nkv = cfg_.kv_heads; t.hd = cfg_.head_dim;
         AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_; w.x = xn_;
         if (awo_rows_) { QPH_CK(launch_attn_wo_rows(t, w, st_)); break; }

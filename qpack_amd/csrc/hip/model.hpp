@@ -108,7 +108,11 @@ class HipLlama {
   float *xs_ = nullptr;         // x + the attention block's output (written by the gate / up prologue)
   int *awo_cnt_ = nullptr;      // [row chunks] k_attn_wo arrival counters: its last arrivals add the parts to x
   bool awo_sum_ = false;        // the group parts are added by k_attn_wo (else by the gate / up prologue)
-  hipGraphExec_t g_fs_state_ = nullptr, g_fs_logits_ = nullptr, g_fs_greedy_ = nullptr;
+  // the fused graphs per early-load count e = 1..8 (the one-split attention's waves that load their first block before
+  // the context is known: ceil(context / 32) up to 8), [e][parts]
+  static constexpr int kEarlyMax = 8;
+  hipGraphExec_t g_fs_[kEarlyMax + 1][3] = {};
+  int early_ = 0;   // enqueue_layer: AttnArgs::early of the fused kernels (set with fuse_)
   hipGraphExec_t g_lm_state_ = nullptr, g_lm_logits_ = nullptr, g_lm_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
   void run_step(int parts, int pos);
@@ -145,7 +149,9 @@ class HipLlama {
   void qkv_rope(MvArgs &a, uint16_t *kc, uint16_t *vc) const;
   void enqueue_head();
   void build_graphs();
-  hipGraphExec_t capture(int parts, bool fused = false, bool long_merge = false);
+  hipGraphExec_t capture(int parts, bool fused = false, bool long_merge = false, int early = 0);
+  // the early-load count of a one-split attention at this position (pos + 1 positions)
+  static int early_for(int pos) { return std::min(kEarlyMax, (pos + 1 + 31) / 32); }
   void check_status();
   void write_ctl(int tok, int pos);
 };
