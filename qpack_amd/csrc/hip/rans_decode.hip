@@ -7,9 +7,10 @@
 //   - the decode table sits in LDS: per 12-bit slot m one word freq | (m - cum) << 16, so the state update
 //     freq * (x >> 12) + (m - cum) is one multiply-add, and the symbol in a byte table read alongside;
 //   - lanes 0..3 hold states 0..3 and decode the group of four symbols 4g .. 4g + 3 together: each lane needs 0, 1 or 2
-//     renormalisation bytes; a two-step DPP prefix sum gives each lane its byte offset in the stream, and the bytes come
-//     from an 8-byte window of the stream read (as three dwords) at the same time as the table, picked out with one
-//     byte permute;
+//     renormalisation bytes; two ballots (x < 2^23, x < 2^15) give every lane its byte offset in the stream (mbcnt of
+//     both below the lane) and the group's total (their popcount, in scalar registers for the next group's window),
+//     and the bytes come from an 8-byte window of the stream read (as three dwords) at the same time as the table,
+//     picked out with one byte permute;
 //   - the coded stream is staged in an 8 KiB LDS ring by 1 KiB coalesced loads issued one step (512 symbols) before use;
 //   - symbols collect in LDS and leave as 8-byte (bytes) or 4-byte (nibbles) stores of all 64 lanes per step.
 // The decoded bytes equal rans::decode's (bit-exact); a stream that needs a byte past its plane's end reports an
@@ -122,21 +123,22 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
       const uint32_t w0 = ring[qa >> 2], w1 = ring[(qa >> 2) + 1], w2 = ring[(qa >> 2) + 2];
       __builtin_amdgcn_sched_barrier(0);   // keep the four reads ahead of the first use: one wait for all
       uint32_t x = (e & 0xffffu) * hi_st + (e >> 16);
-      // renormalisation bytes: 2 below 2^15, 1 below 2^23 (x >= 2^11 and < 2^31 here, so clz(x) is 1 .. 20)
-      uint32_t cnt = (uint32_t)(__builtin_clz(x) - 1) >> 3;
-      bool live = true;
-      if (decltype(masked)::value) { live = lane < 4 && g + lane < ng; cnt = live ? cnt : 0u; }
-      // inclusive prefix of cnt over lanes 0..3 (row shifts fill with zeros)
-      uint32_t inc = cnt + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)cnt, 0x111, 0xf, 0xf, true);
-      inc = inc + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)inc, 0x112, 0xf, 0xf, true);
-      const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)inc, 3);
+      // renormalisation bytes: 2 below 2^15, 1 below 2^23 (x >= 2^11 and < 2^31 here).  Each count is a ballot over
+      // lanes 0..3 (the other lanes compute on their own state without effect); a lane's byte offset is the bits of
+      // both ballots below it (mbcnt), the group's total their popcount - no cross-lane chain on the state's path
+      // lanes whose state advances: 0..3, or in the step's last group those below ng - g (a scalar mask)
+      const uint64_t lm = decltype(masked)::value ? (1ull << (ng - g)) - 1ull : 0xfull;
+      const uint64_t b1 = __builtin_amdgcn_ballot_w64(x < (1u << 23)) & lm, b2 = __builtin_amdgcn_ballot_w64(x < (1u << 15)) & lm;
+      const uint32_t excl = __builtin_amdgcn_mbcnt_lo((uint32_t)b2, __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
+      const uint32_t total = (uint32_t)__builtin_popcountll(b1) + (uint32_t)__builtin_popcountll(b2);
+      const uint32_t sh8 = (x < (1u << 23) ? 8u : 0u) + (x < (1u << 15) ? 8u : 0u);
       const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh), hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
       // the lane's bytes b0 = window[excl], b1 = window[excl + 1] as b0 << 8 | b1 (v_perm selectors; 0x0c gives 0)
-      const uint32_t sel = (inc - cnt) * 0x101u + 0x0c0c0001u;
+      const uint32_t sel = excl * 0x101u + 0x0c0c0001u;
       const uint32_t be = __builtin_amdgcn_perm(hi, lo, sel);
-      const uint32_t sh8 = 8 * cnt;
       x = (x << sh8) | (be >> (16 - sh8));
-      st = live ? x : st;
+      const uint32_t keep = (uint32_t)0 - (uint32_t)((lm >> lane) & 1ull);   // all ones where the state advances
+      st = (x & keep) | (st & ~keep);
       symb[sbase + g] = (uint8_t)sy;
       q += total;
     };
