@@ -1035,7 +1035,12 @@ template <int HD>
 __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
-  constexpr int KS = HD + 8, VS = kPfKB + 8, DT = HD / 16;   // VS: transposed rows of 36 dwords (see the V stores)
+  // KS: K rows of HD / 2 + 8 dwords. A b128 LDS read serves 16 lanes a cycle from 64 banks, the 16 being four 4-lane
+  // groups of one 32-lane half with lane bit 4 = bit 2 ^ bit 3 (or its complement; measured with bank-conflict counters
+  // on gfx950); the K fragment reads below (lanes: row lr, quad lg) then cover 16 distinct bank quads per cycle, where
+  // the HD / 2 + 4 stride put rows lr and lr + 1 one quad apart and collided (3.5 conflict cycles per read).
+  // VS: transposed V rows of 36 dwords (see the V stores)
+  constexpr int KS = HD + 16, VS = kPfKB + 8, DT = HD / 16;
   constexpr int NH = kPfKB / 32, NM = kPfKB / 16;              // 32-position value steps, 16-position score tiles
   constexpr int NT = kPfAttnWaves * 64;
   constexpr int NPC = kPfKB * (HD / 8);                        // 16-byte pieces of K (and of V) per block
@@ -1105,12 +1110,17 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
   float m = -INFINITY, l = 0.f;
   const uint16_t *kg = a.kc + g * HD, *vg = a.vc + g * HD;
 
-  // piece i of a block: position (tid + NT i) / (HD / 8), dims 8 ((tid + NT i) % (HD / 8)) + 0..7; the next block's
-  // pieces are loaded while the current one is computed (named registers, not an array: a two-entry array indexed in the rolled-up loop ended in scratch)
+  // piece c = tid + NT i of a block: a wave holds 8 positions x 8 dim octets (each position's 128 bytes in 8 adjacent
+  // lanes, one cache line), HD / 64 waves side by side cover a position's dims; the next block's pieces are loaded
+  // while the current one is computed (named registers, not an array: a two-entry array indexed in the rolled-up loop
+  // ended in scratch)
   static_assert(NP == 1 || NP == 2, "one or two pieces per thread");
+  constexpr int WPO = HD / 64;   // waves per 8-position group
+  auto piece_pos = [&](int c) { return ((c >> 6) / WPO) * 8 + ((c & 63) >> 3); };
+  auto piece_dim = [&](int c) { return (((c >> 6) % WPO) * 8 + (c & 7)) * 8; };
   uint4 kr0, vr0, kr1, vr1;
   auto load_piece = [&](int pb, int i, uint4 &k, uint4 &v) {
-    const int c = tid + NT * i, pos = pb + c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+    const int c = tid + NT * i, pos = pb + piece_pos(c), d0 = piece_dim(c);
     const int pc = pos <= wg_last ? pos : wg_last;   // rows past the last one re-read it (masked out)
     k = *(const uint4 *)(kg + (size_t)pc * kvd + d0);
     v = *(const uint4 *)(vg + (size_t)pc * kvd + d0);
@@ -1119,23 +1129,24 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
     load_piece(pb, 0, kr0, vr0);
     if (NP == 2) load_piece(pb, 1, kr1, vr1);
   };
-  // K as stored; V transposed: the lane HD / 8 away holds position p ^ 1 with the same dims, the two swap halves so
-  // the even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each writes
+  // K as stored; V transposed: the lane 8 away holds position p ^ 1 with the same dims, the two swap halves so the
+  // even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each writes
   // four (p even, p odd) pairs as 32-bit words
   auto store_piece = [&](int i, const uint4 &k, const uint4 &vrr) {
-    const int c = tid + NT * i, p = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+    const int c = tid + NT * i, p = piece_pos(c), d0 = piece_dim(c);
     *(uint4 *)(ks + p * KS + d0) = k;
     const uint32_t vv[4] = {vrr.x, vrr.y, vrr.z, vrr.w};
     const bool ev = (p & 1) == 0;
-    const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, 64);
-    const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, 64);
+    const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), 8, 64);
+    const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), 8, 64);
     const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
     const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-    // dword (p / 2) of the row, XOR 2 (d0 / 16 mod 8) (even, so the pairs the reads take stay adjacent; a lane's rows
-    // d0 .. d0 + 7 share it): with 36-dword rows both these stores and the V^T fragment reads below hit 64 distinct
-    // banks per instruction (a bank model of both patterns over 32-47-dword rows and five swizzles chose it; XOR
-    // 2 (d0 / 8 mod 8) left every store 2-way conflicted)
-    const int sw = 2 * ((d0 >> 4) & 7);
+    // dword (p / 2) of the row, XOR 2 (row / 8 mod 8) (even, so the pairs the reads take stay adjacent; a lane's rows
+    // d0 .. d0 + 7 share it). gfx950 serves b32 LDS accesses 32 lanes a cycle from 32 banks and b64 ones 32 lanes a
+    // cycle from 64 banks (measured): with 36-dword rows, 8 positions x 8 octets per wave and this swizzle both these
+    // stores and the V^T fragment reads below are conflict-free; 4 positions x 16 octets per wave put a 32-lane
+    // phase's stores on 16 banks (every lane the same dword column, every address even)
+    const int sw = 2 * ((d0 >> 3) & 7);
     uint32_t *w = (uint32_t *)(vt + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ sw);
     w[0] = (lo_x & 0xffffu) | (hi_x << 16);
     w[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
@@ -1198,7 +1209,7 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
       o[d] *= corr;
       // V^T fragment of step hs: dim 16 d + lr, positions 32 hs + 4 lg + 0..3 and 32 hs + 16 + 4 lg + 0..3 (the k order
       // of ph / pl); the writes' swizzle XORs the low four bits of the dword index only
-      const int row = 16 * d + lr, sw = 2 * ((row >> 4) & 7);
+      const int row = 16 * d + lr, sw = 2 * ((row >> 3) & 7);
       const uint32_t *vr = (const uint32_t *)(vt + row * VS);
 #pragma unroll
       for (int hs = 0; hs < NH; hs++) {
