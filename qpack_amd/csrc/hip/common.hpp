@@ -110,6 +110,27 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// exchanges with lane ^ 8, ^ 16, ^ 32 as VALU instructions (__shfl_xor goes through the LDS crossbar, ds_bpermute):
+// lane ^ 8 is a DPP rotation by 8 inside each 16-lane row; the gfx950 v_permlane16_swap / v_permlane32_swap of a
+// value and a copy of it leave, in some order, the lane's own value and that of lane ^ 16 (^ 32) in the two registers -
+// a max or a sum of the two is the pair's, the same bits as with the shuffle (both operations are commutative).  The
+// swaps are written as asm: clang's builtins for them (ROCm 7.2) lost the second result once inlined (both read as the
+// first); s_nop 1 on either side covers the VALU hazards the compiler inserted itself around the builtin.
+__device__ __forceinline__ uint32_t xchg8_u32(uint32_t v) { return __builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, false); }
+__device__ __forceinline__ void swap16(float v, float &a, float &b) {
+  a = v; b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float v, float &a, float &b) {
+  a = v; b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float pair_max16(float v) { float a, b; swap16(v, a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float pair_max32(float v) { float a, b; swap32(v, a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float pair_sum16(float v) { float a, b; swap16(v, a, b); return a + b; }
+__device__ __forceinline__ float pair_sum32(float v) { float a, b; swap32(v, a, b); return a + b; }
+__device__ __forceinline__ float xchg8_f(float v) { return __builtin_bit_cast(float, xchg8_u32(__builtin_bit_cast(uint32_t, v))); }
+
 // full-wave reductions (shuffles; not on the hot inner loops)
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

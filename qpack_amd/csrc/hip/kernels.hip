@@ -604,10 +604,10 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
     const bool on = w < nact && j < REP;
     const float mw = on ? wm[w][j] : -INFINITY, lw = on ? wl[w][j] : 0.f;
     float M = mw;
-    M = fmaxf(M, __shfl_xor(M, 8, 64)); M = fmaxf(M, __shfl_xor(M, 16, 64)); M = fmaxf(M, __shfl_xor(M, 32, 64));
+    M = fmaxf(M, xchg8_f(M)); M = pair_max16(M); M = pair_max32(M);
     const float f = mw == -INFINITY ? 0.f : expf(mw - M);
     float L = lw * f;
-    L += __shfl_xor(L, 8, 64); L += __shfl_xor(L, 16, 64); L += __shfl_xor(L, 32, 64);
+    L += xchg8_f(L); L = pair_sum16(L); L = pair_sum32(L);
     if (on) fwv[w][j] = f;
     if (w == 0 && j < REP) { mlv[j][0] = M; mlv[j][1] = L; }
   }
@@ -661,10 +661,16 @@ struct MfK {   // K of one 32-position block in the A layout: [2 tiles][HD / 32]
   u32x4 k[2][KS];
 };
 template <int HD>
-struct MfV {   // V of one block: HD / 16 16-byte pieces, piece i = position (lane + 64 i) / (HD / 8)
+struct MfV {   // V of one block: HD / 16 16-byte pieces; piece i of a lane: position mfv_pos, dims mfv_dim .. + 7
   static constexpr int NV = HD / 16;
   u32x4 v[NV];
 };
+// piece i of lane l: 8 positions x 8 dim octets per piece (each position's 8 octets in 8 adjacent lanes, one 128-byte
+// line); at HD 128 pieces 2 j and 2 j + 1 hold the two halves of positions 8 j ..  The lane 8 away holds position ^ 1.
+template <int HD>
+__device__ __forceinline__ int mfv_pos(int lane, int i) { return (i / (HD / 64)) * 8 + (lane >> 3); }
+template <int HD>
+__device__ __forceinline__ int mfv_dim(int lane, int i) { return 8 * ((lane & 7) + 8 * (i % (HD / 64))); }
 // rows at or past te (the cache allocation) read row tb instead
 template <int HD>
 __device__ __forceinline__ void mf_load_k(const uint16_t *kc, int kvd, int g, int tb, int te, int lane, MfK<HD> &b) {
@@ -680,8 +686,8 @@ template <int HD>
 __device__ __forceinline__ void mf_load_v(const uint16_t *vc, int kvd, int g, int tb, int te, int lane, MfV<HD> &b) {
 #pragma unroll
   for (int i = 0; i < MfV<HD>::NV; i++) {
-    const int c = lane + 64 * i, t = tb + c / (HD / 8), tc = t < te ? t : te - 1;
-    b.v[i] = *(const u32x4 *)(vc + (size_t)tc * kvd + g * HD + 8 * (c % (HD / 8)));
+    const int t = tb + mfv_pos<HD>(lane, i), tc = t < te ? t : te - 1;
+    b.v[i] = *(const u32x4 *)(vc + (size_t)tc * kvd + g * HD + mfv_dim<HD>(lane, i));
   }
 }
 
@@ -745,21 +751,26 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   // scores from this block's K registers
   auto block = [&](MfK<HD> &kcur, MfK<HD> &knxt, int tb) {
     // V -> LDS transposed (this wave's tile).  Piece i of lane l holds position
-    // p, dims d0 .. d0 + 7; the lane HD / 8 away holds position p ^ 1, same dims.  The two swap halves so that the
+    // p, dims d0 .. d0 + 7; the lane 8 away holds position p ^ 1, same dims.  The two swap halves so that the
     // even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each writes
     // four (p even, p odd) pairs of its dims as 32-bit words.
+    // (the addresses are formed here - the empty asm keeps them in the loop: hoisted, they stayed live and spilled)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-      const int c = lane + 64 * i, p = c / (HD / 8), d0 = 8 * (c % (HD / 8));
+      const int p = mfv_pos<HD>(ln, i), d0 = mfv_dim<HD>(ln, i);
       const u32x4 vv = tb + p < t1 ? vb.v[i] : (u32x4){0u, 0u, 0u, 0u};
       const bool ev = (p & 1) == 0;
-      const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), HD / 8, kWave);
-      const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), HD / 8, kWave);
+      const uint32_t rx = xchg8_u32(ev ? vv[2] : vv[0]);
+      const uint32_t ry = xchg8_u32(ev ? vv[3] : vv[1]);
       const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];   // own dims (low / high pair)
       // word for dim pair member: (even position) | (odd position) << 16
       const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-      // dword (p / 2) XOR 2 (d0 / 8 mod 8): with 20-dword rows the stores of rows 8 apart and the fragment reads
-      // below spread over the LDS banks (the XOR is even: the position pairs stay adjacent)
+      // dword (p / 2) XOR 2 (d0 / 8 mod 8) (even: the position pairs stay adjacent).  gfx950 serves b32 LDS stores 32
+      // lanes a cycle from 32 banks and b64 reads 32 lanes a cycle from 64 banks (measured with bank-conflict
+      // counters): with 20-dword rows and 8 positions x 8 octets per piece both these stores and the fragment reads
+      // below are conflict-free (4 x 16 per piece put every 32-lane store on 16 banks)
       uint32_t *wr = (uint32_t *)(vw + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ (2 * ((d0 >> 3) & 7)));
       wr[0] = (lo_x & 0xffffu) | (hi_x << 16);
       wr[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
@@ -791,8 +802,8 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
         const float x = tb + 16 * mt + 4 * lg + i < t1 ? sc[mt][i] * scl : -INFINITY;
         sv[4 * mt + i] = x; bm = fmaxf(bm, x);
       }
-    bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+    bm = pair_max16(bm);
+    bm = pair_max32(bm);
     // e^(x - mn) as the hardware exp2 of (x - mn) log2(e) (v_exp_f32, one instruction against ~20 for expf; the
     // default order's attention is held to the logit tolerance - the reference-order kernels keep glibc's expf)
     constexpr float kL2E = 1.44269504088896340736f;
@@ -807,8 +818,8 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
       const _Float16 h = (_Float16)pv;
       ph[j] = h; pl[j] = (_Float16)(pv - (float)h);
     }
-    rs += __shfl_xor(rs, 16, kWave);
-    rs += __shfl_xor(rs, 32, kWave);
+    rs = pair_sum16(rs);
+    rs = pair_sum32(rs);
     l = l * corr + rs;
     m = mn;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1092,10 +1103,19 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
   const int g = blockIdx.x, c = blockIdx.y, d = w.wo.rows, cols = w.wo.cols;
   const int r0 = c * w.R, R = min(w.R, d - r0);
   const int8_t *wq = (const int8_t *)w.wo.q + (size_t)g * CG;
-  uint64_t t0 = 0, t1 = 0, t2 = 0;
+  uint64_t t0 = 0, t1 = 0, t2 = 0, tm = 0;
   if (w.stamps) t0 = __builtin_amdgcn_s_memrealtime();
   uint4 wr[NL];
+  // the first row of each thread (threadIdx.x < R): its scale and, for the last arrival, its residual, loaded with the
+  // tile so that they are in registers by the epilogue (loaded there, each was a memory round trip on its path)
+  const float *wsc = (const float *)w.wo.s;
+  float rsc = 0.f, xpre = 0.f;
   auto issue = [&]() {
+    if (w.stamps) tm = __builtin_amdgcn_s_memrealtime();
+    if ((int)threadIdx.x < R) {
+      rsc = wsc[r0 + threadIdx.x];
+      if (w.counters) xpre = w.x[r0 + threadIdx.x];   // this launch changes x only in the last arrival, below
+    }
 #pragma unroll
     for (int i = 0; i < NL; i++) {
       const int p = threadIdx.x + NT * i, lr = p / PPR, c16 = p % PPR;
@@ -1163,7 +1183,7 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
 #pragma unroll
     for (int b = 0; b < NBG; b++) ch = __builtin_fmaf(bsl[b], (float)isl[lr * NBG + b], ch);
     const int row = r0 + lr;
-    const float y = ch * ((const float *)w.wo.s)[row];
+    const float y = ch * (lr == (int)threadIdx.x ? rsc : wsc[row]);
     float *dst = w.part + (size_t)g * d + row;
     if (w.counters) asm volatile("global_store_dword %0, %1, off sc1" ::"v"(dst), "v"(y) : "memory");
     else *dst = y;
@@ -1197,12 +1217,12 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
 #pragma unroll
         for (int j = 1; j < kAwoMaxGroups; j++)
           if (j < ng) y += p[j];
-        w.x[row] += y;
+        w.x[row] = (lr == (int)threadIdx.x ? xpre : w.x[row]) + y;
       }
   }
   if (w.stamps && threadIdx.x == 0) {
-    uint64_t *o = w.stamps + 4 * (blockIdx.y * gridDim.x + blockIdx.x);
-    o[0] = t0; o[1] = t1; o[2] = t2; o[3] = __builtin_amdgcn_s_memrealtime();
+    uint64_t *o = w.stamps + 5 * (blockIdx.y * gridDim.x + blockIdx.x);
+    o[0] = t0; o[1] = tm; o[2] = t1; o[3] = t2; o[4] = __builtin_amdgcn_s_memrealtime();
   }
 }
 

@@ -911,10 +911,10 @@ float HipLlama::time_kernel(int which, int iters, double *bytes) {
     std::vector<uint64_t> h(5 * 4096);
     QPH_CK(hipMemcpy(h.data(), stamps, h.size() * 8, hipMemcpyDeviceToHost));
     if (FILE *f = fopen(stf, "w")) {
-      if (which == 6)
+      if (which == 6)   // start, the wo tile issued (block loops done), attention out, block sums, end
         for (int i = 0; i < cfg_.kv_heads * awo_rc_; i++)
-          fprintf(f, "%llu %llu %llu %llu\n", (unsigned long long)h[4 * i], (unsigned long long)h[4 * i + 1],
-                  (unsigned long long)h[4 * i + 2], (unsigned long long)h[4 * i + 3]);
+          fprintf(f, "%llu %llu %llu %llu %llu\n", (unsigned long long)h[5 * i], (unsigned long long)h[5 * i + 1],
+                  (unsigned long long)h[5 * i + 2], (unsigned long long)h[5 * i + 3], (unsigned long long)h[5 * i + 4]);
       else
         for (int i = 0; i < cfg_.kv_heads * max_chunks_ && 5 * i + 4 < (int)h.size(); i++)
           if (h[5 * i])

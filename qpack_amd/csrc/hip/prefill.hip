@@ -1137,8 +1137,8 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
     *(uint4 *)(ks + p * KS + d0) = k;
     const uint32_t vv[4] = {vrr.x, vrr.y, vrr.z, vrr.w};
     const bool ev = (p & 1) == 0;
-    const uint32_t rx = (uint32_t)__shfl_xor((int)(ev ? vv[2] : vv[0]), 8, 64);
-    const uint32_t ry = (uint32_t)__shfl_xor((int)(ev ? vv[3] : vv[1]), 8, 64);
+    const uint32_t rx = xchg8_u32(ev ? vv[2] : vv[0]);
+    const uint32_t ry = xchg8_u32(ev ? vv[3] : vv[1]);
     const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];
     const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
     // dword (p / 2) of the row, XOR 2 (row / 8 mod 8) (even, so the pairs the reads take stay adjacent; a lane's rows
@@ -1184,8 +1184,8 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
         const float x = (tok_ok && p <= ptok) ? sc[mt][i] : -INFINITY;
         sv[4 * mt + i] = x; bm = fmaxf(bm, x);
       }
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    bm = pair_max16(bm);
+    bm = pair_max32(bm);
     const float mn = fmaxf(m, bm);
     // exp2 of -inf is 0: masked scores need no select; a token with no valid position yet (only tokens past the
     // batch, never stored) keeps mn = -inf, replaced by 0 so no -inf - -inf appears
@@ -1200,8 +1200,8 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
       const _Float16 h = (_Float16)pv;
       ph[j / 8][j % 8] = h; pl[j / 8][j % 8] = (_Float16)(pv - (float)h);
     }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
+    rs = pair_sum16(rs);
+    rs = pair_sum32(rs);
     l = l * corr + rs;
     m = mn;
 #pragma unroll
@@ -1231,8 +1231,8 @@ __global__ __launch_bounds__(kPfAttnWaves * 64) void k_pf_attn(PfAttnArgs a) {
     for (int d = 0; d < DT; d++)
 #pragma unroll
       for (int i = 0; i < 4; i++) { v[d][i] = o[d][i] * inv; mx = fmaxf(mx, fabsf(v[d][i])); }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = pair_max16(mx);
+    mx = pair_max32(mx);
     const float isx = mx > 0 ? kActMax / mx : 0.f;
     if (lg == 0) {
       const float bs = mx / kActMax;
