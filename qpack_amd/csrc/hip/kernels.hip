@@ -700,7 +700,7 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   // LDS rows padded so the MFMA-layout accesses (16 heads / dims apart per lane) spread over the banks
-  constexpr int NW = kAttnMfWaves, HALF = HD / 2, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 8;   // VS: rows of 20 dwords
+  constexpr int NW = kAttnMfWaves, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 8;   // VS: rows of 20 dwords
   constexpr int QS = HD + 4;
   __shared__ float wm[NW][REP], wl[NW][REP];
   __shared__ __align__(16) uint16_t vt[NW][HD * VS];
