@@ -82,6 +82,8 @@ constexpr int kDppQuadXor1 = 0xb1;       // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4e;       // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;    // row_half_mirror: lane i <-> 7 - i within 8 lanes
 constexpr int kDppMirror = 0x140;        // row_mirror: lane i <-> 15 - i within 16 lanes
+constexpr int kDppRowShl4 = 0x104;       // row_shl:4: lane i reads lane i + 4 of its 16-lane row (0 past the row)
+constexpr int kDppRowRor8 = 0x128;       // row_ror:8: lane i reads lane i ^ 8 of its 16-lane row
 
 // sum over aligned groups of 8 lanes, result in every lane of the group (exact for integers)
 __device__ __forceinline__ int sum8_i(int v) {

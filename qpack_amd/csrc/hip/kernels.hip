@@ -328,7 +328,11 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
         ch = __builtin_fmaf(bv.z, sv.z, ch); ch = __builtin_fmaf(bv.w, sv.w, ch);
       }
       for (; b < b1; b++) ch = __builtin_fmaf(av.bs[b], sf[b], ch);
-      for (int o = 1; o < lpr; o <<= 1) ch += __shfl_xor(ch, o, kWave);
+      // the lane partials summed over lanes l ^ 1, l ^ 2 (quad permutations) and l + 4, which is l ^ 4 in the lanes
+      // that keep the row's value (part 0): DPP, the same sums as xor shuffles without the LDS crossbar
+      if (lpr > 1) ch += dpp_f<kDppQuadXor1>(ch);
+      if (lpr > 2) ch += dpp_f<kDppQuadXor2>(ch);
+      if (lpr > 4) ch += dpp_f<kDppRowShl4>(ch);
       v = ch * sc_pre;
     } else if (live) {
       if (isq8) {
@@ -364,7 +368,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
       const float *const bias_seg = sg == 0 ? a.bias[0] : (sg == 1 ? a.bias[1] : a.bias[2]);
       float y = v;
       if (store && bias_seg) y = y + bias_seg[row];
-      const float yo = __shfl_xor(y, 1, kWave);
+      const float yo = dpp_f<kDppQuadXor1>(y);   // the pair's other row, lane ^ 1
       const bool rope = sg == 0 ? a.rope[0] : (sg == 1 ? a.rope[1] : a.rope[2]);
       uint16_t *const cache = sg == 0 ? a.cache[0] : (sg == 1 ? a.cache[1] : a.cache[2]);
       if (store) {
@@ -383,7 +387,9 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
         }
       }
     } else if (EPI == EPI_SWIGLU) {
-      const float up = __shfl_xor(v, lpr, kWave);   // slot 1 (up) sits in the lanes after slot 0 (gate)
+      // slot 1 (up) sits lpr lanes after slot 0 (gate): lane ^ lpr for the gate lanes that store (part 0)
+      const float up = lpr == 1 ? dpp_f<kDppQuadXor1>(v) : lpr == 2 ? dpp_f<kDppQuadXor2>(v)
+                     : lpr == 4 ? dpp_f<kDppRowShl4>(v) : dpp_f<kDppRowRor8>(v);
       if (store && s == 0) a.out[0][row] = v / (1.f + exp_poly(0.f - v)) * up;   // silu_mul, kernels_x86.cpp:427-431
     } else if (store) {
       float *const out_seg = og.seg == 0 ? a.out[0] : (og.seg == 1 ? a.out[1] : a.out[2]);
