@@ -517,10 +517,12 @@ __global__ __launch_bounds__(512) void k_gemm2_q8(GemmArgs a) {
       for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   v16i T[2][2] = {{zero, zero}, {zero, zero}};
-  v4i A0[4], A1[4], f0a, f0b, f1a, f1b, w0, w1, w2, w3, x0, x1, x2, x3;
+  v4i A0[4], A1[4], w0, w1, w2, w3, x0, x1, x2, x3;
+  [[maybe_unused]] v4i f0a, f0b, f1a, f1b;   // the other schedules' fragment pairs
   [[maybe_unused]] v4i f2a, f2b;   // the staggered-halves schedule's third fragment pair
   [[maybe_unused]] v4i bq[4];   // the eighths / pairs schedules' token fragments (rolling)
-  float nb0 = 0.f, nb1 = 0.f, pb0 = 0.f, pb1 = 0.f;   // token scales of this block / of the previous one
+  float nb0 = 0.f, nb1 = 0.f, pb1 = 0.f;   // token scales of this block / of the previous one
+  [[maybe_unused]] float pb0 = 0.f;
 
   // one block per iteration: it has landed (every wave's loads: the barrier), every wave is done with the previous
   // block, whose slot now takes the next one
