@@ -127,10 +127,28 @@ __device__ __forceinline__ void swap32(float v, float &a, float &b) {
   a = v; b = v;
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
 }
+__device__ __forceinline__ int pair_sum16_i(int v) {
+  int a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return a + b;
+}
 __device__ __forceinline__ float pair_max16(float v) { float a, b; swap16(v, a, b); return fmaxf(a, b); }
 __device__ __forceinline__ float pair_max32(float v) { float a, b; swap32(v, a, b); return fmaxf(a, b); }
 __device__ __forceinline__ float pair_sum16(float v) { float a, b; swap16(v, a, b); return a + b; }
 __device__ __forceinline__ float pair_sum32(float v) { float a, b; swap32(v, a, b); return a + b; }
+
+// max / integer sum over aligned groups of 32 lanes, in every lane of the group: 8-lane steps, the row mirror, then
+// the two rows of the half
+__device__ __forceinline__ float max32_f(float v) {
+  v = max8_f(v);
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  return pair_max16(v);
+}
+__device__ __forceinline__ int sum32_i(int v) {
+  v = sum8_i(v);
+  v += dpp_i<kDppMirror>(v);
+  return pair_sum16_i(v);
+}
 __device__ __forceinline__ float xchg8_f(float v) { return __builtin_bit_cast(float, xchg8_u32(__builtin_bit_cast(uint32_t, v))); }
 
 // full-wave reductions (shuffles; not on the hot inner loops)

@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "act.hpp"
 #include "launch.hpp"
@@ -597,10 +598,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // the waves of a split -> its [m, l, o]: S == 1 writes the normalised heads to a.att, otherwise the unnormalised
 // output and (max, sum) to a.part (waves 0 .. nact - 1 hold positions; ored rows HS floats apart)
-template <int HD, int REP, int NW, int HS>
+// S == 1 with an Epi other than AttnNoEpi: epi(j, i, v) takes the normalised dims i .. i + 3 of head j instead of
+// the store (thread e takes column e: REP * HD / 4 threads, whole 32-lane groups per 128 columns)
+struct AttnNoEpi { __device__ void operator()(int, int, float4) const {} };
+template <int HD, int REP, int NW, int HS, typename Epi = AttnNoEpi>
 __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s, int S, int ys, int nact,
                                                 const float (*wm)[REP], const float (*wl)[REP], const float *ored,
-                                                int ows, float *lout) {
+                                                int ows, float *lout, const Epi &epi = Epi()) {
   __shared__ float fwv[NW][REP], mlv[REP][2];
   // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M).  Wave 0 holds every
   // (wave w, head j) pair, lane 8 w + j (NW, REP <= 8), and reduces over w with xor shuffles of 8, 16 and 32
@@ -632,8 +636,13 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
     const float M = mlv[j][0], L = mlv[j][1];
     if (S == 1) {
       const float li = 1.f / L;
-      float *dst = lout ? lout + j * HD + i : a.att + (size_t)(g * REP + j) * HD + i;
-      *(float4 *)dst = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
+      const float4 y = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
+      if constexpr (!std::is_same<Epi, AttnNoEpi>::value) {
+        epi(j, i, y);
+      } else {
+        float *dst = lout ? lout + j * HD + i : a.att + (size_t)(g * REP + j) * HD + i;
+        *(float4 *)dst = y;
+      }
     } else {
       // coherent (sc1) stores: the merging workgroup may sit on another XCD, and this avoids an L2 writeback; the
       // caller's s_waitcnt vmcnt(0) before the arrival counter covers them.
@@ -701,8 +710,9 @@ __device__ __forceinline__ void mf_load_v(const uint16_t *vc, int kvd, int g, in
 // partials are in LDS, before their merge (the block loop's registers are free by then).  ONE: S == 1 is known before
 // the position is: each wave's first block (positions 32 w ..) is loaded before ctl->pos arrives.
 struct AttnNoMid { __device__ void operator()() const {} };
-template <int HD, int REP, bool ONE = false, typename Mid = AttnNoMid>
-__device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float *lout = nullptr, const Mid &mid = Mid()) {
+template <int HD, int REP, bool ONE = false, typename Mid = AttnNoMid, typename Epi = AttnNoEpi>
+__device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float *lout = nullptr, const Mid &mid = Mid(),
+                           const Epi &epi = Epi()) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   // LDS rows padded so the MFMA-layout accesses (16 heads / dims apart per lane) spread over the banks
@@ -862,7 +872,7 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   }
   mid();
   __syncthreads();
-  attn_wave_merge<HD, REP, NW, QS>(a, g, s, S, ys, nact, wm, wl, ored, OWS, lout);
+  attn_wave_merge<HD, REP, NW, QS, Epi>(a, g, s, S, ys, nact, wm, wl, ored, OWS, lout, epi);
 }
 
 // One workgroup merges every head of group g over S < kAttnParMerge splits, in one round of loads: P threads share
@@ -1100,7 +1110,6 @@ template <int HD, int REP, int NL>
 __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoArgs w) {
   constexpr int NT = kAttnMfWaves * 64, CG = REP * HD, PPR = CG / 16, NBG = CG / kQB;
   static_assert(CG % kQB == 0, "a group's columns are whole quantisation blocks");
-  __shared__ __align__(16) float ao[REP * HD];
   __shared__ __align__(16) int8_t xh[CG];
   __shared__ __align__(16) uint8_t xl[CG];
   __shared__ float bsl[NBG];
@@ -1129,41 +1138,29 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
       wr[i] = ld16(wq + (size_t)row * cols + 16 * c16);
     }
   };
-  attn_split<HD, REP, true>(a, g, 0, 1, 1, ao, issue);
-  __syncthreads();
-  if (w.stamps) t1 = __builtin_amdgcn_s_memrealtime();
-  if (threadIdx.x < 8 * NBG) {   // eight lanes per block, 16 columns each (act_build's arithmetic)
-    const int b = threadIdx.x >> 3, sub = threadIdx.x & 7, c0 = b * kQB + sub * 16;
-    float v[16];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const float4 t = *(const float4 *)(ao + c0 + 4 * k);
-      v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
-    }
-    float m = 0;
-#pragma unroll
-    for (int k = 0; k < 16; k++) m = fmaxf(m, fabsf(v[k]));
-    m = max8_f(m);
+  // the merge hands each thread 4 normalised dims; a 128-column block is 32 lanes, which quantise it with
+  // quant_rows' arithmetic (act_build's expressions: max |v| over the block, isx = 32767 / max, q = rint(v isx),
+  // planes hi = q >> 8 and lo = q & 255, the block's sum of lo) straight into the planes the products read
+  auto quant = [&](int j, int i, float4 v) {
+    const int c0 = j * HD + i, b = c0 / kQB;
+    const float m = max32_f(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float isx = m > 0 ? kActMax / m : 0.f;
-    if (sub == 0) bsl[b] = m / kActMax;
-    uint32_t hw[4], lw[4]; int ls = 0;
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t hh = 0, ll = 0; int ls = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      uint32_t hh = 0, ll = 0;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int q = (int)__builtin_rintf(v[4 * k + j] * isx);
-        hh |= (uint32_t)((q >> 8) & 0xff) << (8 * j);
-        ll |= (uint32_t)(q & 0xff) << (8 * j);
-        ls += q & 0xff;
-      }
-      hw[k] = hh; lw[k] = ll;
+      const int q = (int)__builtin_rintf(vv[k] * isx);
+      hh |= (uint32_t)((q >> 8) & 0xff) << (8 * k);
+      ll |= (uint32_t)(q & 0xff) << (8 * k);
+      ls += q & 0xff;
     }
-    *(uint4 *)(xh + c0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    *(uint4 *)(xl + c0) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    ls = sum8_i(ls);
-    if (sub == 0) lsl[b] = ls;
-  }
+    *(uint32_t *)(xh + c0) = hh;
+    *(uint32_t *)(xl + c0) = ll;
+    ls = sum32_i(ls);
+    if ((c0 & (kQB - 1)) == 0) { bsl[b] = m / kActMax; lsl[b] = ls; }
+  };
+  attn_split<HD, REP, true, decltype(issue), decltype(quant)>(a, g, 0, 1, 1, nullptr, issue, quant);
+  if (w.stamps) t1 = __builtin_amdgcn_s_memrealtime();
   __syncthreads();
   const int lane = threadIdx.x & 63;
 #pragma unroll
