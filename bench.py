@@ -244,6 +244,28 @@ def qpack3_cpu_decode(path3, threads):
     return time.perf_counter() - t, sum(r for _, _, r in tasks)
 
 
+def graph_timeline(path):
+    """Summary of the per-launch lines QPH_GRAPH_STAMPS writes for the last replayed decode step: kernel name, earliest
+    wave start and latest wave end in 100 MHz realtime ticks, in launch order."""
+    rows = [l.split() for l in open(path) if l.strip()]
+    names = [r[0] for r in rows]
+    t = [(int(r[1]) / 100.0, int(r[2]) / 100.0) for r in rows]   # us
+    span = t[-1][1] - t[0][0]
+    per, gaps = {}, {}
+    for i, (n, (b, e)) in enumerate(zip(names, t)):
+        per.setdefault(n, []).append(e - b)
+        if i + 1 < len(t):
+            gaps.setdefault(n + "->" + names[i + 1], []).append(t[i + 1][0] - e)
+    busy = sum(e - b for b, e in t)
+    mean = lambda v: round(sum(v) / len(v), 2)
+    return {"launches": len(rows), "span_us": round(span, 1), "kernel_us": round(busy, 1),
+            "kernel_frac": round(busy / span, 4),
+            "kernel_mean_us": {n: mean(v) for n, v in per.items()},
+            "gap_mean_us": {n: mean(v) for n, v in gaps.items()},
+            "note": "last timed step, replayed from its HIP graph: first wave start to last wave end of every stamped "
+                    "launch (the matvecs and k_attn_wo; embedding and argmax finish are not stamped)"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -266,6 +288,10 @@ def main():
     ap.add_argument("--dominant", choices=sorted(DOMINANT), default="norm",
                     help="which gate / up kernel --pmc-summary reads: 'norm' (PRO_NORM, what the token loop runs) or "
                          "'sum' (PRO_NORM_SUM, run only under QPH_AWO_SUM=0)")
+    ap.add_argument("--graph-timeline", metavar="FILE",
+                    help="capture the decode graphs with per-launch realtime stamps (QPH_GRAPH_STAMPS) and add the "
+                         "last timed step's launches - per-kernel in-kernel time and the gaps between launches - to "
+                         "the line as graph_timeline (the raw per-launch lines go to FILE)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the dominant kernel's per-launch HBM traffic from two rocprofv3 --pmc runs "
                          "(FETCH_SIZE, WRITE_SIZE) of --profile, scaled by the calibration copy; no GPU work")
@@ -284,6 +310,11 @@ def main():
         return
     if a.profile:
         os.environ["QPH_NO_GRAPH"] = "1"
+    if a.graph_timeline:
+        if a.profile:
+            print("bench.py: --graph-timeline needs the graphs (drop --profile)", file=sys.stderr)
+            sys.exit(2)
+        os.environ["QPH_GRAPH_STAMPS"] = a.graph_timeline
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); the multi-GPU sharding plan is "
               "documented as a design, not built", file=sys.stderr)
@@ -324,6 +355,11 @@ def main():
     step_gbs = sb / (ms / 1e3 / a.steps) / 1e9
     log(f"decode: {a.steps} tokens in {ms:.2f} ms (HIP events), wall {wall * 1e3:.2f} ms -> {tok_s:.1f} tok/s, "
         f"{step_gbs:.0f} GB/s algorithmic ({100 * step_gbs / HBM_PEAK_GBS:.1f}% of peak)")
+    timeline = None
+    if a.graph_timeline:   # written by the timed time_greedy; later models load without the hook
+        timeline = graph_timeline(a.graph_timeline)
+        os.environ.pop("QPH_GRAPH_STAMPS", None)
+        log(f"graph timeline: {json.dumps(timeline)}")
 
     if a.profile:
         calibration_copy()
@@ -450,6 +486,8 @@ def main():
         "qpack3_load": qpack3,
         "cpu_baseline": cpu,
     }
+    if timeline:
+        out["graph_timeline"] = timeline
     print(json.dumps(out), flush=True)
 
 

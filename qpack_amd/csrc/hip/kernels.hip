@@ -465,6 +465,7 @@ static hipError_t launch_mv_t(MvArgs a, int grid_cap, hipStream_t st) {
   if (grid > grid_cap) return hipErrorInvalidValue;
   // a wave may own one unit more than u when the grid rounds: size the per-wave LDS for ceil(units / waves)
   const int waves = grid * w;
+  if (a.stamps && a.stamp_waves > 0 && waves > a.stamp_waves) a.stamps = nullptr;
   a.upw = (units + waves - 1) / waves;
   if (KIND == MK_MIX) {
     // q8 segments first: their units [0, u8) go to the first w8 waves, w8 in proportion to their bytes

@@ -54,6 +54,7 @@ struct MvArgs {
   const float *part; int nparts; size_t pstride; float *xsum;
   int plan_only;   // launch_matvec checks the launch (shape, LDS) and returns without enqueueing it
   uint64_t *stamps;   // measurement only (optional): per wave 4 realtime stamps (start, prologue done, loop done, end)
+  int stamp_waves;    // with stamps: the waves they have room for (0: any); a larger launch runs without stamps
   const float *resid_in;   // EPI_RESID: the residual input when it is not out[0]
   // EPI_STORE (q / k / v of the decode step; needs 2-row units): segment s with rope[s] pairs rows i and i + hd / 2 of
   // each head in a unit and rotates them after the bias (model_llama.cpp:176: a' = fma(a, cos, -(b sin)),

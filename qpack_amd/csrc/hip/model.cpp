@@ -276,6 +276,7 @@ void HipLlama::enqueue_layer(int l) {
     MvArgs a{}; a.m[0] = ly.wq; a.m[1] = ly.wk; a.m[2] = ly.wv; a.nseg = 3; a.x = x_; a.norm_w = ly.an; a.eps = eps;
     a.out[0] = q_; a.out[1] = k_; a.out[2] = v_; a.bias[0] = ly.bq; a.bias[1] = ly.bk; a.bias[2] = ly.bv;
     qkv_rope(a, kc, vc);
+    a.stamps = gst_take("qkv", kGstWaves, 4, 0, 3); a.stamp_waves = kGstWaves;
     mv_plan(a, EPI_STORE); QPH_CK(launch_matvec(PRO_NORM, EPI_STORE, a, cap, st_));
   }
   AttnArgs at{}; at.q = q_; at.q16 = q16_; at.ctx = ctx_; at.kc = kc; at.vc = vc; at.ctl = ctl_; at.part = part_;
@@ -290,6 +291,7 @@ void HipLlama::enqueue_layer(int l) {
     // attention and the wo product per kv group in one launch; each row chunk's last workgroup adds the group parts
     // to the residual stream
     AwoArgs w{}; w.wo = ly.wo; w.part = awo_part_; w.x = x_; w.counters = awo_cnt_;
+    w.stamps = gst_take("attn_wo", cfg_.kv_heads * awo_rc_, 5, 0, 4);
     QPH_CK(launch_attn_wo(at, w, st_));
   } else if (fuse_) {
     // RoPE, fp16 KV append, attention and the wo product per kv group in one launch; the group partials are added to
@@ -310,10 +312,12 @@ void HipLlama::enqueue_layer(int l) {
   {  // RMSNorm + gate / up + SwiGLU
     MvArgs a{}; a.m[0] = ly.wg; a.m[1] = ly.wu; a.nseg = 2; a.x = x_; a.norm_w = ly.fn; a.eps = eps; a.out[0] = h_;
     a.split_chain = split_chain_;
+    a.stamps = gst_take("gate_up", kGstWaves, 4, 0, 3); a.stamp_waves = kGstWaves;
     mv_plan(a, EPI_SWIGLU); QPH_CK(launch_matvec(PRO_NORM, EPI_SWIGLU, a, cap, st_));
   }
   {  // down + residual (the fp32 block chain split over eight lanes per row)
     MvArgs a{}; a.m[0] = ly.wd; a.nseg = 1; a.x = h_; a.out[0] = x_; a.split_chain = split_chain_;
+    a.stamps = gst_take("down", kGstWaves, 4, 0, 3); a.stamp_waves = kGstWaves;
     mv_plan(a, EPI_RESID); QPH_CK(launch_matvec(PRO_QUANT, EPI_RESID, a, cap, st_));
   }
 }
@@ -325,6 +329,7 @@ void HipLlama::enqueue_layers() {
 
 void HipLlama::enqueue_head() {
   MvArgs a{}; a.m[0] = head_; a.nseg = 1; a.x = x_; a.norm_w = fnorm_; a.eps = cfg_.rms_eps; a.out[0] = logits_; a.amax = amax_;
+  a.stamps = gst_take("head", kGstWaves, 4, 0, 3); a.stamp_waves = kGstWaves;
   mv_plan(a, EPI_ARGMAX);
   QPH_CK(launch_matvec(PRO_NORM, EPI_ARGMAX, a, head_grid_, st_));
 }
@@ -349,12 +354,13 @@ void HipLlama::enqueue_step(int parts) {
 hipGraphExec_t HipLlama::capture(int parts, bool fused, bool long_merge, int early) {
   hipGraph_t g = nullptr; hipGraphExec_t ge = nullptr;
   fuse_ = fused; lm_ = long_merge; early_ = early;
+  gst_off_ = 0; gst_cur_.clear(); gst_capturing_ = gst_ != nullptr;
   QPH_CK(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
   try {
     enqueue_step(parts);
-    fuse_ = false; lm_ = false;
+    fuse_ = false; lm_ = false; gst_capturing_ = false;
   } catch (...) {
-    fuse_ = false; lm_ = false;
+    fuse_ = false; lm_ = false; gst_capturing_ = false;
     (void)hipStreamEndCapture(st_, &g);
     if (g) (void)hipGraphDestroy(g);
     throw;
@@ -362,7 +368,39 @@ hipGraphExec_t HipLlama::capture(int parts, bool fused, bool long_merge, int ear
   QPH_CK(hipStreamEndCapture(st_, &g));
   QPH_CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
   QPH_CK(hipGraphDestroy(g));
+  if (gst_) gst_graphs_.emplace_back(ge, gst_cur_);
   return ge;
+}
+
+uint64_t *HipLlama::gst_take(const char *name, int n, int stride, int first, int last) {
+  if (!gst_capturing_ || gst_off_ + (size_t)n * stride > gst_cap_) return nullptr;
+  gst_cur_.push_back({name, gst_off_, n, stride, first, last});
+  uint64_t *p = gst_ + gst_off_;
+  gst_off_ += (size_t)n * stride;
+  return p;
+}
+
+void HipLlama::gst_write(const char *path) {
+  const std::vector<GStamp> *recs = nullptr;
+  for (const auto &g : gst_graphs_) if (g.first == gst_last_) recs = &g.second;
+  if (!recs || recs->empty()) return;
+  const GStamp &e = recs->back();
+  std::vector<uint64_t> h(e.off + (size_t)e.n * e.stride);
+  QPH_CK(hipMemcpy(h.data(), gst_, h.size() * 8, hipMemcpyDeviceToHost));
+  FILE *f = fopen(path, "w");
+  if (!f) return;
+  // one line per launch in enqueue order: kernel, earliest start, latest end (100 MHz realtime ticks; units that did
+  // not run, with a zero start, are left out)
+  for (const GStamp &r : *recs) {
+    uint64_t t0 = ~0ull, t1 = 0;
+    for (int u = 0; u < r.n; u++) {
+      const uint64_t a = h[r.off + (size_t)u * r.stride + r.first], b = h[r.off + (size_t)u * r.stride + r.last];
+      if (!a) continue;
+      t0 = std::min(t0, a); t1 = std::max(t1, b);
+    }
+    if (t1) fprintf(f, "%s %llu %llu\n", r.name, (unsigned long long)t0, (unsigned long long)t1);
+  }
+  fclose(f);
 }
 
 void HipLlama::build_graphs() {
@@ -372,6 +410,11 @@ void HipLlama::build_graphs() {
   // the first replay) while direct launches of the same kernels profile normally.
   const char *prof = getenv("ROCP_TOOL_LIBRARIES");
   if ((ng && atoi(ng) > 0) || (prof && *prof)) { use_graphs_ = false; return; }
+  if (getenv("QPH_GRAPH_STAMPS")) {   // measurement hook: one step's launches, each its own region
+    gst_cap_ = (size_t)(4 * cfg_.layers + 2) * 4 * kGstWaves;
+    gst_ = (uint64_t *)dalloc(gst_cap_ * 8);
+    QPH_CK(hipMemset(gst_, 0, gst_cap_ * 8));
+  }
   g_state_ = capture(0);
   g_logits_ = capture(1);
   g_greedy_ = capture(2);
@@ -396,6 +439,7 @@ void HipLlama::run_step(int parts, int pos) {
                        : lm    ? (parts == 0 ? g_lm_state_ : parts == 1 ? g_lm_logits_ : g_lm_greedy_)
                                : (parts == 0 ? g_state_ : parts == 1 ? g_logits_ : g_greedy_);
     QPH_CK(hipGraphLaunch(g, st_));
+    gst_last_ = g;
     return;
   }
   fuse_ = fused; lm_ = lm; early_ = fused ? early_for(pos) : 0;
@@ -793,6 +837,7 @@ float HipLlama::time_greedy(int tok, int n) {
   QPH_CK(hipEventSynchronize(e1)); check_status();
   float ms = 0; QPH_CK(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0); (void)hipEventDestroy(e1);
+  if (const char *gp = getenv("QPH_GRAPH_STAMPS")) if (gst_) gst_write(gp);
   return ms;
 }
 

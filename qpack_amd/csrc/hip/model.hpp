@@ -116,6 +116,18 @@ class HipLlama {
   hipGraphExec_t g_lm_state_ = nullptr, g_lm_logits_ = nullptr, g_lm_greedy_ = nullptr;
   bool use_graphs_ = true;   // QPH_NO_GRAPH=1: enqueue the kernels directly (profilers that cannot trace graph launches)
   void run_step(int parts, int pos);
+  // QPH_GRAPH_STAMPS=file (measurement hook): the graphs are captured with a realtime-stamp region per matvec and
+  // k_attn_wo launch, and time_greedy writes the last replayed step's launches (kernel, first start, last end) to file
+  struct GStamp { const char *name; size_t off; int n, stride, first, last; };
+  static constexpr int kGstWaves = 16384;   // stamp room per matvec launch (waves; its launches have at most ~4K)
+  uint64_t *gst_ = nullptr;
+  size_t gst_off_ = 0, gst_cap_ = 0;
+  bool gst_capturing_ = false;
+  std::vector<GStamp> gst_cur_;
+  std::vector<std::pair<hipGraphExec_t, std::vector<GStamp>>> gst_graphs_;
+  hipGraphExec_t gst_last_ = nullptr;
+  uint64_t *gst_take(const char *name, int n, int stride, int first, int last);
+  void gst_write(const char *path);
   // reference-order mode (exact.hip)
   int order_ = 0, ex_ncmax_ = 0;
   float *ex_qr_ = nullptr, *ex_part_ = nullptr, *ex_u_ = nullptr, *ex_xn_ = nullptr;

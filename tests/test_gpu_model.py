@@ -420,3 +420,25 @@ def test_fused_attention_wo(cfg, synth, monkeypatch):
         np.testing.assert_array_equal(m.greedy_run(tok, 40), o)
         m.close()
     orc.close()
+
+
+@pytest.mark.gpu
+def test_graph_timeline_hook(synth, monkeypatch, tmp_path):
+    """QPH_GRAPH_STAMPS: the graphs are captured with per-launch realtime stamps and time_greedy writes the last
+    replayed step's launches (4 per layer and the head, in launch order, each ending after it starts and starting
+    no earlier than the previous one started), without changing the tokens."""
+    path = synth("mini")
+    ref = qa.HipLlama.load(path, max_ctx=128)
+    want = ref.greedy_run(5, 12)
+    out = tmp_path / "tl.txt"
+    monkeypatch.setenv("QPH_GRAPH_STAMPS", str(out))
+    m = qa.HipLlama.load(path, max_ctx=128)
+    m.time_greedy(5, 12)
+    rows = [l.split() for l in out.read_text().splitlines()]
+    names = [r[0] for r in rows]
+    assert names == ["qkv", "attn_wo", "gate_up", "down"] * m.config.layers + ["head"], names
+    t = [(int(r[1]), int(r[2])) for r in rows]
+    assert all(b < e for b, e in t)
+    assert all(t[i + 1][0] >= t[i][0] for i in range(len(t) - 1))
+    m.rewind(0); ref.rewind(0)
+    assert list(m.greedy_run(5, 12)) == list(want)
