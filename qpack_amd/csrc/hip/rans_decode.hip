@@ -4,8 +4,9 @@
 // A coded plane is one sequential stream: its four interleaved states share one byte stream, so symbol i + 1's bytes
 // start where symbol i's end and a plane decodes in order.  The parallelism is across planes (16 MiB chunks of large
 // blobs, the blobs themselves), so the kernel runs one wave per plane and spends that wave on the plane's latency chain:
-//   - the decode table sits in LDS: per 12-bit slot m one word freq | (m - cum) << 16, so the state update
-//     freq * (x >> 12) + (m - cum) is one multiply-add, and the symbol in a byte table read alongside;
+//   - the decode table sits in LDS: per 12-bit slot m the frequency and m - cum as two 16-bit entries, so the state
+//     update freq * (x >> 12) + (m - cum) is one multiply-add on the two loaded values, and the symbol in a byte table
+//     read alongside;
 //   - lanes 0..3 hold states 0..3 and decode the group of four symbols 4g .. 4g + 3 together: each lane needs 0, 1 or 2
 //     renormalisation bytes; two ballots (x < 2^23, x < 2^15) give every lane its byte offset in the stream (mbcnt of
 //     both below the lane) and the group's total (their popcount, in scalar registers for the next group's window),
@@ -32,7 +33,7 @@ constexpr int kRansAhead = 4096;   // a refill is issued while fewer bytes than 
 
 __device__ __forceinline__ uint32_t rd_u8(const uint8_t *p) { return *p; }
 __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, int *status) {
-  __shared__ uint32_t tab[rans::kProbScale];             // slot m: freq | (m - cum) << 16
+  __shared__ uint16_t tfq[rans::kProbScale], tbi[rans::kProbScale];   // slot m: freq, m - cum
   __shared__ uint8_t tsym[rans::kProbScale];             // slot m: symbol
   __shared__ uint32_t ring[kRansRing / 4 + 4];           // + a copy of the first 16 bytes, so a window never wraps
   __shared__ __align__(16) uint8_t symb[kRansStep + 64];
@@ -74,7 +75,8 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
     int s = lo;
     for (uint32_t m = m0; m < m0 + 64; m++) {
       while (cum[s + 1] <= m) s++;
-      tab[m] = (cum[s + 1] - cum[s]) | ((m - cum[s]) << 16);
+      tfq[m] = (uint16_t)(cum[s + 1] - cum[s]);   // <= 4096
+      tbi[m] = (uint16_t)(m - cum[s]);
       tsym[m] = (uint8_t)s;
     }
   }
@@ -118,11 +120,11 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
       const uint32_t qa = (uint32_t)q & (kRansRing - 4), sh = (uint32_t)q & 3u;
       const uint32_t m = st & (rans::kProbScale - 1), hi_st = st >> rans::kProbBits;
       // table entry, symbol and stream window (bytes q .. q + 7 within three dwords) are read together
-      const uint32_t e = tab[m];
+      const uint32_t fq = tfq[m], bi = tbi[m];
       const uint32_t sy = tsym[m];
       const uint32_t w0 = ring[qa >> 2], w1 = ring[(qa >> 2) + 1], w2 = ring[(qa >> 2) + 2];
       __builtin_amdgcn_sched_barrier(0);   // keep the four reads ahead of the first use: one wait for all
-      uint32_t x = (e & 0xffffu) * hi_st + (e >> 16);
+      uint32_t x = fq * hi_st + bi;   // freq <= 2^12 (16-bit load), x >> 12 < 2^20: one 24-bit multiply-add
       // renormalisation bytes: 2 below 2^15, 1 below 2^23 (x >= 2^11 and < 2^31 here).  Each count is a ballot over
       // lanes 0..3 (the other lanes compute on their own state without effect); a lane's byte offset is the bits of
       // both ballots below it (mbcnt), the group's total their popcount - no cross-lane chain on the state's path
@@ -137,8 +139,12 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
       const uint32_t sel = excl * 0x101u + 0x0c0c0001u;
       const uint32_t be = __builtin_amdgcn_perm(hi, lo, sel);
       x = (x << sh8) | (be >> (16 - sh8));
-      const uint32_t keep = (uint32_t)0 - (uint32_t)((lm >> lane) & 1ull);   // all ones where the state advances
-      st = (x & keep) | (st & ~keep);
+      if (decltype(masked)::value) {   // lanes past the group keep their state
+        const uint32_t keep = (uint32_t)0 - (uint32_t)((lm >> lane) & 1ull);
+        st = (x & keep) | (st & ~keep);
+      } else {
+        st = x;   // lanes 4..63 advance their own (unused) state: every index they form stays in range
+      }
       symb[sbase + g] = (uint8_t)sy;
       q += total;
     };
