@@ -107,9 +107,10 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     layers_.push_back(ly);
   }
   rans_.run(st_, &rans_tm_);   // QPACK3: every coded blob decodes in HBM in one launch
-  // context splits per kv group: one per 64 positions of the full context, at most 64 (the kernel activates
-  // min(this, ceil(T / 64)) of them beyond one workgroup's reach)
-  max_chunks_ = std::max(1, std::min(64, (ctx_ + 63) / 64));
+  // context splits per kv group: one per 64 positions of the full context, at most 48 (the kernel activates
+  // min(this, ceil(T / 64)) of them beyond one workgroup's reach).  At C5's 16K context 48 splits beat 64: fewer
+  // partials for the merge launch outweigh the idle CUs (same-box greedy 546.8 -> 550.8 tok/s; 40: 538.9, 56: 548.6)
+  max_chunks_ = std::max(1, std::min(48, (ctx_ + 63) / 64));
   if (const char *e = getenv("QPH_ATTN_SPLITS")) max_chunks_ = std::max(1, std::min(64, atoi(e)));
   if (const char *e = getenv("QPH_ATTN_SINGLE")) attn_single_ = std::max(0, atoi(e));
   if (const char *e = getenv("QPH_ATTN_SPLIT_POS")) attn_split_pos_ = std::max(0, atoi(e));
