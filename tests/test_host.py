@@ -159,3 +159,29 @@ def test_config_json_reader(tmp_path):
     _container(p, [("manifest.json", man), ("config.json", b'{"arch": "lfm2"}')])
     with pytest.raises(qa.QphError, match="not a Llama-family model"):
         qa.HipLlama.load(p)
+
+
+def test_bench_graph_timeline_summary(tmp_path):
+    """bench.py's graph_timeline(): per-kernel mean in-kernel time (first start to last end, 100 MHz ticks -> us), the
+    mean gap between consecutive launches by kernel pair, and the share of the span inside launches."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench", os.path.join(os.path.dirname(__file__), "..", "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    # two layers and the head: qkv 0-700, attn 800-1700, gate_up 1850-3800, down 3950-5200, then again, head
+    rows, t = [], 0
+    for _ in range(2):
+        for name, dur, gap in (("qkv", 700, 100), ("attn_wo", 900, 150), ("gate_up", 1950, 150), ("down", 1250, 150)):
+            rows.append((name, t, t + dur)); t += dur + gap
+    rows.append(("head", t, t + 8000))
+    p = tmp_path / "tl.txt"
+    p.write_text("".join(f"{n} {a} {b}\n" for n, a, b in rows))
+    s = bench.graph_timeline(str(p))
+    assert s["launches"] == 9
+    assert s["kernel_mean_us"] == {"qkv": 7.0, "attn_wo": 9.0, "gate_up": 19.5, "down": 12.5, "head": 80.0}
+    assert s["gap_mean_us"] == {"qkv->attn_wo": 1.0, "attn_wo->gate_up": 1.5, "gate_up->down": 1.5,
+                                "down->qkv": 1.5, "down->head": 1.5}
+    span = (rows[-1][2] - rows[0][1]) / 100.0
+    busy = sum(b - a for _, a, b in rows) / 100.0
+    assert s["span_us"] == round(span, 1) and s["kernel_us"] == round(busy, 1)
+    assert s["kernel_frac"] == round(busy / span, 4)
