@@ -1193,36 +1193,55 @@ __global__ __launch_bounds__(kAttnMfWaves * 64) void k_attn_wo(AttnArgs a, AwoAr
     else *dst = y;
   }
   if (w.counters) {
-    // the last of the chunk's nkv workgroups to arrive adds the groups' parts to the residual stream:
+    // the last of the nkv groups to arrive adds their parts to the residual stream:
     // x[row] += ((p_0 + p_1) + ...) + p_{nkv-1}.  The parts went through to memory (coherent stores, drained before the
     // counter bump) and are read back with coherent loads; the last arrival resets the counter for the next launch.
-    __shared__ int last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int n = __hip_atomic_fetch_add(w.counters + c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = n == (int)gridDim.x - 1;
-      if (last) __hip_atomic_store(w.counters + c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (last)
-      for (int lr = threadIdx.x; lr < R; lr += NT) {
-        const int row = r0 + lr, ng = (int)gridDim.x;
-        float p[kAwoMaxGroups];
+    // With one row per thread (R <= NT) the arrivals are per wave - counter [c][wave] for rows [64 wave, 64 wave + 64)
+    // of the chunk - so no workgroup barrier sits between a wave's stores and its hand-off; else per workgroup.
+    auto add_parts = [&](int lr, float xp) {
+      const int row = r0 + lr, ng = (int)gridDim.x;
+      float p[kAwoMaxGroups];
 #pragma unroll
-        for (int j = 0; j < kAwoMaxGroups; j++) {   // clamped in range; unused ones are not summed
-          const float *src = w.part + (size_t)(j < ng ? j : 0) * d + row;
-          asm volatile("global_load_dword %0, %1, off sc1" : "=v"(p[j]) : "v"(src));
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < kAwoMaxGroups; j++) asm volatile("" : "+v"(p[j]));   // used only after the wait
-        float y = p[0];
-#pragma unroll
-        for (int j = 1; j < kAwoMaxGroups; j++)
-          if (j < ng) y += p[j];
-        w.x[row] = (lr == (int)threadIdx.x ? xpre : w.x[row]) + y;
+      for (int j = 0; j < kAwoMaxGroups; j++) {   // clamped in range; unused ones are not summed
+        const float *src = w.part + (size_t)(j < ng ? j : 0) * d + row;
+        asm volatile("global_load_dword %0, %1, off sc1" : "=v"(p[j]) : "v"(src));
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < kAwoMaxGroups; j++) asm volatile("" : "+v"(p[j]));   // used only after the wait
+      float y = p[0];
+#pragma unroll
+      for (int j = 1; j < kAwoMaxGroups; j++)
+        if (j < ng) y += p[j];
+      w.x[row] = xp + y;
+    };
+    if (R <= NT) {
+      const int wv = threadIdx.x >> 6;
+      if (64 * wv < R) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part stores have completed
+        int *cnt = w.counters + c * kAttnMfWaves + wv;
+        int n = 0;
+        if (lane == 0) n = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        n = __builtin_amdgcn_readfirstlane(n);
+        if (n == (int)gridDim.x - 1) {
+          if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if ((int)threadIdx.x < R) add_parts(threadIdx.x, xpre);
+        }
+      }
+    } else {
+      __shared__ int last;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int *cnt = w.counters + c * kAttnMfWaves;
+        const int n = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = n == (int)gridDim.x - 1;
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (last)
+        for (int lr = threadIdx.x; lr < R; lr += NT) add_parts(lr, lr == (int)threadIdx.x ? xpre : w.x[r0 + lr]);
+    }
   }
   if (w.stamps && threadIdx.x == 0) {
     uint64_t *o = w.stamps + 5 * (blockIdx.y * gridDim.x + blockIdx.x);

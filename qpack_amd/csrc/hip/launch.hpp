@@ -138,8 +138,9 @@ struct AwoArgs {
   DMat wo;      // q8 [d][nh * hd]
   float *part;  // [nkv][d] per-group partial products
   float *x;     // k_attn_wo_rows, and k_attn_wo with counters: the residual stream [d] (x += wo . att)
-  int *counters;   // k_attn_wo: [row chunks] arrival counters, zero before the first launch (each launch leaves them
-                   // zero); when set, the chunk's last workgroup adds the group parts to x, else the next kernel does
+  int *counters;   // k_attn_wo: [row chunks][8] arrival counters (per wave of the chunk's rows, or [c][0] per
+                   // workgroup), zero before the first launch (each launch leaves them zero); when set, the last
+                   // arrival adds the group parts to x, else the next kernel does
   int R;        // rows per chunk (set by the launcher)
   uint64_t *stamps;   // measurement only (optional): per workgroup realtime at start, after the attention, after the
                       // weights arrived, at the end

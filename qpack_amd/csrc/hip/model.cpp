@@ -162,8 +162,8 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
       awo_rc_ = rc;
       awo_part_ = (float *)dalloc(4ull * nkv * d);
       xs_ = (float *)dalloc(4ull * d);
-      awo_cnt_ = (int *)dalloc(4ull * rc);
-      QPH_CK(hipMemset(awo_cnt_, 0, 4ull * rc));
+      awo_cnt_ = (int *)dalloc(4ull * rc * 8);   // [row chunk][wave]
+      QPH_CK(hipMemset(awo_cnt_, 0, 4ull * rc * 8));
     }
   }
   head_grid_ = cus_ * 4;
