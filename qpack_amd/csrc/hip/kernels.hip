@@ -606,12 +606,18 @@ template <int HD, int REP, int NW, int HS, typename Epi = AttnNoEpi>
 __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s, int S, int ys, int nact,
                                                 const float (*wm)[REP], const float (*wl)[REP], const float *ored,
                                                 int ows, float *lout, const Epi &epi = Epi()) {
-  __shared__ float fwv[NW][REP], mlv[REP][2];
-  // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M).  Wave 0 holds every
-  // (wave w, head j) pair, lane 8 w + j (NW, REP <= 8), and reduces over w with xor shuffles of 8, 16 and 32
+  // per head: M = max over the waves, wave factors e^(m_w - M), L = sum l_w e^(m_w - M).  Each wave that sums output
+  // columns (thread e takes column e; REP * HD / 4 <= 4 x 64 columns) forms them itself - a wave holds every (wave w,
+  // head j) pair, lane 8 w + j (NW, REP <= 8), reduces over w with exchanges of lanes 8, 16 and 32 apart and keeps
+  // them in its own LDS copy - so only a wave-level fence, no workgroup barrier, stands before the sums
   static_assert(NW <= 8, "one lane per (wave, head)");
-  if (threadIdx.x < 64) {
-    const int w = threadIdx.x >> 3, j = threadIdx.x & 7;
+  constexpr int NMW = (REP * HD / 4 + 63) / 64;   // waves with columns
+  static_assert(NMW <= NW, "every column has a thread");
+  __shared__ float fwv[NMW][NW][REP], mlv[NMW][REP][2];
+  const int mwv = threadIdx.x >> 6;
+  if (mwv >= NMW) return;
+  {
+    const int w = (threadIdx.x & 63) >> 3, j = threadIdx.x & 7;
     const bool on = w < nact && j < REP;
     const float mw = on ? wm[w][j] : -INFINITY, lw = on ? wl[w][j] : 0.f;
     float M = mw;
@@ -619,22 +625,25 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
     const float f = mw == -INFINITY ? 0.f : expf(mw - M);
     float L = lw * f;
     L += xchg8_f(L); L = pair_sum16(L); L = pair_sum32(L);
-    if (on) fwv[w][j] = f;
-    if (w == 0 && j < REP) { mlv[j][0] = M; mlv[j][1] = L; }
+    if (on) fwv[mwv][w][j] = f;
+    if (w == 0 && j < REP) { mlv[mwv][j][0] = M; mlv[mwv][j][1] = L; }
   }
-  __syncthreads();
-  // 4 dims per thread (one pass over every head at REP * HD <= 4 x 512): float4 reads of the padded rows, one 16-byte
-  // store
-  for (int e = threadIdx.x; e < REP * HD / 4; e += blockDim.x) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // 4 dims per thread: float4 reads of the padded rows, one 16-byte store
+  {
+    const int e = threadIdx.x;
+    if (e >= REP * HD / 4) return;
     const int j = e / (HD / 4), i = 4 * (e % (HD / 4));
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int w = 0; w < nact; w++) {
-      const float f = fwv[w][j];
+      const float f = fwv[mwv][w][j];
       const float4 x = *(const float4 *)(ored + w * ows + j * HS + i);
       O.x = __builtin_fmaf(f, x.x, O.x); O.y = __builtin_fmaf(f, x.y, O.y);
       O.z = __builtin_fmaf(f, x.z, O.z); O.w = __builtin_fmaf(f, x.w, O.w);
     }
-    const float M = mlv[j][0], L = mlv[j][1];
+    const float M = mlv[mwv][j][0], L = mlv[mwv][j][1];
     if (S == 1) {
       const float li = 1.f / L;
       const float4 y = make_float4(O.x * li, O.y * li, O.z * li, O.w * li);
