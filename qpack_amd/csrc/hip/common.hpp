@@ -84,6 +84,7 @@ constexpr int kDppHalfMirror = 0x141;    // row_half_mirror: lane i <-> 7 - i wi
 constexpr int kDppMirror = 0x140;        // row_mirror: lane i <-> 15 - i within 16 lanes
 constexpr int kDppRowShl4 = 0x104;       // row_shl:4: lane i reads lane i + 4 of its 16-lane row (0 past the row)
 constexpr int kDppRowRor8 = 0x128;       // row_ror:8: lane i reads lane i ^ 8 of its 16-lane row
+constexpr int kDppRowRor4 = 0x124;       // row_ror:4: lane i reads lane (i + 4) mod 16 of its row
 
 // sum over aligned groups of 8 lanes, result in every lane of the group (exact for integers)
 __device__ __forceinline__ int sum8_i(int v) {
@@ -151,13 +152,25 @@ __device__ __forceinline__ int sum32_i(int v) {
 }
 __device__ __forceinline__ float xchg8_f(float v) { return __builtin_bit_cast(float, xchg8_u32(__builtin_bit_cast(uint32_t, v))); }
 
-// full-wave reductions (shuffles; not on the hot inner loops)
+// full-wave butterfly reductions, partners lane ^ 32, ^ 16, ^ 8, ^ 4, ^ 2, ^ 1 in that order (the same sums as xor
+// shuffles), each exchange a VALU instruction: the permlane swaps, DPP row rotations by 8 and by 4 (after the ^ 8 step
+// lanes i and i ^ 8 hold equal values, so lane i + 4 within the row stands for lane i ^ 4), quad permutations
 __device__ __forceinline__ float wave_sum(float v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  v = pair_sum32(v);
+  v = pair_sum16(v);
+  v += dpp_f<kDppRowRor8>(v);
+  v += dpp_f<kDppRowRor4>(v);
+  v += dpp_f<kDppQuadXor2>(v);
+  v += dpp_f<kDppQuadXor1>(v);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  v = pair_max32(v);
+  v = pair_max16(v);
+  v = fmaxf(v, dpp_f<kDppRowRor8>(v));
+  v = fmaxf(v, dpp_f<kDppRowRor4>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
   return v;
 }
 
