@@ -32,12 +32,21 @@ constexpr int kRansStep = 512;     // symbols between ring refills / output flus
 constexpr int kRansAhead = 4096;   // a refill is issued while fewer bytes than this are loaded past the read position
 
 __device__ __forceinline__ uint32_t rd_u8(const uint8_t *p) { return *p; }
+// LDS layout (one array, so it starts at LDS address 0 - checked - and the loop's LDS instructions take the tables'
+// addresses as immediate offsets):
+// ring (+ a copy of its first 16 bytes, so a window never wraps) | tables [3][4096] u16: slot m's freq, m - cum, symbol
+// | symbol staging (4 bytes before it take the first group's empty deferred store) | cumulative frequencies
+constexpr int kLdsTab = kRansRing + 16, kLdsSymb = kLdsTab + 3 * 2 * rans::kProbScale + 16;
+constexpr int kLdsCum = kLdsSymb + kRansStep + 64, kLdsBytes = kLdsCum + 4 * 260;
+
 __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, int *status) {
-  __shared__ uint16_t tfq[rans::kProbScale], tbi[rans::kProbScale];   // slot m: freq, m - cum
-  __shared__ uint8_t tsym[rans::kProbScale];             // slot m: symbol
-  __shared__ uint32_t ring[kRansRing / 4 + 4];           // + a copy of the first 16 bytes, so a window never wraps
-  __shared__ __align__(16) uint8_t symb[kRansStep + 64];
-  __shared__ uint32_t cum[257];
+  __shared__ __align__(16) uint8_t lds[kLdsBytes];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
+  if (lds0 != 0) { if (threadIdx.x == 0) status[blockIdx.x] = 2; return; }
+  uint32_t *const ring = (uint32_t *)lds;
+  uint16_t *const tfq = (uint16_t *)(lds + kLdsTab), *const tbi = tfq + rans::kProbScale, *const tsym = tbi + rans::kProbScale;
+  uint8_t *const symb = lds + kLdsSymb;
+  uint32_t *const cum = (uint32_t *)(lds + kLdsCum);
   const int lane = threadIdx.x;
   const RansTaskDev t = tasks[blockIdx.x];
   const int nsym = t.nsym;
@@ -77,7 +86,7 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
       while (cum[s + 1] <= m) s++;
       tfq[m] = (uint16_t)(cum[s + 1] - cum[s]);   // <= 4096
       tbi[m] = (uint16_t)(m - cum[s]);
-      tsym[m] = (uint8_t)s;
+      tsym[m] = (uint16_t)s;
     }
   }
 
@@ -105,7 +114,6 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
   bool pending = false;
 
   const int64_t n = t.n;
-  const int sbase = lane < 4 ? lane : kRansStep + lane;   // lanes 4..63 store their symbols in a spare area
   for (int64_t s0 = 0; s0 < n; s0 += kRansStep) {
     // refill: write the block loaded one step ago, issue the next while less than kRansAhead bytes are ahead
     if (pending) ring_put(pend_at, pend);
@@ -113,44 +121,72 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
     if (pending) { pend = *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane); pend_at = issued; issued += kRansBlk; }
     __syncthreads();
     const int ng = (int)std::min<int64_t>(kRansStep, n - s0);
-    // one group of four symbols; MASKED: the step's last group may hold fewer (lanes 0..3 past ng keep their state).
-    // Lanes 4..63 compute on their own state without effect: the prefix reads lanes 0..3 only, their symbols go to a
-    // spare area, and every table index is in range.
-    auto group = [&](int g, auto masked) {
-      const uint32_t qa = (uint32_t)q & (kRansRing - 4), sh = (uint32_t)q & 3u;
-      const uint32_t m = st & (rans::kProbScale - 1), hi_st = st >> rans::kProbBits;
-      // table entry, symbol and stream window (bytes q .. q + 7 within three dwords) are read together
-      const uint32_t fq = tfq[m], bi = tbi[m];
-      const uint32_t sy = tsym[m];
-      const uint32_t w0 = ring[qa >> 2], w1 = ring[(qa >> 2) + 1], w2 = ring[(qa >> 2) + 2];
-      __builtin_amdgcn_sched_barrier(0);   // keep the four reads ahead of the first use: one wait for all
-      uint32_t x = fq * hi_st + bi;   // freq <= 2^12 (16-bit load), x >> 12 < 2^20: one 24-bit multiply-add
-      // renormalisation bytes: 2 below 2^15, 1 below 2^23 (x >= 2^11 and < 2^31 here).  Each count is a ballot over
-      // lanes 0..3 (the other lanes compute on their own state without effect); a lane's byte offset is the bits of
-      // both ballots below it (mbcnt), the group's total their popcount - no cross-lane chain on the state's path
-      // lanes whose state advances: 0..3, or in the step's last group those below ng - g (a scalar mask)
-      const uint64_t lm = decltype(masked)::value ? (1ull << (ng - g)) - 1ull : 0xfull;
-      const uint64_t b1 = __builtin_amdgcn_ballot_w64(x < (1u << 23)) & lm, b2 = __builtin_amdgcn_ballot_w64(x < (1u << 15)) & lm;
-      const uint32_t excl = __builtin_amdgcn_mbcnt_lo((uint32_t)b2, __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
-      const uint32_t total = (uint32_t)__builtin_popcountll(b1) + (uint32_t)__builtin_popcountll(b2);
-      const uint32_t sh8 = (x < (1u << 23) ? 8u : 0u) + (x < (1u << 15) ? 8u : 0u);
-      const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh), hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
-      // the lane's bytes b0 = window[excl], b1 = window[excl + 1] as b0 << 8 | b1 (v_perm selectors; 0x0c gives 0)
-      const uint32_t sel = excl * 0x101u + 0x0c0c0001u;
-      const uint32_t be = __builtin_amdgcn_perm(hi, lo, sel);
-      x = (x << sh8) | (be >> (16 - sh8));
-      if (decltype(masked)::value) {   // lanes past the group keep their state
-        const uint32_t keep = (uint32_t)0 - (uint32_t)((lm >> lane) & 1ull);
-        st = (x & keep) | (st & ~keep);
-      } else {
-        st = x;   // lanes 4..63 advance their own (unused) state: every index they form stays in range
+    // the groups run on lanes 0..3 alone (the ballots then hold just the four states' bits).  A single wave issues
+    // about one instruction per 4 cycles, so a group costs its instruction count plus the table reads' exposed
+    // latency: the stream offset lives in a VGPR (two v_bcnt per group, the window address without a copy), and the
+    // window's three dwords are read one group ahead, so aligning them and storing the symbol fill that latency.
+    uint32_t qv = (uint32_t)q;
+    if (lane < 4) {
+      // every LDS access of the loop is written out with its waits.  A group issues its table reads (freq, m - cum,
+      // symbol) first; in their latency it adds the previous group's byte counts to the stream offset, reads its
+      // window there and stores the previous group's symbol; it waits for freq and m - cum (lgkmcnt(3)), and for the
+      // window just before the bytes are picked out of it (lgkmcnt(1)).  Only the table reads and the state's own
+      // arithmetic are on the chain from one group to the next.
+      asm volatile("" : "+v"(qv));
+      uint32_t sp = kLdsSymb - 4 + lane;   // the previous group's symbol slot (the first store lands before symb)
+      uint32_t sy = 0, b1p = 0, b2p = 0;   // the previous group's symbol and renormalisation ballots
+      // one group of four symbols; MASKED: the step's last group may hold fewer (lanes past it keep their state)
+      auto group = [&](int g, auto masked, auto off) {
+        const uint32_t a = (st & (rans::kProbScale - 1)) << 1;
+        uint32_t fq, bi, sy_new;
+        uint2 win;
+        asm volatile("ds_read_u16 %0, %3 offset:%4\n\tds_read_u16 %1, %3 offset:%5\n\tds_read_u16 %2, %3 offset:%6"
+                     : "=&v"(fq), "=&v"(bi), "=&v"(sy_new)
+                     : "v"(a), "i"(kLdsTab), "i"(kLdsTab + 2 * rans::kProbScale), "i"(kLdsTab + 4 * rans::kProbScale));
+        asm volatile("v_bcnt_u32_b32 %0, %1, %0\n\tv_bcnt_u32_b32 %0, %2, %0" : "+v"(qv) : "s"(b1p), "s"(b2p));
+        asm volatile("ds_read_b64 %0, %1" : "=v"(win) : "v"(qv & (kRansRing - 1)));   // stream bytes qv .. qv + 7
+        asm volatile("ds_write_b8 %0, %1 offset:%2" : : "v"(sp), "v"(sy), "i"(decltype(off)::value));
+        const uint32_t hs = st >> rans::kProbBits;
+        asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(fq), "+v"(bi) : "v"(hs));
+        __builtin_assume(fq <= (uint32_t)rans::kProbScale); __builtin_assume(bi < (uint32_t)rans::kProbScale);
+        __builtin_assume(hs < (1u << 20));
+        uint32_t x = fq * hs + bi;   // freq <= 2^12, x >> 12 < 2^20: one 24-bit multiply-add
+        // renormalisation bytes: 2 below 2^15, 1 below 2^23 (x >= 2^11 and < 2^31 here).  Each count is a ballot; a
+        // lane's byte offset is the bits of both ballots below it (mbcnt), the group's total their popcount
+        const bool c1 = x < (1u << 23), c2 = x < (1u << 15);
+        uint32_t b1 = (uint32_t)__builtin_amdgcn_ballot_w64(c1), b2 = (uint32_t)__builtin_amdgcn_ballot_w64(c2);
+        const uint32_t lm = decltype(masked)::value ? (1u << (ng - g)) - 1u : 0xfu;
+        if (decltype(masked)::value) { b1 &= lm; b2 &= lm; }
+        const uint32_t excl = __builtin_amdgcn_mbcnt_lo(b2, __builtin_amdgcn_mbcnt_lo(b1, 0u));
+        const uint32_t sel = excl * 0x101u + 0x0c0c0001u;
+        asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(win), "+v"(sy_new) : "v"(sel));
+        // the lane's bytes b0 = window[excl], b1 = window[excl + 1] into bytes 1, 0 of w (v_perm; selector 0x0c gives
+        // 0), then the renormalised state is a byte permutation of x and w: x, x << 8 | b0, x << 16 | b0 << 8 | b1
+        const uint32_t w = __builtin_amdgcn_perm(win.y, win.x, sel);
+        x = __builtin_amdgcn_perm(x, w, c1 ? (c2 ? 0x05040100u : 0x06050401u) : 0x07060504u);
+        if (decltype(masked)::value) {
+          const uint32_t keep = (uint32_t)0 - ((lm >> lane) & 1u);
+          st = (x & keep) | (st & ~keep);
+        } else {
+          st = x;
+        }
+        sy = sy_new; b1p = b1; b2p = b2;
+      };
+      using O0 = std::integral_constant<int, 0>;
+      using O4 = std::integral_constant<int, 4>;
+      const int nfull = ng & ~3;
+      int g = 0;
+      for (; g + 8 <= nfull; g += 8) {
+        group(g, std::false_type{}, O0{});
+        group(g + 4, std::false_type{}, O4{});
+        sp += 8;
       }
-      symb[sbase + g] = (uint8_t)sy;
-      q += total;
-    };
-    const int nfull = ng & ~3;
-    for (int g = 0; g < nfull; g += 4) group(g, std::false_type{});
-    if (nfull < ng) group(nfull, std::true_type{});
+      if (g < nfull) { group(g, std::false_type{}, O0{}); sp += 4; g += 4; }
+      if (g < ng) { group(g, std::true_type{}, O0{}); sp += 4; }
+      asm volatile("v_bcnt_u32_b32 %0, %1, %0\n\tv_bcnt_u32_b32 %0, %2, %0" : "+v"(qv) : "s"(b1p), "s"(b2p));
+      asm volatile("ds_write_b8 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(sp), "v"(sy) : "memory");
+    }
+    q = (uint64_t)__builtin_amdgcn_readfirstlane(qv);
     __syncthreads();
     // flush: lane l owns symbols [8 l, 8 l + 8) of the step
     const int i0 = 8 * lane;
@@ -231,7 +267,10 @@ void RansBatch::run(hipStream_t st, RansTiming *tm) {
     std::vector<int> status(tasks.size());
     ck(hipMemcpyAsync(status.data(), dst, status.size() * sizeof(int), hipMemcpyDeviceToHost, st), "status copy");
     ck(hipStreamSynchronize(st), "decode");
-    for (int s : status) if (s) throw std::runtime_error("rans: stream overrun");
+    for (int s : status) {
+      if (s == 2) throw std::runtime_error("rans: decoder LDS layout (the ring must start at LDS address 0)");
+      if (s) throw std::runtime_error("rans: stream overrun");
+    }
     if (tm) {
       tm->planes = (int)tasks.size(); tm->coded = coded_; tm->raw = raw_;
       ck(hipEventElapsedTime(&tm->upload_ms, e[0], e[1]), "event");
