@@ -66,12 +66,15 @@ int qph_create(const qph_config *cfg, const qph_tensor *tensors, int n_tensors, 
 /* load_model(path, max_ctx) for arch "llama" (model_llama.cpp:221-235): mmap a QPACK1/QPACK2/QPACK3 file, read
  * config.json and the manifest, upload to HBM; QPACK3's coded blobs are uploaded coded and decoded on the GPU */
 int qph_load(const char *path, int max_ctx, qph_model **out);
-/* the QPACK3 decode of the model's load: coded planes, coded / raw bytes, upload and decode-kernel HIP-event times
- * (zeros for a plain file) */
+/* the QPACK3 decode of the model's load: coded planes, coded / raw bytes, HIP-event times of the upload (first copy
+ * to last), of the decode (first launch to last; the launches run under the upload, one per upload round) and of both,
+ * and the number of upload rounds (zeros for a plain file) */
 typedef struct {
   int planes;
   int64_t coded_bytes, raw_bytes;
   float upload_ms, decode_ms;
+  float total_ms;
+  int rounds;
 } qph_load_stats;
 int qph_load_stats_of(const qph_model *m, qph_load_stats *out);
 void qph_destroy(qph_model *m);   /* ~LlamaCuda */

@@ -29,7 +29,7 @@ class Tensor(C.Structure):
 
 class LoadStatsC(C.Structure):
     _fields_ = [("planes", C.c_int), ("coded_bytes", C.c_int64), ("raw_bytes", C.c_int64), ("upload_ms", C.c_float),
-                ("decode_ms", C.c_float)]
+                ("decode_ms", C.c_float), ("total_ms", C.c_float), ("rounds", C.c_int)]
 
 
 class SynthSpecC(C.Structure):

@@ -101,7 +101,7 @@ int qph_load_stats_of(const qph_model *m, qph_load_stats *out) {
     need(m, "model"); need(out, "out");
     const qph::RansTiming &t = m->m->load_timing();
     out->planes = t.planes; out->coded_bytes = (int64_t)t.coded; out->raw_bytes = (int64_t)t.raw;
-    out->upload_ms = t.upload_ms; out->decode_ms = t.decode_ms;
+    out->upload_ms = t.upload_ms; out->decode_ms = t.decode_ms; out->total_ms = t.total_ms; out->rounds = t.rounds;
   });
 }
 
@@ -343,7 +343,7 @@ int qph_kernel_rans_decode(const uint8_t *blob, int64_t len, uint8_t *out, int64
       qph::RansBatch b;
       qph::RansTiming tm;
       b.add(blob, (size_t)len, d, n);
-      b.run(nullptr, &tm);
+      b.run(nullptr, &tm, qph::RansBatch::default_round());
       if (n) hck(hipMemcpy(out, d, n, hipMemcpyDeviceToHost), "download");
       if (ms) *ms = tm.decode_ms;
     } catch (...) { (void)hipFree(d); throw; }

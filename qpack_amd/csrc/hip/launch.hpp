@@ -312,18 +312,30 @@ struct RansTaskDev {
   uint32_t comp_len;      // bytes after the comp_len field
   int nsym, stride, nibbles;
 };
-hipError_t launch_rans(const RansTaskDev *tasks, int ntasks, int *status, hipStream_t st);
-struct RansTiming {
-  int planes = 0;
-  uint64_t coded = 0, raw = 0;
-  float upload_ms = 0, decode_ms = 0;
+struct RansState {   // a plane's decoder between launches
+  uint32_t st[4];
+  uint64_t q;   // stream offset from the 16-byte aligned address at or below the first stream byte
+  int64_t s0;   // symbols decoded
 };
-// Coded blobs (host memory) with their device destinations, decoded in one launch: run() uploads the blobs into one
-// staging buffer, plans the planes (throwing on malformed headers), decodes, waits, and throws on a stream overrun.
+// decode every plane as far as its first `avail` bytes (from the comp_len field) allow (state[].s0 = -1 before the
+// first launch)
+hipError_t launch_rans(const RansTaskDev *tasks, int ntasks, int *status, RansState *state, uint64_t avail, hipStream_t st);
+struct RansTiming {
+  int planes = 0, rounds = 0;
+  uint64_t coded = 0, raw = 0;
+  float upload_ms = 0, decode_ms = 0, total_ms = 0;
+};
+// Coded blobs (host memory) with their device destinations: run() plans the planes (throwing on malformed headers),
+// uploads the coded bytes into one staging buffer and decodes them there, waits, and throws on a stream overrun.
+// round_bytes > 0 streams the upload: round r brings bytes [r R, (r + 1) R) of every plane (R = round_bytes) on a copy
+// stream, and a decode launch after each round takes every plane as far as its uploaded bytes allow, so the decode
+// runs under the upload; 0: the whole upload, then one launch.
 class RansBatch {
  public:
   void add(const uint8_t *blob, size_t len, void *out, size_t out_cap);
-  void run(hipStream_t st, RansTiming *tm = nullptr);
+  void run(hipStream_t st, RansTiming *tm = nullptr, uint64_t round_bytes = 0);
+  // the round size loads use: QPH_RANS_ROUND (bytes; 0 = no streaming), else 1 MiB
+  static uint64_t default_round();
   bool empty() const { return items_.empty(); }
 
  private:

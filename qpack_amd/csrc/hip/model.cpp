@@ -106,7 +106,7 @@ HipLlama::HipLlama(const qph_config &cfg, const qph_tensor *tensors, int n, int 
     if (bq) { ly.bq = upload_f32(*bq, qd_); ly.bk = upload_f32(need(p + "bk"), kvd_); ly.bv = upload_f32(need(p + "bv"), kvd_); }
     layers_.push_back(ly);
   }
-  rans_.run(st_, &rans_tm_);   // QPACK3: every coded blob decodes in HBM in one launch
+  rans_.run(st_, &rans_tm_, RansBatch::default_round());   // QPACK3: the coded blobs decode in HBM under their upload
   // context splits per kv group: one per 64 positions of the full context, at most 48 (the kernel activates
   // min(this, ceil(T / 64)) of them beyond one workgroup's reach).  At C5's 16K context 48 splits beat 64: fewer
   // partials for the merge launch outweigh the idle CUs (same-box greedy 546.8 -> 550.8 tok/s; 40: 538.9, 56: 548.6)

@@ -17,6 +17,7 @@
 // The decoded bytes equal rans::decode's (bit-exact); a stream that needs a byte past its plane's end reports an
 // overrun, where the reference throws "rans: stream overrun".
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 #include <stdexcept>
 #include <vector>
@@ -35,21 +36,31 @@ __device__ __forceinline__ uint32_t rd_u8(const uint8_t *p) { return *p; }
 // LDS layout (one array, so it starts at LDS address 0 - checked - and the loop's LDS instructions take the tables'
 // addresses as immediate offsets):
 // ring (+ a copy of its first 16 bytes, so a window never wraps) | tables [3][4096] u16: slot m's freq, m - cum, symbol
-// | symbol staging (4 bytes before it take the first group's empty deferred store) | cumulative frequencies
-constexpr int kLdsTab = kRansRing + 16, kLdsSymb = kLdsTab + 3 * 2 * rans::kProbScale + 16;
-constexpr int kLdsCum = kLdsSymb + kRansStep + 64, kLdsBytes = kLdsCum + 4 * 260;
+// | slot staging (each group's 2m, 16 bits per symbol) | cumulative frequencies
+constexpr int kLdsTab = kRansRing + 16, kLdsSlots = kLdsTab + 3 * 2 * rans::kProbScale;
+constexpr int kLdsCum = kLdsSlots + 2 * kRansStep, kLdsBytes = kLdsCum + 4 * 260;
 
-__global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, int *status) {
+// One launch decodes every plane as far as `avail` allows: the bytes of each plane from its comp_len field up to
+// avail are in HBM (all of them when avail >= 4 + comp_len).  A step of 512 symbols starts only while its bytes (at
+// most 2 per symbol, plus the 8-byte window) are there; a plane that stops keeps its four states, stream offset and
+// symbol count in `state` for the next launch, which rebuilds its table and ring from them.  A plane starts (states
+// from its header) in the first launch that has its whole header; state[].s0 < 0 marks one not started.
+__global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, int *status, RansState *state, uint64_t avail) {
   __shared__ __align__(16) uint8_t lds[kLdsBytes];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
   if (lds0 != 0) { if (threadIdx.x == 0) status[blockIdx.x] = 2; return; }
   uint32_t *const ring = (uint32_t *)lds;
   uint16_t *const tfq = (uint16_t *)(lds + kLdsTab), *const tbi = tfq + rans::kProbScale, *const tsym = tbi + rans::kProbScale;
-  uint8_t *const symb = lds + kLdsSymb;
   uint32_t *const cum = (uint32_t *)(lds + kLdsCum);
   const int lane = threadIdx.x;
   const RansTaskDev t = tasks[blockIdx.x];
+  RansState *const S = state + blockIdx.x;
+  const int64_t n = t.n;
   const int nsym = t.nsym;
+  const bool first = S->s0 < 0;
+  if (first && avail < 4ull + 2 * nsym + 16) return;   // the header is not all in HBM yet
+  int64_t s0 = first ? 0 : S->s0;
+  if (!first && s0 >= n) return;   // done in an earlier launch
   const uint8_t *fq = t.plane + 4;
 
   // cumulative frequencies: lane l sums symbols [l * per, (l + 1) * per), then an exclusive scan over the lanes
@@ -94,27 +105,38 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
   const uint8_t *sp = t.plane + 4 + 2 * nsym + 16;
   const uint8_t *base = (const uint8_t *)((uintptr_t)sp & ~(uintptr_t)15);
   const uint64_t end_off = (uint64_t)(t.plane + 4 + t.comp_len - base);
-  uint64_t q = (uint64_t)(sp - base);
+  // stream offsets below lim are in HBM (the whole plane: no limit, an overrunning stream reads on and is reported)
+  const bool whole = avail >= 4ull + t.comp_len;
+  const uint64_t lim = whole ? ~0ull : (uint64_t)(t.plane + avail - base);
+  uint64_t q;
   uint32_t st = 0;
-  if (lane < 4) {
-    const uint8_t *xs = t.plane + 4 + 2 * nsym + 4 * lane;
-    st = rd_u8(xs) | (rd_u8(xs + 1) << 8) | (rd_u8(xs + 2) << 16) | (rd_u8(xs + 3) << 24);
+  if (first) {
+    q = (uint64_t)(sp - base);
+    if (lane < 4) {
+      const uint8_t *xs = t.plane + 4 + 2 * nsym + 4 * lane;
+      st = rd_u8(xs) | (rd_u8(xs + 1) << 8) | (rd_u8(xs + 2) << 16) | (rd_u8(xs + 3) << 24);
+    }
+  } else {
+    q = S->q;
+    if (lane < 4) st = S->st[lane];
   }
-  // loads stop at the plane's end (the bytes past it only feed a stream that has overrun, reported below)
+  // loads stop at the plane's end (the bytes past it only feed a stream that has overrun, reported below); the ring
+  // is filled from the block holding q (bytes loaded past lim are never used in this launch)
   const uint64_t load_max = (end_off + 15) & ~(uint64_t)15;
-  uint64_t issued = 0;
+  uint64_t issued = q & ~(uint64_t)(kRansBlk - 1);
+  const uint64_t fill_end = issued + kRansAhead;
   auto ring_put = [&](uint64_t at, const uint4 &v) {
     const uint32_t o = (uint32_t)(at + 16 * lane) & (kRansRing - 1);
     *(uint4 *)((uint8_t *)ring + o) = v;
     if (o == 0) *(uint4 *)((uint8_t *)ring + kRansRing) = v;
   };
-  for (; issued < (uint64_t)kRansAhead; issued += kRansBlk) ring_put(issued, *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane));
+  for (; issued < fill_end; issued += kRansBlk) ring_put(issued, *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane));
   uint4 pend = {0, 0, 0, 0};
   uint64_t pend_at = 0;
   bool pending = false;
 
-  const int64_t n = t.n;
-  for (int64_t s0 = 0; s0 < n; s0 += kRansStep) {
+  for (; s0 < n; s0 += kRansStep) {
+    if (q + 2 * kRansStep + 8 > lim) break;   // this step's bytes are not all in HBM yet
     // refill: write the block loaded one step ago, issue the next while less than kRansAhead bytes are ahead
     if (pending) ring_put(pend_at, pend);
     pending = issued - q < (uint64_t)kRansAhead;
@@ -122,32 +144,30 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
     __syncthreads();
     const int ng = (int)std::min<int64_t>(kRansStep, n - s0);
     // the groups run on lanes 0..3 alone (the ballots then hold just the four states' bits).  A single wave issues
-    // about one instruction per 4 cycles, so a group costs its instruction count plus the table reads' exposed
-    // latency: the stream offset lives in a VGPR (two v_bcnt per group, the window address without a copy), and the
-    // window's three dwords are read one group ahead, so aligning them and storing the symbol fill that latency.
+    // about one instruction per 8 cycles (measured), so a group costs its instruction count plus the table reads'
+    // exposed latency; the stream offset lives in a VGPR (two v_bcnt per group, the window address without a copy).
     uint32_t qv = (uint32_t)q;
     if (lane < 4) {
-      // every LDS access of the loop is written out with its waits.  A group issues its table reads (freq, m - cum,
-      // symbol) first; in their latency it adds the previous group's byte counts to the stream offset, reads its
-      // window there and stores the previous group's symbol; it waits for freq and m - cum (lgkmcnt(3)), and for the
-      // window just before the bytes are picked out of it (lgkmcnt(1)).  Only the table reads and the state's own
-      // arithmetic are on the chain from one group to the next.
+      // every LDS access of the loop is written out with its waits.  A group issues its two table reads (freq,
+      // m - cum) first; in their latency it adds the previous group's byte counts to the stream offset and reads its
+      // window there; it waits for the table (lgkmcnt(1)), and for the window just before the bytes are picked out of
+      // it (lgkmcnt(0)).  Only the table reads and the state's own arithmetic are on the chain from one group to the
+      // next.  The symbols are not read here: each group's slot (as 2m, the table offset) stays in a register, four
+      // groups leave in one 8-byte store, and the flush maps the slots to symbols.
       asm volatile("" : "+v"(qv));
-      uint32_t sp = kLdsSymb - 4 + lane;   // the previous group's symbol slot (the first store lands before symb)
-      uint32_t sy = 0, b1p = 0, b2p = 0;   // the previous group's symbol and renormalisation ballots
-      // one group of four symbols; MASKED: the step's last group may hold fewer (lanes past it keep their state)
-      auto group = [&](int g, auto masked, auto off) {
+      uint32_t b1p = 0, b2p = 0;   // the previous group's renormalisation ballots
+      // one group of four symbols, returning its slots; MASKED: the step's last group may hold fewer (lanes past it
+      // keep their state)
+      auto group = [&](int g, auto masked) {
         const uint32_t a = (st & (rans::kProbScale - 1)) << 1;
-        uint32_t fq, bi, sy_new;
+        uint32_t fq, bi;
         uint2 win;
-        asm volatile("ds_read_u16 %0, %3 offset:%4\n\tds_read_u16 %1, %3 offset:%5\n\tds_read_u16 %2, %3 offset:%6"
-                     : "=&v"(fq), "=&v"(bi), "=&v"(sy_new)
-                     : "v"(a), "i"(kLdsTab), "i"(kLdsTab + 2 * rans::kProbScale), "i"(kLdsTab + 4 * rans::kProbScale));
+        asm volatile("ds_read_u16 %0, %2 offset:%3\n\tds_read_u16 %1, %2 offset:%4"
+                     : "=&v"(fq), "=&v"(bi) : "v"(a), "i"(kLdsTab), "i"(kLdsTab + 2 * rans::kProbScale));
         asm volatile("v_bcnt_u32_b32 %0, %1, %0\n\tv_bcnt_u32_b32 %0, %2, %0" : "+v"(qv) : "s"(b1p), "s"(b2p));
         asm volatile("ds_read_b64 %0, %1" : "=v"(win) : "v"(qv & (kRansRing - 1)));   // stream bytes qv .. qv + 7
-        asm volatile("ds_write_b8 %0, %1 offset:%2" : : "v"(sp), "v"(sy), "i"(decltype(off)::value));
         const uint32_t hs = st >> rans::kProbBits;
-        asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(fq), "+v"(bi) : "v"(hs));
+        asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(fq), "+v"(bi) : "v"(hs));
         __builtin_assume(fq <= (uint32_t)rans::kProbScale); __builtin_assume(bi < (uint32_t)rans::kProbScale);
         __builtin_assume(hs < (1u << 20));
         uint32_t x = fq * hs + bi;   // freq <= 2^12, x >> 12 < 2^20: one 24-bit multiply-add
@@ -159,7 +179,7 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
         if (decltype(masked)::value) { b1 &= lm; b2 &= lm; }
         const uint32_t excl = __builtin_amdgcn_mbcnt_lo(b2, __builtin_amdgcn_mbcnt_lo(b1, 0u));
         const uint32_t sel = excl * 0x101u + 0x0c0c0001u;
-        asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(win), "+v"(sy_new) : "v"(sel));
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(win) : "v"(sel));
         // the lane's bytes b0 = window[excl], b1 = window[excl + 1] into bytes 1, 0 of w (v_perm; selector 0x0c gives
         // 0), then the renormalised state is a byte permutation of x and w: x, x << 8 | b0, x << 16 | b0 << 8 | b1
         const uint32_t w = __builtin_amdgcn_perm(win.y, win.x, sel);
@@ -170,29 +190,44 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
         } else {
           st = x;
         }
-        sy = sy_new; b1p = b1; b2p = b2;
+        b1p = b1; b2p = b2;
+        return a;
       };
-      using O0 = std::integral_constant<int, 0>;
-      using O4 = std::integral_constant<int, 4>;
+      // slot staging: groups 4k .. 4k + 3 of the step form batch k; lane j stores its four slots at
+      // kLdsSlots + 32 k + 8 j (symbol 4 g + j of the step is batch g / 4, lane j, entry g % 4)
+      uint32_t sp = kLdsSlots + 8 * lane;
       const int nfull = ng & ~3;
       int g = 0;
-      for (; g + 8 <= nfull; g += 8) {
-        group(g, std::false_type{}, O0{});
-        group(g + 4, std::false_type{}, O4{});
-        sp += 8;
+      for (; g + 16 <= nfull; g += 16) {
+        const uint32_t a0 = group(g, std::false_type{}), a1 = group(g + 4, std::false_type{});
+        const uint32_t a2 = group(g + 8, std::false_type{}), a3 = group(g + 12, std::false_type{});
+        asm volatile("ds_write_b64 %0, %1" : : "v"(sp), "v"(make_uint2(a0 | (a1 << 16), a2 | (a3 << 16))));
+        sp += 32;
       }
-      if (g < nfull) { group(g, std::false_type{}, O0{}); sp += 4; g += 4; }
-      if (g < ng) { group(g, std::true_type{}, O0{}); sp += 4; }
-      asm volatile("v_bcnt_u32_b32 %0, %1, %0\n\tv_bcnt_u32_b32 %0, %2, %0" : "+v"(qv) : "s"(b1p), "s"(b2p));
-      asm volatile("ds_write_b8 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(sp), "v"(sy) : "memory");
+      // the plane's last step: up to three more full groups and a partial one, one 16-bit store each
+      for (int e = 0; g < ng; g += 4, e += 2) {
+        const uint32_t a = g < nfull ? group(g, std::false_type{}) : group(g, std::true_type{});
+        asm volatile("ds_write_b16 %0, %1" : : "v"(sp + e), "v"(a));
+      }
+      asm volatile("v_bcnt_u32_b32 %0, %1, %0\n\tv_bcnt_u32_b32 %0, %2, %0\n\ts_waitcnt lgkmcnt(0)" : "+v"(qv) : "s"(b1p), "s"(b2p) : "memory");
     }
     q = (uint64_t)__builtin_amdgcn_readfirstlane(qv);
     __syncthreads();
-    // flush: lane l owns symbols [8 l, 8 l + 8) of the step
+    // flush: lane l owns symbols [8 l, 8 l + 8) of the step: batch l / 2, entries 2 (l & 1) and 2 (l & 1) + 1 of the
+    // four lanes' slots, mapped to symbols through the symbol table
     const int i0 = 8 * lane;
     if (i0 < ng) {
-      const uint2 v = *(const uint2 *)(symb + i0);
+      const uint8_t *const sl = lds + kLdsSlots + 32 * (lane >> 1) + 4 * (lane & 1);
+      const uint8_t *const tsy = lds + kLdsTab + 4 * rans::kProbScale;
+      uint2 v = {0, 0};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t pr = *(const uint32_t *)(sl + 8 * j);   // slots of symbols 8 l + j and 8 l + 4 + j
+        v.x |= (uint32_t)*(const uint16_t *)(tsy + (pr & 0xffff)) << (8 * j);
+        v.y |= (uint32_t)*(const uint16_t *)(tsy + (pr >> 16)) << (8 * j);
+      }
       const int64_t gi = s0 + i0;
+      auto byte = [&](int k) { return (uint8_t)((k < 4 ? v.x : v.y) >> (8 * (k & 3))); };
       if (t.nibbles) {
         const uint32_t b = (v.x & 0x0f) | ((v.x >> 4) & 0xf0) | ((v.x >> 8) & 0x0f00) | ((v.x >> 12) & 0xf000) |
                            ((v.y & 0x0f) << 16) | ((v.y << 12) & 0xf00000) | ((v.y & 0x0f0000) << 8) | ((v.y << 4) & 0xf0000000);
@@ -202,22 +237,26 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
       } else if (t.stride == 1) {
         uint8_t *o = t.out + gi;
         if (i0 + 8 <= ng && !((uintptr_t)o & 7)) *(uint2 *)o = v;   // wide stores where aligned (always, for 16 MiB chunks)
-        else for (int k = 0; k < 8 && k < ng - i0; k++) o[k] = symb[i0 + k];
+        else for (int k = 0; k < 8 && k < ng - i0; k++) o[k] = byte(k);
       } else {
-        for (int k = 0; k < 8 && i0 + k < ng; k++) t.out[(gi + k) * t.stride] = symb[i0 + k];
+        for (int k = 0; k < 8 && i0 + k < ng; k++) t.out[(gi + k) * t.stride] = byte(k);
       }
     }
   }
-  if (lane == 0) status[blockIdx.x] = q > end_off ? 1 : 0;
+  if (lane < 4) S->st[lane] = st;
+  if (lane == 0) {
+    S->q = q; S->s0 = s0;
+    if (s0 >= n) status[blockIdx.x] = q > end_off ? 1 : 0;
+  }
 }
 
-hipError_t launch_rans(const RansTaskDev *tasks, int ntasks, int *status, hipStream_t st) {
+hipError_t launch_rans(const RansTaskDev *tasks, int ntasks, int *status, RansState *state, uint64_t avail, hipStream_t st) {
   if (ntasks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rans_decode, dim3(ntasks), dim3(64), 0, st, tasks, status);
+  hipLaunchKernelGGL(k_rans_decode, dim3(ntasks), dim3(64), 0, st, tasks, status, state, avail);
   return hipGetLastError();
 }
 
-// ------------------------------------------------------------------ host side: many blobs, one launch
+// ------------------------------------------------------------------ host side: many blobs, one staging buffer
 void RansBatch::add(const uint8_t *blob, size_t len, void *out, size_t out_cap) {
   const uint64_t raw = rans::raw_size(blob, len);
   if (raw > out_cap) throw std::runtime_error("rans: decoded size exceeds the destination");
@@ -226,12 +265,20 @@ void RansBatch::add(const uint8_t *blob, size_t len, void *out, size_t out_cap) 
   raw_ += raw;
 }
 
-// a wave reads up to kRansAhead bytes from its stream's aligned start, and at most kRansBlk + 16 past its plane's end
+// a wave reads up to kRansAhead + kRansBlk bytes from the block holding its stream offset, and at most kRansBlk + 16
+// past its plane's end
 static constexpr size_t kRansSlack = kRansAhead + 2 * kRansBlk + 64;
 
-void RansBatch::run(hipStream_t st, RansTiming *tm) {
+uint64_t RansBatch::default_round() {
+  const char *e = getenv("QPH_RANS_ROUND");
+  return e ? (uint64_t)strtoull(e, nullptr, 10) : (uint64_t)1 << 20;
+}
+
+void RansBatch::run(hipStream_t st, RansTiming *tm, uint64_t round_bytes) {
   if (items_.empty()) return;
+  struct Seg { const uint8_t *src; size_t off, len; };   // a plane's bytes: host source, staging offset
   std::vector<RansTaskDev> tasks;
+  std::vector<Seg> segs;
   for (const Item &it : items_)
     for (const rans::PlaneTask &p : rans::plan(it.blob, it.len)) {
       RansTaskDev d{};
@@ -239,31 +286,57 @@ void RansBatch::run(hipStream_t st, RansTiming *tm) {
       d.out = it.out + p.out_off;
       d.n = p.n; d.comp_len = p.comp_len; d.nsym = p.nsym; d.stride = p.stride; d.nibbles = p.nibbles ? 1 : 0;
       tasks.push_back(d);
+      segs.push_back({it.blob + p.hdr, it.stage_off + p.hdr, 4 + (size_t)p.comp_len});
     }
   // longest planes first, so the last waves to start are short ones
   std::stable_sort(tasks.begin(), tasks.end(), [](const RansTaskDev &a, const RansTaskDev &b) { return a.n > b.n; });
-  uint8_t *stage = nullptr; RansTaskDev *dt = nullptr; int *dst = nullptr;
-  hipEvent_t e[3] = {};
+  size_t longest = 0;
+  for (const Seg &g : segs) longest = std::max(longest, g.len);
+  const int rounds = round_bytes ? (int)std::max<uint64_t>(1, (longest + round_bytes - 1) / round_bytes) : 1;
+  uint8_t *stage = nullptr; RansTaskDev *dt = nullptr; int *dst = nullptr; RansState *dstate = nullptr;
+  hipStream_t up = nullptr;
+  std::vector<hipEvent_t> ev(rounds, nullptr);
+  hipEvent_t e[4] = {};
   auto cleanup = [&] {
+    if (up) (void)hipStreamSynchronize(up);
     if (stage) (void)hipFree(stage);
     if (dt) (void)hipFree(dt);
     if (dst) (void)hipFree(dst);
+    if (dstate) (void)hipFree(dstate);
     for (hipEvent_t &x : e) if (x) (void)hipEventDestroy(x);
+    for (hipEvent_t &x : ev) if (x) (void)hipEventDestroy(x);
+    if (up) (void)hipStreamDestroy(up);
   };
   try {
     auto ck = [](hipError_t r, const char *what) { if (r != hipSuccess) throw std::runtime_error(std::string("rans: ") + what + ": " + hipGetErrorString(r)); };
     for (hipEvent_t &x : e) ck(hipEventCreate(&x), "event");
+    for (hipEvent_t &x : ev) ck(hipEventCreateWithFlags(&x, hipEventDisableTiming), "event");
+    ck(hipStreamCreateWithFlags(&up, hipStreamNonBlocking), "copy stream");
     ck(hipMalloc(&stage, coded_ + kRansSlack), "staging allocation");
     ck(hipMalloc(&dt, tasks.size() * sizeof(RansTaskDev) + 1), "task allocation");
     ck(hipMalloc(&dst, tasks.size() * sizeof(int) + 4), "status allocation");
+    ck(hipMalloc(&dstate, tasks.size() * sizeof(RansState) + 8), "state allocation");
     for (RansTaskDev &d : tasks) d.plane = stage + (uintptr_t)d.plane;
-    ck(hipEventRecord(e[0], st), "event");
-    for (const Item &it : items_) ck(hipMemcpyAsync(stage + it.stage_off, it.blob, it.len, hipMemcpyHostToDevice, st), "upload");
-    ck(hipMemsetAsync(stage + coded_, 0, kRansSlack, st), "staging clear");
+    // the task table, the status words and the staging slack go first, on the decode stream
     ck(hipMemcpyAsync(dt, tasks.data(), tasks.size() * sizeof(RansTaskDev), hipMemcpyHostToDevice, st), "task upload");
-    ck(hipEventRecord(e[1], st), "event");
-    ck(launch_rans(dt, (int)tasks.size(), dst, st), "decode launch");
-    ck(hipEventRecord(e[2], st), "event");
+    ck(hipMemsetAsync(dst, 0, tasks.size() * sizeof(int), st), "status clear");
+    ck(hipMemsetAsync(dstate, 0xff, tasks.size() * sizeof(RansState), st), "state clear");   // s0 = -1: not started
+    ck(hipMemsetAsync(stage + coded_, 0, kRansSlack, st), "staging clear");
+    ck(hipEventRecord(e[0], up), "event");
+    for (int r = 0; r < rounds; r++) {
+      const uint64_t lo = rounds == 1 ? 0 : (uint64_t)r * round_bytes, hi = rounds == 1 ? ~0ull : lo + round_bytes;
+      for (const Seg &g : segs)
+        if (lo < g.len) {
+          const size_t n = (size_t)std::min<uint64_t>(g.len, hi) - (size_t)lo;
+          ck(hipMemcpyAsync(stage + g.off + lo, g.src + lo, n, hipMemcpyHostToDevice, up), "upload");
+        }
+      ck(hipEventRecord(ev[r], up), "event");
+      if (r == rounds - 1) ck(hipEventRecord(e[1], up), "event");
+      ck(hipStreamWaitEvent(st, ev[r], 0), "stream wait");
+      if (r == 0) ck(hipEventRecord(e[2], st), "event");
+      ck(launch_rans(dt, (int)tasks.size(), dst, dstate, r == rounds - 1 ? ~0ull : hi, st), "decode launch");
+    }
+    ck(hipEventRecord(e[3], st), "event");
     std::vector<int> status(tasks.size());
     ck(hipMemcpyAsync(status.data(), dst, status.size() * sizeof(int), hipMemcpyDeviceToHost, st), "status copy");
     ck(hipStreamSynchronize(st), "decode");
@@ -272,9 +345,10 @@ void RansBatch::run(hipStream_t st, RansTiming *tm) {
       if (s) throw std::runtime_error("rans: stream overrun");
     }
     if (tm) {
-      tm->planes = (int)tasks.size(); tm->coded = coded_; tm->raw = raw_;
+      tm->planes = (int)tasks.size(); tm->rounds = rounds; tm->coded = coded_; tm->raw = raw_;
       ck(hipEventElapsedTime(&tm->upload_ms, e[0], e[1]), "event");
-      ck(hipEventElapsedTime(&tm->decode_ms, e[1], e[2]), "event");
+      ck(hipEventElapsedTime(&tm->decode_ms, e[2], e[3]), "event");
+      ck(hipEventElapsedTime(&tm->total_ms, e[0], e[3]), "event");
     }
   } catch (...) { cleanup(); items_.clear(); coded_ = raw_ = 0; throw; }
   cleanup();

@@ -139,11 +139,12 @@ class HipLlama:
 
     # ---- measurement
     def load_stats(self):
-        """the QPACK3 decode of this model's load: planes, coded / raw bytes, upload and decode-kernel ms"""
+        """the QPACK3 decode of this model's load: planes, coded / raw bytes, upload / decode / both ms (the decode
+        launches run under the upload, one per upload round), rounds"""
         st = LoadStatsC()
         check(lib().qph_load_stats_of(self._h, C.byref(st)))
         return {"planes": st.planes, "coded_bytes": st.coded_bytes, "raw_bytes": st.raw_bytes, "upload_ms": st.upload_ms,
-                "decode_ms": st.decode_ms}
+                "decode_ms": st.decode_ms, "total_ms": st.total_ms, "rounds": st.rounds}
 
     def time_greedy(self, token, n):
         ms = C.c_float(0)

@@ -67,6 +67,30 @@ def test_chunked_blobs(chunk, codec):
     np.testing.assert_array_equal(gpu_decode(blob), raw)
 
 
+@pytest.mark.parametrize("round_bytes", [0, 520, 600, 1037, 4096, 65536])
+def test_streamed_rounds(round_bytes, monkeypatch):
+    """the upload in rounds of round_bytes per plane (QPH_RANS_ROUND), each followed by a decode launch that takes every
+    plane as far as its uploaded bytes allow: planes stop between steps, keep their states and resume in the next launch.
+    Bit-exact for every round size, with planes of unequal length (a chunked blob with a short last chunk and a two-plane
+    codec-1 blob), and an overrun still reported"""
+    monkeypatch.setenv("QPH_RANS_ROUND", str(round_bytes))
+    rng = np.random.default_rng(round_bytes + 11)
+    raw = np.clip(rng.normal(100, 6, 150000), 0, 255).astype(np.uint8)
+    C = 40000
+    blob = O.rans_assemble_chunked(len(raw), C, [O.rans_encode(raw[o:o + C], 1, 1) for o in range(0, len(raw), C)])
+    print(f"rans streamed rounds {round_bytes}: chunked", flush=True)
+    np.testing.assert_array_equal(gpu_decode(blob), raw)
+    raw2 = raw_of(rng, "uniform", 30001)
+    print(f"rans streamed rounds {round_bytes}: codec 1 planes 2", flush=True)
+    np.testing.assert_array_equal(gpu_decode(O.rans_encode(raw2, 1, 2)), raw2)
+    b = O.rans_encode(raw2, 1, 1)
+    cl = int(np.frombuffer(b[6:10].tobytes(), np.uint32)[0])
+    b[6:10] = np.frombuffer(np.uint32(cl - 3000).tobytes(), np.uint8)
+    print(f"rans streamed rounds {round_bytes}: overrun", flush=True)
+    with pytest.raises(qa.QphError, match="stream overrun"):
+        gpu_decode(b)
+
+
 def test_overrun_matches_oracle():
     rng = np.random.default_rng(5)
     blob = O.rans_encode(rng.integers(0, 256, 5000, dtype=np.uint8), 1, 1)
@@ -101,7 +125,7 @@ def test_qpack3_model_equals_qpack2(cfg, synth, tmp_path):
     a = qa.HipLlama.load(src, 128)
     b = qa.HipLlama.load(dst, 128)
     st = b.load_stats()
-    assert st["planes"] > 0 and st["raw_bytes"] > st["coded_bytes"] > 0
+    assert st["planes"] > 0 and st["raw_bytes"] > st["coded_bytes"] > 0 and st["rounds"] >= 1
     assert a.load_stats()["planes"] == 0
     np.testing.assert_array_equal(a.prefill(toks, 1), b.prefill(toks, 1))
     np.testing.assert_array_equal(a.greedy_run(7, 24), b.greedy_run(7, 24))
