@@ -334,7 +334,7 @@ class RansBatch {
  public:
   void add(const uint8_t *blob, size_t len, void *out, size_t out_cap);
   void run(hipStream_t st, RansTiming *tm = nullptr, uint64_t round_bytes = 0);
-  // the round size loads use: QPH_RANS_ROUND (bytes; 0 = no streaming), else 1 MiB
+  // the round size loads use: QPH_RANS_ROUND (bytes; 0 = no streaming), else 512 KiB
   static uint64_t default_round();
   bool empty() const { return items_.empty(); }
 

@@ -3,17 +3,20 @@
 //
 // A coded plane is one sequential stream: its four interleaved states share one byte stream, so symbol i + 1's bytes
 // start where symbol i's end and a plane decodes in order.  The parallelism is across planes (16 MiB chunks of large
-// blobs, the blobs themselves), so the kernel runs one wave per plane and spends that wave on the plane's latency chain:
+// blobs, the blobs themselves), so the kernel runs one wave per plane and spends that wave on the plane's latency chain
+// (a wave issues about one instruction per 8 cycles, an LDS read returns after ~85: the group's instruction count and
+// the table read's exposed latency are the whole cost):
 //   - the decode table sits in LDS: per 12-bit slot m the frequency and m - cum as two 16-bit entries, so the state
-//     update freq * (x >> 12) + (m - cum) is one multiply-add on the two loaded values, and the symbol in a byte table
-//     read alongside;
+//     update freq * (x >> 12) + (m - cum) is one multiply-add on the two loaded values; the symbol table is read only
+//     when a step's output leaves (the slots wait in registers, then in LDS);
 //   - lanes 0..3 hold states 0..3 and decode the group of four symbols 4g .. 4g + 3 together: each lane needs 0, 1 or 2
 //     renormalisation bytes; two ballots (x < 2^23, x < 2^15) give every lane its byte offset in the stream (mbcnt of
-//     both below the lane) and the group's total (their popcount, in scalar registers for the next group's window),
-//     and the bytes come from an 8-byte window of the stream read (as three dwords) at the same time as the table,
-//     picked out with one byte permute;
+//     both below the lane) and the group's total (their popcount); the bytes come from an unaligned 8-byte window of the
+//     stream, picked out with one byte permute, and the renormalised state is a second byte permute of x and them;
 //   - the coded stream is staged in an 8 KiB LDS ring by 1 KiB coalesced loads issued one step (512 symbols) before use;
-//   - symbols collect in LDS and leave as 8-byte (bytes) or 4-byte (nibbles) stores of all 64 lanes per step.
+//   - the output leaves as 8-byte (bytes) or 4-byte (nibbles) stores of all 64 lanes per step;
+//   - a launch can stop a plane between steps and a later one resume it (RansState), so the decode runs under the
+//     upload of the coded bytes (RansBatch::run).
 // The decoded bytes equal rans::decode's (bit-exact); a stream that needs a byte past its plane's end reports an
 // overrun, where the reference throws "rans: stream overrun".
 #include <algorithm>
@@ -271,7 +274,7 @@ static constexpr size_t kRansSlack = kRansAhead + 2 * kRansBlk + 64;
 
 uint64_t RansBatch::default_round() {
   const char *e = getenv("QPH_RANS_ROUND");
-  return e ? (uint64_t)strtoull(e, nullptr, 10) : (uint64_t)1 << 20;
+  return e ? (uint64_t)strtoull(e, nullptr, 10) : (uint64_t)1 << 19;   // C3: 0.45 s load (1 MiB 0.47, 2 MiB 0.49)
 }
 
 void RansBatch::run(hipStream_t st, RansTiming *tm, uint64_t round_bytes) {
