@@ -39,23 +39,30 @@ __device__ __forceinline__ uint32_t rd_u8(const uint8_t *p) { return *p; }
 // LDS layout (one array, so it starts at LDS address 0 - checked - and the loop's LDS instructions take the tables'
 // addresses as immediate offsets):
 // ring (+ a copy of its first 16 bytes, so a window never wraps) | tables [3][4096] u16: slot m's freq, m - cum, symbol
-// | slot staging (each group's 2m, 16 bits per symbol) | cumulative frequencies
+// | slot staging, two steps (each group's 2m, 16 bits per symbol) | cumulative frequencies | the decoder's offset
 constexpr int kLdsTab = kRansRing + 16, kLdsSlots = kLdsTab + 3 * 2 * rans::kProbScale;
-constexpr int kLdsCum = kLdsSlots + 2 * kRansStep, kLdsBytes = kLdsCum + 4 * 260;
+constexpr int kLdsCum = kLdsSlots + 2 * 2 * kRansStep, kLdsQ = kLdsCum + 4 * 260, kLdsBytes = kLdsQ + 16;
 
 // One launch decodes every plane as far as `avail` allows: the bytes of each plane from its comp_len field up to
 // avail are in HBM (all of them when avail >= 4 + comp_len).  A step of 512 symbols starts only while its bytes (at
 // most 2 per symbol, plus the 8-byte window) are there; a plane that stops keeps its four states, stream offset and
 // symbol count in `state` for the next launch, which rebuilds its table and ring from them.  A plane starts (states
 // from its header) in the first launch that has its whole header; state[].s0 < 0 marks one not started.
-__global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, int *status, RansState *state, uint64_t avail) {
+//
+// Two waves per plane: wave 0 decodes and touches no global memory inside the step loop; wave 1 keeps the ring filled
+// and stores the previous step's symbols.  A wave with a global load in flight had the compiler wait for it
+// (vmcnt(0)) at the head of the group loop, next to the loop's LDS asm - a stall at every step; in wave 0 that wait
+// now finds nothing outstanding.  The waves meet at one barrier per step: the decoder's stream offset goes to LDS,
+// the slot staging alternates between two buffers, and the ring runs at least 2 KiB ahead of the decoder.
+__global__ __launch_bounds__(128) void k_rans_decode(const RansTaskDev *tasks, int *status, RansState *state, uint64_t avail) {
   __shared__ __align__(16) uint8_t lds[kLdsBytes];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds;
   if (lds0 != 0) { if (threadIdx.x == 0) status[blockIdx.x] = 2; return; }
   uint32_t *const ring = (uint32_t *)lds;
   uint16_t *const tfq = (uint16_t *)(lds + kLdsTab), *const tbi = tfq + rans::kProbScale, *const tsym = tbi + rans::kProbScale;
   uint32_t *const cum = (uint32_t *)(lds + kLdsCum);
-  const int lane = threadIdx.x;
+  uint32_t *const qsh = (uint32_t *)(lds + kLdsQ);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const RansTaskDev t = tasks[blockIdx.x];
   RansState *const S = state + blockIdx.x;
   const int64_t n = t.n;
@@ -64,45 +71,6 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
   if (first && avail < 4ull + 2 * nsym + 16) return;   // the header is not all in HBM yet
   int64_t s0 = first ? 0 : S->s0;
   if (!first && s0 >= n) return;   // done in an earlier launch
-  const uint8_t *fq = t.plane + 4;
-
-  // cumulative frequencies: lane l sums symbols [l * per, (l + 1) * per), then an exclusive scan over the lanes
-  const int per = nsym / 64 ? nsym / 64 : 1;
-  uint32_t fl[4] = {0, 0, 0, 0}, own = 0;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int s = lane * per + k;
-    if (k < per && s < nsym) { fl[k] = rd_u8(fq + 2 * s) | (rd_u8(fq + 2 * s + 1) << 8); own += fl[k]; }
-  }
-  uint32_t incl = own;
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t v = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += v;
-  }
-  uint32_t run = incl - own;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int s = lane * per + k;
-    if (k < per && s < nsym) { cum[s] = run; run += fl[k]; }
-  }
-  if (lane == 0) cum[nsym] = rans::kProbScale;
-  __syncthreads();
-  // table: lane l fills slots [64 l, 64 l + 64): the symbol of slot m is the s with cum[s] <= m < cum[s + 1]
-  {
-    const uint32_t m0 = lane * 64;
-    int lo = 0, hi = nsym - 1;   // largest s with cum[s] <= m0
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (cum[mid] <= m0) lo = mid; else hi = mid - 1;
-    }
-    int s = lo;
-    for (uint32_t m = m0; m < m0 + 64; m++) {
-      while (cum[s + 1] <= m) s++;
-      tfq[m] = (uint16_t)(cum[s + 1] - cum[s]);   // <= 4096
-      tbi[m] = (uint16_t)(m - cum[s]);
-      tsym[m] = (uint16_t)s;
-    }
-  }
 
   // stream bytes: offsets are counted from `base`, the 16-byte aligned address at or below the first stream byte
   const uint8_t *sp = t.plane + 4 + 2 * nsym + 16;
@@ -111,52 +79,144 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
   // stream offsets below lim are in HBM (the whole plane: no limit, an overrunning stream reads on and is reported)
   const bool whole = avail >= 4ull + t.comp_len;
   const uint64_t lim = whole ? ~0ull : (uint64_t)(t.plane + avail - base);
-  uint64_t q;
-  uint32_t st = 0;
-  if (first) {
-    q = (uint64_t)(sp - base);
-    if (lane < 4) {
-      const uint8_t *xs = t.plane + 4 + 2 * nsym + 4 * lane;
-      st = rd_u8(xs) | (rd_u8(xs + 1) << 8) | (rd_u8(xs + 2) << 16) | (rd_u8(xs + 3) << 24);
-    }
-  } else {
-    q = S->q;
-    if (lane < 4) st = S->st[lane];
-  }
+  uint64_t q = first ? (uint64_t)(sp - base) : S->q;
   // loads stop at the plane's end (the bytes past it only feed a stream that has overrun, reported below); the ring
   // is filled from the block holding q (bytes loaded past lim are never used in this launch)
   const uint64_t load_max = (end_off + 15) & ~(uint64_t)15;
   uint64_t issued = q & ~(uint64_t)(kRansBlk - 1);
-  const uint64_t fill_end = issued + kRansAhead;
   auto ring_put = [&](uint64_t at, const uint4 &v) {
     const uint32_t o = (uint32_t)(at + 16 * lane) & (kRansRing - 1);
     *(uint4 *)((uint8_t *)ring + o) = v;
     if (o == 0) *(uint4 *)((uint8_t *)ring + kRansRing) = v;
   };
-  for (; issued < fill_end; issued += kRansBlk) ring_put(issued, *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane));
-  uint4 pend = {0, 0, 0, 0};
-  uint64_t pend_at = 0;
-  bool pending = false;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  auto gload = [&](uint64_t at) {
+    const u32x4 v = *(const __attribute__((address_space(1))) u32x4 *)(uintptr_t)(base + std::min(at, load_max) + 16 * lane);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  };
+  // refill (wave 1): the blocks from `issued` while fewer than kRansAhead bytes are loaded past the decoder
+  auto refill = [&]() {
+    uint4 v[kRansAhead / kRansBlk];
+    int k = 0;
+#pragma unroll
+    for (int j = 0; j < kRansAhead / kRansBlk; j++)
+      if ((int64_t)(issued + (uint64_t)j * kRansBlk) - (int64_t)q < kRansAhead) { v[j] = gload(issued + (uint64_t)j * kRansBlk); k = j + 1; }
+#pragma unroll
+    for (int j = 0; j < kRansAhead / kRansBlk; j++)
+      if (j < k) ring_put(issued + (uint64_t)j * kRansBlk, v[j]);
+    issued += (uint64_t)k * kRansBlk;
+  };
 
-  for (; s0 < n; s0 += kRansStep) {
-    if (q + 2 * kRansStep + 8 > lim) break;   // this step's bytes are not all in HBM yet
-    // refill: write the block loaded one step ago, issue the next while less than kRansAhead bytes are ahead
-    if (pending) ring_put(pend_at, pend);
-    pending = issued - q < (uint64_t)kRansAhead;
-    if (pending) { pend = *(const uint4 *)(base + std::min(issued, load_max) + 16 * lane); pend_at = issued; issued += kRansBlk; }
-    __syncthreads();
-    const int ng = (int)std::min<int64_t>(kRansStep, n - s0);
-    // the groups run on lanes 0..3 alone (the ballots then hold just the four states' bits).  A single wave issues
-    // about one instruction per 8 cycles (measured), so a group costs its instruction count plus the table reads'
-    // exposed latency; the stream offset lives in a VGPR (two v_bcnt per group, the window address without a copy).
-    uint32_t qv = (uint32_t)q;
+  uint32_t st = 0;
+  if (wave == 0) {
     if (lane < 4) {
-      // every LDS access of the loop is written out with its waits.  A group issues its two table reads (freq,
-      // m - cum) first; in their latency it adds the previous group's byte counts to the stream offset and reads its
-      // window there; it waits for the table (lgkmcnt(1)), and for the window just before the bytes are picked out of
-      // it (lgkmcnt(0)).  Only the table reads and the state's own arithmetic are on the chain from one group to the
-      // next.  The symbols are not read here: each group's slot (as 2m, the table offset) stays in a register, four
-      // groups leave in one 8-byte store, and the flush maps the slots to symbols.
+      if (first) {
+        const uint8_t *xs = t.plane + 4 + 2 * nsym + 4 * lane;
+        st = rd_u8(xs) | (rd_u8(xs + 1) << 8) | (rd_u8(xs + 2) << 16) | (rd_u8(xs + 3) << 24);
+      } else {
+        st = S->st[lane];
+      }
+    }
+    // cumulative frequencies: lane l sums symbols [l * per, (l + 1) * per), then an exclusive scan over the lanes
+    const uint8_t *fq = t.plane + 4;
+    const int per = nsym / 64 ? nsym / 64 : 1;
+    uint32_t fl[4] = {0, 0, 0, 0}, own = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int s = lane * per + k;
+      if (k < per && s < nsym) { fl[k] = rd_u8(fq + 2 * s) | (rd_u8(fq + 2 * s + 1) << 8); own += fl[k]; }
+    }
+    uint32_t incl = own;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    uint32_t run = incl - own;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int s = lane * per + k;
+      if (k < per && s < nsym) { cum[s] = run; run += fl[k]; }
+    }
+    if (lane == 0) cum[nsym] = rans::kProbScale;
+  } else {
+    refill();   // the ring's first kRansAhead bytes, under the table build
+  }
+  __syncthreads();
+  // table (both waves): thread i fills slots [32 i, 32 i + 32): the symbol of slot m is the s with cum[s] <= m < cum[s + 1]
+  {
+    const uint32_t m0 = threadIdx.x * 32;
+    int lo = 0, hi = nsym - 1;   // largest s with cum[s] <= m0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cum[mid] <= m0) lo = mid; else hi = mid - 1;
+    }
+    int s = lo;
+    for (uint32_t m = m0; m < m0 + 32; m++) {
+      while (cum[s + 1] <= m) s++;
+      tfq[m] = (uint16_t)(cum[s + 1] - cum[s]);   // <= 4096
+      tbi[m] = (uint16_t)(m - cum[s]);
+      tsym[m] = (uint16_t)s;
+    }
+  }
+  __syncthreads();
+
+  // flush (wave 1): lane l owns symbols [8 l, 8 l + 8) of a step: batch l / 2, entries 2 (l & 1) and 2 (l & 1) + 1 of
+  // the four lanes' slots, mapped to symbols through the symbol table
+  typedef __attribute__((address_space(1))) uint8_t glb_u8;
+  auto flush = [&](int64_t fs0, int ng, int buf) {
+    const int i0 = 8 * lane;
+    if (i0 < ng) {
+      const uint8_t *const sl = lds + kLdsSlots + 2 * kRansStep * buf + 32 * (lane >> 1) + 4 * (lane & 1);
+      const uint8_t *const tsy = lds + kLdsTab + 4 * rans::kProbScale;
+      uint2 v = {0, 0};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t pr = *(const uint32_t *)(sl + 8 * j);   // slots of symbols 8 l + j and 8 l + 4 + j
+        v.x |= (uint32_t)*(const uint16_t *)(tsy + (pr & 0xffff)) << (8 * j);
+        v.y |= (uint32_t)*(const uint16_t *)(tsy + (pr >> 16)) << (8 * j);
+      }
+      const int64_t gi = fs0 + i0;
+      auto byte = [&](int k) { return (uint8_t)((k < 4 ? v.x : v.y) >> (8 * (k & 3))); };
+      if (t.nibbles) {
+        const uint32_t b = (v.x & 0x0f) | ((v.x >> 4) & 0xf0) | ((v.x >> 8) & 0x0f00) | ((v.x >> 12) & 0xf000) |
+                           ((v.y & 0x0f) << 16) | ((v.y << 12) & 0xf00000) | ((v.y & 0x0f0000) << 8) | ((v.y << 4) & 0xf0000000);
+        glb_u8 *o = (glb_u8 *)(uintptr_t)(t.out + gi / 2);
+        if (i0 + 8 <= ng && !((uintptr_t)o & 3)) *(__attribute__((address_space(1))) uint32_t *)o = b;
+        else for (int k = 0; k < 4 && 2 * k < ng - i0; k++) o[k] = (uint8_t)(b >> (8 * k));
+      } else if (t.stride == 1) {
+        glb_u8 *o = (glb_u8 *)(uintptr_t)(t.out + gi);
+        if (i0 + 8 <= ng && !((uintptr_t)o & 7)) {   // wide stores where aligned (always, for 16 MiB chunks)
+          *(__attribute__((address_space(1))) uint32_t *)o = v.x;
+          *(__attribute__((address_space(1))) uint32_t *)(o + 4) = v.y;
+        } else {
+          for (int k = 0; k < 8 && k < ng - i0; k++) o[k] = byte(k);
+        }
+      } else {
+        glb_u8 *o = (glb_u8 *)(uintptr_t)t.out;
+        for (int k = 0; k < 8 && i0 + k < ng; k++) o[(gi + k) * t.stride] = byte(k);
+      }
+    }
+  };
+
+  // the step loop, run by both waves with the same s0 and q (q from the decoder through LDS after every step)
+  int prev_ng = 0, buf = 0;
+  for (;; s0 += kRansStep, buf ^= 1) {
+    const bool go = s0 < n && q + 2 * kRansStep + 8 <= lim;   // this step's bytes are all in HBM
+    const int ng = go ? (int)std::min<int64_t>(kRansStep, n - s0) : 0;
+    if (wave == 1) {
+      if (prev_ng) flush(s0 - kRansStep, prev_ng, buf ^ 1);
+      if (go) refill();
+    } else if (go && lane < 4) {
+      // the groups run on lanes 0..3 alone (the ballots then hold just the four states' bits).  A single wave
+      // issues about one instruction per 5-6 cycles (measured), so a group costs its instruction count plus the
+      // table reads' exposed latency; the stream offset lives in a VGPR (two v_bcnt per group, the window address
+      // without a copy).  Every LDS access of the loop is written out with its waits.  A group issues its two table
+      // reads (freq, m - cum) first; in their latency it adds the previous group's byte counts to the stream offset
+      // and reads its window there; it waits for the table (lgkmcnt(1)), and for the window just before the bytes
+      // are picked out of it (lgkmcnt(0)).  Only the table reads and the state's own arithmetic are on the chain from
+      // one group to the next.  The symbols are not read here: each group's slot (as 2m, the table offset) stays in
+      // a register, four groups leave in one 8-byte store, and wave 1 maps the slots to symbols.
+      uint32_t qv = (uint32_t)q;
       asm volatile("" : "+v"(qv));
       uint32_t b1p = 0, b2p = 0;   // the previous group's renormalisation ballots
       // one group of four symbols, returning its slots; MASKED: the step's last group may hold fewer (lanes past it
@@ -183,8 +243,8 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
         const uint32_t excl = __builtin_amdgcn_mbcnt_lo(b2, __builtin_amdgcn_mbcnt_lo(b1, 0u));
         const uint32_t sel = excl * 0x101u + 0x0c0c0001u;
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(win) : "v"(sel));
-        // the lane's bytes b0 = window[excl], b1 = window[excl + 1] into bytes 1, 0 of w (v_perm; selector 0x0c gives
-        // 0), then the renormalised state is a byte permutation of x and w: x, x << 8 | b0, x << 16 | b0 << 8 | b1
+        // the lane's bytes b0 = window[excl], b1 = window[excl + 1] into bytes 1, 0 of w (v_perm; selector 0x0c
+        // gives 0), then the renormalised state is a byte permutation of x and w: x, x << 8 | b0, x << 16 | b0 << 8 | b1
         const uint32_t w = __builtin_amdgcn_perm(win.y, win.x, sel);
         x = __builtin_amdgcn_perm(x, w, c1 ? (c2 ? 0x05040100u : 0x06050401u) : 0x07060504u);
         if (decltype(masked)::value) {
@@ -197,8 +257,8 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
         return a;
       };
       // slot staging: groups 4k .. 4k + 3 of the step form batch k; lane j stores its four slots at
-      // kLdsSlots + 32 k + 8 j (symbol 4 g + j of the step is batch g / 4, lane j, entry g % 4)
-      uint32_t sp = kLdsSlots + 8 * lane;
+      // 32 k + 8 j of the step's buffer (symbol 4 g + j of the step is batch g / 4, lane j, entry g % 4)
+      uint32_t sp = kLdsSlots + 2 * kRansStep * buf + 8 * lane;
       const int nfull = ng & ~3;
       int g = 0;
       for (; g + 16 <= nfull; g += 16) {
@@ -213,49 +273,25 @@ __global__ __launch_bounds__(64) void k_rans_decode(const RansTaskDev *tasks, in
         asm volatile("ds_write_b16 %0, %1" : : "v"(sp + e), "v"(a));
       }
       asm volatile("v_bcnt_u32_b32 %0, %1, %0\n\tv_bcnt_u32_b32 %0, %2, %0\n\ts_waitcnt lgkmcnt(0)" : "+v"(qv) : "s"(b1p), "s"(b2p) : "memory");
+      if (lane == 0) qsh[buf] = qv;   // two slots: wave 1 reads this one after the barrier, before the next write to it
     }
-    q = (uint64_t)__builtin_amdgcn_readfirstlane(qv);
+    if (!go) break;
     __syncthreads();
-    // flush: lane l owns symbols [8 l, 8 l + 8) of the step: batch l / 2, entries 2 (l & 1) and 2 (l & 1) + 1 of the
-    // four lanes' slots, mapped to symbols through the symbol table
-    const int i0 = 8 * lane;
-    if (i0 < ng) {
-      const uint8_t *const sl = lds + kLdsSlots + 32 * (lane >> 1) + 4 * (lane & 1);
-      const uint8_t *const tsy = lds + kLdsTab + 4 * rans::kProbScale;
-      uint2 v = {0, 0};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t pr = *(const uint32_t *)(sl + 8 * j);   // slots of symbols 8 l + j and 8 l + 4 + j
-        v.x |= (uint32_t)*(const uint16_t *)(tsy + (pr & 0xffff)) << (8 * j);
-        v.y |= (uint32_t)*(const uint16_t *)(tsy + (pr >> 16)) << (8 * j);
-      }
-      const int64_t gi = s0 + i0;
-      auto byte = [&](int k) { return (uint8_t)((k < 4 ? v.x : v.y) >> (8 * (k & 3))); };
-      if (t.nibbles) {
-        const uint32_t b = (v.x & 0x0f) | ((v.x >> 4) & 0xf0) | ((v.x >> 8) & 0x0f00) | ((v.x >> 12) & 0xf000) |
-                           ((v.y & 0x0f) << 16) | ((v.y << 12) & 0xf00000) | ((v.y & 0x0f0000) << 8) | ((v.y << 4) & 0xf0000000);
-        uint8_t *o = t.out + gi / 2;
-        if (i0 + 8 <= ng && !((uintptr_t)o & 3)) *(uint32_t *)o = b;
-        else for (int k = 0; k < 4 && 2 * k < ng - i0; k++) o[k] = (uint8_t)(b >> (8 * k));
-      } else if (t.stride == 1) {
-        uint8_t *o = t.out + gi;
-        if (i0 + 8 <= ng && !((uintptr_t)o & 7)) *(uint2 *)o = v;   // wide stores where aligned (always, for 16 MiB chunks)
-        else for (int k = 0; k < 8 && k < ng - i0; k++) o[k] = byte(k);
-      } else {
-        for (int k = 0; k < 8 && i0 + k < ng; k++) t.out[(gi + k) * t.stride] = byte(k);
-      }
-    }
+    q = (uint64_t)qsh[buf];
+    prev_ng = ng;
   }
-  if (lane < 4) S->st[lane] = st;
-  if (lane == 0) {
-    S->q = q; S->s0 = s0;
-    if (s0 >= n) status[blockIdx.x] = q > end_off ? 1 : 0;
+  if (wave == 0) {
+    if (lane < 4) S->st[lane] = st;
+    if (lane == 0) {
+      S->q = q; S->s0 = s0;
+      if (s0 >= n) status[blockIdx.x] = q > end_off ? 1 : 0;
+    }
   }
 }
 
 hipError_t launch_rans(const RansTaskDev *tasks, int ntasks, int *status, RansState *state, uint64_t avail, hipStream_t st) {
   if (ntasks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rans_decode, dim3(ntasks), dim3(64), 0, st, tasks, status, state, avail);
+  hipLaunchKernelGGL(k_rans_decode, dim3(ntasks), dim3(128), 0, st, tasks, status, state, avail);
   return hipGetLastError();
 }
 
