@@ -3,7 +3,8 @@
 //
 // A coded plane is one sequential stream: its four interleaved states share one byte stream, so symbol i + 1's bytes
 // start where symbol i's end and a plane decodes in order.  The parallelism is across planes (16 MiB chunks of large
-// blobs, the blobs themselves), so the kernel runs one wave per plane and spends that wave on the plane's latency chain
+// blobs, the blobs themselves), so the kernel runs one decoding wave per plane and spends that wave on the plane's
+// latency chain (a second wave of the workgroup keeps its stream ring filled and stores its symbols)
 // (a wave issues about one instruction per 8 cycles, an LDS read returns after ~85: the group's instruction count and
 // the table read's exposed latency are the whole cost):
 //   - the decode table sits in LDS: per 12-bit slot m the frequency and m - cum as two 16-bit entries, so the state
@@ -13,8 +14,8 @@
 //     renormalisation bytes; two ballots (x < 2^23, x < 2^15) give every lane its byte offset in the stream (mbcnt of
 //     both below the lane) and the group's total (their popcount); the bytes come from an unaligned 8-byte window of the
 //     stream, picked out with one byte permute, and the renormalised state is a second byte permute of x and them;
-//   - the coded stream is staged in an 8 KiB LDS ring by 1 KiB coalesced loads issued one step (512 symbols) before use;
-//   - the output leaves as 8-byte (bytes) or 4-byte (nibbles) stores of all 64 lanes per step;
+//   - the coded stream is staged in an 8 KiB LDS ring by 1 KiB coalesced loads, at least 2 KiB ahead of the decoder;
+//   - the output leaves as 8-byte (bytes) or 4-byte (nibbles) stores of all 64 lanes of the second wave per step;
 //   - a launch can stop a plane between steps and a later one resume it (RansState), so the decode runs under the
 //     upload of the coded bytes (RansBatch::run).
 // The decoded bytes equal rans::decode's (bit-exact); a stream that needs a byte past its plane's end reports an
