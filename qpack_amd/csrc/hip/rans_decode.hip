@@ -4,9 +4,9 @@
 // A coded plane is one sequential stream: its four interleaved states share one byte stream, so symbol i + 1's bytes
 // start where symbol i's end and a plane decodes in order.  The parallelism is across planes (16 MiB chunks of large
 // blobs, the blobs themselves), so the kernel runs one decoding wave per plane and spends that wave on the plane's
-// latency chain (a second wave of the workgroup keeps its stream ring filled and stores its symbols)
-// (a wave issues about one instruction per 8 cycles, an LDS read returns after ~85: the group's instruction count and
-// the table read's exposed latency are the whole cost):
+// latency chain; a second wave of the workgroup keeps its stream ring filled and stores its symbols.  A wave issues
+// about one instruction per 5-6 cycles and an LDS read returns after ~85, so a group's instruction count and its table
+// read's exposed latency are the whole cost:
 //   - the decode table sits in LDS: per 12-bit slot m the frequency and m - cum as two 16-bit entries, so the state
 //     update freq * (x >> 12) + (m - cum) is one multiply-add on the two loaded values; the symbol table is read only
 //     when a step's output leaves (the slots wait in registers, then in LDS);
