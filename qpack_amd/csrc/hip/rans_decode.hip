@@ -338,7 +338,9 @@ void RansBatch::run(hipStream_t st, RansTiming *tm, uint64_t round_bytes) {
   std::vector<hipEvent_t> ev(rounds, nullptr);
   hipEvent_t e[4] = {};
   auto cleanup = [&] {
+    // an error can come between launches: every copy and decode launch already queued finishes before the buffers go
     if (up) (void)hipStreamSynchronize(up);
+    (void)hipStreamSynchronize(st);
     if (stage) (void)hipFree(stage);
     if (dt) (void)hipFree(dt);
     if (dst) (void)hipFree(dst);
