@@ -45,6 +45,26 @@ __device__ __forceinline__ uint4 ld16(const void *p) {
 }
 __device__ __forceinline__ float lane_bcast(float v, int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane)); }
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+// (max, lowest index) over the wave, in every lane: the butterfly of wave_max (partners lane ^ 32, ^ 16 by permlane
+// swaps, ^ 8, ^ 4 by row rotations, ^ 2, ^ 1 by quad permutations), each step keeping the better of the pair - a total
+// order, so both lanes of a pair keep the same (value, index), which the rotation by 4 relies on
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+  auto pick = [&](float ov, int oi) { if (better(ov, oi, v, i)) { v = ov; i = oi; } };
+  {
+    float a, b, c, d;
+    swap32(v, a, b); swap32(__builtin_bit_cast(float, i), c, d);
+    v = a; i = __builtin_bit_cast(int, c); pick(b, __builtin_bit_cast(int, d));
+  }
+  {
+    float a, b, c, d;
+    swap16(v, a, b); swap16(__builtin_bit_cast(float, i), c, d);
+    v = a; i = __builtin_bit_cast(int, c); pick(b, __builtin_bit_cast(int, d));
+  }
+  pick(dpp_f<kDppRowRor8>(v), dpp_i<kDppRowRor8>(i));
+  pick(dpp_f<kDppRowRor4>(v), dpp_i<kDppRowRor4>(i));
+  pick(dpp_f<kDppQuadXor2>(v), dpp_i<kDppQuadXor2>(i));
+  pick(dpp_f<kDppQuadXor1>(v), dpp_i<kDppQuadXor1>(i));
+}
 
 // A unit is NS rows of one segment (EPI_SWIGLU: row r of the gate and of the up matrix).  Waves own units
 // round-robin and stream them chunk by chunk (1 KiB of every row of the unit per step: lane i reads bytes [16 i, 16 i + 16)).
@@ -401,10 +421,7 @@ __global__ __launch_bounds__(1024) void k_matvec(MvArgs a) {
     }
   }
   if (EPI == EPI_ARGMAX) {
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(best_v, o, kWave); const int oi = __shfl_xor(best_i, o, kWave);
-      if (better(ov, oi, best_v, best_i)) { best_v = ov; best_i = oi; }
-    }
+    wave_argmax(best_v, best_i);
     __syncthreads();
     float *rv = av.red; int *ri = (int *)(av.red + 16);
     if (lane == 0) { rv[wave] = best_v; ri[wave] = best_i; }
@@ -1433,11 +1450,8 @@ __global__ __launch_bounds__(kThreads) void k_argmax_finish(const float2 *amax, 
     const float v = amax[i].x; const int idx = __builtin_bit_cast(int, amax[i].y);
     if (better(v, idx, bv, bi)) { bv = v; bi = idx; }
   }
-  // strict > with the lower index winning ties is associative: wave shuffles, then the wave results in order
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, kWave); const int oi = __shfl_xor(bi, o, kWave);
-    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-  }
+  // strict > with the lower index winning ties is associative: the wave butterfly, then the wave results in order
+  wave_argmax(bv, bi);
   if ((threadIdx.x & (kWave - 1)) == 0) { bv_s[threadIdx.x / kWave] = bv; bi_s[threadIdx.x / kWave] = bi; }
   __syncthreads();
   if (threadIdx.x == 0) {
