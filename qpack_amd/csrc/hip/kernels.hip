@@ -693,27 +693,17 @@ __device__ __forceinline__ void attn_wave_merge(const AttnArgs &a, int g, int s,
 //           enters as hi + lo halves (hi = f16(q), lo = f16(q - hi)) - two MFMAs, exact products, fp32 sums;
 //           scaled by 1/sqrt(hd) like attend() (model_llama.cpp:137-146);
 //   softmax online per head column: lane l holds head l % 16 at positions 4 (l / 16) + i of each 16-row tile;
-//   values  O^T[d][h] += V^T[d][p] P^T[p][h]; V goes through a per-wave LDS tile transposed (dims x positions) for
-//           the A operand; P (hi + lo halves) stays in registers: the C layout of the two score tiles is the B
-//           layout once the k index runs over positions {4 (l / 16) + i} and {16 + 4 (l / 16) + i}.
+//   values  O^T[d][h] += V^T[d][p] P^T[p][h]; V lands in a per-wave LDS tile as stored (positions x dims) and the
+//           A operand comes out of it transposed by the LDS read; P (hi + lo halves) stays in registers: the C layout
+//           of the two score tiles is the B layout once the k index runs over positions {4 (l / 16) + i} and
+//           {16 + 4 (l / 16) + i}.
 constexpr int kAttnMfWaves = 8, kAttnMfBlk = 32;
 template <int HD>
 struct MfK {   // K of one 32-position block in the A layout: [2 tiles][HD / 32] 16-byte pieces
   static constexpr int KS = HD / 32;
   u32x4 k[2][KS];
 };
-template <int HD>
-struct MfV {   // V of one block: HD / 16 16-byte pieces; piece i of a lane: position mfv_pos, dims mfv_dim .. + 7
-  static constexpr int NV = HD / 16;
-  u32x4 v[NV];
-};
-// piece i of lane l: 8 positions x 8 dim octets per piece (each position's 8 octets in 8 adjacent lanes, one 128-byte
-// line); at HD 128 pieces 2 j and 2 j + 1 hold the two halves of positions 8 j ..  The lane 8 away holds position ^ 1.
-template <int HD>
-__device__ __forceinline__ int mfv_pos(int lane, int i) { return (i / (HD / 64)) * 8 + (lane >> 3); }
-template <int HD>
-__device__ __forceinline__ int mfv_dim(int lane, int i) { return 8 * ((lane & 7) + 8 * (i % (HD / 64))); }
-// rows at or past te (the cache allocation) read row tb instead
+// rows at or past te (the cache allocation) read row te - 1 instead
 template <int HD>
 __device__ __forceinline__ void mf_load_k(const uint16_t *kc, int kvd, int g, int tb, int te, int lane, MfK<HD> &b) {
   const int lr = lane & 15, lg = lane >> 4;
@@ -724,12 +714,23 @@ __device__ __forceinline__ void mf_load_k(const uint16_t *kc, int kvd, int g, in
     for (int s = 0; s < MfK<HD>::KS; s++) b.k[mt][s] = *(const u32x4 *)(kc + (size_t)tc * kvd + g * HD + 32 * s + 8 * lg);
   }
 }
+// V of one block goes to LDS as stored - [32 positions][HD] fp16, rows of HD * 2 bytes - by direct-to-LDS loads (no
+// registers), and the PV product reads its A fragments (V^T: dims x positions) with ds_read_b64_tr_b16.  The 16-byte
+// segment c of row p sits at segment c ^ vswz(p), so the 8 rows of a 32-lane transpose read (positions 4 lg + r / 4
+// over two lane groups) cover all 64 banks: 2 (p & 7) at 256-byte rows, 2 ((p >> 1) & 3) at 128-byte rows (the row's
+// parity picks the bank half)
 template <int HD>
-__device__ __forceinline__ void mf_load_v(const uint16_t *vc, int kvd, int g, int tb, int te, int lane, MfV<HD> &b) {
+__device__ __forceinline__ int vswz(int p) { return HD == 128 ? 2 * (p & 7) : 2 * ((p >> 1) & 3); }
+// rows at or past te (the cache allocation) read row te - 1 instead.  buf: the wave's 32 x HD tile (wave-uniform)
+template <int HD>
+__device__ __forceinline__ void mf_dma_v(const uint16_t *vc, int kvd, int g, int tb, int te, int lane, uint16_t *buf) {
+  constexpr int SEG = HD / 8, RPI = 64 / SEG;   // 16-byte segments per row; rows per 1 KiB load instruction
+  const int r = lane / SEG, sp = lane % SEG;
 #pragma unroll
-  for (int i = 0; i < MfV<HD>::NV; i++) {
-    const int t = tb + mfv_pos<HD>(lane, i), tc = t < te ? t : te - 1;
-    b.v[i] = *(const u32x4 *)(vc + (size_t)tc * kvd + g * HD + mfv_dim<HD>(lane, i));
+  for (int q = 0; q < kAttnMfBlk / RPI; q++) {
+    const int p = q * RPI + r, t = tb + p, tc = t < te ? t : te - 1;
+    // lane l writes bytes [16 l, 16 l + 16) of the instruction's 1 KiB: row q RPI + r, segment position sp
+    dma16(vc + (size_t)tc * kvd + g * HD + 8 * (sp ^ vswz<HD>(p)), buf + q * RPI * HD);
   }
 }
 
@@ -742,26 +743,28 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
                            const Epi &epi = Epi()) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
-  // LDS rows padded so the MFMA-layout accesses (16 heads / dims apart per lane) spread over the banks
-  constexpr int NW = kAttnMfWaves, KS = MfK<HD>::KS, NV = MfV<HD>::NV, DT = HD / 16, VS = kAttnMfBlk + 8;   // VS: rows of 20 dwords
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  typedef __attribute__((address_space(3))) s4 lds_s4;
+  constexpr int NW = kAttnMfWaves, KS = MfK<HD>::KS, DT = HD / 16;
   constexpr int QS = HD + 4;
   __shared__ float wm[NW][REP], wl[NW][REP];
-  __shared__ __align__(16) uint16_t vt[NW][HD * VS];
+  __shared__ __align__(16) uint16_t vt[NW][kAttnMfBlk * HD];   // each wave's V block as stored (swizzled segments)
   // a wave's (unnormalised) output rows go into its own V tile once its block loop is done: [REP][QS] floats
-  static_assert(REP * QS * 4 <= HD * VS * 2, "the output rows fit in the wave's V tile");
-  constexpr int OWS = HD * VS / 2;   // floats between two waves' output rows
+  static_assert(REP * QS * 4 <= kAttnMfBlk * HD * 2, "the output rows fit in the wave's V tile");
+  constexpr int OWS = kAttnMfBlk * HD / 2;   // floats between two waves' output rows
   const int kvd = a.nkv * HD;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  uint16_t *vw = vt[wave];
   MfK<HD> ka, kb;
-  MfV<HD> vb;
   const int pos_s = ctl_pos_issue(a.ctl);
   // positions past the context or the split are loaded from rows below a.ctx (in the allocation) and masked: their
-  // scores become -inf and their V pieces zero.  ONE: the first a.early waves (all when 0) load their first block now;
+  // scores become -inf and their V rows zero.  ONE: the first a.early waves (all when 0) load their first block now;
   // the host sets a.early to the blocks the step's context can need, so no wave loads a block past it
   const bool early = ONE && (a.early <= 0 || wave < a.early);
   if (early) {
+    mf_dma_v<HD>(a.vc, kvd, g, kAttnMfBlk * wave, a.ctx, lane, vw);
     mf_load_k<HD>(a.kc, kvd, g, kAttnMfBlk * wave, a.ctx, lane, ka);
-    mf_load_v<HD>(a.vc, kvd, g, kAttnMfBlk * wave, a.ctx, lane, vb);
   }
   // q^T fragments straight from the q / k / v epilogue's fp16 planes (hi = f16(q), lo = f16(q - hi)): lane holds head
   // lr (zero past REP), dims 32 k + 8 lg + 0..7
@@ -781,47 +784,50 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
   // wave w takes blocks w, w + NW, ... of the split's 32-position blocks (waves without a block idle)
   const int nblk = (t1 - t0 + kAttnMfBlk - 1) / kAttnMfBlk, nact = min(nblk, NW);
   if (!early && wave < nblk) {
+    mf_dma_v<HD>(a.vc, kvd, g, t0 + kAttnMfBlk * wave, a.ctx, lane, vw);
     mf_load_k<HD>(a.kc, kvd, g, t0 + kAttnMfBlk * wave, a.ctx, lane, ka);
-    mf_load_v<HD>(a.vc, kvd, g, t0 + kAttnMfBlk * wave, a.ctx, lane, vb);
   }
   const float scl = 1.f / sqrtf((float)HD);
   f4 o[DT];
 #pragma unroll
   for (int d = 0; d < DT; d++) o[d] = (f4){0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
-  uint16_t *vw = vt[wave];
-  // one block: V -> LDS, then the next block's loads (V into the same registers, K into the other set), then the
-  // scores from this block's K registers
+  // one block: wait for its V (in LDS) and K (registers), read the V^T fragments, issue the next block's loads into
+  // the same LDS tile and the other K set, then the scores, the softmax and the PV product
   auto block = [&](MfK<HD> &kcur, MfK<HD> &knxt, int tb) {
-    // V -> LDS transposed (this wave's tile).  Piece i of lane l holds position
-    // p, dims d0 .. d0 + 7; the lane 8 away holds position p ^ 1, same dims.  The two swap halves so that the
-    // even-position lane owns dims d0 .. d0 + 3 and the odd one d0 + 4 .. d0 + 7 of both positions, and each writes
-    // four (p even, p odd) pairs of its dims as 32-bit words.
-    // (the addresses are formed here - the empty asm keeps them in the loop: hoisted, they stayed live and spilled)
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
+    // the block's K registers and V tile: its K loads were issued after the V tile's, so the compiler's wait for K
+    // (forced here by a use of every K register, which it sees; an s_waitcnt in asm it would not) covers V too
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-      const int p = mfv_pos<HD>(ln, i), d0 = mfv_dim<HD>(ln, i);
-      const u32x4 vv = tb + p < t1 ? vb.v[i] : (u32x4){0u, 0u, 0u, 0u};
-      const bool ev = (p & 1) == 0;
-      const uint32_t rx = xchg8_u32(ev ? vv[2] : vv[0]);
-      const uint32_t ry = xchg8_u32(ev ? vv[3] : vv[1]);
-      const uint32_t ox = ev ? vv[0] : vv[2], oy = ev ? vv[1] : vv[3];   // own dims (low / high pair)
-      // word for dim pair member: (even position) | (odd position) << 16
-      const uint32_t lo_x = ev ? ox : rx, hi_x = ev ? rx : ox, lo_y = ev ? oy : ry, hi_y = ev ? ry : oy;
-      // dword (p / 2) XOR 2 (d0 / 8 mod 8) (even: the position pairs stay adjacent).  gfx950 serves b32 LDS stores 32
-      // lanes a cycle from 32 banks and b64 reads 32 lanes a cycle from 64 banks (measured with bank-conflict
-      // counters): with 20-dword rows and 8 positions x 8 octets per piece both these stores and the fragment reads
-      // below are conflict-free (4 x 16 per piece put every 32-lane store on 16 banks)
-      uint32_t *wr = (uint32_t *)(vw + (d0 + (ev ? 0 : 4)) * VS) + ((p >> 1) ^ (2 * ((d0 >> 3) & 7)));
-      wr[0] = (lo_x & 0xffffu) | (hi_x << 16);
-      wr[VS / 2] = (lo_x >> 16) | (hi_x & 0xffff0000u);
-      wr[VS] = (lo_y & 0xffffu) | (hi_y << 16);
-      wr[3 * VS / 2] = (lo_y >> 16) | (hi_y & 0xffff0000u);
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int k = 0; k < KS; k++) asm volatile("" ::"v"(kcur.k[mt][k]));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tb + kAttnMfBlk > t1) {
+      // rows past the split become zeros: their probabilities are 0, but 0 x a stale NaN would not be
+      constexpr int SEG = HD / 8, RPI = 64 / SEG;
+#pragma unroll
+      for (int q = 0; q < kAttnMfBlk / RPI; q++) {
+        const int p = q * RPI + lane / SEG;
+        if (tb + p >= t1) *(u32x4 *)(vw + p * HD + 8 * (lane % SEG)) = (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+    // V^T fragment of tile d: dim 16 d + lr, positions 4 lg + 0..3 and 16 + 4 lg + 0..3 (the k order of ph / pl).
+    // ds_read_b64_tr_b16 hands lane i of a 16-lane group element i % 4 of the 4 values that lane 4 j + i / 4
+    // addresses, as its element j: so source lane r addresses row 4 lg + r / 4 (+ 16), dims 16 d + 4 (r % 4) .. + 3
+    h8 vf[DT];
+    {
+      const int pr = 4 * lg + (lr >> 2), dq = 4 * (lr & 3), sw = vswz<HD>(pr);   // rows pr and pr + 16: same swizzle
+#pragma unroll
+      for (int d = 0; d < DT; d++) {
+        const int off = 8 * (((16 * d + dq) >> 3) ^ sw) + (dq & 4);
+        const s4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(vw + pr * HD + off));
+        const s4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(vw + (pr + 16) * HD + off));
+        vf[d] = __builtin_bit_cast(h8, (s8)__builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
     }
     if (tb + NW * kAttnMfBlk < t1) {
-      mf_load_v<HD>(a.vc, kvd, g, tb + NW * kAttnMfBlk, a.ctx, lane, vb);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the tile's reads are done before the DMA rewrites it
+      mf_dma_v<HD>(a.vc, kvd, g, tb + NW * kAttnMfBlk, a.ctx, lane, vw);
       mf_load_k<HD>(a.kc, kvd, g, tb + NW * kAttnMfBlk, a.ctx, lane, knxt);
     }
     // scores of the two 16-position tiles
@@ -865,30 +871,20 @@ __device__ void attn_split(const AttnArgs &a, int g, int s, int S, int ys, float
     rs = pair_sum32(rs);
     l = l * corr + rs;
     m = mn;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int d = 0; d < DT; d++) {
       o[d] *= corr;
-      // V^T fragment: dim 16 d + lr, positions 4 lg + 0..3 and 16 + 4 lg + 0..3 (the k order of ph / pl)
-      const int row = 16 * d + lr, sw = 2 * ((row >> 3) & 7);   // the stores' swizzle
-      const uint32_t *vr = (const uint32_t *)(vw + row * VS);
-      const uint2 v0 = *(const uint2 *)(vr + ((2 * lg) ^ sw)), v1 = *(const uint2 *)(vr + ((8 + 2 * lg) ^ sw));
-      const h8 vf = __builtin_bit_cast(h8, make_uint4(v0.x, v0.y, v1.x, v1.y));
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[d], ph, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[d], pl, o[d], 0, 0, 0);
     }
-    // the tile is rewritten by the next block: its reads are done first
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
   for (int tb = t0 + kAttnMfBlk * wave; tb < t1; tb += 2 * NW * kAttnMfBlk) {
     block(ka, kb, tb);
     if (tb + NW * kAttnMfBlk >= t1) break;
     block(kb, ka, tb + NW * kAttnMfBlk);
   }
+  // a wave without a block may still have its early loads in flight: they land before its tile is reused
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // this wave's (m, l, o) -> LDS (its own V tile, free now): lane holds head lr, dims 16 d + 4 lg + i
   float *ored = (float *)&vt[0][0];
   if (lr < REP) {
