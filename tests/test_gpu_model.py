@@ -93,6 +93,42 @@ def test_snapshot_restore_rewind(synth):
     assert gpu.pos() == 20
 
 
+@pytest.mark.parametrize("cfg,path", [("mini128", "fused"), ("mini128", "single"), ("mini128", "splits"),
+                                      ("mini", "fused"), ("mini", "splits"), ("mini_r7", "fused")])
+def test_stale_nan_rows_past_context(cfg, path, synth, monkeypatch):
+    """cache rows past the context hold whatever a longer sequence left there - NaN here (a restored snapshot 19
+    positions longer, then a rewind).  The decode attention loads whole 32-position blocks of K and V; the rows past
+    the context (or past a split's end) must not reach the output: their scores are -inf and their V rows are zeroed
+    in LDS (0 x NaN would be NaN).  The logits of every step through that region equal a clean cache's bit for bit, on
+    the fused attention + wo kernel, the one-split attention kernel and forced small splits (a partial block at every
+    split's end)"""
+    if path != "fused":
+        monkeypatch.setenv("QPH_AWO_MAX", "0")
+    if path == "splits":
+        monkeypatch.setenv("QPH_ATTN_SINGLE", "16")
+        monkeypatch.setenv("QPH_ATTN_SPLIT_POS", "16")
+    model = synth(cfg)
+    shape = qa.CONFIGS[cfg]
+    kvd = shape.kv_heads * shape.head_dim
+    clean = qa.HipLlama.load(model, max_ctx=128)
+    dirty = qa.HipLlama.load(model, max_ctx=128)
+    rng = np.random.default_rng(5)
+    P, extra = 45, 19
+    clean.prefill(rng.integers(0, clean.vocab(), P).astype(np.int32), 0)
+    pos, k, v = split_snapshot(clean.snapshot(), shape.layers, kvd)
+    assert pos == P
+    nan = np.full((shape.layers, extra, kvd), np.nan, np.float16)
+    body = np.stack([np.concatenate([k, nan], 1), np.concatenate([v, nan], 1)], 1)   # [layers][K, V][rows][kvd]
+    dirty.restore(np.int32(P + extra).tobytes() + body.tobytes())
+    assert dirty.rewind(P) and dirty.pos() == P
+    print(f"{cfg} {path}: NaN rows {P}..{P + extra - 1}, steps {P}..{P + 24}", flush=True)
+    for t in rng.integers(0, clean.vocab(), 25):
+        a, b = clean.step(int(t), 1), dirty.step(int(t), 1)
+        assert np.isfinite(b).all(), f"non-finite logits at position {dirty.pos() - 1}"
+        np.testing.assert_array_equal(b, a)
+    clean.close(); dirty.close()
+
+
 def test_errors_are_reported(synth):
     path = synth("mini")
     gpu = qa.HipLlama.load(path, max_ctx=8)
