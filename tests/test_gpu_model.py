@@ -93,15 +93,16 @@ def test_snapshot_restore_rewind(synth):
     assert gpu.pos() == 20
 
 
-@pytest.mark.parametrize("cfg,path", [("mini128", "fused"), ("mini128", "single"), ("mini128", "splits"),
-                                      ("mini", "fused"), ("mini", "splits"), ("mini_r7", "fused")])
-def test_stale_nan_rows_past_context(cfg, path, synth, monkeypatch):
+@pytest.mark.parametrize("cfg,path,P", [("mini128", "fused", 45), ("mini128", "single", 45), ("mini128", "splits", 45),
+                                        ("mini", "fused", 45), ("mini", "splits", 45), ("mini_r7", "fused", 45),
+                                        ("mini128", "fused", 560), ("mini", "fused", 560)])
+def test_stale_nan_rows_past_context(cfg, path, P, synth, monkeypatch):
     """cache rows past the context hold whatever a longer sequence left there - NaN here (a restored snapshot 19
     positions longer, then a rewind).  The decode attention loads whole 32-position blocks of K and V; the rows past
     the context (or past a split's end) must not reach the output: their scores are -inf and their V rows are zeroed
     in LDS (0 x NaN would be NaN).  The logits of every step through that region equal a clean cache's bit for bit, on
     the fused attention + wo kernel, the one-split attention kernel and forced small splits (a partial block at every
-    split's end)"""
+    split's end); at 560 positions the fused kernel's waves run three blocks each in its block loop"""
     if path != "fused":
         monkeypatch.setenv("QPH_AWO_MAX", "0")
     if path == "splits":
@@ -110,10 +111,10 @@ def test_stale_nan_rows_past_context(cfg, path, synth, monkeypatch):
     model = synth(cfg)
     shape = qa.CONFIGS[cfg]
     kvd = shape.kv_heads * shape.head_dim
-    clean = qa.HipLlama.load(model, max_ctx=128)
-    dirty = qa.HipLlama.load(model, max_ctx=128)
+    clean = qa.HipLlama.load(model, max_ctx=P + 80)
+    dirty = qa.HipLlama.load(model, max_ctx=P + 80)
     rng = np.random.default_rng(5)
-    P, extra = 45, 19
+    extra = 19
     clean.prefill(rng.integers(0, clean.vocab(), P).astype(np.int32), 0)
     pos, k, v = split_snapshot(clean.snapshot(), shape.layers, kvd)
     assert pos == P
